@@ -1,0 +1,130 @@
+/*
+ * tabicl_attn.h - C ABI of the MI355X (gfx950) small-head and cached-KV attention library
+ * (libtabicl_attn.so).
+ *
+ * Every entry point takes raw device pointers, element strides and sizes, a dtype code and a
+ * hipStream_t (passed as void* so that this header needs no HIP include). Outputs are allocated by
+ * the caller. Return value: 0 = ok, >0 = unsupported shape or argument (the caller falls back),
+ * <0 = HIP launch error. tabicl_attn_last_error() gives the message of the last non-zero status
+ * on the calling host thread. No entry point synchronizes the stream, allocates device memory or
+ * keeps mutable global state; all are safe to call from any host thread.
+ *
+ * Layout conventions (the reference's merged-head layout): E = h * d with d = 16 for the small-head
+ * ops, rows are E (q/k/v), 2E (packed K|V) or 3E (packed Q|K|V) wide, heads are contiguous d-wide
+ * column blocks. Softmax is fp32; scores accumulate in fp32; probabilities are cast to the value
+ * dtype before the PV product; outputs are written in the query dtype.
+ */
+#ifndef TABICL_ATTN_H
+#define TABICL_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define TABICL_DTYPE_BF16 0
+#define TABICL_DTYPE_F32 1
+
+/* RoPE codes, as returned by rope_tables (reference scripts/tabicl_tpu_pallas_attn.py:681-698) */
+#define TABICL_ROPE_NONE 0
+#define TABICL_ROPE_PAIRS 1
+#define TABICL_ROPE_HALVES 2
+
+/* op codes for tabicl_attn_supported */
+#define TABICL_OP_HX 0
+#define TABICL_OP_HXQ 1
+#define TABICL_OP_PK_SELF 2
+#define TABICL_OP_PK_CROSS 3
+#define TABICL_OP_ICL 4
+
+/*
+ * Merged-head small-head attention, q pre-scaled.
+ * Replaces tabicl_pk::hx_fwd (reference scripts/tabicl_tpu_pallas_attn.py:179-182, 194, 767-790).
+ * q [B, Lq, E], k/v [B, Lk, E] contiguous; bias fp32 [bias_b, Lk] with bias_b in {1, B} or NULL;
+ * out [B, Lq, E]. Any Lk >= 1 (the reference caps Lk at 1024; this kernel streams key tiles).
+ */
+int tabicl_hx_fwd(const void* q, const void* k, const void* v, const float* bias, int64_t bias_b,
+                  void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
+                  void* stream);
+
+/*
+ * Few queries over many keys with a key-validity length, q pre-scaled, K/V read from the packed
+ * [B, Lk, 2E] projection (K = columns [0, E), V = columns [E, 2E)).
+ * Replaces tabicl_pk::hxq_fwd (reference scripts/tabicl_tpu_pallas_attn.py:299-306, 323-336).
+ * valid: device int32 [valid_n] with valid_n in {1, B} (valid_n = B extends the reference to ragged
+ * batches); keys at positions >= valid are ignored; a row with no valid key is written as 0.
+ */
+int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const void* kv, void* out,
+                   int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
+                   void* stream);
+
+/*
+ * Self attention over the packed in-projection qkv [B, L, 3E] with in-kernel RoPE on q and k, then
+ * q * scale (fp32, cast to the input dtype), additive fp32 key bias.
+ * Replaces tabicl_pk::pk_self_fwd (reference scripts/tabicl_tpu_pallas_attn.py:611-615, 722-732).
+ * cos/sin: fp32 [L, E] tables (ignored when rope == TABICL_ROPE_NONE); out [B, L, E].
+ */
+int tabicl_pk_self_fwd(const void* qkv, const float* bias, int64_t bias_b, const float* cos_t,
+                       const float* sin_t, void* out, int64_t B, int64_t L, int64_t E, int32_t h,
+                       int32_t rope, int32_t half, int32_t rot, float scale, int32_t dtype,
+                       void* stream);
+
+/*
+ * Cross attention: q [B, Lq, E] (q_b = 1 broadcasts one query set over the batch), packed kv
+ * [B, Lk, 2E]; RoPE with positions 0..Lq-1 on q (cq/sq [Lq, E]) and 0..Lk-1 on k (ck/sk [Lk, E]).
+ * Replaces tabicl_pk::pk_cross_fwd (reference scripts/tabicl_tpu_pallas_attn.py:625-630, 735-752).
+ */
+int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float* bias,
+                        int64_t bias_b, const float* cq, const float* sq, const float* ck,
+                        const float* sk, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                        int32_t h, int32_t rope, int32_t half, int32_t rot, float scale,
+                        int32_t dtype, void* stream);
+
+/*
+ * Dataset-wise in-context attention over cached train-row K/V (head_dim 64).
+ * Replaces the Splash hook _tpu_pallas_splash_sdpa / tabicl::tpu_splash_sdpa_{seg,full}
+ * (reference results/tpu_patch.diff:95-155; scripts/tabicl_tpu_bucketed.py:221-246).
+ * q [N, H, Tq, D], k/v [N, H, Tkv, D], out [N, H, Tq, D]; every tensor has a contiguous last dim and
+ * arbitrary element strides for n, h and row (so a [est, block, head, row, d] cache is passed as
+ * views). q is NOT pre-scaled: scores are multiplied by `scale` (D^-0.5 in the reference) in fp32.
+ * valid: device int32 [valid_n] (valid_n in {1, N}) or NULL (= Tkv): keys >= valid are masked;
+ * no padding of q or k is required. A query with no valid key gets output 0.
+ */
+int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
+                   int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                   int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh,
+                   int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn,
+                   int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* stream);
+
+/*
+ * Fit-time cache append: copies rows [0, T) of one block's K and V (src [N, H, T, D] with element
+ * strides) into rows [row0, row0 + T) of that block's slice of the [N, NB, H, cap, D] caches
+ * (dst pointers already offset to the block; element strides dst_sn, dst_sh, row stride D).
+ * Replaces the per-block `k_l.to(cache_dtype)` stores of the prefill
+ * (reference scripts/tabicl_tpu_bucketed.py:659-692, 736-764). src and dst share the dtype.
+ */
+int tabicl_icl_cache_append(void* k_cache, void* v_cache, int64_t dst_sn, int64_t dst_sh,
+                            int64_t row0, int64_t cap, const void* k_src, const void* v_src,
+                            int64_t src_sn, int64_t src_sh, int64_t src_st, int64_t N, int64_t H,
+                            int64_t T, int64_t D, int32_t dtype, void* stream);
+
+/*
+ * Shape predicate, mirroring supported / hxq_supported / packed_supported
+ * (reference scripts/tabicl_tpu_pallas_attn.py:319-320, 715-719, 762-764). Returns 1 if the op
+ * accepts the shape, 0 otherwise. Lq/Lk are query/key lengths, E the merged width (ICL: head dim).
+ */
+int tabicl_attn_supported(int32_t op, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype);
+
+/* Message of the last non-zero status returned on this host thread ("" if none). */
+const char* tabicl_attn_last_error(void);
+
+/* Library version string. */
+const char* tabicl_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TABICL_ATTN_H */

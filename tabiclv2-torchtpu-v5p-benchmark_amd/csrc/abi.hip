@@ -1,0 +1,259 @@
+// C ABI of libtabicl_attn.so: argument checks, stride/layout translation from the reference's op
+// signatures to the two kernel families, and the fit-time cache append kernel.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/tabicl_attn.h"
+#include "common.h"
+
+int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
+                          int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
+                          int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
+                          int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
+                          int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
+                          hipStream_t stream);
+int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
+                            int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
+                            const float* bias, int64_t bias_sb, const int32_t* valid,
+                            int64_t valid_n, const float* cq, const float* sq, const float* ck,
+                            const float* sk, int rope, int half, int rot, float scale, int64_t B,
+                            int64_t Lq, int64_t Lk, int dtype, hipStream_t stream);
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int launch_status(int err, const char* what) {
+  if (err == 0) return 0;
+  return fail(-err, "%s: HIP launch failed: %s", what, hipGetErrorString((hipError_t)err));
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+size_t esize(int32_t dtype) { return dtype == TABICL_DTYPE_BF16 ? 2 : 4; }
+bool stride_ok(int64_t s, int32_t dtype) { return (s * (int64_t)esize(dtype)) % 16 == 0; }
+
+// Shape rules of the small-head kernel: d = 16, h = 8, E = 128.
+int smallhead_shape(const char* op, int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h,
+                    int32_t dtype) {
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
+    return fail(1, "%s: dtype code %d not supported", op, dtype);
+  if (E != 128 || h != 8)
+    return fail(1, "%s: needs E == 128 and h == 8 (head dim 16), got E=%lld h=%d", op,
+                (long long)E, h);
+  if (B < 0 || Lq < 0 || Lk < 1 || B > (1LL << 30) || Lq > (1LL << 30) || Lk > (1LL << 30))
+    return fail(1, "%s: bad sizes B=%lld Lq=%lld Lk=%lld", op, (long long)B, (long long)Lq,
+                (long long)Lk);
+  return 0;
+}
+
+int rope_args(const char* op, int32_t rope, int32_t half, int32_t rot) {
+  if (rope == TABICL_ROPE_NONE) return 0;
+  if (rope != TABICL_ROPE_PAIRS && rope != TABICL_ROPE_HALVES)
+    return fail(1, "%s: rope code %d not supported", op, rope);
+  if (rot < 2 || rot > 16 || (rot & 1) || half * 2 != rot)
+    return fail(1, "%s: rope needs even rot in [2, 16] and half == rot/2 (rot=%d half=%d)", op,
+                rot, half);
+  return 0;
+}
+
+template <typename T>
+__global__ void cache_append_kernel(T* kc, T* vc, int64_t dst_sn, int64_t dst_sh, int64_t row0,
+                                    const T* ks, const T* vs, int64_t src_sn, int64_t src_sh,
+                                    int64_t src_st, int H, int T_rows, int D) {
+  constexpr int EPC = 16 / sizeof(T);
+  const int cpr = D / EPC;
+  const int64_t total = (int64_t)gridDim.y * H * T_rows * cpr;  // gridDim.y = N
+  const int n = blockIdx.y;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total / gridDim.y;
+       c += (int64_t)gridDim.x * blockDim.x) {
+    const int cc = (int)(c % cpr);
+    const int64_t rowg = c / cpr;
+    const int t = (int)(rowg % T_rows);
+    const int h = (int)(rowg / T_rows);
+    const int64_t so = n * src_sn + h * src_sh + t * src_st + cc * EPC;
+    const int64_t dofs = n * dst_sn + h * dst_sh + (row0 + t) * D + cc * EPC;
+    *(uint4*)(kc + dofs) = ldg16(ks + so);
+    *(uint4*)(vc + dofs) = ldg16(vs + so);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tabicl_attn_last_error(void) { return g_err; }
+
+const char* tabicl_attn_version(void) { return "tabicl_attn 0.1 gfx950"; }
+
+int tabicl_attn_supported(int32_t op, int64_t Lq, int64_t Lk, int64_t E, int32_t h,
+                          int32_t dtype) {
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) return 0;
+  if (Lq < 0 || Lk < 1 || Lq > (1LL << 30) || Lk > (1LL << 30)) return 0;
+  switch (op) {
+    case TABICL_OP_HX:
+    case TABICL_OP_HXQ:
+    case TABICL_OP_PK_SELF:
+    case TABICL_OP_PK_CROSS:
+      return E == 128 && h == 8;
+    case TABICL_OP_ICL:
+      return E == 64;
+    default:
+      return 0;
+  }
+}
+
+int tabicl_hx_fwd(const void* q, const void* k, const void* v, const float* bias, int64_t bias_b,
+                  void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
+                  void* stream) {
+  int st = smallhead_shape("hx_fwd", B, Lq, Lk, E, h, dtype);
+  if (st) return st;
+  if (bias && bias_b != 1 && bias_b != B)
+    return fail(1, "hx_fwd: bias batch %lld must be 1 or B=%lld", (long long)bias_b, (long long)B);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (bias && !aligned16(bias)))
+    return fail(1, "hx_fwd: pointers must be 16-byte aligned");
+  if (B == 0 || Lq == 0) return 0;
+  return launch_status(
+      tabicl_launch_smallhead(q, Lq * E, E, k, Lk * E, E, v, Lk * E, E, out, bias,
+                              bias && bias_b == B ? Lk : 0, nullptr, 0, nullptr, nullptr, nullptr,
+                              nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype, (hipStream_t)stream),
+      "hx_fwd");
+}
+
+int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const void* kv, void* out,
+                   int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
+                   void* stream) {
+  int st = smallhead_shape("hxq_fwd", B, Lq, Lk, E, h, dtype);
+  if (st) return st;
+  if (!valid || (valid_n != 1 && valid_n != B))
+    return fail(1, "hxq_fwd: valid must hold 1 or B=%lld entries (got %lld)", (long long)B,
+                (long long)valid_n);
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out))
+    return fail(1, "hxq_fwd: pointers must be 16-byte aligned");
+  if (B == 0 || Lq == 0) return 0;
+  const char* kvb = (const char*)kv;
+  return launch_status(
+      tabicl_launch_smallhead(q, Lq * E, E, kvb, Lk * 2 * E, 2 * E, kvb + E * esize(dtype),
+                              Lk * 2 * E, 2 * E, out, nullptr, 0, valid, valid_n, nullptr, nullptr,
+                              nullptr, nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype,
+                              (hipStream_t)stream),
+      "hxq_fwd");
+}
+
+int tabicl_pk_self_fwd(const void* qkv, const float* bias, int64_t bias_b, const float* cos_t,
+                       const float* sin_t, void* out, int64_t B, int64_t L, int64_t E, int32_t h,
+                       int32_t rope, int32_t half, int32_t rot, float scale, int32_t dtype,
+                       void* stream) {
+  int st = smallhead_shape("pk_self_fwd", B, L, L, E, h, dtype);
+  if (st) return st;
+  if ((st = rope_args("pk_self_fwd", rope, half, rot))) return st;
+  if (rope && (!cos_t || !sin_t)) return fail(1, "pk_self_fwd: rope tables missing");
+  if (bias && bias_b != 1 && bias_b != B)
+    return fail(1, "pk_self_fwd: bias batch %lld must be 1 or B", (long long)bias_b);
+  if (!aligned16(qkv) || !aligned16(out) || (rope && (!aligned16(cos_t) || !aligned16(sin_t))))
+    return fail(1, "pk_self_fwd: pointers must be 16-byte aligned");
+  if (B == 0 || L == 0) return 0;
+  const char* base = (const char*)qkv;
+  const size_t es = esize(dtype);
+  return launch_status(
+      tabicl_launch_smallhead(base, L * 3 * E, 3 * E, base + E * es, L * 3 * E, 3 * E,
+                              base + 2 * E * es, L * 3 * E, 3 * E, out, bias,
+                              bias && bias_b == B ? L : 0, nullptr, 0, cos_t, sin_t, cos_t, sin_t,
+                              rope, half, rot, scale, B, L, L, dtype, (hipStream_t)stream),
+      "pk_self_fwd");
+}
+
+int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float* bias,
+                        int64_t bias_b, const float* cq, const float* sq, const float* ck,
+                        const float* sk, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                        int32_t h, int32_t rope, int32_t half, int32_t rot, float scale,
+                        int32_t dtype, void* stream) {
+  int st = smallhead_shape("pk_cross_fwd", B, Lq, Lk, E, h, dtype);
+  if (st) return st;
+  if ((st = rope_args("pk_cross_fwd", rope, half, rot))) return st;
+  if (rope && (!cq || !sq || !ck || !sk)) return fail(1, "pk_cross_fwd: rope tables missing");
+  if (q_b != 1 && q_b != B) return fail(1, "pk_cross_fwd: q batch must be 1 or B");
+  if (bias && bias_b != 1 && bias_b != B)
+    return fail(1, "pk_cross_fwd: bias batch %lld must be 1 or B", (long long)bias_b);
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out))
+    return fail(1, "pk_cross_fwd: pointers must be 16-byte aligned");
+  if (B == 0 || Lq == 0) return 0;
+  const char* kvb = (const char*)kv;
+  return launch_status(
+      tabicl_launch_smallhead(q, q_b == 1 && B > 1 ? 0 : Lq * E, E, kvb, Lk * 2 * E, 2 * E,
+                              kvb + E * esize(dtype), Lk * 2 * E, 2 * E, out, bias,
+                              bias && bias_b == B ? Lk : 0, nullptr, 0, cq, sq, ck, sk, rope, half,
+                              rot, scale, B, Lq, Lk, dtype, (hipStream_t)stream),
+      "pk_cross_fwd");
+}
+
+int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
+                   int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                   int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh,
+                   int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn,
+                   int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* stream) {
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
+    return fail(1, "icl_fwd: dtype code %d not supported", dtype);
+  if (D != 64) return fail(1, "icl_fwd: head dim must be 64, got %lld", (long long)D);
+  if (N < 0 || H < 0 || Tq < 0 || Tkv < 1 || Tq > (1LL << 30) || Tkv > (1LL << 30))
+    return fail(1, "icl_fwd: bad sizes");
+  if (valid && valid_n != 1 && valid_n != N)
+    return fail(1, "icl_fwd: valid must hold 1 or N entries");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(1, "icl_fwd: pointers must be 16-byte aligned");
+  const int64_t strides[12] = {q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st};
+  for (int i = 0; i < 12; ++i)
+    if (strides[i] < 0 || !stride_ok(strides[i], dtype))
+      return fail(1, "icl_fwd: strides must be non-negative multiples of 16 bytes");
+  if (N == 0 || H == 0 || Tq == 0) return 0;
+  if (N * H * ((Tq + 127) / 128) > (1LL << 31) - 1) return fail(1, "icl_fwd: grid too large");
+  return launch_status(
+      tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, q_sn, q_sh,
+                            q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale,
+                            dtype, (hipStream_t)stream),
+      "icl_fwd");
+}
+
+int tabicl_icl_cache_append(void* k_cache, void* v_cache, int64_t dst_sn, int64_t dst_sh,
+                            int64_t row0, int64_t cap, const void* k_src, const void* v_src,
+                            int64_t src_sn, int64_t src_sh, int64_t src_st, int64_t N, int64_t H,
+                            int64_t T, int64_t D, int32_t dtype, void* stream) {
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
+    return fail(1, "icl_cache_append: dtype code %d not supported", dtype);
+  if (D < 1 || (D * (int64_t)esize(dtype)) % 16) return fail(1, "icl_cache_append: bad head dim");
+  if (row0 < 0 || T < 0 || row0 + T > cap)
+    return fail(1, "icl_cache_append: rows [%lld, %lld) exceed capacity %lld", (long long)row0,
+                (long long)(row0 + T), (long long)cap);
+  if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(k_src) || !aligned16(v_src))
+    return fail(1, "icl_cache_append: pointers must be 16-byte aligned");
+  const int64_t s[5] = {dst_sn, dst_sh, src_sn, src_sh, src_st};
+  for (int i = 0; i < 5; ++i)
+    if (s[i] < 0 || !stride_ok(s[i], dtype))
+      return fail(1, "icl_cache_append: strides must be non-negative multiples of 16 bytes");
+  if (N == 0 || H == 0 || T == 0) return 0;
+  if (N > 65535) return fail(1, "icl_cache_append: N too large");
+  const int64_t per_n = H * T * (D * (int64_t)esize(dtype) / 16);
+  int64_t gx = (per_n + 255) / 256;
+  if (gx > 65536) gx = 65536;
+  hipStream_t s0 = (hipStream_t)stream;
+  if (dtype == TABICL_DTYPE_BF16)
+    hipLaunchKernelGGL(cache_append_kernel<bf16>, dim3((unsigned)gx, (unsigned)N), dim3(256), 0, s0,
+                       (bf16*)k_cache, (bf16*)v_cache, dst_sn, dst_sh, row0, (const bf16*)k_src,
+                       (const bf16*)v_src, src_sn, src_sh, src_st, (int)H, (int)T, (int)D);
+  else
+    hipLaunchKernelGGL(cache_append_kernel<float>, dim3((unsigned)gx, (unsigned)N), dim3(256), 0, s0,
+                       (float*)k_cache, (float*)v_cache, dst_sn, dst_sh, row0, (const float*)k_src,
+                       (const float*)v_src, src_sn, src_sh, src_st, (int)H, (int)T, (int)D);
+  return launch_status((int)hipGetLastError(), "icl_cache_append");
+}
+
+}  // extern "C"

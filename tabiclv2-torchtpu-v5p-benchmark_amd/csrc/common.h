@@ -1,0 +1,71 @@
+// Shared device helpers for the gfx950 attention kernels: vector types, MFMA wrappers with a
+// uniform lane layout for bf16 and fp32 operands, cross-lane reductions, XCD-aware block mapping.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define TA_LOG2E 1.4426950408889634f
+#define TA_NEG_INF (-__builtin_inff())
+
+// Operand vectors: N consecutive k-values of one row held by one lane.
+template <typename T, int N> struct OpVec;
+template <> struct OpVec<bf16, 4> { typedef bf16x4 type; };
+template <> struct OpVec<bf16, 8> { typedef bf16x8 type; };
+template <> struct OpVec<float, 4> { typedef f32x4 type; };
+template <> struct OpVec<float, 8> { typedef f32x8 type; };
+
+// 16x16 tile, 16-deep contraction. Lane l holds A[l%16][4*(l/16)+j] and B[4*(l/16)+j][l%16]
+// (j = 0..3); result lane l, reg r = C[4*(l/16)+r][l%16].
+// bf16: one v_mfma_f32_16x16x16_bf16. fp32: four v_mfma_f32_16x16x4_f32, the j-th one contracting
+// k = 4*kappa + j over kappa = l/16 (so the lane data is the same four values in both cases).
+__device__ __forceinline__ f32x4 mfma16x16x16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(f32x4 a, f32x4 b, f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
+  return c;
+}
+
+// 32x32 tile, 16-deep contraction. Lane l holds A[l%32][8*(l/32)+j] and B[8*(l/32)+j][l%32]
+// (j = 0..7); result lane l, reg r = C[8*(r/4) + 4*(l/32) + r%4][l%32].
+// bf16: one v_mfma_f32_32x32x16_bf16. fp32: eight v_mfma_f32_32x32x2_f32 (k = 8*kappa + j).
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(f32x8 a, f32x8 b, f32x16 c) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], c, 0, 0, 0);
+  return c;
+}
+
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+
+// Max / sum across the lane pairs (l, l^32) and quads (l, l^16, l^32, l^48).
+__device__ __forceinline__ float xor_max(float x, int mask) {
+  return fmaxf(x, __shfl_xor(x, mask, 64));
+}
+__device__ __forceinline__ float xor_sum(float x, int mask) { return x + __shfl_xor(x, mask, 64); }
+
+__device__ __forceinline__ bool wave_any(bool p) { return __ballot(p) != 0ull; }
+
+// Hardware dispatch places workgroup b on XCD b % 8. Map it to a work index so that each XCD
+// receives a contiguous range of work items (neighbouring items share K/V in that XCD's L2).
+__device__ __forceinline__ int xcd_remap(int bid, int nblk) {
+  const int q8 = nblk >> 3, r8 = nblk & 7;
+  const int xcd = bid & 7, idx = bid >> 3;
+  return xcd * q8 + (xcd < r8 ? xcd : r8) + idx;
+}
+
+struct u32x4 { uint32_t x, y, z, w; };
+__device__ __forceinline__ uint4 ldg16(const void* p) { return *(const uint4*)p; }

@@ -1,0 +1,344 @@
+// Fused small-head attention (8 heads x 16 dims, merged width E = 128) for gfx950.
+//
+// One kernel serves the four small-head ops of the reference (hx, hxq, pk_self, pk_cross;
+// scripts/tabicl_tpu_pallas_attn.py): q/k/v are read straight from their merged-head rows
+// (separate [B, L, E], packed K|V [B, L, 2E] or packed Q|K|V [B, L, 3E]) and the output is
+// written merged [B, Lq, E]. Per (batch, head):
+//   O = softmax(q' k'^T + bias [+ -inf past valid]) V,
+//   q' = cast(rope(q) * scale), k' = cast(rope(k)) (RoPE and scale in fp32; no RoPE = identity),
+// fp32 scores/softmax, probabilities cast to the value dtype before PV.
+//
+// Work decomposition: a workgroup of 8 waves owns one batch element and a block of 128 queries
+// (wave w: queries 16w..16w+15, all 8 heads; per-head online-softmax state in registers).
+// Keys stream through LDS in tiles of KT keys x all heads (K row-major, V transposed to
+// [E][KT], per-key bias pre-multiplied by log2(e), -inf past the valid length). When all keys
+// fit one tile the workgroup keeps them resident and walks several query blocks.
+// MFMA 16x16x16 (bf16) or 4 x 16x16x4 (fp32), in the orientation
+//   S^T (16 keys x 16 queries) = K Q^T,  O^T (16 dims x 16 queries) += V^T P^T
+// so that the S^T accumulator is already the B operand of the PV product and every softmax
+// statistic of a query lives in the four lanes l%16 + 16j.
+#include "common.h"
+
+namespace {
+
+constexpr int SH_E = 128;
+constexpr int SH_H = 8;
+constexpr int SH_D = 16;
+constexpr int SH_NW = 8;
+constexpr int SH_QB = 16 * SH_NW;
+constexpr float SH_LAZY = 8.0f;
+constexpr float SH_BIAS_FLOOR = -1e37f;
+
+struct ShParams {
+  const void* q;
+  int64_t q_sb, q_sr;
+  const void* k;
+  int64_t k_sb, k_sr;
+  const void* v;
+  int64_t v_sb, v_sr;
+  void* o;
+  int64_t o_sb, o_sr;
+  const float* bias;
+  int64_t bias_sb;
+  const int32_t* valid;
+  int valid_n;
+  const float* cq;
+  const float* sq;
+  const float* ck;
+  const float* sk;
+  int rope, half, rot;
+  float scale;
+  int B, Lq, Lk;
+  int nqb, qbpw, nwg_b;
+};
+
+template <typename T, int KT> struct ShLds {
+  static constexpr int PAD = 16 / sizeof(T);
+  static constexpr int KSTR = SH_E + PAD;
+  static constexpr int VSTR = KT + PAD;
+  static constexpr int K_ELEMS = KT * KSTR;
+  static constexpr int V_ELEMS = SH_E * VSTR;
+};
+
+// RoPE partner of dim jd (0..15) of a head: R(x)_jd = sign * x[partner]
+// (reference: x*cos + R(x)*sin, R = signed rotate-half per head, pairs or halves, zero past rot;
+// scripts/tabicl_tpu_pallas_attn.py:465-473).
+__device__ __forceinline__ void rope_partner(int jd, int rope, int half, int rot, int* partner,
+                                             float* sign) {
+  if (rope == 1) {
+    *partner = jd ^ 1;
+    *sign = (jd & 1) ? 1.f : -1.f;
+  } else if (jd < half) {
+    *partner = jd + half;
+    *sign = -1.f;
+  } else {
+    *partner = jd - half;
+    *sign = 1.f;
+  }
+  if (jd >= rot) {
+    *partner = jd;
+    *sign = 0.f;
+  }
+}
+
+// Four consecutive dims d0..d0+3 (d0 % 4 == 0) of one row after RoPE, in fp32.
+template <typename T>
+__device__ __forceinline__ f32x4 rope4(const T* row, const float* cs, const float* sn, int d0,
+                                       int rope, int half, int rot) {
+  const int hb = d0 & ~15;
+  const float4 c = *(const float4*)(cs + d0);
+  const float4 s = *(const float4*)(sn + d0);
+  const float cv[4] = {c.x, c.y, c.z, c.w};
+  const float sv[4] = {s.x, s.y, s.z, s.w};
+  f32x4 y;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    int pt;
+    float sg;
+    rope_partner((d0 & 15) + r, rope, half, rot, &pt, &sg);
+    const float x = to_f32<T>(row[d0 + r]);
+    const float xp = to_f32<T>(row[hb + pt]);
+    y[r] = x * cv[r] + sg * xp * sv[r];
+  }
+  return y;
+}
+
+template <typename T, int KT>
+__device__ __forceinline__ void sh_fill(const ShParams& p, T* lds_k, T* lds_vt, float* lds_b2,
+                                        int b, int k0, int lk) {
+  typedef ShLds<T, KT> L;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const T* kbase = (const T*)p.k + b * p.k_sb;
+  const T* vbase = (const T*)p.v + b * p.v_sb;
+  // K: unit = (key row, 4 dims); RoPE applied in fp32 then cast
+#pragma unroll 1
+  for (int u = tid; u < KT * (SH_E / 4); u += nt) {
+    const int row = u >> 5, d0 = (u & 31) * 4, key = k0 + row;
+    typedef typename OpVec<T, 4>::type Op4;
+    Op4 val;
+    if (key < lk) {
+      const T* src = kbase + (int64_t)key * p.k_sr;
+      if (p.rope) {
+        const f32x4 y = rope4<T>(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0,
+                                 p.rope, p.half, p.rot);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) val[r] = from_f32<T>(y[r]);
+      } else {
+        val = *(const Op4*)(src + d0);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) val[r] = from_f32<T>(0.f);
+    }
+    *(Op4*)(lds_k + row * L::KSTR + d0) = val;
+  }
+  // V: unit = (key pair, head), transposed store [E][KT]
+#pragma unroll 1
+  for (int u = tid; u < (KT / 2) * SH_H; u += nt) {
+    const int pr = u >> 3, g = u & 7, key = k0 + 2 * pr;
+    constexpr int EPC = 16 / sizeof(T);
+    union { uint4 u4[SH_D / EPC]; T e[SH_D]; } a, c;
+#pragma unroll
+    for (int i = 0; i < SH_D / EPC; ++i) {
+      a.u4[i] = make_uint4(0, 0, 0, 0);
+      c.u4[i] = make_uint4(0, 0, 0, 0);
+    }
+    if (key < lk) {
+#pragma unroll
+      for (int i = 0; i < SH_D / EPC; ++i)
+        a.u4[i] = ldg16(vbase + (int64_t)key * p.v_sr + g * SH_D + i * EPC);
+    }
+    if (key + 1 < lk) {
+#pragma unroll
+      for (int i = 0; i < SH_D / EPC; ++i)
+        c.u4[i] = ldg16(vbase + (int64_t)(key + 1) * p.v_sr + g * SH_D + i * EPC);
+    }
+    typedef T T2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int j = 0; j < SH_D; ++j) {
+      T2 pair;
+      pair[0] = a.e[j];
+      pair[1] = c.e[j];
+      *(T2*)(lds_vt + (g * SH_D + j) * L::VSTR + 2 * pr) = pair;
+    }
+  }
+  // per-key additive term in log2 units
+  for (int j = tid; j < KT; j += nt) {
+    const int key = k0 + j;
+    float b2 = TA_NEG_INF;
+    if (key < lk) {
+      b2 = 0.f;
+      if (p.bias) b2 = fmaxf(p.bias[b * p.bias_sb + key] * TA_LOG2E, SH_BIAS_FLOOR);
+    }
+    lds_b2[j] = b2;
+  }
+}
+
+template <typename T, int KT>
+__global__ __launch_bounds__(SH_NW * 64) void smallhead_fwd_kernel(ShParams p) {
+  typedef ShLds<T, KT> L;
+  typedef typename OpVec<T, 4>::type Op4;
+  constexpr int NKT = KT / 16;
+  __shared__ __attribute__((aligned(16))) T lds_k[L::K_ELEMS];
+  __shared__ __attribute__((aligned(16))) T lds_vt[L::V_ELEMS];
+  __shared__ __attribute__((aligned(16))) float lds_b2[KT];
+
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = work / p.nwg_b;
+  const int qb0 = (work % p.nwg_b) * p.qbpw;
+
+  int lk = p.Lk;
+  if (p.valid) {
+    int vl = p.valid[p.valid_n == 1 ? 0 : b];
+    vl = vl < 0 ? 0 : vl;
+    lk = vl < lk ? vl : lk;
+  }
+  const int ntiles = (lk + KT - 1) / KT;
+  const bool resident = ntiles <= 1;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, kap = lane >> 4;
+  const T* qbase = (const T*)p.q + b * p.q_sb;
+  T* obase = (T*)p.o + b * p.o_sb;
+
+  for (int qbi = 0; qbi < p.qbpw; ++qbi) {
+    const int qb = qb0 + qbi;
+    if (qb >= p.nqb) break;
+    const int qw0 = qb * SH_QB + wave * 16;
+    const int qi = qw0 + l16;
+    const bool qok = qi < p.Lq;
+    const bool wave_active = qw0 < p.Lq;
+
+    Op4 qop[SH_H];
+    f32x4 o[SH_H];
+    float m_run[SH_H], l_run[SH_H];
+#pragma unroll
+    for (int g = 0; g < SH_H; ++g) {
+      m_run[g] = TA_NEG_INF;
+      l_run[g] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { o[g][r] = 0.f; qop[g][r] = from_f32<T>(0.f); }
+    }
+    if (qok) {
+      const T* qrow = qbase + (int64_t)qi * p.q_sr;
+      if (p.rope) {
+#pragma unroll
+        for (int g = 0; g < SH_H; ++g) {
+          const f32x4 y = rope4<T>(qrow, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E,
+                                   g * SH_D + 4 * kap, p.rope, p.half, p.rot);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) qop[g][r] = from_f32<T>(y[r] * p.scale);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < SH_H; ++g) {
+          const Op4 raw = *(const Op4*)(qrow + g * SH_D + 4 * kap);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            qop[g][r] = p.scale == 1.f ? raw[r] : from_f32<T>(to_f32<T>(raw[r]) * p.scale);
+        }
+      }
+    }
+
+    for (int t = 0; t < ntiles; ++t) {
+      if (!(resident && qbi > 0)) {
+        __syncthreads();
+        sh_fill<T, KT>(p, lds_k, lds_vt, lds_b2, b, t * KT, lk);
+        __syncthreads();
+      }
+      if (!wave_active) continue;
+#pragma unroll
+      for (int g = 0; g < SH_H; ++g) {
+        f32x4 s[NKT];
+        float mx = TA_NEG_INF;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+          const Op4 a = *(const Op4*)(lds_k + (16 * kt + l16) * L::KSTR + g * SH_D + 4 * kap);
+          f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          s[kt] = mfma16x16x16(a, qop[g], z);
+          const f32x4 b2 = *(const f32x4*)(lds_b2 + 16 * kt + 4 * kap);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            s[kt][r] = fmaf(s[kt][r], TA_LOG2E, b2[r]);
+            mx = fmaxf(mx, s[kt][r]);
+          }
+        }
+        mx = xor_max(mx, 16);
+        mx = xor_max(mx, 32);
+        const float m_new = fmaxf(m_run[g], mx);
+        if (wave_any(m_new - m_run[g] > SH_LAZY)) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run[g] - m_new);
+          l_run[g] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[g][r] *= alpha;
+          m_run[g] = m_new;
+        }
+        const float mr = m_run[g];
+        float lsum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+          Op4 pv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(s[kt][r] - mr);
+            lsum += pr;
+            pv[r] = from_f32<T>(pr);
+          }
+          const Op4 a = *(const Op4*)(lds_vt + (g * SH_D + l16) * L::VSTR + 16 * kt + 4 * kap);
+          o[g] = mfma16x16x16(a, pv, o[g]);
+        }
+        l_run[g] += lsum;
+        // keep the per-head bodies apart: interleaving heads only raises register pressure
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+
+    if (qok) {
+      T* orow = obase + (int64_t)qi * p.o_sr;
+#pragma unroll
+      for (int g = 0; g < SH_H; ++g) {
+        float lt = xor_sum(l_run[g], 16);
+        lt = xor_sum(lt, 32);
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        Op4 ov;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ov[r] = from_f32<T>(o[g][r] * inv);
+        *(Op4*)(orow + g * SH_D + 4 * kap) = ov;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
+                            int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
+                            const float* bias, int64_t bias_sb, const int32_t* valid,
+                            int64_t valid_n, const float* cq, const float* sq, const float* ck,
+                            const float* sk, int rope, int half, int rot, float scale, int64_t B,
+                            int64_t Lq, int64_t Lk, int dtype, hipStream_t stream) {
+  ShParams p;
+  p.q = q; p.q_sb = q_sb; p.q_sr = q_sr;
+  p.k = k; p.k_sb = k_sb; p.k_sr = k_sr;
+  p.v = v; p.v_sb = v_sb; p.v_sr = v_sr;
+  p.o = o; p.o_sb = Lq * SH_E; p.o_sr = SH_E;
+  p.bias = bias; p.bias_sb = bias_sb;
+  p.valid = valid; p.valid_n = (int)valid_n;
+  p.cq = cq; p.sq = sq; p.ck = ck; p.sk = sk;
+  p.rope = rope; p.half = half; p.rot = rot;
+  p.scale = scale;
+  p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
+  p.nqb = (int)((Lq + SH_QB - 1) / SH_QB);
+  const int kt = 64;
+  // all keys in one tile: keep them resident and walk up to 8 query blocks per workgroup
+  p.qbpw = Lk <= kt ? (p.nqb < 8 ? p.nqb : 8) : 1;
+  p.nwg_b = (p.nqb + p.qbpw - 1) / p.qbpw;
+  const int64_t nblk = B * (int64_t)p.nwg_b;
+  if (dtype == 0)
+    hipLaunchKernelGGL((smallhead_fwd_kernel<bf16, 64>), dim3((unsigned)nblk), dim3(SH_NW * 64), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((smallhead_fwd_kernel<float, 64>), dim3((unsigned)nblk), dim3(SH_NW * 64), 0,
+                       stream, p);
+  return (int)hipGetLastError();
+}

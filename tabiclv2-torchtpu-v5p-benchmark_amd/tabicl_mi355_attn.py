@@ -1,0 +1,296 @@
+"""Fused small-head attention (8 heads x 16 dims) on MI355X, as torch custom ops over HIP kernels.
+
+Drop-in for the reference's scripts/tabicl_tpu_pallas_attn.py: same public functions, argument
+meaning and op names (tabicl_pk::hx_fwd, hxq_fwd, pk_self_fwd, pk_cross_fwd), with the math done by
+hand-written gfx950 kernels in libtabicl_attn.so (C ABI: include/tabicl_attn.h).
+
+  hx_attention(q, k, v, h, key_bias=None)            q pre-scaled; merged [.., L, E] in and out
+  hxq_attention(q, kv, valid_len, h)                 few queries, packed [.., Lk, 2E] K|V, keys >= valid ignored
+  pk_self_attention(qkv, h, key_bias, rope, scale)   packed [.., L, 3E], in-kernel RoPE + scale
+  pk_cross_attention(q, kv, h, key_bias, rope, scale)
+
+Semantics per head g: softmax(q_g k_g^T + bias) v_g with fp32 scores and softmax, probabilities cast
+to the value dtype before the PV product, output in the query dtype. Differences from the reference,
+all extensions: any key length (keys stream through LDS; the reference stops at 1024), any query
+length, a per-batch valid length for hxq, and a defined output (0) for a row with no valid key.
+The HIP library is the only compute path: the ops raise when it is missing (no CPU fallback).
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+import tabicl_mi355_native as _nat
+
+_NEG = -1e30
+_MAX_LKP = int(os.environ.get("TABICL_TPU_PK_MAX_LK", "1024") or 1024)  # reference knob; see supported()
+H_DEFAULT = 8
+
+
+# ---------------------------------------------------------------------------------------------
+# host-side helpers with the reference's names and meaning
+# ---------------------------------------------------------------------------------------------
+def _pick_bq(Lq: int, lkp: int) -> int:
+    """Query block of the reference kernel (scripts/tabicl_tpu_pallas_attn.py:36-44): divides Lq,
+    multiple of 8 (or == Lq), cap min(512, 65536 // lkp). Kept for the op schema; the HIP kernel
+    tiles queries by 128 itself and accepts any Lq."""
+    cap = max(8, min(512, 65536 // lkp))
+    if Lq <= cap:
+        return Lq
+    for bq in range(cap - cap % 8, 7, -8):
+        if Lq % bq == 0:
+            return bq
+    return 0
+
+
+def _pick_bk(Lk: int) -> int:
+    """Key block of the reference hxq kernel (scripts/tabicl_tpu_pallas_attn.py:312-316)."""
+    for bk in (512, 1024, 256, 128):
+        if Lk % bk == 0:
+            return bk
+    return 0
+
+
+def _fp32_prec_code() -> int:
+    """fp32 matmul precision code (reference scripts/tabicl_tpu_pallas_attn.py:755-759): highest=2,
+    high=1, else 0. The HIP fp32 kernels always multiply in full fp32 (fp32 MFMA), i.e. 'highest'."""
+    p = torch.get_float32_matmul_precision()
+    return 2 if p == "highest" else 1 if p == "high" else 0
+
+
+def _bias3(key_bias: Optional[Tensor], lead, Lk: int, device) -> Tensor:
+    """Normalise an additive key bias to [1, 1, Lk] (shared) or [B, 1, Lk] fp32
+    (reference scripts/tabicl_tpu_pallas_attn.py:701-712)."""
+    if key_bias is None:
+        return torch.zeros(1, 1, Lk, device=device, dtype=torch.float32)
+    kb = key_bias.float()
+    while kb.dim() < len(lead) + 1:
+        kb = kb.unsqueeze(0)
+    if all(s_ == 1 for s_ in kb.shape[:-1]):
+        return kb.reshape(1, 1, Lk).contiguous()
+    B = 1
+    for s_ in lead:
+        B *= s_
+    return kb.expand(*lead, Lk).reshape(B, 1, Lk).contiguous()
+
+
+def rope_tables(rope_mod, L: int, E: int, h: int, device) -> tuple:  # noqa: ANN001
+    """(cos, sin) [L, E] fp32 tiled per head (cos=1, sin=0 beyond the rotary dims), rope code
+    (0 none, 1 pairs, 2 halves), half, rot (reference scripts/tabicl_tpu_pallas_attn.py:681-698).
+    rope_mod follows the upstream RotaryEmbedding surface: get_seq_pos, interleaved, freqs, forward."""
+    d = E // h
+    if rope_mod is None:
+        return (torch.ones(L, E, device=device), torch.zeros(L, E, device=device), 0, 0, 0)
+    seq = rope_mod.get_seq_pos(L, device=device, dtype=torch.float32)
+    if rope_mod.interleaved:
+        freqs = rope_mod.forward(seq, seq_len=L).float()
+    else:
+        f = seq.float().unsqueeze(-1) * rope_mod.freqs.float().to(device)
+        freqs = torch.cat([f, f], dim=-1)
+    rot = freqs.shape[-1]
+    cos, sin = freqs.cos(), freqs.sin()
+    if rot < d:
+        cos = torch.cat([cos, torch.ones(L, d - rot, device=device)], dim=-1)
+        sin = torch.cat([sin, torch.zeros(L, d - rot, device=device)], dim=-1)
+    return (cos.repeat(1, h).contiguous(), sin.repeat(1, h).contiguous(), 1 if rope_mod.interleaved else 2,
+            rot // 2, rot)
+
+
+def _dt_ok(dt: torch.dtype) -> bool:
+    return dt in (torch.bfloat16, torch.float32)
+
+
+def supported(Lq: int, Lk: int, E: int, h: int, dtype: torch.dtype = torch.bfloat16) -> bool:
+    """hx kernel shape predicate (reference scripts/tabicl_tpu_pallas_attn.py:762-764). The HIP
+    kernel needs E == 128, h == 8; it has no key-length cap (keys stream through LDS)."""
+    return _dt_ok(dtype) and _nat.supported(_nat.OP_HX, Lq, Lk, E, h, dtype)
+
+
+def hxq_supported(Lq: int, Lk: int, E: int, h: int, dtype: torch.dtype = torch.bfloat16) -> bool:
+    """hxq predicate (reference scripts/tabicl_tpu_pallas_attn.py:319-320): the reference needs
+    Lq % 8 == 0, Lq <= 256 and a key block dividing Lk; the HIP kernel takes any Lq and Lk."""
+    return _dt_ok(dtype) and _nat.supported(_nat.OP_HXQ, Lq, Lk, E, h, dtype)
+
+
+def packed_supported(Lq: int, Lk: int, E: int, h: int, self_attn: bool,
+                     dtype: torch.dtype = torch.bfloat16) -> bool:
+    """pk_self / pk_cross predicate (reference scripts/tabicl_tpu_pallas_attn.py:715-719)."""
+    op = _nat.OP_PK_SELF if self_attn else _nat.OP_PK_CROSS
+    if self_attn and Lq != Lk:
+        return False
+    return _dt_ok(dtype) and _nat.supported(op, Lq, Lk, E, h, dtype)
+
+
+def hxf_supported(hq: int, Lk: int, E: int) -> bool:  # noqa: ARG001
+    """Folded first-ISAB kernel (reference :425-426) is not built: always False, so the dispatcher
+    keeps the hxq path (the reference's best preset does not enable hxf either)."""
+    return False
+
+
+# ---------------------------------------------------------------------------------------------
+# torch custom ops (reference op names and schemas)
+# ---------------------------------------------------------------------------------------------
+def _contig(*ts: Tensor) -> None:
+    for t in ts:
+        if not t.is_contiguous():
+            raise ValueError("tabicl_pk ops need contiguous inputs")
+
+
+@torch.library.custom_op("tabicl_pk::hx_fwd", mutates_args=())
+def _hx_fwd(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, h: int, lkp: int, bq: int, prec: int) -> Tensor:
+    _nat.require_device(q, k, v, bias)
+    _contig(q, k, v, bias)
+    B, Lq, E = q.shape
+    Lk = k.shape[1]
+    out = torch.empty_like(q)
+    _nat.call("tabicl_hx_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), bias.shape[0],
+              out.data_ptr(), B, Lq, Lk, E, h, _nat.dtype_code(q.dtype), _nat.stream_of(q))
+    return out
+
+
+@_hx_fwd.register_fake
+def _(q, k, v, bias, h, lkp, bq, prec):  # noqa: ANN001
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("tabicl_pk::hxq_fwd", mutates_args=())
+def _hxq_fwd(valid: Tensor, q: Tensor, kv: Tensor, h: int, bk: int, prec: int) -> Tensor:
+    _nat.require_device(valid, q, kv)
+    _contig(valid, q, kv)
+    B, Lq, E = q.shape
+    Lk = kv.shape[1]
+    if valid.dtype != torch.int32:
+        raise ValueError("valid must be int32")
+    out = torch.empty_like(q)
+    _nat.call("tabicl_hxq_fwd", valid.data_ptr(), valid.numel(), q.data_ptr(), kv.data_ptr(), out.data_ptr(),
+              B, Lq, Lk, E, h, _nat.dtype_code(q.dtype), _nat.stream_of(q))
+    return out
+
+
+@_hxq_fwd.register_fake
+def _(valid, q, kv, h, bk, prec):  # noqa: ANN001
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("tabicl_pk::pk_self_fwd", mutates_args=())
+def _pk_self_fwd(qkv: Tensor, bias: Tensor, cos: Tensor, sin: Tensor, h: int, lkp: int, rope: int, half: int,
+                 rot: int, prec: int, scale: float) -> Tensor:
+    _nat.require_device(qkv, bias, cos, sin)
+    _contig(qkv, bias, cos, sin)
+    B, L, E3 = qkv.shape
+    E = E3 // 3
+    out = torch.empty(B, L, E, device=qkv.device, dtype=qkv.dtype)
+    _nat.call("tabicl_pk_self_fwd", qkv.data_ptr(), bias.data_ptr(), bias.shape[0], cos.data_ptr(), sin.data_ptr(),
+              out.data_ptr(), B, L, E, h, rope, half, rot, float(scale), _nat.dtype_code(qkv.dtype),
+              _nat.stream_of(qkv))
+    return out
+
+
+@_pk_self_fwd.register_fake
+def _(qkv, bias, cos, sin, h, lkp, rope, half, rot, prec, scale):  # noqa: ANN001
+    B, L, E3 = qkv.shape
+    return qkv.new_empty(B, L, E3 // 3)
+
+
+@torch.library.custom_op("tabicl_pk::pk_cross_fwd", mutates_args=())
+def _pk_cross_fwd(q: Tensor, kv: Tensor, bias: Tensor, cq: Tensor, sq: Tensor, ck: Tensor, sk: Tensor, h: int,
+                  lkp: int, bq: int, rope: int, half: int, rot: int, prec: int, scale: float) -> Tensor:
+    _nat.require_device(q, kv, bias, cq, sq, ck, sk)
+    _contig(q, kv, bias, cq, sq, ck, sk)
+    Bq, Lq, E = q.shape
+    B, Lk, _ = kv.shape
+    out = torch.empty(B, Lq, E, device=q.device, dtype=q.dtype)
+    _nat.call("tabicl_pk_cross_fwd", q.data_ptr(), Bq, kv.data_ptr(), bias.data_ptr(), bias.shape[0],
+              cq.data_ptr(), sq.data_ptr(), ck.data_ptr(), sk.data_ptr(), out.data_ptr(), B, Lq, Lk, E, h,
+              rope, half, rot, float(scale), _nat.dtype_code(q.dtype), _nat.stream_of(q))
+    return out
+
+
+@_pk_cross_fwd.register_fake
+def _(q, kv, bias, cq, sq, ck, sk, h, lkp, bq, rope, half, rot, prec, scale):  # noqa: ANN001
+    return q.new_empty(kv.shape[0], q.shape[1], q.shape[2])
+
+
+HX_FWD = torch.ops.tabicl_pk.hx_fwd
+HXQ_FWD = torch.ops.tabicl_pk.hxq_fwd
+PK_SELF = torch.ops.tabicl_pk.pk_self_fwd
+PK_CROSS = torch.ops.tabicl_pk.pk_cross_fwd
+HXF_FWD = None
+
+
+# ---------------------------------------------------------------------------------------------
+# Python wrappers (reference signatures)
+# ---------------------------------------------------------------------------------------------
+def hx_attention(q: Tensor, k: Tensor, v: Tensor, h: int, key_bias: Optional[Tensor] = None) -> Tensor:
+    """q [..., Lq, E] (pre-scaled), k / v [..., Lk, E]; key_bias additive, broadcastable to [..., Lk]
+    (reference scripts/tabicl_tpu_pallas_attn.py:767-790)."""
+    lead = q.shape[:-2]
+    Lq, E = q.shape[-2], q.shape[-1]
+    Lk = k.shape[-2]
+    lkp = -(-Lk // 128) * 128
+    q3 = q.reshape(-1, Lq, E)
+    k3 = k.reshape(-1, Lk, E)
+    v3 = v.reshape(-1, Lk, E)
+    bias = _bias3(key_bias, lead, Lk, q.device)
+    prec = _fp32_prec_code() if q.dtype == torch.float32 else 0
+    out = HX_FWD(q3.contiguous(), k3.contiguous(), v3.contiguous(), bias, h, lkp, _pick_bq(Lq, lkp), prec)
+    return out.reshape(*lead, Lq, E)
+
+
+def hxq_attention(q: Tensor, kv: Tensor, valid_len: Tensor, h: int) -> Tensor:
+    """Inference only. q [..., Lq, E] (pre-scaled), kv [..., Lk, 2E] packed (K = lanes [0, E),
+    V = [E, 2E)); keys at positions >= valid_len are ignored (reference :323-336). valid_len may be
+    a scalar or hold one entry per flattened batch element (ragged batches)."""
+    lead = q.shape[:-2]
+    Lq, E = q.shape[-2], q.shape[-1]
+    Lk = kv.shape[-2]
+    q3 = q.reshape(-1, Lq, E).contiguous()
+    kv3 = kv.reshape(-1, Lk, 2 * E).contiguous()
+    if q3.shape[0] != kv3.shape[0]:
+        q3 = q3.expand(kv3.shape[0], Lq, E).contiguous()
+    valid = torch.as_tensor(valid_len, device=q.device).to(dtype=torch.int32).reshape(-1).contiguous()
+    prec = _fp32_prec_code() if q.dtype == torch.float32 else 0
+    out = HXQ_FWD(valid, q3, kv3, h, _pick_bk(Lk), prec)
+    return out.reshape(*lead, Lq, E) if len(lead) else out.reshape(Lq, E)
+
+
+def pk_self_attention(qkv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod, scale: float) -> Tensor:  # noqa: ANN001
+    """qkv [..., L, 3E] (packed in-projection), RoPE (optional) on q and k, returns [..., L, E]
+    (reference :722-732)."""
+    lead = qkv.shape[:-2]
+    L, E3 = qkv.shape[-2], qkv.shape[-1]
+    E = E3 // 3
+    lkp = -(-L // 128) * 128
+    cos, sin, rc, half, rot = rope_tables(rope_mod, L, E, h, qkv.device)
+    prec = _fp32_prec_code() if qkv.dtype == torch.float32 else 0
+    out = PK_SELF(qkv.reshape(-1, L, E3).contiguous(), _bias3(key_bias, lead, L, qkv.device), cos, sin, h, lkp, rc,
+                  half, rot, prec, float(scale))
+    return out.reshape(*lead, L, E)
+
+
+def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,  # noqa: ANN001
+                       scale: float) -> Tensor:
+    """q [..., Lq, E], kv [..., Lk, 2E] (packed K | V projection); RoPE (optional) with positions
+    0..L-1 each (reference :735-752). A q that is one query set broadcast over kv's batch (a single
+    leading element, or an expanded view with batch stride 0) is read once by the kernel, not copied."""
+    lead = q.shape[:-2]
+    Lq, E = q.shape[-2], q.shape[-1]
+    Lk = kv.shape[-2]
+    lkp = -(-Lk // 128) * 128
+    bq = _pick_bq(Lq, lkp)
+    cq, sq, rc, half, rot = rope_tables(rope_mod, Lq, E, h, q.device)
+    ck, sk, _, _, _ = rope_tables(rope_mod, Lk, E, h, q.device)
+    prec = _fp32_prec_code() if q.dtype == torch.float32 else 0
+    q3 = q.reshape(-1, Lq, E)
+    kv3 = kv.reshape(-1, Lk, 2 * E)
+    if q3.shape[0] == 1 or (q3.stride(0) == 0 and q3.shape[0] == kv3.shape[0]):
+        q3 = q3[:1]
+    elif q3.shape[0] != kv3.shape[0]:
+        q3 = q3.expand(kv3.shape[0], Lq, E)
+    out_lead = lead if q.shape[:-2].numel() == kv3.shape[0] else kv.shape[:-2]
+    out = PK_CROSS(q3.contiguous(), kv3.contiguous(), _bias3(key_bias, out_lead, Lk, q.device), cq, sq, ck, sk,
+                   h, lkp, bq, rc, half, rot, prec, float(scale))
+    return out.reshape(*out_lead, Lq, E)

@@ -1,0 +1,157 @@
+"""Dataset-wise in-context attention over a cached train-row K/V (8 heads x 64 dims) on MI355X.
+
+Replaces the reference's Splash path for the ICL stage:
+  * icl_sdpa(q, k, v, valid_kv_len) keeps the contract of the hook _tpu_pallas_splash_sdpa
+    (results/tpu_patch.diff:123-155; knob version scripts/tabicl_tpu_bucketed.py:221-246): q, k, v
+    [..., H, T, D], q not pre-scaled (D^-0.5 applied inside), keys at positions >= valid_kv_len
+    ignored, output [..., H, Tq, D] in q's dtype. Unlike the reference nothing is padded: the kernel
+    masks the key tail and any Tq works.
+  * torch op tabicl::icl_cached_attn(q, k, v, valid, scale) is the registered kernel (the
+    counterpart of tabicl::tpu_splash_sdpa_seg / _full, diff:95-120).
+  * IclKVCache holds the fit-time cache in one [estimator, block, head, row, d] tensor per K and V
+    (the reference keeps tuples of per-block [B, H, T, d] tensors, tabicl_tpu_bucketed.py:413-435),
+    appended once per block at fit time and read per block at query time (:803-817).
+"""
+from __future__ import annotations
+
+from typing import Optional, Union
+
+import torch
+from torch import Tensor
+
+import tabicl_mi355_native as _nat
+
+
+def _strides3(t: Tensor):
+    """(n, h, row) element strides of a [N, H, T, D] view whose last dim is contiguous."""
+    if t.stride(-1) != 1:
+        raise ValueError("icl attention needs a contiguous last dimension")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float, out: Tensor) -> None:
+    _nat.require_device(q, k, v, valid, out)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("icl_cached_attn expects [N, H, T, D] tensors")
+    N, H, Tq, D = q.shape
+    Tkv = k.shape[2]
+    if k.shape != v.shape or k.shape[0] != N or k.shape[1] != H or k.shape[3] != D:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if out.shape != q.shape:
+        raise ValueError(f"out {tuple(out.shape)} must match q {tuple(q.shape)}")
+    if q.dtype != k.dtype or k.dtype != v.dtype or out.dtype != q.dtype:
+        raise ValueError("q, k, v and out must share a dtype (promote q to the cache dtype first)")
+    vptr, vn = None, 0
+    if valid is not None:
+        if valid.dtype != torch.int32 or not valid.is_contiguous():
+            raise ValueError("valid must be a contiguous int32 tensor")
+        vptr, vn = valid.data_ptr(), valid.numel()
+    _nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
+              N, H, Tq, Tkv, D, *_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out), float(scale),
+              _nat.dtype_code(q.dtype), _nat.stream_of(q))
+
+
+@torch.library.custom_op("tabicl::icl_cached_attn", mutates_args=())
+def _icl_cached_attn(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float) -> Tensor:
+    out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    _launch(q, k, v, valid, scale, out)
+    return out
+
+
+@_icl_cached_attn.register_fake
+def _(q, k, v, valid, scale):  # noqa: ANN001
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("tabicl::icl_cached_attn_out", mutates_args=("out",))
+def _icl_cached_attn_out(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float,
+                         out: Tensor) -> None:
+    """Same as icl_cached_attn, written into `out` (any [N, H, Tq, D] view with a contiguous last
+    dim, e.g. one block of a [est, block, head, row, d] result buffer)."""
+    _launch(q, k, v, valid, scale, out)
+
+
+@_icl_cached_attn_out.register_fake
+def _(q, k, v, valid, scale, out):  # noqa: ANN001
+    return None
+
+
+ICL_FWD = torch.ops.tabicl.icl_cached_attn
+ICL_FWD_OUT = torch.ops.tabicl.icl_cached_attn_out
+
+
+def icl_supported(Tq: int, Tkv: int, D: int, dtype: torch.dtype) -> bool:
+    return dtype in (torch.bfloat16, torch.float32) and _nat.supported(_nat.OP_ICL, Tq, Tkv, D, 1, dtype)
+
+
+def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None) -> Tensor:
+    """softmax(q k^T * D^-0.5 + key mask) v for q [..., H, Tq, D], k/v [..., H, Tkv, D]; keys at
+    positions >= valid_kv_len are masked (a tensor may hold one length per flattened batch entry).
+    Contract of the reference hook _tpu_pallas_splash_sdpa (results/tpu_patch.diff:123-155)."""
+    D = q.shape[-1]
+    lead = q.shape[:-3]
+    H, Tq = q.shape[-3], q.shape[-2]
+    Tkv = k.shape[-2]
+    q4 = q.reshape(-1, H, Tq, D)
+    k4 = k.reshape(-1, H, Tkv, D)
+    v4 = v.reshape(-1, H, Tkv, D)
+    valid = None
+    if isinstance(valid_kv_len, Tensor):
+        valid = valid_kv_len.to(device=q.device, dtype=torch.int32).reshape(-1).contiguous()
+    elif valid_kv_len is not None and int(valid_kv_len) < Tkv:
+        valid = torch.full((1,), int(valid_kv_len), dtype=torch.int32, device=q.device)
+    out = ICL_FWD(q4, k4, v4, valid, float(D) ** -0.5)
+    return out.reshape(*lead, H, Tq, D)
+
+
+class IclKVCache:
+    """Fit-time K/V cache of the ICL stage, one tensor per K and V of shape
+    [estimators, blocks, heads, capacity, head_dim] (rows past the valid length are never read).
+
+    append(block, k, v, row0) writes rows [row0, row0 + T) of one block from k/v [E, H, T, d]
+    (the per-block K/V the prefill produces, reference scripts/tabicl_tpu_bucketed.py:659-692);
+    block_kv(block) returns the [E, H, capacity, d] views the query reads (:803-817)."""
+
+    def __init__(self, estimators: int, blocks: int, heads: int, capacity: int, head_dim: int,
+                 dtype: torch.dtype = torch.bfloat16, device: Union[str, torch.device] = "cuda"):
+        shape = (estimators, blocks, heads, capacity, head_dim)
+        self.keys = torch.empty(shape, dtype=dtype, device=device)
+        self.values = torch.empty(shape, dtype=dtype, device=device)
+        self.capacity = capacity
+        self.length = torch.zeros(estimators, dtype=torch.int32, device=device)
+
+    @property
+    def shape(self):
+        return tuple(self.keys.shape)
+
+    def nbytes(self) -> int:
+        return 2 * self.keys.numel() * self.keys.element_size()
+
+    def append(self, block: int, k: Tensor, v: Tensor, row0: int = 0) -> None:
+        E, NB, H, cap, D = self.keys.shape
+        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != E or k.shape[1] != H or k.shape[3] != D:
+            raise ValueError(f"append expects k/v [{E}, {H}, T, {D}], got {tuple(k.shape)} / {tuple(v.shape)}")
+        if k.stride() != v.stride():
+            raise ValueError("k and v must share strides")
+        if k.dtype != self.keys.dtype or v.dtype != self.keys.dtype:
+            raise ValueError(f"append expects {self.keys.dtype} (cast before appending)")
+        if not 0 <= block < NB:
+            raise ValueError(f"block {block} out of range [0, {NB})")
+        _nat.require_device(k, v, self.keys)
+        T = k.shape[2]
+        kc = self.keys[:, block]
+        vc = self.values[:, block]
+        _nat.call("tabicl_icl_cache_append", kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), row0, cap,
+                  k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), E, H, T, D,
+                  _nat.dtype_code(k.dtype), _nat.stream_of(k))
+
+    def block_kv(self, block: int):
+        return self.keys[:, block], self.values[:, block]
+
+    def query(self, block: int, q: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None) -> Tensor:
+        """Attention of q [E, H, Tq, D] over block `block` of the cache (keys >= valid_kv_len masked)."""
+        k, v = self.block_kv(block)
+        # promote_types(q, cache) as in the reference's cached branch (results/tpu_patch.diff:314-317)
+        attn_dtype = torch.promote_types(q.dtype, k.dtype)
+        q, k, v = q.to(attn_dtype), k.to(attn_dtype), v.to(attn_dtype)
+        return icl_sdpa(q, k, v, valid_kv_len)

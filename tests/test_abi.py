@@ -1,0 +1,116 @@
+"""CPU checks of the C ABI and the host logic: the library loads, exports every symbol that
+include/tabicl_attn.h declares, rejects bad arguments before any device work, and the Python host
+helpers keep the reference's semantics. No kernel is launched here."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as O
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tabicl_attn.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tabicl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import tabicl_mi355_native as nat
+    lib = nat.load()
+    names = _declared()
+    assert len(names) == 9, names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in nat.SIGNATURES, name
+    assert nat.version().startswith("tabicl_attn")
+
+
+def test_supported_predicate():
+    import tabicl_mi355_native as nat
+    bf, f32 = torch.bfloat16, torch.float32
+    assert nat.supported(nat.OP_HX, 1024, 128, 128, 8, bf)
+    assert nat.supported(nat.OP_HXQ, 128, 53248, 128, 8, f32)
+    assert not nat.supported(nat.OP_HX, 16, 16, 256, 16, bf)  # head dim 16 but 16 heads: not built
+    assert not nat.supported(nat.OP_HX, 16, 0, 128, 8, bf)
+    assert not nat.supported(nat.OP_HX, 16, 16, 128, 8, torch.float16)
+    assert nat.supported(nat.OP_ICL, 5000, 45000, 64, 8, bf)
+    assert not nat.supported(nat.OP_ICL, 5000, 45000, 128, 8, bf)
+
+
+def test_bad_arguments_rejected_before_launch():
+    import tabicl_mi355_native as nat
+    lib = nat.load()
+    # E != 128 -> status 1 and a message, with NULL pointers (nothing is dereferenced or launched)
+    st = lib.tabicl_hx_fwd(None, None, None, None, 1, None, 2, 3, 4, 64, 8, 0, None)
+    assert st == 1 and "E == 128" in nat.last_error()
+    st = lib.tabicl_icl_fwd(None, None, None, None, 0, None, 1, 1, 1, 1, 32, *([64] * 12), 1.0, 0, None)
+    assert st == 1 and "head dim" in nat.last_error()
+    st = lib.tabicl_pk_self_fwd(None, None, 1, None, None, None, 1, 8, 128, 8, 2, 3, 16, 0.25, 0, None)
+    assert st == 1 and "rope" in nat.last_error()
+    st = lib.tabicl_icl_cache_append(None, None, 64, 64, 10, 12, None, None, 64, 64, 64, 1, 1, 5, 64, 0, None)
+    assert st == 1 and "capacity" in nat.last_error()
+    with pytest.raises(nat.UnsupportedShapeError):
+        nat.check(1, "x")
+
+
+def test_ops_refuse_cpu_tensors():
+    import tabicl_mi355_attn as pk
+    import tabicl_mi355_native as nat
+    q = torch.zeros(1, 4, 128)
+    with pytest.raises(nat.NativeLibraryError):
+        pk.hx_attention(q, q, q, 8)
+
+
+def test_pick_blocks_match_reference_rules():
+    import tabicl_mi355_attn as pk
+    assert pk._pick_bq(1024, 128) == 512
+    assert pk._pick_bq(104, 128) == 104
+    assert pk._pick_bq(53248, 128) == 512
+    assert pk._pick_bq(4, 128) == 4
+    assert pk._pick_bq(1001, 1024) == 0
+    assert pk._pick_bk(53248) == 512
+    assert pk._pick_bk(1024) == 512
+    assert pk._pick_bk(384) == 128
+    assert pk._pick_bk(100) == 0
+
+
+def test_bias3_forms():
+    import tabicl_mi355_attn as pk
+    assert pk._bias3(None, (4, 2), 7, "cpu").shape == (1, 1, 7)
+    b = torch.arange(7.0)
+    assert torch.equal(pk._bias3(b, (4, 2), 7, "cpu"), b.reshape(1, 1, 7))
+    b2 = torch.randn(4, 1, 7)
+    out = pk._bias3(b2, (4, 2), 7, "cpu")
+    assert out.shape == (8, 1, 7)
+    assert torch.equal(out[3], b2[1])
+
+
+class _Rope:
+    def __init__(self, interleaved):
+        self.interleaved = interleaved
+        self.freqs = torch.tensor(O.textbook_freqs(16, 10000.0), dtype=torch.float32)
+
+    def get_seq_pos(self, L, device=None, dtype=torch.float32):
+        return torch.arange(L, device=device, dtype=dtype)
+
+    def forward(self, seq, seq_len=None):
+        return (seq.float().unsqueeze(-1) * self.freqs).repeat_interleave(2, dim=-1)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_tables_match_oracle(interleaved):
+    import tabicl_mi355_attn as pk
+    cos, sin, code, half, rot = pk.rope_tables(_Rope(interleaved), 104, 128, 8, "cpu")
+    c2, s2, code2, half2, rot2 = O.rope_tables_ref(O.textbook_freqs(16, 10000.0), 104, 128, 8, interleaved)
+    assert (code, half, rot) == (code2, half2, rot2)
+    np.testing.assert_allclose(cos.numpy(), c2, atol=1e-5)
+    np.testing.assert_allclose(sin.numpy(), s2, atol=1e-5)
+    c0, s0, code0, _, _ = pk.rope_tables(None, 4, 128, 8, "cpu")
+    assert code0 == 0 and torch.all(c0 == 1) and torch.all(s0 == 0)

@@ -1,0 +1,227 @@
+"""GPU parity of the small-head kernels (hx, hxq, pk_self, pk_cross) against the CPU oracle.
+
+Shapes follow the reference's own test matrix (scripts/tests/test_pallas_attn.py:371-403) plus edge
+cases. Tolerance (written here): max abs error <= 2e-2 for bf16 inputs
+with fp32 accumulation, <= 1e-4 for fp32 inputs, against the fp32/fp64 oracle on the same inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as O
+
+H = 8
+E = 128
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
+
+pytestmark = pytest.mark.gpu
+
+
+def _attn():
+    import tabicl_mi355_attn as pk
+    return pk
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _err(out, ref):
+    return float(np.abs(out.detach().double().cpu().numpy() - ref).max())
+
+
+class _Rope:
+    """Minimal stand-in for upstream RotaryEmbedding (get_seq_pos / interleaved / freqs / forward)."""
+
+    def __init__(self, dim=16, theta=100000.0, interleaved=False):
+        self.interleaved = interleaved
+        self.freqs = torch.tensor(O.textbook_freqs(dim, theta), dtype=torch.float32)
+
+    def get_seq_pos(self, L, device=None, dtype=torch.float32):
+        return torch.arange(L, device=device, dtype=dtype)
+
+    def forward(self, seq, seq_len=None):
+        f = seq.float().unsqueeze(-1) * self.freqs.to(seq.device)
+        return f.repeat_interleave(2, dim=-1)
+
+
+def _rope_np(rope, L):
+    freqs = rope.freqs.double().numpy()
+    return O.rope_tables_ref(freqs, L, E, H, rope.interleaved)
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk,dtype,bias", [
+    ("col2_bf16", 4, 1024, 128, torch.bfloat16, False),
+    ("col2_fp32", 4, 1024, 128, torch.float32, False),
+    ("col1_bf16", 4, 128, 576, torch.bfloat16, False),
+    ("row_bf16", 16, 104, 104, torch.bfloat16, False),
+    ("row_fp32_bias", 16, 108, 108, torch.float32, True),
+    ("cls_bf16", 16, 4, 104, torch.bfloat16, False),
+    ("ragged_bf16_bias", 3, 77, 1500, torch.bfloat16, True),
+    ("one_key_fp32", 2, 5, 1, torch.float32, False),
+])
+def test_hx(dev, name, B, Lq, Lk, dtype, bias):
+    pk = _attn()
+    g = _gen(0)
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(dtype)
+    k = torch.randn(B, Lk, E, generator=g).to(dtype)
+    v = torch.randn(B, Lk, E, generator=g).to(dtype)
+    kb = None
+    if bias:
+        kb = torch.zeros(B, Lk)
+        kb[:, Lk - 9:] = -1e30
+    print(f"[hx] {name} B={B} Lq={Lq} Lk={Lk} {dtype}", flush=True)
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, None if kb is None else kb.to(dev))
+    torch.cuda.synchronize()
+    ref = O.hx_ref(q, k, v, H, kb)
+    assert out.shape == q.shape and out.dtype == dtype
+    assert _err(out, ref) <= TOL[dtype]
+
+
+def test_hx_fp32_long_queries(dev):
+    pk = _attn()
+    g = _gen(1)
+    q = torch.randn(2, 53248, E, generator=g) * 0.25
+    k = torch.randn(2, 128, E, generator=g)
+    v = torch.randn(2, 128, E, generator=g)
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H)
+    ref = O.ref_attn(q, k, v, H).double().numpy()
+    assert _err(out, ref) <= 1e-4
+
+
+def test_hx_shared_bias_matches_broadcast(dev):
+    pk = _attn()
+    g = _gen(2)
+    q = (torch.randn(3, 40, E, generator=g) * 0.25).to(torch.bfloat16).to(dev)
+    k = torch.randn(3, 200, E, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(3, 200, E, generator=g).to(torch.bfloat16).to(dev)
+    kb = torch.randn(200, generator=g).to(dev)
+    a = pk.hx_attention(q, k, v, H, kb)
+    b = pk.hx_attention(q, k, v, H, kb.expand(3, 200).contiguous())
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk,valid,dtype", [
+    ("col1_small_fp32", 4, 128, 4096, 3000, torch.float32),
+    ("col1_small_bf16", 4, 128, 4096, 3000, torch.bfloat16),
+    ("valid_full", 2, 128, 1000, 1000, torch.bfloat16),
+    ("valid_not_tile_aligned", 2, 64, 777, 129, torch.bfloat16),
+    ("valid_beyond_lk_clamped", 2, 16, 300, 100000, torch.float32),
+])
+def test_hxq(dev, name, B, Lq, Lk, valid, dtype):
+    pk = _attn()
+    g = _gen(3)
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(dtype)
+    kv = torch.randn(B, Lk, 2 * E, generator=g).to(dtype)
+    print(f"[hxq] {name}", flush=True)
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(valid, dtype=torch.int32).to(dev), H)
+    ref = O.hxq_ref(q, kv, np.array([min(valid, Lk)]), H)
+    assert _err(out, ref) <= TOL[dtype]
+
+
+def test_hxq_ragged_valid_and_empty(dev):
+    pk = _attn()
+    g = _gen(4)
+    B, Lq, Lk = 4, 128, 2048
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16)
+    kv = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
+    valid = torch.tensor([2048, 1, 0, 1000], dtype=torch.int32)
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), valid.to(dev), H)
+    ref = O.hxq_ref(q, kv, valid.numpy(), H)
+    assert _err(out, ref) <= 2e-2
+    assert torch.all(out[2] == 0)
+
+
+def test_hxq_inference_tile_subset(dev):
+    # reference shape col1_infer_tile54 (54 x 128 queries over 53248 keys, 45000 valid); 6 of the
+    # 54 batch elements keep the CPU oracle within seconds
+    pk = _attn()
+    g = _gen(5)
+    B, Lq, Lk, valid = 6, 128, 53248, 45000
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16)
+    kv = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(valid).to(dev), H)
+    ref = O.ref_attn(q.float(), kv[:, :valid, :E].float(), kv[:, :valid, E:].float(), H).double().numpy()
+    assert _err(out, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("name,B,L,dtype,interleaved,bias", [
+    ("self_bf16_rope_halves", 16, 104, torch.bfloat16, False, False),
+    ("self_fp32_rope_halves_bias", 16, 108, torch.float32, False, True),
+    ("self_fp32_rope_pairs", 8, 104, torch.float32, True, False),
+    ("self_bf16_norope", 4, 300, torch.bfloat16, None, False),
+])
+def test_pk_self(dev, name, B, L, dtype, interleaved, bias):
+    pk = _attn()
+    g = _gen(6)
+    x = torch.randn(B, L, 3 * E, generator=g).to(dtype)
+    rope = None if interleaved is None else _Rope(interleaved=interleaved)
+    kb = None
+    if bias:
+        kb = torch.zeros(B, L)
+        kb[:, L - 7:] = -1e30
+    print(f"[pk_self] {name}", flush=True)
+    out = pk.pk_self_attention(x.to(dev), H, None if kb is None else kb.to(dev), rope, 16 ** -0.5)
+    ref = O.pk_self_ref(x, H, kb, None if rope is None else _rope_np(rope, L), 16 ** -0.5)
+    assert out.shape == (B, L, E)
+    assert _err(out, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk,dtype,interleaved", [
+    ("cross_cls_bf16_rope", 16, 4, 104, torch.bfloat16, False),
+    ("cross_col2_bf16", 4, 1024, 128, torch.bfloat16, None),
+    ("cross_col1_bf16", 4, 128, 576, torch.bfloat16, None),
+    ("cross_col2_fp32", 2, 4096, 128, torch.float32, None),
+])
+def test_pk_cross(dev, name, B, Lq, Lk, dtype, interleaved):
+    pk = _attn()
+    g = _gen(7)
+    x = torch.randn(B, Lq, E, generator=g).to(dtype)
+    y = torch.randn(B, Lk, 2 * E, generator=g).to(dtype)
+    rope = None if interleaved is None else _Rope(interleaved=interleaved)
+    print(f"[pk_cross] {name}", flush=True)
+    out = pk.pk_cross_attention(x.to(dev), y.to(dev), H, None, rope, 16 ** -0.5)
+    rq = None if rope is None else _rope_np(rope, Lq)
+    rk = None if rope is None else _rope_np(rope, Lk)
+    ref = O.pk_cross_ref(x, y, H, None, rq, rk, 16 ** -0.5)
+    assert _err(out, ref) <= TOL[dtype]
+
+
+def test_pk_cross_broadcast_query_no_copy(dev):
+    # inducing points expanded over the batch (batch stride 0) are read once by the kernel
+    pk = _attn()
+    g = _gen(8)
+    ind = torch.randn(1, 128, E, generator=g).to(torch.bfloat16)
+    kv = torch.randn(5, 300, 2 * E, generator=g).to(torch.bfloat16)
+    q_exp = ind.to(dev).expand(5, 128, E)
+    out = pk.pk_cross_attention(q_exp, kv.to(dev), H, None, None, 0.25)
+    ref = O.pk_cross_ref(ind, kv, H, None, None, None, 0.25)
+    assert out.shape == (5, 128, E)
+    assert _err(out, ref) <= 2e-2
+
+
+def test_all_keys_masked_by_bias_is_uniform(dev):
+    # every key at -1e30: the reference's fp32 softmax sees equal scores -> uniform weights
+    pk = _attn()
+    g = _gen(9)
+    q = torch.randn(2, 8, E, generator=g) * 0.25
+    k = torch.randn(2, 20, E, generator=g)
+    v = torch.randn(2, 20, E, generator=g)
+    kb = torch.full((2, 20), -1e30)
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev))
+    want = v.mean(dim=1, keepdim=True).expand_as(out.cpu())
+    assert float((out.cpu() - want).abs().max()) <= 1e-4
+    assert torch.isfinite(out).all()
+
+
+def test_no_nan_with_garbage_past_valid(dev):
+    # NaN/inf in key/value rows past valid must not leak into the output
+    pk = _attn()
+    g = _gen(10)
+    q = (torch.randn(2, 32, E, generator=g) * 0.25).to(torch.bfloat16)
+    kv = torch.randn(2, 500, 2 * E, generator=g).to(torch.bfloat16)
+    kv[:, 300:] = float("nan")
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(300).to(dev), H)
+    assert torch.isfinite(out.float()).all()
+    ref = O.hxq_ref(q, kv[:, :300], np.array([300]), H)
+    assert _err(out, ref) <= 2e-2

@@ -1,0 +1,197 @@
+"""Pins the CPU oracle (oracle/attention.py) with closed forms, invariants and brute force, so that a
+dropped term, a wrong sign or index, or a transposed operand in the oracle fails one of these."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as O
+
+H = 8
+E = 128
+
+
+def _rand(rng, *shape, scale=1.0):
+    return rng.standard_normal(shape) * scale
+
+
+def test_loops_vs_vectorised_vs_torch_fp32():
+    rng = np.random.default_rng(0)
+    q, k, v = _rand(rng, 2, 5, 16, scale=0.5), _rand(rng, 2, 7, 16), _rand(rng, 2, 7, 16)
+    bias = _rand(rng, 2, 7)
+    a = O.attention_loops(q, k, v, 2, bias)
+    b = O.attention_f64(q, k, v, 2, bias)
+    c = O.ref_attn(torch.tensor(q), torch.tensor(k), torch.tensor(v), 2, torch.tensor(bias)).double().numpy()
+    np.testing.assert_allclose(a, b, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(b, c, rtol=0, atol=1e-5)
+
+
+def test_two_keys_closed_form():
+    # p(key0) = sigmoid(s0 - s1); out = p v0 + (1 - p) v1, per head
+    rng = np.random.default_rng(1)
+    q, k, v = _rand(rng, 1, 3, E), _rand(rng, 1, 2, E), _rand(rng, 1, 2, E)
+    out = O.attention_f64(q, k, v, H)
+    d = E // H
+    for g in range(H):
+        sl = slice(g * d, (g + 1) * d)
+        s0 = q[0, :, sl] @ k[0, 0, sl]
+        s1 = q[0, :, sl] @ k[0, 1, sl]
+        p0 = 1.0 / (1.0 + np.exp(-(s0 - s1)))
+        want = p0[:, None] * v[0, 0, sl] + (1 - p0)[:, None] * v[0, 1, sl]
+        np.testing.assert_allclose(out[0, :, sl], want, atol=1e-12)
+
+
+def test_one_key_gives_value_row():
+    rng = np.random.default_rng(2)
+    q, k, v = _rand(rng, 2, 4, E), _rand(rng, 2, 1, E), _rand(rng, 2, 1, E)
+    out = O.attention_f64(q, k, v, H)
+    np.testing.assert_allclose(out, np.broadcast_to(v, out.shape), atol=1e-12)
+
+
+def test_key_permutation_invariance_and_row_shift():
+    rng = np.random.default_rng(3)
+    q, k, v = _rand(rng, 2, 6, E, scale=0.3), _rand(rng, 2, 9, E), _rand(rng, 2, 9, E)
+    bias = _rand(rng, 2, 9)
+    base = O.attention_f64(q, k, v, H, bias)
+    perm = rng.permutation(9)
+    np.testing.assert_allclose(O.attention_f64(q, k[:, perm], v[:, perm], H, bias[:, perm]), base, atol=1e-12)
+    # a constant added to every key's bias shifts every score of a row equally -> no change
+    np.testing.assert_allclose(O.attention_f64(q, k, v, H, bias + 7.5), base, atol=1e-12)
+
+
+def test_masked_keys_equal_slicing_and_valid_len():
+    rng = np.random.default_rng(4)
+    q, k, v = _rand(rng, 3, 5, E, scale=0.3), _rand(rng, 3, 11, E), _rand(rng, 3, 11, E)
+    bias = np.zeros((3, 11))
+    bias[:, 8:] = O.NEG
+    masked = O.attention_f64(q, k, v, H, bias)
+    sliced = O.attention_f64(q, k[:, :8], v[:, :8], H)
+    np.testing.assert_allclose(masked, sliced, atol=1e-12)
+    np.testing.assert_allclose(O.attention_f64(q, k, v, H, valid=8), sliced, atol=1e-12)
+    # ragged valid lengths, one per batch element; 0 valid keys -> output 0 (defined behaviour)
+    got = O.attention_f64(q, k, v, H, valid=np.array([11, 3, 0]))
+    np.testing.assert_allclose(got[0], O.attention_f64(q[:1], k[:1], v[:1], H)[0], atol=1e-12)
+    np.testing.assert_allclose(got[1], O.attention_f64(q[1:2], k[1:2, :3], v[1:2, :3], H)[0], atol=1e-12)
+    assert np.all(got[2] == 0)
+
+
+def test_zero_query_is_mean_and_convex_hull():
+    rng = np.random.default_rng(5)
+    q, k, v = np.zeros((1, 2, E)), _rand(rng, 1, 13, E), _rand(rng, 1, 13, E)
+    out = O.attention_f64(q, k, v, H)
+    np.testing.assert_allclose(out[0, 0], v[0].mean(axis=0), atol=1e-12)
+    q2 = _rand(rng, 1, 20, E)
+    out2 = O.attention_f64(q2, k, v, H)
+    assert np.all(out2 <= v.max(axis=1, keepdims=True) + 1e-12)
+    assert np.all(out2 >= v.min(axis=1, keepdims=True) - 1e-12)
+
+
+def test_heads_are_independent_column_blocks():
+    # changing head 3's keys must leave every other head's output unchanged
+    rng = np.random.default_rng(6)
+    q, k, v = _rand(rng, 1, 4, E), _rand(rng, 1, 6, E), _rand(rng, 1, 6, E)
+    base = O.attention_f64(q, k, v, H)
+    k2 = k.copy()
+    k2[..., 48:64] = _rand(rng, 1, 6, 16)
+    alt = O.attention_f64(q, k2, v, H)
+    same = np.ones(E, bool)
+    same[48:64] = False
+    np.testing.assert_allclose(alt[..., same], base[..., same], atol=1e-12)
+    assert np.abs(alt[..., 48:64] - base[..., 48:64]).max() > 1e-3
+
+
+def test_splash_ref_scale_and_valid():
+    rng = np.random.default_rng(7)
+    q, k, v = _rand(rng, 2, 2, 5, 64), _rand(rng, 2, 2, 9, 64), _rand(rng, 2, 2, 9, 64)
+    got = O.splash_sdpa_ref(q, k, v, valid=np.array([9, 4]))
+    # same thing through the merged-layout oracle: one head per [N*H] slice, q pre-scaled by 1/8
+    for n, nv in ((0, 9), (1, 4)):
+        for hh in range(2):
+            want = O.attention_f64(q[n, hh][None] / 8.0, k[n, hh, :nv][None], v[n, hh, :nv][None], 1)[0]
+            np.testing.assert_allclose(got[n, hh], want, atol=1e-12)
+    qt, kt, vt = (torch.tensor(x, dtype=torch.float32) for x in (q, k, v))
+    np.testing.assert_allclose(O.splash_sdpa_torch(qt[:1], kt[:1], vt[:1]).double().numpy(),
+                               O.splash_sdpa_ref(q[:1], k[:1], v[:1]), atol=2e-5)
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 4, 64])
+def test_online_softmax_equals_one_shot(chunk):
+    rng = np.random.default_rng(8)
+    q, k, v = _rand(rng, 1, 2, 6, 64), _rand(rng, 1, 2, 10, 64), _rand(rng, 1, 2, 10, 64)
+    np.testing.assert_allclose(O.tiled_online_sdpa_ref(q, k, v, chunk), O.splash_sdpa_ref(q, k, v), atol=1e-12)
+    np.testing.assert_allclose(O.tiled_online_sdpa_ref(q, k, v, chunk, valid=7), O.splash_sdpa_ref(q, k, v, 7),
+                               atol=1e-12)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_closed_form_norm_and_relative_position(interleaved):
+    rng = np.random.default_rng(9)
+    h, d = 8, 16
+    freqs = O.textbook_freqs(16, 10000.0)
+    L = 7
+    cos, sin, code, half, rot = O.rope_tables_ref(freqs, L, h * d, h, interleaved)
+    assert (code, half, rot) == ((1 if interleaved else 2), 8, 16)
+    x = _rand(rng, L, h * d)
+    y = O.rope_merged_ref(x, cos, sin, h, code, half, rot)
+    # position 0 is the identity
+    np.testing.assert_allclose(y[0], x[0], atol=1e-12)
+    # explicit 2-D rotation of each (a, b) pair by angle pos * freq_i
+    for pos in range(L):
+        for g in range(h):
+            for i in range(d // 2):
+                a_i, b_i = (g * d + 2 * i, g * d + 2 * i + 1) if interleaved else (g * d + i, g * d + i + 8)
+                th = pos * freqs[i]
+                a, b = x[pos, a_i], x[pos, b_i]
+                assert abs(y[pos, a_i] - (a * np.cos(th) - b * np.sin(th))) < 1e-12
+                assert abs(y[pos, b_i] - (b * np.cos(th) + a * np.sin(th))) < 1e-12
+    # rotation preserves each head's norm
+    np.testing.assert_allclose(np.linalg.norm(y.reshape(L, h, d), axis=-1),
+                               np.linalg.norm(x.reshape(L, h, d), axis=-1), atol=1e-12)
+    # <R_m q, R_n k> depends only on m - n
+    qv, kv = _rand(rng, 1, h * d), _rand(rng, 1, h * d)
+    def rot_at(vec, pos):
+        c, s_, *_ = O.rope_tables_ref(freqs, 1, h * d, h, interleaved, positions=[pos])
+        return O.rope_merged_ref(vec, c, s_, h, code, half, rot)
+    d1 = (rot_at(qv, 5) * rot_at(kv, 2)).reshape(h, d).sum(-1)
+    d2 = (rot_at(qv, 9) * rot_at(kv, 6)).reshape(h, d).sum(-1)
+    np.testing.assert_allclose(d1, d2, atol=1e-10)
+
+
+def test_rope_partial_rotary_dims_pass_through():
+    rng = np.random.default_rng(10)
+    freqs = O.textbook_freqs(8, 100000.0)  # rot = 8 < d = 16
+    cos, sin, code, half, rot = O.rope_tables_ref(freqs, 4, E, H, False)
+    assert (half, rot) == (4, 8)
+    x = _rand(rng, 4, E)
+    y = O.rope_merged_ref(x, cos, sin, H, code, half, rot)
+    for g in range(H):
+        np.testing.assert_allclose(y[:, g * 16 + 8:(g + 1) * 16], x[:, g * 16 + 8:(g + 1) * 16], atol=1e-12)
+
+
+def test_op_oracles_compose():
+    rng = np.random.default_rng(11)
+    B, L = 2, 6
+    qkv = _rand(rng, B, L, 3 * E)
+    freqs = O.textbook_freqs(16, 10000.0)
+    cos, sin, code, half, rot = O.rope_tables_ref(freqs, L, E, H, False)
+    got = O.pk_self_ref(qkv, H, None, (cos, sin, code, half, rot), 0.25)
+    q = O.rope_merged_ref(qkv[..., :E], cos, sin, H, code, half, rot) * 0.25
+    k = O.rope_merged_ref(qkv[..., E:2 * E], cos, sin, H, code, half, rot)
+    np.testing.assert_allclose(got, O.attention_f64(q, k, qkv[..., 2 * E:], H), atol=1e-12)
+    kv = _rand(rng, B, 9, 2 * E)
+    qq = _rand(rng, 1, 3, E)
+    got = O.pk_cross_ref(qq, kv, H, None, None, None, 0.25)
+    np.testing.assert_allclose(got[1], O.attention_f64(qq * 0.25, kv[1:, :, :E], kv[1:, :, E:], H)[0], atol=1e-12)
+    np.testing.assert_allclose(O.hxq_ref(qq.repeat(2, 0), kv, np.array([5]), H),
+                               O.attention_f64(qq.repeat(2, 0), kv[:, :5, :E], kv[:, :5, E:], H), atol=1e-12)
+
+
+def test_combined_mask_forms():
+    m = O.combined_mask_ref(np.zeros((3, 5), np.float32), None, (2,), 8, 3, 5)
+    assert m.shape == (1, 1, 3, 5)
+    kp = np.zeros((2, 5), np.float32)
+    kp[1, 3:] = -np.inf
+    m = O.combined_mask_ref(None, kp, (2,), 8, 3, 5)
+    assert m.shape == (2, 1, 1, 5) and np.isneginf(m[1, 0, 0, 4])
+    assert O.combined_mask_ref(np.zeros((3, 5), bool), None, (2,), 8, 3, 5) is False
+    assert O.combined_mask_ref(np.zeros((4, 5), np.float32), None, (2,), 8, 3, 5) is False
+    assert O.combined_mask_ref(None, None, (2,), 8, 3, 5) is None
