@@ -91,12 +91,25 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
  * views). q is NOT pre-scaled: scores are multiplied by `scale` (D^-0.5 in the reference) in fp32.
  * valid: device int32 [valid_n] (valid_n in {1, N}) or NULL (= Tkv): keys >= valid are masked;
  * no padding of q or k is required. A query with no valid key gets output 0.
+ * workspace: device memory of at least tabicl_icl_workspace_bytes(...) bytes, or NULL. With it the
+ * key range may be split over more workgroups (to fill whole rounds of the GPU) and the partial
+ * results merged by a second kernel on the same stream; without it the call runs unsplit. The
+ * workspace is scratch: it must not be shared by calls that overlap on the GPU.
  */
 int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
                    int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
                    int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh,
                    int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn,
-                   int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* stream);
+                   int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace size (bytes) that tabicl_icl_fwd uses for these sizes on the current device (0 when
+ * the call would not split). Queries the device's CU count and occupancy; no device memory is
+ * touched. Returns <0 on bad arguments.
+ */
+int64_t tabicl_icl_workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                                   int32_t dtype);
 
 /*
  * Fit-time cache append: copies rows [0, T) of one block's K and V (src [N, H, T, D] with element

@@ -12,7 +12,8 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
-                          hipStream_t stream);
+                          void* ws, int64_t ws_bytes, hipStream_t stream);
+int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int dtype);
 int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
                             int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
                             const float* bias, int64_t bias_sb, const int32_t* valid,
@@ -200,7 +201,8 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
                    int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
                    int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh,
                    int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn,
-                   int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* stream) {
+                   int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
   if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
     return fail(1, "icl_fwd: dtype code %d not supported", dtype);
   if (D != 64) return fail(1, "icl_fwd: head dim must be 64, got %lld", (long long)D);
@@ -219,8 +221,18 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
   return launch_status(
       tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, q_sn, q_sh,
                             q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale,
-                            dtype, (hipStream_t)stream),
+                            dtype, workspace && aligned16(workspace) ? workspace : nullptr,
+                            workspace_bytes, (hipStream_t)stream),
       "icl_fwd");
+}
+
+int64_t tabicl_icl_workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                                   int32_t dtype) {
+  if ((dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) || D != 64 || N < 0 || H < 0 ||
+      Tq < 0 || Tkv < 1)
+    return fail(-1, "icl_workspace_bytes: bad arguments");
+  if (N == 0 || H == 0 || Tq == 0) return 0;
+  return tabicl_launch_icl_ws_bytes(N, H, Tq, Tkv, dtype);
 }
 
 int tabicl_icl_cache_append(void* k_cache, void* v_cache, int64_t dst_sn, int64_t dst_sh,

@@ -37,6 +37,10 @@ struct IclParams {
   int N, H, Tq, Tkv, nqb;
   int64_t q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st;
   float sc;  // scale * log2(e)
+  // key split: nsplit > 1 writes unnormalised partials (O, m, l) per split to the workspace
+  int nsplit;
+  float* ws_o;   // [nsplit][N*H][Tq][64]
+  float* ws_ml;  // [nsplit][N*H][Tq][2]
 };
 
 template <typename T> struct IclLds {
@@ -242,9 +246,12 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   __shared__ __attribute__((aligned(16))) T lds_k[2][L::K_ELEMS];
   __shared__ __attribute__((aligned(16))) T lds_vt[2][L::V_ELEMS];
 
+  // work item = (n, h, split, query block); consecutive items share (n, h) and stay on one XCD
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = work % p.nqb;
-  const int nh = work / p.nqb;
+  const int rest = work / p.nqb;
+  const int split = rest % p.nsplit;
+  const int nh = rest / p.nsplit;
   const int h = nh % p.H, n = nh / p.H;
 
   int valid = p.Tkv;
@@ -279,22 +286,51 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   }
   const float sc = p.sc;
 
+  // this split's tiles [t0, t1) of the ceil(valid / KT) key tiles
   const int ntiles = (valid + ICL_KT - 1) / ICL_KT;
-  if (ntiles > 0) {
+  const int per = (ntiles + p.nsplit - 1) / p.nsplit;
+  const int t0 = min(split * per, ntiles), t1 = min(t0 + per, ntiles);
+  if (t1 > t0) {
     Stage<T, NT> stg;
-    stg.load(kbase, vbase, p.k_st, p.v_st, 0, valid);
+    stg.load(kbase, vbase, p.k_st, p.v_st, t0 * ICL_KT, valid);
     stg.store(lds_k[0], lds_vt[0]);
     __syncthreads();
-    // all tiles but the last: no key past `valid`
-    for (int t = 0; t + 1 < ntiles; ++t) {
-      const int k0 = t * ICL_KT, buf = t & 1;
+    // all tiles but the last one of the range: no key past `valid`
+    for (int t = t0; t + 1 < t1; ++t) {
+      const int k0 = t * ICL_KT, buf = (t - t0) & 1;
       stg.load(kbase, vbase, p.k_st, p.v_st, k0 + ICL_KT, valid);
       icl_tile<T, QC, false>(st, lds_k[buf], lds_vt[buf], k0, valid, sc, lr, hh);
       stg.store(lds_k[buf ^ 1], lds_vt[buf ^ 1]);
       __syncthreads();
     }
-    const int tl = ntiles - 1;
-    icl_tile<T, QC, true>(st, lds_k[tl & 1], lds_vt[tl & 1], tl * ICL_KT, valid, sc, lr, hh);
+    const int tl = t1 - 1, bl = (tl - t0) & 1;
+    if (t1 == ntiles)
+      icl_tile<T, QC, true>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
+    else
+      icl_tile<T, QC, false>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
+  }
+
+  if (p.nsplit > 1) {
+    // unnormalised partial result of this key range: O (fp32), running max m and sum l
+#pragma unroll
+    for (int qc = 0; qc < QC; ++qc) {
+      const float lt = lane_pair_sum(st.l_run[qc]);
+      const int qi = qw0 + qc * 32 + lr;
+      if (qi < p.Tq) {
+        const int64_t row = ((int64_t)split * p.N * p.H + nh) * p.Tq + qi;
+        float* orow = p.ws_o + row * ICL_D;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float4 ov = make_float4(st.o[qc][db][4 * j], st.o[qc][db][4 * j + 1], st.o[qc][db][4 * j + 2],
+                                    st.o[qc][db][4 * j + 3]);
+            *(float4*)(orow + 32 * db + 8 * j + 4 * hh) = ov;
+          }
+        if (hh == 0) *(float2*)(p.ws_ml + row * 2) = make_float2(st.m_run[qc], lt);
+      }
+    }
+    return;
   }
 
 #pragma unroll
@@ -317,23 +353,106 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   }
 }
 
+// Combines the per-split partials: m* = max_s m_s, w_s = 2^((m_s - m*) sc),
+// O = sum_s w_s O_s / sum_s w_s l_s (0 when no split saw a valid key). One thread per 4 outputs.
+template <typename T>
+__global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
+  const int64_t rows = (int64_t)p.N * p.H * p.Tq;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * (ICL_D / 4)) return;
+  const int64_t row = idx / (ICL_D / 4);
+  const int c4 = (int)(idx % (ICL_D / 4)) * 4;
+  float mstar = TA_NEG_INF;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)s * rows + row) * 2);
+    if (ml.y > 0.f) mstar = fmaxf(mstar, ml.x);
+  }
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float l = 0.f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)s * rows + row) * 2);
+    if (!(ml.y > 0.f)) continue;
+    const float w = __builtin_amdgcn_exp2f((ml.x - mstar) * p.sc);
+    const float4 o = *(const float4*)(p.ws_o + ((int64_t)s * rows + row) * ICL_D + c4);
+    acc.x += w * o.x; acc.y += w * o.y; acc.z += w * o.z; acc.w += w * o.w;
+    l += w * ml.y;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int64_t nh = row / p.Tq;
+  const int qi = (int)(row % p.Tq);
+  const int n = (int)(nh / p.H), h = (int)(nh % p.H);
+  T* dst = (T*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st + c4;
+  typename OpVec<T, 4>::type ov;
+  ov[0] = from_f32<T>(acc.x * inv); ov[1] = from_f32<T>(acc.y * inv);
+  ov[2] = from_f32<T>(acc.z * inv); ov[3] = from_f32<T>(acc.w * inv);
+  *(typename OpVec<T, 4>::type*)dst = ov;
+}
+
 template <typename T, int NW, int QC>
-void launch(const IclParams& p0, hipStream_t stream) {
+int blocks_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC>, NW * 64, 0) != hipSuccess)
+    return 1;
+  return n > 0 ? n : 1;
+}
+
+// Number of key splits that best fills whole rounds of resident workgroups:
+// minimises ceil(items * S / slots) / S over S = 1..4, each split keeping >= 8 key tiles.
+template <typename T, int NW, int QC>
+int pick_splits(int64_t items, int64_t Tkv) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 1;
+  const int64_t slots = (int64_t)cus * blocks_per_cu<T, NW, QC>();
+  const int64_t tiles = (Tkv + ICL_KT - 1) / ICL_KT;
+  int best = 1;
+  double best_cost = (double)((items + slots - 1) / slots);
+  for (int s = 2; s <= 4; ++s) {
+    if (tiles / s < 8) break;
+    const double cost = (double)((items * s + slots - 1) / slots) / s;
+    if (cost < best_cost - 1e-9) { best = s; best_cost = cost; }
+  }
+  return best;
+}
+
+template <typename T, int NW, int QC>
+int64_t workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv) {
+  const int64_t nqb = (Tq + 32 * QC * NW - 1) / (32 * QC * NW);
+  const int s = pick_splits<T, NW, QC>(N * H * nqb, Tkv);
+  return s > 1 ? (int64_t)s * N * H * Tq * (ICL_D + 2) * (int64_t)sizeof(float) : 0;
+}
+
+template <typename T, int NW, int QC>
+void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
   IclParams p = p0;
   p.nqb = (p.Tq + 32 * QC * NW - 1) / (32 * QC * NW);
-  const int64_t nblk = (int64_t)p.N * p.H * p.nqb;
+  const int64_t rows = (int64_t)p.N * p.H * p.Tq;
+  p.nsplit = pick_splits<T, NW, QC>((int64_t)p.N * p.H * p.nqb, p.Tkv);
+  if (p.nsplit > 1 && (ws == nullptr || ws_bytes < (int64_t)p.nsplit * rows * (ICL_D + 2) * 4)) p.nsplit = 1;
+  p.ws_o = (float*)ws;
+  p.ws_ml = p.ws_o + (p.nsplit > 1 ? (int64_t)p.nsplit * rows * ICL_D : 0);
+  const int64_t nblk = (int64_t)p.N * p.H * p.nsplit * p.nqb;
   hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
+  if (p.nsplit > 1) {
+    const int64_t threads = rows * (ICL_D / 4);
+    hipLaunchKernelGGL((icl_merge_kernel<T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
+  }
 }
 
 }  // namespace
 
-// Host launcher (called from the C ABI in abi.hip).
+// Host launchers (called from the C ABI in abi.hip).
+int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int dtype) {
+  return dtype == 0 ? workspace_bytes<bf16, 4, 2>(N, H, Tq, Tkv) : workspace_bytes<float, 4, 1>(N, H, Tq, Tkv);
+}
+
 int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
                           int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
                           int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
-                          hipStream_t stream) {
+                          void* ws, int64_t ws_bytes, hipStream_t stream) {
   IclParams p;
   p.q = q; p.k = k; p.v = v; p.o = out;
   p.valid = valid; p.valid_n = (int)valid_n;
@@ -344,9 +463,10 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.v_sn = v_sn; p.v_sh = v_sh; p.v_st = v_st;
   p.o_sn = o_sn; p.o_sh = o_sh; p.o_st = o_st;
   p.sc = scale * TA_LOG2E;
+  p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr;
   if (dtype == 0)
-    launch<bf16, 4, 2>(p, stream);
+    launch<bf16, 4, 2>(p, ws, ws_bytes, stream);
   else
-    launch<float, 4, 1>(p, stream);
+    launch<float, 4, 1>(p, ws, ws_bytes, stream);
   return (int)hipGetLastError();
 }

@@ -29,6 +29,22 @@ def _strides3(t: Tensor):
     return t.stride(0), t.stride(1), t.stride(2)
 
 
+_WS_BYTES: dict = {}
+
+
+def _workspace(N: int, H: int, Tq: int, Tkv: int, D: int, code: int, device) -> Optional[Tensor]:
+    """Scratch for the key-split path of the kernel (size from the library, per shape and device),
+    taken from torch's caching allocator on the launch stream; None when the call does not split."""
+    key = (N, H, Tq, Tkv, D, code, device.index)
+    nbytes = _WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = int(_nat.load().tabicl_icl_workspace_bytes(N, H, Tq, Tkv, D, code))
+        if nbytes < 0:
+            raise RuntimeError(f"tabicl_icl_workspace_bytes: {_nat.last_error()}")
+        _WS_BYTES[key] = nbytes
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
+
+
 def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float, out: Tensor) -> None:
     _nat.require_device(q, k, v, valid, out)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -46,9 +62,11 @@ def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: flo
         if valid.dtype != torch.int32 or not valid.is_contiguous():
             raise ValueError("valid must be a contiguous int32 tensor")
         vptr, vn = valid.data_ptr(), valid.numel()
+    code = _nat.dtype_code(q.dtype)
+    ws = _workspace(N, H, Tq, Tkv, D, code, q.device)
     _nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
               N, H, Tq, Tkv, D, *_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out), float(scale),
-              _nat.dtype_code(q.dtype), _nat.stream_of(q))
+              code, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _nat.stream_of(q))
 
 
 @torch.library.custom_op("tabicl::icl_cached_attn", mutates_args=())

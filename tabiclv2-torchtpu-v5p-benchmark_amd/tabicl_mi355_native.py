@@ -31,14 +31,16 @@ SIGNATURES = {
     "tabicl_pk_cross_fwd": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
                             _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_p],
     "tabicl_icl_fwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i64] + [_i64] * 12
-                      + [_f32, _i32, _c_p],
+                      + [_f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i32],
     "tabicl_icl_cache_append": [_c_p, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _i32, _c_p],
     "tabicl_attn_supported": [_i32, _i64, _i64, _i64, _i32, _i32],
     "tabicl_attn_last_error": [],
     "tabicl_attn_version": [],
 }
-_RESTYPES = {"tabicl_attn_last_error": ctypes.c_char_p, "tabicl_attn_version": ctypes.c_char_p}
+_RESTYPES = {"tabicl_attn_last_error": ctypes.c_char_p, "tabicl_attn_version": ctypes.c_char_p,
+             "tabicl_icl_workspace_bytes": ctypes.c_int64}
 
 
 class NativeLibraryError(RuntimeError):

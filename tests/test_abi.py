@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     import tabicl_mi355_native as nat
     lib = nat.load()
     names = _declared()
-    assert len(names) == 9, names
+    assert len(names) == 10, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in nat.SIGNATURES, name
@@ -50,7 +50,7 @@ def test_bad_arguments_rejected_before_launch():
     # E != 128 -> status 1 and a message, with NULL pointers (nothing is dereferenced or launched)
     st = lib.tabicl_hx_fwd(None, None, None, None, 1, None, 2, 3, 4, 64, 8, 0, None)
     assert st == 1 and "E == 128" in nat.last_error()
-    st = lib.tabicl_icl_fwd(None, None, None, None, 0, None, 1, 1, 1, 1, 32, *([64] * 12), 1.0, 0, None)
+    st = lib.tabicl_icl_fwd(None, None, None, None, 0, None, 1, 1, 1, 1, 32, *([64] * 12), 1.0, 0, None, 0, None)
     assert st == 1 and "head dim" in nat.last_error()
     st = lib.tabicl_pk_self_fwd(None, None, 1, None, None, None, 1, 8, 128, 8, 2, 3, 16, 0.25, 0, None)
     assert st == 1 and "rope" in nat.last_error()

@@ -104,6 +104,29 @@ def test_icl_cache_append_and_query(dev):
         cache.append(0, ks[0].to(dev), vs[0].to(dev), row0=400)  # past capacity
 
 
+def test_icl_split_matches_unsplit(dev):
+    # the key-split path (workspace given) and the single-pass path (no workspace) agree; ragged
+    # valid lengths leave some splits empty
+    import tabicl_mi355_native as nat
+    icl = _icl()
+    g = torch.Generator().manual_seed(8)
+    N, H, Tq, Tkv, D = 3, 4, 200, 3000, 64
+    q = torch.randn(N, H, Tq, D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16).to(dev)
+    valid = torch.tensor([3000, 700, 64], dtype=torch.int32, device=dev)
+    assert nat.load().tabicl_icl_workspace_bytes(N, H, Tq, Tkv, D, 0) > 0
+    split = icl.icl_sdpa(q, k, v, valid)
+    single = torch.empty_like(q)
+    nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), valid.data_ptr(), N, single.data_ptr(),
+             N, H, Tq, Tkv, D, *q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *single.stride()[:3],
+             D ** -0.5, 0, None, 0, nat.stream_of(q))
+    torch.cuda.synchronize()
+    assert float((split.float() - single.float()).abs().max()) <= 1e-2
+    ref = O.splash_sdpa_ref(q.cpu(), k.cpu(), v.cpu(), valid.cpu().numpy())
+    assert _err(split, ref) <= 2e-2
+
+
 def test_icl_full_c4_slice(dev):
     # BASELINE config 4 at full size for one block: 8 est x 8 heads, 5000 q over 45000 cached keys.
     # Oracle on 2 (est, head) slices x 256 query rows; whole output finite and in the value hull.
