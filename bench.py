@@ -80,12 +80,104 @@ def cpu_baseline(seed: int = 3) -> dict:
                       f"median of {reps}, scaled x{EST * BLOCKS}"}
 
 
+def _time(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn() over `steps` calls (HIP events on the current stream)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def bench_smallhead(config: str, steps: int, warmup: int) -> list:
+    """Secondary lines for the d=16 configs of BASELINE.json (C1 column ISAB fp32, C2 row RoPE bf16,
+    C3 inference column ISAB bf16): ms per pass, algorithmic TFLOP/s and GB/s per kernel."""
+    import torch
+
+    import tabicl_mi355_attn as pk
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    E, H = 128, 8
+    recs = []
+
+    def line(name, ms, flops, nbytes, dtype, bound, workload):
+        peak = 157.3 if dtype == "f32" else PEAK_BF16_TFLOPS
+        tf = flops / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        roof = ({"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s", "frac": round(tf / peak, 4)}
+                if bound == "mfma" else
+                {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        recs.append({"metric": f"ms per {name} pass", "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps,
+                     "warmup": warmup, "higher_is_better": False, "dtype": dtype, "data": "synthetic N(0,1)",
+                     "config": {"workload": workload}, "attn_tflops": round(tf, 2), "hbm_gbs_algorithmic": round(gbs, 1),
+                     "roofline": roof})
+
+    if config in ("c1", "all"):
+        g.manual_seed(0)
+        B = 400
+        q1 = torch.randn(B, 128, E, generator=g, device=dev) * 0.25
+        k1 = torch.randn(B, 1024, E, generator=g, device=dev)
+        v1 = torch.randn(B, 1024, E, generator=g, device=dev)
+        q2 = torch.randn(B, 1024, E, generator=g, device=dev) * 0.25
+        k2 = torch.randn(B, 128, E, generator=g, device=dev)
+        v2 = torch.randn(B, 128, E, generator=g, device=dev)
+        ms1 = _time(lambda: pk.hx_attention(q1, k1, v1, H), steps, warmup)
+        ms2 = _time(lambda: pk.hx_attention(q2, k2, v2, H), steps, warmup)
+        fl = 4.0 * 128 * 1024 * 16 * H * B
+        by = 4.0 * B * (128 * E + 2 * 1024 * E + 128 * E)  # Q + K + V + O; the same for both passes
+        line("C1 column ISAB-1 fp32 (hx)", ms1, fl, by, "f32", "mfma", "400 x 128 q over 1024 keys, 8x16, fp32")
+        line("C1 column ISAB-2 fp32 (hx)", ms2, fl, by, "f32", "mfma", "400 x 1024 q over 128 keys, 8x16, fp32")
+    if config in ("c2", "all"):
+        g.manual_seed(1)
+        B, L = 16384, 104
+        qkv = torch.randn(B, L, 3 * E, generator=g, device=dev).to(torch.bfloat16)
+
+        class _Rope:
+            interleaved = False
+            freqs = 10000.0 ** (-torch.arange(0, 16, 2, dtype=torch.float32) / 16)
+
+            def get_seq_pos(self, n, device=None, dtype=torch.float32):
+                return torch.arange(n, device=device, dtype=dtype)
+
+        rope = _Rope()
+        ms = _time(lambda: pk.pk_self_attention(qkv, H, None, rope, 0.25), steps, warmup)
+        line("C2 row interaction (pk_self, RoPE)", ms, 4.0 * L * L * 16 * H * B, 2.0 * B * L * 4 * E, "bf16", "hbm",
+             "16384 x 104 tokens, packed qkv, RoPE halves base 1e4, 8x16, bf16")
+    if config in ("c3", "all"):
+        g.manual_seed(2)
+        B, T, valid = 800, 50000, 45000
+        q = (torch.randn(B, 128, E, generator=g, device=dev) * 0.25).to(torch.bfloat16)
+        kv = torch.randn(B, T, 2 * E, generator=g, device=dev).to(torch.bfloat16)
+        vt = torch.tensor([valid], dtype=torch.int32, device=dev)
+        ms1 = _time(lambda: pk.hxq_attention(q, kv, vt, H), steps, warmup)
+        line("C3 column ISAB-1 (hxq, 128 q over 45k of 50k keys)", ms1, 4.0 * 128 * valid * 16 * H * B,
+             2.0 * B * (128 * E * 2 + valid * 2 * E), "bf16", "hbm", "800 x 128 q, packed kv 50000 rows, valid 45000")
+        del kv
+        q2 = torch.randn(B, T, E, generator=g, device=dev).to(torch.bfloat16)
+        kv2 = torch.randn(B, 128, 2 * E, generator=g, device=dev).to(torch.bfloat16)
+        ms2 = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25), steps, warmup)
+        line("C3 column ISAB-2 (pk_cross, 50k q over 128 keys)", ms2, 4.0 * T * 128 * 16 * H * B,
+             2.0 * B * (2 * T * E + 128 * 2 * E), "bf16", "hbm", "800 x 50000 q over 128 inducing keys")
+    return recs
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "all"],
+                    help="c4 (default) is the headline line; c1/c2/c3/all print the d=16 kernel lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -93,6 +185,12 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.config != "c4":
+        torch.cuda.set_device(0)
+        for rec in bench_smallhead(args.config, args.steps, args.warmup):
+            print(json.dumps(rec), flush=True)
+        return 0
 
     import tabicl_mi355_icl as icl
 
