@@ -309,6 +309,189 @@ __global__ __launch_bounds__(SH_NW * 64) void smallhead_fwd_kernel(ShParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Resident-keys kernel (bf16, Lk <= 128: row self attention over 104 tokens, CLS, ISAB-2 over the
+// 128 inducing points). The workgroup loads all keys of its batch element once (K with RoPE,
+// row-major V, per-key bias) and then walks query blocks of 64; each wave takes 16 queries and runs
+// the 8 heads one after the other, each head a single pass (scores for all keys, exact softmax,
+// PV) with no online-softmax state, which keeps the register count low enough for two workgroups
+// per CU. The V^T operands come from ds_read_b64_tr_b16 on the row-major V tile (the LDS
+// transposes 16-bit elements across lanes), so V is never transposed by threads.
+// ---------------------------------------------------------------------------------------------
+constexpr int RS_NW = 4;
+constexpr int RS_QB = 16 * RS_NW;
+constexpr int RS_LK = 128;
+constexpr int RS_NKT = RS_LK / 16;
+constexpr int RS_KSTR = SH_E + 8;   // K rows: 8-byte operand reads of 16 rows spread over banks
+constexpr int RS_VSTR = SH_E + 16;  // V rows: the 4-row x 32-byte groups of a transposed read hit
+                                    // disjoint banks
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// RoPE of dims d0..d0+3 of one bf16 row (fp32 math). Fast paths for the full-width rotations
+// (rot = 16): halves (partner chunk d0 ^ 8) and pairs (partner inside the chunk).
+__device__ __forceinline__ f32x4 rope4_bf16(const bf16* row, const float* cs, const float* sn, int d0,
+                                            int rope, int half, int rot) {
+  const bf16x4 own = *(const bf16x4*)(row + d0);
+  const float4 c = *(const float4*)(cs + d0);
+  const float4 s = *(const float4*)(sn + d0);
+  const float cv[4] = {c.x, c.y, c.z, c.w};
+  const float sv[4] = {s.x, s.y, s.z, s.w};
+  f32x4 y;
+  if (rope == 2 && half == 8 && rot == 16) {
+    const bf16x4 pt = *(const bf16x4*)(row + (d0 ^ 8));
+    const float sg = (d0 & 8) ? 1.f : -1.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = (float)own[r] * cv[r] + sg * (float)pt[r] * sv[r];
+  } else if (rope == 1 && rot == 16) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float xp = (float)own[r ^ 1];
+      y[r] = (float)own[r] * cv[r] + ((r & 1) ? xp : -xp) * sv[r];
+    }
+  } else {
+    y = rope4<bf16>(row, cs, sn, d0, rope, half, rot);
+  }
+  return y;
+}
+
+__device__ __forceinline__ float quad_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <bool BIAS>
+__global__ __launch_bounds__(RS_NW * 64, 2) void sh_resident_kernel(ShParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 lds_k[RS_LK * RS_KSTR];
+  __shared__ __attribute__((aligned(16))) bf16 lds_v[RS_LK * RS_VSTR];
+  __shared__ __attribute__((aligned(16))) float lds_b2[RS_LK];
+
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = work / p.nwg_b;
+  const int qb0 = (work % p.nwg_b) * p.qbpw;
+  const int lk = p.Lk;
+  const int nkt = (lk + 15) >> 4;
+  const int tid = threadIdx.x;
+
+  // fill: K rows with RoPE (fp32 math, cast), V rows as they are, log2-scaled key bias; keys past
+  // Lk (up to the 16-key tile boundary) get zero K/V and a -inf bias
+  {
+    const bf16* kbase = (const bf16*)p.k + b * p.k_sb;
+    const bf16* vbase = (const bf16*)p.v + b * p.v_sb;
+    const int nk = nkt * 16;
+    for (int u = tid; u < nk * (SH_E / 4); u += RS_NW * 64) {
+      const int key = u >> 5, d0 = (u & 31) * 4;
+      bf16x4 val = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+      if (key < lk) {
+        const bf16* src = kbase + (int64_t)key * p.k_sr;
+        if (p.rope) {
+          const f32x4 y = rope4_bf16(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0, p.rope,
+                                     p.half, p.rot);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) val[r] = (bf16)y[r];
+        } else {
+          val = *(const bf16x4*)(src + d0);
+        }
+      }
+      *(bf16x4*)(lds_k + key * RS_KSTR + d0) = val;
+    }
+    for (int u = tid; u < nk * (SH_E / 8); u += RS_NW * 64) {
+      const int key = u >> 4, c8 = (u & 15) * 8;
+      const uint4 val = key < lk ? ldg16(vbase + (int64_t)key * p.v_sr + c8) : make_uint4(0, 0, 0, 0);
+      *(uint4*)(lds_v + key * RS_VSTR + c8) = val;
+    }
+    for (int j = tid; j < nk; j += RS_NW * 64) {
+      float b2 = TA_NEG_INF;
+      if (j < lk) b2 = BIAS ? fmaxf(p.bias[b * p.bias_sb + j] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
+      lds_b2[j] = b2;
+    }
+  }
+  __syncthreads();
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, kap = lane >> 4;
+  const bf16* qbase = (const bf16*)p.q + b * p.q_sb;
+  bf16* obase = (bf16*)p.o + b * p.o_sb;
+  // transposed-read lane roles: lane 4j + q of group kap points at key 4*kap + j, dims 4q..4q+3
+  const int tr_key = 4 * kap + (l16 >> 2), tr_col = 4 * (l16 & 3);
+
+  for (int qbi = 0; qbi < p.qbpw; ++qbi) {
+    const int qb = qb0 + qbi;
+    if (qb >= p.nqb) break;
+    const int qi = qb * RS_QB + wave * 16 + l16;
+    const bool qok = qi < p.Lq;
+    const bf16* qrow = qbase + (int64_t)qi * p.q_sr;
+#pragma unroll 2
+    for (int g = 0; g < SH_H; ++g) {
+      const int d0 = g * SH_D + 4 * kap;
+      bf16x4 qop = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+      if (qok) {
+        if (p.rope) {
+          const f32x4 y = rope4_bf16(qrow, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E, d0, p.rope,
+                                     p.half, p.rot);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) qop[r] = (bf16)(y[r] * p.scale);
+        } else {
+          const bf16x4 raw = *(const bf16x4*)(qrow + d0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) qop[r] = p.scale == 1.f ? raw[r] : (bf16)((float)raw[r] * p.scale);
+        }
+      }
+      f32x4 s[RS_NKT];
+      float mx = TA_NEG_INF;
+#pragma unroll
+      for (int kt = 0; kt < RS_NKT; ++kt) {
+        if (kt < nkt) {
+          const bf16x4 a = *(const bf16x4*)(lds_k + (16 * kt + l16) * RS_KSTR + d0);
+          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          s[kt] = mfma16x16x16(a, qop, z);
+          const f32x4 b2 = *(const f32x4*)(lds_b2 + 16 * kt + 4 * kap);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            s[kt][r] = fmaf(s[kt][r], TA_LOG2E, b2[r]);
+            mx = fmaxf(mx, s[kt][r]);
+          }
+        }
+      }
+      mx = quad_max(mx);
+      float lsum = 0.f;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < RS_NKT; ++kt) {
+        if (kt < nkt) {
+          bf16x4 pv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(s[kt][r] - mx);
+            lsum += pr;
+            pv[r] = (bf16)pr;
+          }
+          const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(lds_v + (16 * kt + tr_key) * RS_VSTR + g * SH_D + tr_col));
+          o = mfma16x16x16(__builtin_bit_cast(bf16x4, t), pv, o);
+        }
+      }
+      const float lt = quad_sum(lsum);
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      if (qok) {
+        bf16x4 ov;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
+        *(bf16x4*)(obase + (int64_t)qi * p.o_sr + d0) = ov;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
@@ -328,6 +511,23 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   p.rope = rope; p.half = half; p.rot = rot;
   p.scale = scale;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
+  if (dtype == 0 && Lk <= RS_LK && valid == nullptr) {
+    // all keys resident in LDS: one (16 queries, head) unit at a time, no online softmax
+    p.nqb = (int)((Lq + RS_QB - 1) / RS_QB);
+    // enough query blocks per workgroup to amortise the key fill, while keeping >= ~8 workgroups
+    // per CU for the whole grid
+    const int64_t target_wgs = 256 * 8;
+    int64_t qbpw = (B * (int64_t)p.nqb + target_wgs - 1) / target_wgs;
+    qbpw = qbpw < 1 ? 1 : (qbpw > 16 ? 16 : qbpw);
+    p.qbpw = (int)(qbpw > p.nqb ? p.nqb : qbpw);
+    p.nwg_b = (p.nqb + p.qbpw - 1) / p.qbpw;
+    const int64_t nblk = B * (int64_t)p.nwg_b;
+    if (bias)
+      hipLaunchKernelGGL((sh_resident_kernel<true>), dim3((unsigned)nblk), dim3(RS_NW * 64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((sh_resident_kernel<false>), dim3((unsigned)nblk), dim3(RS_NW * 64), 0, stream, p);
+    return (int)hipGetLastError();
+  }
   p.nqb = (int)((Lq + SH_QB - 1) / SH_QB);
   const int kt = 64;
   // all keys in one tile: keep them resident and walk up to 8 query blocks per workgroup
