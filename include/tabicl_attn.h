@@ -55,10 +55,21 @@ int tabicl_hx_fwd(const void* q, const void* k, const void* v, const float* bias
  * Replaces tabicl_pk::hxq_fwd (reference scripts/tabicl_tpu_pallas_attn.py:299-306, 323-336).
  * valid: device int32 [valid_n] with valid_n in {1, B} (valid_n = B extends the reference to ragged
  * batches); keys at positions >= valid are ignored; a row with no valid key is written as 0.
+ * workspace: optional device buffer of tabicl_hxq_workspace_bytes(...) bytes (16-byte aligned).
+ * With it the key range of long inputs may be split over more workgroups and merged by a second
+ * kernel on the same stream; NULL (or too small) runs unsplit. Calls that overlap on the GPU must
+ * not share a workspace.
  */
 int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const void* kv, void* out,
                    int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
-                   void* stream);
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes tabicl_hxq_fwd can use for these sizes on the current device (0: it never
+ * splits them). No counterpart in the reference (its Pallas grid needs no scratch in HBM).
+ */
+int64_t tabicl_hxq_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h,
+                                   int32_t dtype);
 
 /*
  * Self attention over the packed in-projection qkv [B, L, 3E] with in-kernel RoPE on q and k, then

@@ -6,20 +6,7 @@
 
 #include "../../include/tabicl_attn.h"
 #include "common.h"
-
-int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
-                          int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
-                          int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
-                          int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
-                          int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
-                          void* ws, int64_t ws_bytes, hipStream_t stream);
-int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int dtype);
-int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
-                            int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
-                            const float* bias, int64_t bias_sb, const int32_t* valid,
-                            int64_t valid_n, const float* cq, const float* sq, const float* ck,
-                            const float* sk, int rope, int half, int rot, float scale, int64_t B,
-                            int64_t Lq, int64_t Lk, int dtype, hipStream_t stream);
+#include "launch.h"
 
 namespace {
 
@@ -126,13 +113,14 @@ int tabicl_hx_fwd(const void* q, const void* k, const void* v, const float* bias
   return launch_status(
       tabicl_launch_smallhead(q, Lq * E, E, k, Lk * E, E, v, Lk * E, E, out, bias,
                               bias && bias_b == B ? Lk : 0, nullptr, 0, nullptr, nullptr, nullptr,
-                              nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype, (hipStream_t)stream),
+                              nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype, nullptr, 0,
+                              (hipStream_t)stream),
       "hx_fwd");
 }
 
 int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const void* kv, void* out,
                    int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
-                   void* stream) {
+                   void* workspace, int64_t workspace_bytes, void* stream) {
   int st = smallhead_shape("hxq_fwd", B, Lq, Lk, E, h, dtype);
   if (st) return st;
   if (!valid || (valid_n != 1 && valid_n != B))
@@ -142,12 +130,20 @@ int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const v
     return fail(1, "hxq_fwd: pointers must be 16-byte aligned");
   if (B == 0 || Lq == 0) return 0;
   const char* kvb = (const char*)kv;
+  void* ws = workspace && aligned16(workspace) ? workspace : nullptr;
   return launch_status(
       tabicl_launch_smallhead(q, Lq * E, E, kvb, Lk * 2 * E, 2 * E, kvb + E * esize(dtype),
                               Lk * 2 * E, 2 * E, out, nullptr, 0, valid, valid_n, nullptr, nullptr,
-                              nullptr, nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype,
-                              (hipStream_t)stream),
+                              nullptr, nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype, ws,
+                              ws ? workspace_bytes : 0, (hipStream_t)stream),
       "hxq_fwd");
+}
+
+int64_t tabicl_hxq_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h,
+                                   int32_t dtype) {
+  if (E != 128 || h != 8 || B <= 0 || Lq <= 0 || Lk <= 0) return 0;
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) return 0;
+  return tabicl_launch_smallhead_ws_bytes(B, Lq, Lk, dtype, false, 0);
 }
 
 int tabicl_pk_self_fwd(const void* qkv, const float* bias, int64_t bias_b, const float* cos_t,
@@ -169,7 +165,8 @@ int tabicl_pk_self_fwd(const void* qkv, const float* bias, int64_t bias_b, const
       tabicl_launch_smallhead(base, L * 3 * E, 3 * E, base + E * es, L * 3 * E, 3 * E,
                               base + 2 * E * es, L * 3 * E, 3 * E, out, bias,
                               bias && bias_b == B ? L : 0, nullptr, 0, cos_t, sin_t, cos_t, sin_t,
-                              rope, half, rot, scale, B, L, L, dtype, (hipStream_t)stream),
+                              rope, half, rot, scale, B, L, L, dtype, nullptr, 0,
+                              (hipStream_t)stream),
       "pk_self_fwd");
 }
 
@@ -193,7 +190,7 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
       tabicl_launch_smallhead(q, q_b == 1 && B > 1 ? 0 : Lq * E, E, kvb, Lk * 2 * E, 2 * E,
                               kvb + E * esize(dtype), Lk * 2 * E, 2 * E, out, bias,
                               bias && bias_b == B ? Lk : 0, nullptr, 0, cq, sq, ck, sk, rope, half,
-                              rot, scale, B, Lq, Lk, dtype, (hipStream_t)stream),
+                              rot, scale, B, Lq, Lk, dtype, nullptr, 0, (hipStream_t)stream),
       "pk_cross_fwd");
 }
 

@@ -1,0 +1,33 @@
+// Host launchers of the kernel families (device pointers, element strides, HIP stream); the C ABI
+// in abi.hip checks arguments and translates the reference's op signatures to these calls.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// d = 64 cached-KV attention (icl_fwd.hip).
+int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
+                          int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
+                          int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
+                          int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
+                          int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
+                          void* ws, int64_t ws_bytes, hipStream_t stream);
+int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int dtype);
+
+// Small-head (8 x 16) attention (smallhead_fwd.hip): picks the resident, streaming or general
+// kernel for the shape. ws may be null (no key split).
+int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
+                            int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
+                            const float* bias, int64_t bias_sb, const int32_t* valid,
+                            int64_t valid_n, const float* cq, const float* sq, const float* ck,
+                            const float* sk, int rope, int half, int rot, float scale, int64_t B,
+                            int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
+                            hipStream_t stream);
+int64_t tabicl_launch_smallhead_ws_bytes(int64_t B, int64_t Lq, int64_t Lk, int dtype, bool bias,
+                                         int rope);
+
+// Streaming bf16 small-head kernel without RoPE / key bias (smallhead_stream.hip).
+int tabicl_launch_ss(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
+                     int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
+                     const int32_t* valid, int64_t valid_n, float scale, int64_t B, int64_t Lq,
+                     int64_t Lk, void* ws, int64_t ws_bytes, hipStream_t stream);
+int64_t tabicl_launch_ss_ws_bytes(int64_t B, int64_t Lq, int64_t Lk);

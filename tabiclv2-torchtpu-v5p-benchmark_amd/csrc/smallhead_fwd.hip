@@ -18,6 +18,7 @@
 // so that the S^T accumulator is already the B operand of the PV product and every softmax
 // statistic of a query lives in the four lanes l%16 + 16j.
 #include "common.h"
+#include "launch.h"
 
 namespace {
 
@@ -326,8 +327,6 @@ constexpr int RS_KSTR = SH_E + 8;   // K rows: 8-byte operand reads of 16 rows s
 constexpr int RS_VSTR = SH_E + 16;  // V rows: the 4-row x 32-byte groups of a transposed read hit
                                     // disjoint banks
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // RoPE of dims d0..d0+3 of one bf16 row (fp32 math). Fast paths for the full-width rotations
 // (rot = 16): halves (partner chunk d0 ^ 8) and pairs (partner inside the chunk).
@@ -356,18 +355,6 @@ __device__ __forceinline__ f32x4 rope4_bf16(const bf16* row, const float* cs, co
   return y;
 }
 
-__device__ __forceinline__ float quad_max(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float quad_sum(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 
 template <bool BIAS>
 __global__ __launch_bounds__(RS_NW * 64, 2) void sh_resident_kernel(ShParams p) {
@@ -499,7 +486,11 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
                             const float* bias, int64_t bias_sb, const int32_t* valid,
                             int64_t valid_n, const float* cq, const float* sq, const float* ck,
                             const float* sk, int rope, int half, int rot, float scale, int64_t B,
-                            int64_t Lq, int64_t Lk, int dtype, hipStream_t stream) {
+                            int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
+                            hipStream_t stream) {
+  if (dtype == 0 && Lk > RS_LK && bias == nullptr && rope == 0)
+    return tabicl_launch_ss(q, q_sb, q_sr, k, k_sb, k_sr, v, v_sb, v_sr, o, valid, valid_n, scale, B,
+                            Lq, Lk, ws, ws_bytes, stream);
   ShParams p;
   p.q = q; p.q_sb = q_sb; p.q_sr = q_sr;
   p.k = k; p.k_sb = k_sb; p.k_sr = k_sr;
@@ -541,4 +532,10 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     hipLaunchKernelGGL((smallhead_fwd_kernel<float, 64>), dim3((unsigned)nblk), dim3(SH_NW * 64), 0,
                        stream, p);
   return (int)hipGetLastError();
+}
+
+int64_t tabicl_launch_smallhead_ws_bytes(int64_t B, int64_t Lq, int64_t Lk, int dtype, bool bias,
+                                         int rope) {
+  if (dtype == 0 && Lk > RS_LK && !bias && rope == 0) return tabicl_launch_ss_ws_bytes(B, Lq, Lk);
+  return 0;
 }

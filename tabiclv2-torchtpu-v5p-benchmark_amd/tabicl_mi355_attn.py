@@ -165,9 +165,26 @@ def _hxq_fwd(valid: Tensor, q: Tensor, kv: Tensor, h: int, bk: int, prec: int) -
     if valid.dtype != torch.int32:
         raise ValueError("valid must be int32")
     out = torch.empty_like(q)
+    code = _nat.dtype_code(q.dtype)
+    ws = _hxq_workspace(B, Lq, Lk, E, h, code, q.device)
     _nat.call("tabicl_hxq_fwd", valid.data_ptr(), valid.numel(), q.data_ptr(), kv.data_ptr(), out.data_ptr(),
-              B, Lq, Lk, E, h, _nat.dtype_code(q.dtype), _nat.stream_of(q))
+              B, Lq, Lk, E, h, code, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+              _nat.stream_of(q))
     return out
+
+
+_HXQ_WS_BYTES: dict = {}
+
+
+def _hxq_workspace(B: int, Lq: int, Lk: int, E: int, h: int, code: int, device) -> Optional[Tensor]:
+    """Scratch for the key-split path of the streaming kernel (size from the library, per shape and
+    device), from torch's caching allocator on the launch stream; None when the call does not split."""
+    key = (B, Lq, Lk, E, h, code, device.index)
+    nbytes = _HXQ_WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = int(_nat.load().tabicl_hxq_workspace_bytes(B, Lq, Lk, E, h, code))
+        _HXQ_WS_BYTES[key] = nbytes
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
 
 
 @_hxq_fwd.register_fake

@@ -25,7 +25,8 @@ _f32 = ctypes.c_float
 # name -> argtypes, in the order of include/tabicl_attn.h
 SIGNATURES = {
     "tabicl_hx_fwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i32, _i32, _c_p],
-    "tabicl_hxq_fwd": [_c_p, _i64, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _i32, _c_p],
+    "tabicl_hxq_fwd": [_c_p, _i64, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _i32, _c_p, _i64, _c_p],
+    "tabicl_hxq_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _i32],
     "tabicl_pk_self_fwd": [_c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
                            _f32, _i32, _c_p],
     "tabicl_pk_cross_fwd": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
@@ -40,7 +41,7 @@ SIGNATURES = {
     "tabicl_attn_version": [],
 }
 _RESTYPES = {"tabicl_attn_last_error": ctypes.c_char_p, "tabicl_attn_version": ctypes.c_char_p,
-             "tabicl_icl_workspace_bytes": ctypes.c_int64}
+             "tabicl_icl_workspace_bytes": ctypes.c_int64, "tabicl_hxq_workspace_bytes": ctypes.c_int64}
 
 
 class NativeLibraryError(RuntimeError):

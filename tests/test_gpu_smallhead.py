@@ -225,3 +225,65 @@ def test_no_nan_with_garbage_past_valid(dev):
     assert torch.isfinite(out.float()).all()
     ref = O.hxq_ref(q, kv[:, :300], np.array([300]), H)
     assert _err(out, ref) <= 2e-2
+
+
+# --- streaming kernel (bf16, Lk > 128, no RoPE / key bias): reference-point moves, key splits ---
+
+@pytest.mark.parametrize("name,B,Lq,Lk", [
+    ("multi_query_groups", 2, 300, 700),
+    ("ragged_queries", 3, 77, 1500),
+    ("one_tile_past_resident", 2, 64, 129),
+])
+def test_stream_shapes(dev, name, B, Lq, Lk):
+    pk = _attn()
+    g = _gen(11)
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16)
+    k = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
+    print(f"[stream] {name}", flush=True)
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H)
+    assert _err(out, O.hx_ref(q, k, v, H)) <= 2e-2
+
+
+@pytest.mark.parametrize("name,qscale,kshift", [
+    ("large_scores", 3.0, 0.0),          # scores reach ~2^70 over the first tile's scale
+    ("very_negative_scores", -3.0, 5.0),  # every score ~ -240 nats: exp underflows without a move
+])
+def test_stream_reference_moves(dev, name, qscale, kshift):
+    pk = _attn()
+    g = _gen(12)
+    B, Lq, Lk = 2, 128, 3000
+    if kshift:
+        q = torch.full((B, Lq, E), qscale) + 0.1 * torch.randn(B, Lq, E, generator=g)
+    else:
+        q = qscale * torch.randn(B, Lq, E, generator=g)
+    q = q.to(torch.bfloat16)
+    kv = (torch.randn(B, Lk, 2 * E, generator=g) + torch.cat(
+        [torch.full((E,), kshift), torch.zeros(E)])).to(torch.bfloat16)
+    print(f"[stream] {name}", flush=True)
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(2900, dtype=torch.int32).to(dev), H)
+    assert torch.isfinite(out.float()).all()
+    assert _err(out, O.hxq_ref(q, kv, np.array([2900]), H)) <= 2e-2
+
+
+def test_stream_split_matches_unsplit(dev):
+    # the key-split path (workspace given) against the one-pass path (no workspace) of the same
+    # library call, and both against the oracle on a subset of rows
+    import tabicl_mi355_native as nat
+    pk = _attn()
+    g = _gen(13)
+    B, Lq, Lk = 2, 128, 40000
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16).to(dev)
+    kv = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16).to(dev)
+    valid = torch.tensor([39000, 20001], dtype=torch.int32).to(dev)
+    nbytes = int(nat.load().tabicl_hxq_workspace_bytes(B, Lq, Lk, E, H, 0))
+    assert nbytes > 0, "this shape should split its keys"
+    split = pk.hxq_attention(q, kv, valid, H)
+    one = torch.empty_like(q)
+    nat.call("tabicl_hxq_fwd", valid.data_ptr(), B, q.data_ptr(), kv.data_ptr(), one.data_ptr(), B, Lq, Lk, E,
+             H, 0, None, 0, nat.stream_of(q))
+    torch.cuda.synchronize()
+    assert float((split.float() - one.float()).abs().max()) <= 1e-2
+    ref = O.hxq_ref(q[:, :16].cpu(), kv.cpu(), valid.cpu().numpy(), H)
+    assert _err(split[:, :16], ref) <= 2e-2
+    assert _err(one[:, :16], ref) <= 2e-2
