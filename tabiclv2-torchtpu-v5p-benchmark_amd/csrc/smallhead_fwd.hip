@@ -312,21 +312,25 @@ __global__ __launch_bounds__(SH_NW * 64) void smallhead_fwd_kernel(ShParams p) {
 
 // ---------------------------------------------------------------------------------------------
 // Resident-keys kernel (bf16, Lk <= 128: row self attention over 104 tokens, CLS, ISAB-2 over the
-// 128 inducing points). The workgroup loads all keys of its batch element once (K with RoPE,
-// row-major V, per-key bias) and then walks query blocks of 64; each wave takes 16 queries and runs
-// the 8 heads one after the other, each head a single pass (scores for all keys, exact softmax,
-// PV) with no online-softmax state, which keeps the register count low enough for two workgroups
-// per CU. The V^T operands come from ds_read_b64_tr_b16 on the row-major V tile (the LDS
-// transposes 16-bit elements across lanes), so V is never transposed by threads.
+// 128 inducing points, hxq over short key sets). The workgroup loads all keys of its batch element
+// once (K with RoPE, row-major V, per-key additive term b2 = bias*log2e, 0 without bias, -inf past
+// the valid length) and then walks query blocks of 16 * NW; each wave takes 16 queries and runs the
+// 8 heads one after the other, each head one pass over all keys:
+//   x = K (q' log2e) + b2         16x16x32 MFMAs: q' log2e as a bf16 high part and the bf16
+//                                 remainder in the two k-halves, b2 as the accumulator input
+//   p = bf16(exp2(x)), l = 1 p    (ones-operand MFMA)
+//   O^T = V^T P^T / l             V^T from ds_read_b64_tr_b16 on the row-major V tile
+// exp2 takes x without the row maximum subtracted; only when l falls outside [2^-64, 2^64] (or is
+// not finite) is the head recomputed with the exact maximum subtracted. Otherwise every p lies
+// below 2^64 and every p that matters above the fp32 floor, and fp32 / bf16 relative precision does
+// not depend on scale, so both give the softmax to rounding.
 // ---------------------------------------------------------------------------------------------
-constexpr int RS_NW = 4;
-constexpr int RS_QB = 16 * RS_NW;
 constexpr int RS_LK = 128;
-constexpr int RS_NKT = RS_LK / 16;
-constexpr int RS_KSTR = SH_E + 8;   // K rows: 8-byte operand reads of 16 rows spread over banks
-constexpr int RS_VSTR = SH_E + 16;  // V rows: the 4-row x 32-byte groups of a transposed read hit
-                                    // disjoint banks
-
+constexpr int RS_NG = RS_LK / 32;   // 32-key groups
+constexpr int RS_KSTR = SH_E + 8;   // K rows of 272 B: a 16-row b128 operand read covers all banks
+constexpr int RS_VSTR = SH_E + 16;  // V rows of 288 B: the transposed reads of 8 rows cover all banks
+constexpr float RS_L_HI = 0x1p64f;
+constexpr float RS_L_LO = 0x1p-64f;
 
 // RoPE of dims d0..d0+3 of one bf16 row (fp32 math). Fast paths for the full-width rotations
 // (rot = 16): halves (partner chunk d0 ^ 8) and pairs (partner inside the chunk).
@@ -355,9 +359,79 @@ __device__ __forceinline__ f32x4 rope4_bf16(const bf16* row, const float* cs, co
   return y;
 }
 
+// q' log2e operand of one (query, head): dims d0..d0+7 as the bf16 high part (G < 2) or the bf16
+// remainder (G >= 2), q' = bf16(rope(q) * scale) as in the reference's packed kernels (:498-502).
+__device__ __forceinline__ bf16x8 rs_qop(const ShParams& p, const bf16* qrow, int qi, int d0, int G) {
+  float f[8];
+  if (p.rope) {
+    const float* cs = p.cq + (int64_t)qi * SH_E;
+    const float* sn = p.sq + (int64_t)qi * SH_E;
+    const f32x4 y0 = rope4_bf16(qrow, cs, sn, d0, p.rope, p.half, p.rot);
+    const f32x4 y1 = rope4_bf16(qrow, cs, sn, d0 + 4, p.rope, p.half, p.rot);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      f[r] = y0[r];
+      f[4 + r] = y1[r];
+    }
+  } else {
+    const bf16x8 raw = *(const bf16x8*)(qrow + d0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = (float)raw[j];
+  }
+  bf16x8 op;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x = (float)(bf16)(f[j] * p.scale) * TA_LOG2E;
+    const bf16 hi = (bf16)x;
+    op[j] = G < 2 ? hi : (bf16)(x - (float)hi);
+  }
+  return op;
+}
 
-template <bool BIAS>
-__global__ __launch_bounds__(RS_NW * 64, 2) void sh_resident_kernel(ShParams p) {
+// p = bf16(exp2(x - sub)) over the 32-key group kg: lane (l16, G) holds keys 32kg + 4G + r and
+// 32kg + 16 + 4G + r of query l16 (the k-slot order 8G + j of the 16x16x32 B operand).
+template <bool SUB>
+__device__ __forceinline__ bf16x8 rs_probs(const bf16* lds_k, const float* lds_b2, bf16x8 qop, int kg,
+                                           int kcol, int l16, int G, float sub) {
+  const bf16x8 ka0 = *(const bf16x8*)(lds_k + (32 * kg + l16) * RS_KSTR + kcol);
+  const bf16x8 ka1 = *(const bf16x8*)(lds_k + (32 * kg + 16 + l16) * RS_KSTR + kcol);
+  const f32x4 c0 = *(const f32x4*)(lds_b2 + 32 * kg + 4 * G);
+  const f32x4 c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
+  const f32x4 x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qop, c0, 0, 0, 0);
+  const f32x4 x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
+  bf16x8 pv;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    pv[r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x0[r] - sub : x0[r]);
+    pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
+  }
+  return pv;
+}
+
+// Largest x over the 32-key group kg (keys past the valid length hold -inf).
+__device__ __forceinline__ float rs_max(const bf16* lds_k, const float* lds_b2, bf16x8 qop, int kg, int kcol,
+                                        int l16, int G) {
+  const bf16x8 ka0 = *(const bf16x8*)(lds_k + (32 * kg + l16) * RS_KSTR + kcol);
+  const bf16x8 ka1 = *(const bf16x8*)(lds_k + (32 * kg + 16 + l16) * RS_KSTR + kcol);
+  const f32x4 c0 = *(const f32x4*)(lds_b2 + 32 * kg + 4 * G);
+  const f32x4 c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
+  const f32x4 x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qop, c0, 0, 0, 0);
+  const f32x4 x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
+  float m = TA_NEG_INF;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(x0[r], x1[r]));
+  return m;
+}
+
+__device__ __forceinline__ float rs_sum(bf16x8 pv) {
+  const bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f,
+                       (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pv, zero, 0, 0, 0)[0];
+}
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 2) void sh_resident_kernel(ShParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lds_k[RS_LK * RS_KSTR];
   __shared__ __attribute__((aligned(16))) bf16 lds_v[RS_LK * RS_VSTR];
   __shared__ __attribute__((aligned(16))) float lds_b2[RS_LK];
@@ -365,17 +439,21 @@ __global__ __launch_bounds__(RS_NW * 64, 2) void sh_resident_kernel(ShParams p) 
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int b = work / p.nwg_b;
   const int qb0 = (work % p.nwg_b) * p.qbpw;
-  const int lk = p.Lk;
-  const int nkt = (lk + 15) >> 4;
+  int lk = p.Lk;
+  if (p.valid) {
+    const int vl = p.valid[p.valid_n == 1 ? 0 : b];
+    lk = vl < 0 ? 0 : (vl < lk ? vl : lk);
+  }
+  const int ng = (lk + 31) / 32;
   const int tid = threadIdx.x;
 
-  // fill: K rows with RoPE (fp32 math, cast), V rows as they are, log2-scaled key bias; keys past
-  // Lk (up to the 16-key tile boundary) get zero K/V and a -inf bias
+  // fill: K rows with RoPE (fp32 math, cast), V rows as they are, b2 per key; keys past lk (up to
+  // the 32-key group boundary) get zero K/V and b2 = -inf
   {
     const bf16* kbase = (const bf16*)p.k + b * p.k_sb;
     const bf16* vbase = (const bf16*)p.v + b * p.v_sb;
-    const int nk = nkt * 16;
-    for (int u = tid; u < nk * (SH_E / 4); u += RS_NW * 64) {
+    const int nk = ng * 32;
+    for (int u = tid; u < nk * (SH_E / 4); u += NW * 64) {
       const int key = u >> 5, d0 = (u & 31) * 4;
       bf16x4 val = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
       if (key < lk) {
@@ -391,89 +469,86 @@ __global__ __launch_bounds__(RS_NW * 64, 2) void sh_resident_kernel(ShParams p) 
       }
       *(bf16x4*)(lds_k + key * RS_KSTR + d0) = val;
     }
-    for (int u = tid; u < nk * (SH_E / 8); u += RS_NW * 64) {
+    for (int u = tid; u < nk * (SH_E / 8); u += NW * 64) {
       const int key = u >> 4, c8 = (u & 15) * 8;
       const uint4 val = key < lk ? ldg16(vbase + (int64_t)key * p.v_sr + c8) : make_uint4(0, 0, 0, 0);
       *(uint4*)(lds_v + key * RS_VSTR + c8) = val;
     }
-    for (int j = tid; j < nk; j += RS_NW * 64) {
+    for (int j = tid; j < nk; j += NW * 64) {
       float b2 = TA_NEG_INF;
-      if (j < lk) b2 = BIAS ? fmaxf(p.bias[b * p.bias_sb + j] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
+      if (j < lk) b2 = p.bias ? fmaxf(p.bias[b * p.bias_sb + j] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
       lds_b2[j] = b2;
     }
   }
   __syncthreads();
 
   const int lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, kap = lane >> 4;
+  const int l16 = lane & 15, G = lane >> 4;
   const bf16* qbase = (const bf16*)p.q + b * p.q_sb;
   bf16* obase = (bf16*)p.o + b * p.o_sb;
-  // transposed-read lane roles: lane 4j + q of group kap points at key 4*kap + j, dims 4q..4q+3
-  const int tr_key = 4 * kap + (l16 >> 2), tr_col = 4 * (l16 & 3);
+  // transposed-read lane roles: lane 4j + c of group G points at key 4G + j, dims 4c..4c+3
+  const int tr_key = 4 * G + (l16 >> 2), tr_col = 4 * (l16 & 3);
 
   for (int qbi = 0; qbi < p.qbpw; ++qbi) {
     const int qb = qb0 + qbi;
     if (qb >= p.nqb) break;
-    const int qi = qb * RS_QB + wave * 16 + l16;
+    const int qw0 = qb * 16 * NW + wave * 16;
+    if (qw0 >= p.Lq) break;  // no barrier below: waves leave independently
+    const int qi = qw0 + l16;
     const bool qok = qi < p.Lq;
     const bf16* qrow = qbase + (int64_t)qi * p.q_sr;
-#pragma unroll 2
+#pragma unroll 1
     for (int g = 0; g < SH_H; ++g) {
-      const int d0 = g * SH_D + 4 * kap;
-      bf16x4 qop = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
-      if (qok) {
-        if (p.rope) {
-          const f32x4 y = rope4_bf16(qrow, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E, d0, p.rope,
-                                     p.half, p.rot);
+      const int kcol = g * SH_D + 8 * (G & 1);
+      bf16x8 qop;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) qop[r] = (bf16)(y[r] * p.scale);
-        } else {
-          const bf16x4 raw = *(const bf16x4*)(qrow + d0);
+      for (int j = 0; j < 8; ++j) qop[j] = (bf16)0.f;
+      if (qok) qop = rs_qop(p, qrow, qi, kcol, G);
+      bf16x8 pv[RS_NG];
+      float l = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) qop[r] = p.scale == 1.f ? raw[r] : (bf16)((float)raw[r] * p.scale);
+      for (int kg = 0; kg < RS_NG; ++kg) {
+        if (kg < ng) {
+          pv[kg] = rs_probs<false>(lds_k, lds_b2, qop, kg, kcol, l16, G, 0.f);
+          l += rs_sum(pv[kg]);
         }
       }
-      f32x4 s[RS_NKT];
-      float mx = TA_NEG_INF;
+      if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
+        // rare: recompute this head with the exact maximum subtracted (lanes in range keep theirs)
+        float mx = TA_NEG_INF;
 #pragma unroll
-      for (int kt = 0; kt < RS_NKT; ++kt) {
-        if (kt < nkt) {
-          const bf16x4 a = *(const bf16x4*)(lds_k + (16 * kt + l16) * RS_KSTR + d0);
-          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-          s[kt] = mfma16x16x16(a, qop, z);
-          const f32x4 b2 = *(const f32x4*)(lds_b2 + 16 * kt + 4 * kap);
+        for (int kg = 0; kg < RS_NG; ++kg)
+          if (kg < ng) mx = fmaxf(mx, rs_max(lds_k, lds_b2, qop, kg, kcol, l16, G));
+        mx = quad_max(mx);
+        const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
+        l = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            s[kt][r] = fmaf(s[kt][r], TA_LOG2E, b2[r]);
-            mx = fmaxf(mx, s[kt][r]);
+        for (int kg = 0; kg < RS_NG; ++kg) {
+          if (kg < ng) {
+            pv[kg] = rs_probs<true>(lds_k, lds_b2, qop, kg, kcol, l16, G, sub);
+            l += rs_sum(pv[kg]);
           }
         }
       }
-      mx = quad_max(mx);
-      float lsum = 0.f;
       f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < RS_NKT; ++kt) {
-        if (kt < nkt) {
-          bf16x4 pv;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pr = __builtin_amdgcn_exp2f(s[kt][r] - mx);
-            lsum += pr;
-            pv[r] = (bf16)pr;
-          }
-          const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(lds_v + (16 * kt + tr_key) * RS_VSTR + g * SH_D + tr_col));
-          o = mfma16x16x16(__builtin_bit_cast(bf16x4, t), pv, o);
+      for (int kg = 0; kg < RS_NG; ++kg) {
+        if (kg < ng) {
+          const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(lds_v + (32 * kg + tr_key) * RS_VSTR + g * SH_D + tr_col));
+          const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(lds_v + (32 * kg + 16 + tr_key) * RS_VSTR + g * SH_D + tr_col));
+          const bf16x4 a0 = __builtin_bit_cast(bf16x4, t0), a1 = __builtin_bit_cast(bf16x4, t1);
+          const bf16x8 va = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+          o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pv[kg], o, 0, 0, 0);
         }
       }
-      const float lt = quad_sum(lsum);
-      const float inv = lt > 0.f ? 1.f / lt : 0.f;
       if (qok) {
+        const float inv = l == 0.f ? 0.f : 1.f / l;
         bf16x4 ov;
 #pragma unroll
         for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
-        *(bf16x4*)(obase + (int64_t)qi * p.o_sr + d0) = ov;
+        *(bf16x4*)(obase + (int64_t)qi * p.o_sr + g * SH_D + 4 * G) = ov;
       }
     }
   }
@@ -502,9 +577,11 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   p.rope = rope; p.half = half; p.rot = rot;
   p.scale = scale;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
-  if (dtype == 0 && Lk <= RS_LK && valid == nullptr) {
-    // all keys resident in LDS: one (16 queries, head) unit at a time, no online softmax
-    p.nqb = (int)((Lq + RS_QB - 1) / RS_QB);
+  if (dtype == 0 && Lk <= RS_LK) {
+    // all keys resident in LDS: one (16 queries, head) unit at a time, no online softmax;
+    // 8 waves for long query sets, 4 when a batch element has at most 64 queries
+    const int nw = Lq > 64 ? 8 : 4;
+    p.nqb = (int)((Lq + 16 * nw - 1) / (16 * nw));
     // enough query blocks per workgroup to amortise the key fill, while keeping >= ~8 workgroups
     // per CU for the whole grid
     const int64_t target_wgs = 256 * 8;
@@ -513,10 +590,10 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     p.qbpw = (int)(qbpw > p.nqb ? p.nqb : qbpw);
     p.nwg_b = (p.nqb + p.qbpw - 1) / p.qbpw;
     const int64_t nblk = B * (int64_t)p.nwg_b;
-    if (bias)
-      hipLaunchKernelGGL((sh_resident_kernel<true>), dim3((unsigned)nblk), dim3(RS_NW * 64), 0, stream, p);
+    if (nw == 8)
+      hipLaunchKernelGGL((sh_resident_kernel<8>), dim3((unsigned)nblk), dim3(8 * 64), 0, stream, p);
     else
-      hipLaunchKernelGGL((sh_resident_kernel<false>), dim3((unsigned)nblk), dim3(RS_NW * 64), 0, stream, p);
+      hipLaunchKernelGGL((sh_resident_kernel<4>), dim3((unsigned)nblk), dim3(4 * 64), 0, stream, p);
     return (int)hipGetLastError();
   }
   p.nqb = (int)((Lq + SH_QB - 1) / SH_QB);

@@ -107,6 +107,8 @@ def test_hx_shared_bias_matches_broadcast(dev):
     ("valid_full", 2, 128, 1000, 1000, torch.bfloat16),
     ("valid_not_tile_aligned", 2, 64, 777, 129, torch.bfloat16),
     ("valid_beyond_lk_clamped", 2, 16, 300, 100000, torch.float32),
+    ("short_keys_resident", 3, 200, 100, 37, torch.bfloat16),
+    ("short_keys_resident_none_valid", 2, 64, 128, 0, torch.bfloat16),
 ])
 def test_hxq(dev, name, B, Lq, Lk, valid, dtype):
     pk = _attn()
