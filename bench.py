@@ -96,7 +96,7 @@ def _time(fn, steps: int, warmup: int) -> float:
     return a.elapsed_time(b) / steps
 
 
-def bench_smallhead(config: str, steps: int, warmup: int) -> list:
+def bench_smallhead(configs: set, steps: int, warmup: int) -> list:
     """Secondary lines for the d=16 configs of BASELINE.json (C1 column ISAB fp32, C2 row RoPE bf16,
     C3 inference column ISAB bf16): ms per pass, algorithmic TFLOP/s and GB/s per kernel."""
     import torch
@@ -121,7 +121,7 @@ def bench_smallhead(config: str, steps: int, warmup: int) -> list:
                      "config": {"workload": workload}, "attn_tflops": round(tf, 2), "hbm_gbs_algorithmic": round(gbs, 1),
                      "roofline": roof})
 
-    if config in ("c1", "all"):
+    if configs & {"c1", "all"}:
         g.manual_seed(0)
         B = 400
         q1 = torch.randn(B, 128, E, generator=g, device=dev) * 0.25
@@ -136,7 +136,7 @@ def bench_smallhead(config: str, steps: int, warmup: int) -> list:
         by = 4.0 * B * (128 * E + 2 * 1024 * E + 128 * E)  # Q + K + V + O; the same for both passes
         line("C1 column ISAB-1 fp32 (hx)", ms1, fl, by, "f32", "mfma", "400 x 128 q over 1024 keys, 8x16, fp32")
         line("C1 column ISAB-2 fp32 (hx)", ms2, fl, by, "f32", "mfma", "400 x 1024 q over 128 keys, 8x16, fp32")
-    if config in ("c2", "all"):
+    if configs & {"c2", "all"}:
         g.manual_seed(1)
         B, L = 16384, 104
         qkv = torch.randn(B, L, 3 * E, generator=g, device=dev).to(torch.bfloat16)
@@ -152,7 +152,7 @@ def bench_smallhead(config: str, steps: int, warmup: int) -> list:
         ms = _time(lambda: pk.pk_self_attention(qkv, H, None, rope, 0.25), steps, warmup)
         line("C2 row interaction (pk_self, RoPE)", ms, 4.0 * L * L * 16 * H * B, 2.0 * B * L * 4 * E, "bf16", "hbm",
              "16384 x 104 tokens, packed qkv, RoPE halves base 1e4, 8x16, bf16")
-    if config in ("c3", "all"):
+    if configs & {"c3", "all"}:
         g.manual_seed(2)
         B, T, valid = 800, 50000, 45000
         q = (torch.randn(B, 128, E, generator=g, device=dev) * 0.25).to(torch.bfloat16)
@@ -176,8 +176,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--config", default="c4", choices=["c4", "c1", "c2", "c3", "all"],
-                    help="c4 (default) is the headline line; c1/c2/c3/all print the d=16 kernel lines")
+    ap.add_argument("--config", default="c4",
+                    help="c4 (default) is the headline line; c1, c2, c3 (comma-separated) or all print the "
+                         "d=16 kernel lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -186,9 +187,12 @@ def main() -> int:
 
     import torch
 
-    if args.config != "c4":
+    configs = set(args.config.split(","))
+    if not configs <= {"c1", "c2", "c3", "c4", "all"}:
+        ap.error(f"unknown --config {args.config}")
+    if configs != {"c4"}:
         torch.cuda.set_device(0)
-        for rec in bench_smallhead(args.config, args.steps, args.warmup):
+        for rec in bench_smallhead(configs, args.steps, args.warmup):
             print(json.dumps(rec), flush=True)
         return 0
 

@@ -6,12 +6,12 @@
 // without RoPE or key bias once Lk exceeds what the resident kernel keeps in LDS.
 //   O = softmax(q k^T, keys < valid) V   per (batch, head), fp32 scores and softmax, P cast to bf16.
 //
-// Work decomposition. A workgroup = (batch b, key split s, head pair hg, 128 queries); 4 waves =
-// 2 heads x 2 halves of 64 queries, each wave four 16-query blocks of one head (145 VGPRs: three
-// workgroups per CU). Its key range streams through LDS in 32-key tiles holding K and V of its 2
-// heads (128 bytes per key, so every K/V byte is read from HBM once), copied by the load unit
-// itself (global_load_lds_dwordx4) seven tiles ahead, with 16-byte chunks XOR-swizzled per key so
-// that the LDS operand reads below do not conflict on banks.
+// Work decomposition. A workgroup = (batch b, key split s, head group hg of 4 heads, 128 queries);
+// 8 waves = 4 heads x 2 halves of 64 queries, each wave four 16-query blocks of one head (<= 128
+// VGPRs, two workgroups per CU). Its key range streams through LDS in 32-key tiles holding K and V
+// of its 4 heads (two whole 128-byte lines per key), copied by the load unit itself
+// (global_load_lds_dwordx4) seven tiles ahead, with 16-byte chunks XOR-swizzled per key so that
+// the LDS operand reads below do not conflict on banks.
 //
 // Per (16-query block, 32-key tile) a wave runs four v_mfma_f32_16x16x32_bf16:
 //   x  = K (q log2e) - m    two MFMAs; the 32-deep contraction holds q*log2e split in a bf16 high
@@ -22,12 +22,14 @@
 //   O^T += V^T P^T          V^T operands come from ds_read_b64_tr_b16 on row-major V.
 // so the VALU work per score is one v_exp_f32 and half a conversion.
 //
-// Softmax reference m (per query and head). m is not the running maximum: it starts at 0 and is
-// only moved when the running row sum l + sum would leave [2^-64, 2^64] (or is not finite). Then
-// the tile is recomputed against m' = m + ceil(max(tile max, log2 l)) and O, l are scaled by the
-// exact power of two 2^(m - m'). Between moves p <= 2^64, far inside the bf16/fp32 range, and the
-// relative precision of every p is that of fp32/bf16 at any scale, so the result equals the
-// max-subtracted softmax to rounding. The first tile of every split takes this path once.
+// Softmax reference m (per query and head). The sweep over a split's keys does not track the
+// running maximum: m is the (ceiled) maximum over the split's first tile and stays fixed, so p =
+// exp2(x) may exceed 1. The row sum l > 1/2 from the first tile on; if at the end of the sweep l <=
+// 2^96 and O is finite, every p stayed far inside the bf16/fp32 range and the result equals the
+// max-subtracted softmax to rounding (fp32/bf16 relative precision does not depend on scale). A
+// score more than ~66 nats above the first tile's maximum (or a NaN / inf) breaks that test; the
+// workgroup then sweeps the split again in exact mode, a classic online softmax that moves m by
+// exact powers of two. No test or branch runs per tile in the fast sweep.
 //
 // Key splits write fp32 partial (O, m, l) into a caller workspace; a merge kernel combines them.
 #include "common.h"
@@ -36,20 +38,19 @@ namespace {
 
 constexpr int SS_E = 128;
 constexpr int SS_H = 8;
-constexpr int SS_HPW = 2;                // heads per workgroup
+constexpr int SS_HPW = 4;                // heads per workgroup
 constexpr int SS_NHG = SS_H / SS_HPW;    // head groups
 constexpr int SS_NW = 2 * SS_HPW;        // waves per workgroup: heads x 2 query halves
 constexpr int SS_NB = 4;                 // 16-query blocks per wave
 constexpr int SS_QG = 2 * 16 * SS_NB;    // queries per workgroup
 constexpr int SS_KT = 32;                // keys per tile
-constexpr int SS_ROW = 32 * SS_HPW * 2;  // tile row bytes: K then V of the heads, bf16 (128)
-constexpr int SS_CPR = SS_ROW / 16;      // 16-byte chunks per row (8)
-constexpr int SS_TILE = SS_KT * SS_ROW;  // 4 KB
+constexpr int SS_ROW = 32 * SS_HPW * 2;  // tile row bytes: K then V of the heads, bf16 (256)
+constexpr int SS_CPR = SS_ROW / 16;      // 16-byte chunks per row (16)
+constexpr int SS_TILE = SS_KT * SS_ROW;  // 8 KB
 constexpr int SS_NBUF = 8;
 constexpr int SS_MAX_SPLIT = 8;
 constexpr int SS_MIN_TILES = 16;         // per key split
-constexpr float SS_L_HI = 0x1p64f;
-constexpr float SS_L_LO = 0x1p-64f;
+constexpr float SS_L_HI = 0x1p96f;   // row-sum bound of the fast sweep
 
 struct SsParams {
   const bf16* q;
@@ -69,11 +70,12 @@ struct SsParams {
   float2* ws_ml;  // [nsplit][B*Lq][H] (m, l), m in log2 units
 };
 
-// 16-byte chunk swizzle of a 128-byte tile row (key r): physical chunk = logical ^ ss_swz(r).
-// The 16 K-operand reads of one chunk column (rows r0..r0+15) and the 32 transposed V reads of
-// rows r0..r0+7 (chunk pairs {c, c^1}) each cover 16 distinct (row parity, chunk) bank slots of a
-// 256-byte bank line.
-__device__ __forceinline__ int ss_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// 16-byte chunk swizzle of a 256-byte tile row (key r): physical chunk = logical ^ ss_swz(r), a
+// bijection on r mod 16. The 16 K-operand reads of one chunk column (rows r0..r0+15) land on 16
+// distinct chunks, and so do the 32 transposed V reads of rows r0..r0+7 (chunk pairs {c, c^1}, c
+// even): each covers all 64 banks once.
+__device__ __forceinline__ int ss_swz(int r) { return ((2 * (r & 7)) | ((r >> 2) & 1)) ^ ((r >> 3) & 1); }
+static_assert(SS_CPR == 16, "swizzle above is for 16 chunks per row");
 
 // One 16-byte global -> LDS copy per lane: LDS[lds_addr + 16 * lane] = *src (lds_addr wave-uniform).
 // Issued as inline assembly so that the compiler does not wait for it before unrelated LDS reads;
@@ -88,130 +90,181 @@ __device__ __forceinline__ void ss_dma(const void* src, uint32_t lds_addr) {
 }
 #pragma clang diagnostic pop
 
-// Wait until at most N of this wave's tile copies are outstanding, then join the workgroup: after
-// it, every wave's copy of the tile N+1 copies back is in LDS and every wave has finished reading
-// the buffer the next copy overwrites.
-#define SS_WAIT_JOIN(N) asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier" ::: "memory")
-__device__ __forceinline__ void ss_wait_join(int n) {
-  static_assert(SS_NBUF - 2 == 6, "one case per possible count");
-  switch (n) {
-    case 0: SS_WAIT_JOIN(0); break;
-    case 1: SS_WAIT_JOIN(1); break;
-    case 2: SS_WAIT_JOIN(2); break;
-    case 3: SS_WAIT_JOIN(3); break;
-    case 4: SS_WAIT_JOIN(4); break;
-    case 5: SS_WAIT_JOIN(5); break;
-    default: SS_WAIT_JOIN(6); break;
-  }
+// Every sweep iteration issues exactly one copy per wave (past the end of the range the last tile
+// is copied again into a buffer nobody reads), so the wait for tile t is always "all but the
+// SS_NBUF - 2 newest copies". The join also waits for this wave's LDS operations (the restart flag).
+__device__ __forceinline__ void ss_wait_join() {
+  static_assert(SS_NBUF - 2 == 6, "vmcnt below");
+  asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-#undef SS_WAIT_JOIN
+__device__ __forceinline__ void ss_drain_join() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
-// Copy tile rows 8*wave .. 8*wave+7 (keys k0 + row, clamped to lk - 1 so that no key past the
-// valid length is read) of the heads at kb / vb into the tile buffer at LDS byte address buf.
-__device__ __forceinline__ void ss_issue(const bf16* kb, const bf16* vb, int64_t k_sr, int64_t v_sr,
-                                         uint32_t buf, int k0, int lk, int wave, int lane) {
+// Per-lane source of the tile copies: lane (row r = 4 * wave + lane / 16, physical chunk lane % 16)
+// copies logical chunk (lane % 16) ^ ss_swz(r) of key row k0 + r: K of the head group for chunks
+// 0..7, V for 8..15.
+struct SsSrc {
+  const char* base;  // chunk column of row 0
+  uint32_t stride;   // bytes between key rows
+  int row;
+};
+
+__device__ __forceinline__ SsSrc ss_src(const SsParams& p, int b, int hg, int wave, int lane) {
   constexpr int HALF = SS_CPR / 2;
-  const int row = (64 / SS_CPR) * wave + lane / SS_CPR;
-  const int lc = (lane % SS_CPR) ^ ss_swz(row);
-  const int64_t key = min(k0 + row, lk - 1);
-  const bf16* src = lc < HALF ? kb + key * k_sr + lc * 8 : vb + key * v_sr + (lc - HALF) * 8;
-  ss_dma(src, buf + 1024 * wave);
+  SsSrc s;
+  s.row = (64 / SS_CPR) * wave + lane / SS_CPR;
+  const int lc = (lane % SS_CPR) ^ ss_swz(s.row);
+  const bf16* kb = p.k + b * p.k_sb + hg * (SS_HPW * 16);
+  const bf16* vb = p.v + b * p.v_sb + hg * (SS_HPW * 16);
+  s.base = lc < HALF ? (const char*)(kb + lc * 8) : (const char*)(vb + (lc - HALF) * 8);
+  s.stride = (uint32_t)((lc < HALF ? p.k_sr : p.v_sr) * (int64_t)sizeof(bf16));
+  return s;
 }
 
-// p = bf16(exp2(x)) of one 16-query block over a 32-key tile. Lane (l16, G) holds keys
-// key0 + r and key0 + 16 + r (key0 = tile start + 4G, r = 0..3) of query l16, which is the
+// Copy the tile starting at key k0 (rows clamped to lk - 1: no key past the valid length is read).
+__device__ __forceinline__ void ss_issue(const SsSrc& s, uint32_t buf, int k0, int lk, int wave) {
+  const uint32_t key = (uint32_t)min(k0 + s.row, lk - 1);
+  ss_dma(s.base + (uint64_t)key * s.stride, buf + 1024 * wave);
+}
+
+// Scores x = K (q log2e) - m of one 16-query block over a 32-key tile. Lane (l16, G) holds keys
+// key0 + r (x0) and key0 + 16 + r (x1), key0 = tile start + 4G, r = 0..3, of query l16, which is the
 // k-slot order 8G + j of the B operand of the 16x16x32 products.
 template <bool MASK>
-__device__ __forceinline__ bf16x8 ss_probs(bf16x8 ka0, bf16x8 ka1, bf16x8 q, f32x4 negm, int key0,
-                                           int lk) {
-  const f32x4 x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, q, negm, 0, 0, 0);
-  const f32x4 x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, q, negm, 0, 0, 0);
+__device__ __forceinline__ void ss_scores(bf16x8 ka0, bf16x8 ka1, bf16x8 q, f32x4 negm, int key0, int lk,
+                                          f32x4& x0, f32x4& x1) {
+  x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, q, negm, 0, 0, 0);
+  x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, q, negm, 0, 0, 0);
+  if (MASK) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (key0 + r >= lk) x0[r] = TA_NEG_INF;
+      if (key0 + 16 + r >= lk) x1[r] = TA_NEG_INF;
+    }
+  }
+}
+
+__device__ __forceinline__ bf16x8 ss_exp(f32x4 x0, f32x4 x1, float d) {
   bf16x8 pv;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float e0 = x0[r], e1 = x1[r];
-    if (MASK) {
-      if (key0 + r >= lk) e0 = TA_NEG_INF;
-      if (key0 + 16 + r >= lk) e1 = TA_NEG_INF;
-    }
-    pv[r] = (bf16)__builtin_amdgcn_exp2f(e0);
-    pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(e1);
+    pv[r] = (bf16)__builtin_amdgcn_exp2f(x0[r] - d);
+    pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(x1[r] - d);
   }
   return pv;
 }
 
-__device__ __forceinline__ float ss_tile_sum(bf16x8 pv) {
-  const bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f,
-                       (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+__device__ __forceinline__ float ss_tile_sum(bf16x8 ones, bf16x8 pv) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pv, zero, 0, 0, 0)[0];
 }
 
-__device__ __forceinline__ bool ss_out_of_range(float nl) { return !(nl >= SS_L_LO && nl <= SS_L_HI); }
-
-// Move the reference m of the queries whose running sum left the range (see the file comment),
-// rescale their O and l exactly, and recompute p and the new running sum for this tile.
-template <bool MASK>
-__device__ __forceinline__ void ss_rebase(bf16x8 ka0, bf16x8 ka1, bf16x8 q, f32x4& negm,
-                                                    f32x4& o, float& l, bf16x8& pv, float& nl,
-                                                    int key0, int lk) {
-  const bool bad = ss_out_of_range(nl);
-  const f32x4 x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, q, negm, 0, 0, 0);
-  const f32x4 x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, q, negm, 0, 0, 0);
-  float mx = TA_NEG_INF;
+__device__ __forceinline__ float ss_tile_max(f32x4 x0, f32x4 x1) {
+  float m = TA_NEG_INF;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (!MASK || key0 + r < lk) mx = fmaxf(mx, x0[r]);
-    if (!MASK || key0 + 16 + r < lk) mx = fmaxf(mx, x1[r]);
-  }
-  mx = quad_max(mx);
-  // l < 2^el; l == 0 (nothing accumulated yet) puts no bound on the new reference
-  const float el = (float)__builtin_amdgcn_frexp_expf(l);
-  float ref = l != 0.f ? fmaxf(mx, el) : mx;
-  ref = fminf(fmaxf(ref, -1e4f), 1e4f);
-  const int d = bad ? (int)ceilf(ref) : 0;
-  if (d != 0) {
-    const float sc = __builtin_amdgcn_ldexpf(1.f, -d);
-    if (l != 0.f) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] *= sc;
-      l *= sc;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) negm[r] -= (float)d;
-  }
-  pv = ss_probs<MASK>(ka0, ka1, q, negm, key0, lk);
-  nl = l + ss_tile_sum(pv);
+  for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(x0[r], x1[r]));
+  return quad_max(m);
 }
 
-template <bool MASK>
-__device__ __forceinline__ void ss_tile(bf16x8 ka0, bf16x8 ka1, bf16x8 va, const bf16x8 (&qop)[SS_NB],
-                                        f32x4 (&negm)[SS_NB], f32x4 (&o)[SS_NB], float (&l)[SS_NB],
-                                        int key0, int lk) {
-  bf16x8 pv[SS_NB];
-  float nl[SS_NB];
+// Integer shift ceil(x) clamped to [-1e4, 1e4] (NaN and -inf give 0).
+__device__ __forceinline__ float ss_ceil_shift(float x) {
+  return x > -1e4f ? fminf(ceilf(x), 1e4f) : 0.f;
+}
+
+struct SsState {
+  bf16x8 ones;  // all-ones A operand of the row-sum products
+  bf16x8 qop[SS_NB];
+  f32x4 negm[SS_NB];
+  f32x4 o[SS_NB];
+  float l[SS_NB];
+};
+
+// One tile. Fast mode: p = exp2(x) against the fixed m. Exact mode: per tile, m moves up to the
+// tile maximum (by a whole number, so that O and l rescale exactly).
+template <bool EXACT, bool MASK>
+__device__ __forceinline__ void ss_tile(SsState& st, bf16x8 ka0, bf16x8 ka1, bf16x8 va, int key0, int lk) {
+#pragma unroll
+  for (int i = 0; i < SS_NB; ++i) {
+    f32x4 x0, x1;
+    ss_scores<MASK>(ka0, ka1, st.qop[i], st.negm[i], key0, lk, x0, x1);
+    bf16x8 pv;
+    if (EXACT) {
+      const float tmax = ss_tile_max(x0, x1);
+      // with nothing accumulated yet m may also move down
+      const float d = st.l[i] == 0.f ? ss_ceil_shift(tmax) : fmaxf(ss_ceil_shift(tmax), 0.f);
+      if (st.l[i] != 0.f) {
+        const float sc = __builtin_amdgcn_ldexpf(1.f, -(int)d);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st.o[i][r] *= sc;
+        st.l[i] *= sc;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.negm[i][r] -= d;
+      pv = ss_exp(x0, x1, d);
+    } else {
+      pv = ss_exp(x0, x1, 0.f);
+    }
+    st.l[i] += ss_tile_sum(st.ones, pv);
+    st.o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pv, st.o[i], 0, 0, 0);
+  }
+}
+
+// True when this lane's fast-sweep result may not be trusted (see the file comment).
+__device__ __forceinline__ bool ss_suspect(const SsState& st) {
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < SS_NB; ++i) {
-    pv[i] = ss_probs<MASK>(ka0, ka1, qop[i], negm[i], key0, lk);
-    nl[i] = l[i] + ss_tile_sum(pv[i]);
-    bad |= ss_out_of_range(nl[i]);
-  }
-  if (wave_any(bad)) {
+    bad |= !(st.l[i] <= SS_L_HI);
 #pragma unroll
-    for (int i = 0; i < SS_NB; ++i)
-      if (wave_any(ss_out_of_range(nl[i])))
-        ss_rebase<MASK>(ka0, ka1, qop[i], negm[i], o[i], l[i], pv[i], nl[i], key0, lk);
+    for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(st.o[i][r]) <= 0x1p127f);
   }
-#pragma unroll
-  for (int i = 0; i < SS_NB; ++i) {
-    l[i] = nl[i];
-    o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pv[i], o[i], 0, 0, 0);
-  }
+  return bad;
 }
 
-__global__ __launch_bounds__(SS_NW * 64, 3) void ss_stream_kernel(SsParams p) {
+// Operands of one tile from LDS: K for the two 16-key halves, V^T via transposed reads.
+__device__ __forceinline__ void ss_operands(const char* buf, int koff, int voff, bf16x8& ka0, bf16x8& ka1,
+                                            bf16x8& va) {
+  ka0 = *(const bf16x8*)(buf + koff);
+  ka1 = *(const bf16x8*)(buf + koff + 16 * SS_ROW);
+  const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(buf + voff));
+  const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(buf + voff + 16 * SS_ROW));
+  const bf16x4 a0 = __builtin_bit_cast(bf16x4, v0), a1 = __builtin_bit_cast(bf16x4, v1);
+  va = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+}
+
+// One sweep over the split's tiles [t0, t0 + nt). Fast mode stops early (returns true) once any wave
+// of the workgroup has flagged a row sum out of bound; all waves see the flag after the same join.
+// Sweep step t: wait for tile t, queue the copy of tile t + SS_NBUF - 1 (clamped to the last tile
+// of the range, whose repeated copies land in buffers nobody reads), process tile t.
+template <bool EXACT, bool MASK>
+__device__ __forceinline__ void ss_step(SsState& st, char* lds, uint32_t lds0, const SsSrc& src, int t0, int t,
+                                        int tlast, int lk, int koff, int voff, int wave, int G) {
+  ss_wait_join();
+  ss_issue(src, lds0 + ((t + SS_NBUF - 1) % SS_NBUF) * SS_TILE, min(t0 + t + SS_NBUF - 1, tlast) * SS_KT, lk,
+           wave);
+  bf16x8 ka0, ka1, va;
+  ss_operands(lds + (t % SS_NBUF) * SS_TILE, koff, voff, ka0, ka1, va);
+  ss_tile<EXACT, MASK>(st, ka0, ka1, va, (t0 + t) * SS_KT + 4 * G, lk);
+}
+
+// One sweep over the split's tiles [t0, t0 + nt), nt >= 1; the last one masks keys past the valid
+// length (a no-op unless it is the last tile of the key range).
+template <bool EXACT>
+__device__ __forceinline__ void ss_sweep(SsState& st, char* lds, const SsSrc& src, int t0, int nt, int lk,
+                                         int koff, int voff, int wave, int G) {
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+  const int tlast = t0 + nt - 1;
+#pragma unroll
+  for (int i = 0; i < SS_NBUF - 1; ++i) ss_issue(src, lds0 + i * SS_TILE, min(t0 + i, tlast) * SS_KT, lk, wave);
+  for (int t = 0; t < nt - 1; ++t) ss_step<EXACT, false>(st, lds, lds0, src, t0, t, tlast, lk, koff, voff, wave, G);
+  ss_step<EXACT, true>(st, lds, lds0, src, t0, nt - 1, tlast, lk, koff, voff, wave, G);
+  ss_drain_join();
+}
+
+__global__ __launch_bounds__(SS_NW * 64, 2) void ss_stream_kernel(SsParams p) {
   __shared__ __attribute__((aligned(1024))) char lds[SS_NBUF * SS_TILE];
+  __shared__ int restart_flag;
 
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int qg = work % p.nqg;
@@ -237,9 +290,10 @@ __global__ __launch_bounds__(SS_NW * 64, 3) void ss_stream_kernel(SsParams p) {
   const int q0 = qg * SS_QG + (wave / SS_HPW) * (16 * SS_NB);
 
   // B operands: q*log2e of dims 8(G&1)..+7 of head g, bf16 high part (G < 2) or remainder (G >= 2)
-  bf16x8 qop[SS_NB];
-  f32x4 negm[SS_NB], o[SS_NB];
-  float l[SS_NB];
+  SsState st;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.ones[j] = (bf16)1.f;
+  asm volatile("" : "+v"(st.ones));  // keep it in registers across the sweep, not rebuilt per use
   const bf16* qb = p.q + b * p.q_sb + g * 16 + 8 * (G & 1);
 #pragma unroll
   for (int i = 0; i < SS_NB; ++i) {
@@ -254,44 +308,49 @@ __global__ __launch_bounds__(SS_NW * 64, 3) void ss_stream_kernel(SsParams p) {
       if (p.scale != 1.f) f = (float)(bf16)(f * p.scale);
       f *= TA_LOG2E;
       const bf16 hi = (bf16)f;
-      qop[i][j] = G < 2 ? hi : (bf16)(f - (float)hi);
+      st.qop[i][j] = G < 2 ? hi : (bf16)(f - (float)hi);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { negm[i][r] = 0.f; o[i][r] = 0.f; }
-    l[i] = 0.f;
+    for (int r = 0; r < 4; ++r) { st.negm[i][r] = 0.f; st.o[i][r] = 0.f; }
+    st.l[i] = 0.f;
   }
-
-  const bf16* kb = p.k + b * p.k_sb + hg * (SS_HPW * 16);
-  const bf16* vb = p.v + b * p.v_sb + hg * (SS_HPW * 16);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
-#pragma unroll
-  for (int i = 0; i < SS_NBUF - 1; ++i)
-    if (i < nt) ss_issue(kb, vb, p.k_sr, p.v_sr, lds0 + i * SS_TILE, (t0 + i) * SS_KT, lk, wave, lane);
+  if (threadIdx.x == 0) restart_flag = 0;
 
   // per-lane operand offsets within a tile (keys 16..31: + 16 rows)
   const int koff = l16 * SS_ROW + (((2 * gl + (G & 1)) ^ ss_swz(l16)) << 4);
   const int vrow = 4 * G + (l16 >> 2), c4 = l16 & 3;
   const int voff =
       vrow * SS_ROW + (((SS_CPR / 2 + 2 * gl + (c4 >> 1)) ^ ss_swz(vrow)) << 4) + 8 * (c4 & 1);
+  const SsSrc src = ss_src(p, b, hg, wave, lane);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
 
-  for (int t = 0; t < nt; ++t) {
-    // copies issued after tile t: min(nt - 1 - t, SS_NBUF - 2)
-    ss_wait_join(min(nt - 1 - t, SS_NBUF - 2));
-    if (t + SS_NBUF - 1 < nt)
-      ss_issue(kb, vb, p.k_sr, p.v_sr, lds0 + ((t + SS_NBUF - 1) % SS_NBUF) * SS_TILE,
-               (t0 + t + SS_NBUF - 1) * SS_KT, lk, wave, lane);
-    const char* buf = lds + (t % SS_NBUF) * SS_TILE;
-    const bf16x8 ka0 = *(const bf16x8*)(buf + koff);
-    const bf16x8 ka1 = *(const bf16x8*)(buf + koff + 16 * SS_ROW);
-    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(buf + voff));
-    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(buf + voff + 16 * SS_ROW));
-    const bf16x4 va0 = __builtin_bit_cast(bf16x4, v0), va1 = __builtin_bit_cast(bf16x4, v1);
-    const bf16x8 va = {va0[0], va0[1], va0[2], va0[3], va1[0], va1[1], va1[2], va1[3]};
-    const int key0 = (t0 + t) * SS_KT + 4 * G;
-    if (t0 + t == ntiles - 1)
-      ss_tile<true>(ka0, ka1, va, qop, negm, o, l, key0, lk);
-    else
-      ss_tile<false>(ka0, ka1, va, qop, negm, o, l, key0, lk);
+  if (nt > 0) {
+    // reference m: ceiled maximum over the split's first tile
+    ss_issue(src, lds0, t0 * SS_KT, lk, wave);
+    ss_drain_join();
+    bf16x8 ka0, ka1, va;
+    ss_operands(lds, koff, voff, ka0, ka1, va);
+#pragma unroll
+    for (int i = 0; i < SS_NB; ++i) {
+      f32x4 x0, x1;
+      ss_scores<true>(ka0, ka1, st.qop[i], st.negm[i], t0 * SS_KT + 4 * G, lk, x0, x1);
+      const float d = ss_ceil_shift(ss_tile_max(x0, x1));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.negm[i][r] = -d;
+    }
+    ss_drain_join();  // everyone has read buffer 0 before the sweep refills it
+    ss_sweep<false>(st, lds, src, t0, nt, lk, koff, voff, wave, G);
+    if (wave_any(ss_suspect(st))) restart_flag = 1;
+    __syncthreads();
+    if (restart_flag) {
+#pragma unroll
+      for (int i = 0; i < SS_NB; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { st.negm[i][r] = 0.f; st.o[i][r] = 0.f; }
+        st.l[i] = 0.f;
+      }
+      ss_sweep<true>(st, lds, src, t0, nt, lk, koff, voff, wave, G);
+    }
   }
 
   // O^T lane layout: dims 4G..4G+3 of query l16
@@ -301,15 +360,15 @@ __global__ __launch_bounds__(SS_NW * 64, 3) void ss_stream_kernel(SsParams p) {
     if (qi >= p.Lq) continue;
     const int64_t row = (int64_t)b * p.Lq + qi;
     if (p.nsplit == 1) {
-      const float inv = l[i] == 0.f ? 0.f : 1.f / l[i];
+      const float inv = st.l[i] == 0.f ? 0.f : 1.f / st.l[i];
       bf16x4 ov;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[i][r] * inv);
+      for (int r = 0; r < 4; ++r) ov[r] = (bf16)(st.o[i][r] * inv);
       *(bf16x4*)(p.o + b * p.o_sb + (int64_t)qi * p.o_sr + g * 16 + 4 * G) = ov;
     } else {
       const int64_t srow = (int64_t)split * p.B * p.Lq + row;
-      *(f32x4*)(p.ws_o + srow * SS_E + g * 16 + 4 * G) = o[i];
-      if (G == 0) p.ws_ml[srow * SS_H + g] = make_float2(-negm[i][0], l[i]);
+      *(f32x4*)(p.ws_o + srow * SS_E + g * 16 + 4 * G) = st.o[i];
+      if (G == 0) p.ws_ml[srow * SS_H + g] = make_float2(-st.negm[i][0], st.l[i]);
     }
   }
 }
