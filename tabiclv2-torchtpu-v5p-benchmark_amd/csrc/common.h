@@ -88,3 +88,26 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblk) {
 
 struct u32x4 { uint32_t x, y, z, w; };
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *(const uint4*)p; }
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): LDS[lds_addr + 16 * lane] =
+// *src, lds_addr wave-uniform. Issued as inline assembly so that the compiler does not wait for it
+// before unrelated LDS reads (it would put s_waitcnt vmcnt(0) in front of the next ds_read); the
+// kernels wait with explicit vmcnt counts. M0 holds nothing else in these kernels.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Byte address of a __shared__ object in the LDS aperture.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding (LDS operations:
+// none), then join the workgroup.
+#define TA_WAIT_JOIN(N) asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory")

@@ -40,7 +40,9 @@ struct IclParams {
   // key split: nsplit > 1 writes unnormalised partials (O, m, l) per split to the workspace
   int nsplit;
   float* ws_o;   // [nsplit][N*H][Tq][64]
-  float* ws_ml;  // [nsplit][N*H][Tq][2]
+  float* ws_ml;  // [nsplit][N*H][Tq][2], m in log2 units
+  // per workgroup: 1 = the fast kernel's result must be recomputed exactly (null: no fast kernel)
+  int* flags;
 };
 
 template <typename T> struct IclLds {
@@ -248,6 +250,8 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
 
   // work item = (n, h, split, query block); consecutive items share (n, h) and stay on one XCD
   const int work = xcd_remap(blockIdx.x, gridDim.x);
+  // behind the pipelined kernel: only the work items it flagged
+  if (p.flags && p.flags[work] == 0) return;
   const int qb = work % p.nqb;
   const int rest = work / p.nqb;
   const int split = rest % p.nsplit;
@@ -327,7 +331,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
                                     st.o[qc][db][4 * j + 3]);
             *(float4*)(orow + 32 * db + 8 * j + 4 * hh) = ov;
           }
-        if (hh == 0) *(float2*)(p.ws_ml + row * 2) = make_float2(st.m_run[qc], lt);
+        if (hh == 0) *(float2*)(p.ws_ml + row * 2) = make_float2(st.m_run[qc] * sc, lt);
       }
     }
     return;
@@ -353,7 +357,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   }
 }
 
-// Combines the per-split partials: m* = max_s m_s, w_s = 2^((m_s - m*) sc),
+// Combines the per-split partials (m in log2 units): m* = max_s m_s, w_s = 2^(m_s - m*),
 // O = sum_s w_s O_s / sum_s w_s l_s (0 when no split saw a valid key). One thread per 4 outputs.
 template <typename T>
 __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
@@ -372,7 +376,7 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
   for (int s = 0; s < p.nsplit; ++s) {
     const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)s * rows + row) * 2);
     if (!(ml.y > 0.f)) continue;
-    const float w = __builtin_amdgcn_exp2f((ml.x - mstar) * p.sc);
+    const float w = __builtin_amdgcn_exp2f(ml.x - mstar);
     const float4 o = *(const float4*)(p.ws_o + ((int64_t)s * rows + row) * ICL_D + c4);
     acc.x += w * o.x; acc.y += w * o.y; acc.z += w * o.z; acc.w += w * o.w;
     l += w * ml.y;
@@ -388,12 +392,375 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
   *(typename OpVec<T, 4>::type*)dst = ov;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Pipelined bf16 kernel (the bf16 path whenever the caller gives a workspace). Same work items and
+// results as icl_fwd_kernel<bf16, 4, 2>, with three changes that let one wave keep the MFMA pipe
+// and the VALU busy at the same time:
+//  * K and V tiles are copied global -> LDS by the load unit (global_load_lds_dwordx4) three tiles
+//    ahead, row-major [key][d] with 128-byte rows whose 16-byte chunks are XOR-swizzled by the key;
+//    the V^T operands of the PV product come from ds_read_b64_tr_b16.
+//  * the softmax reference m (per query) is the ceiled maximum over the first 32 keys of the work
+//    item's key range and then stays fixed: no running max, no rescale, p = exp2(s sc - m) may
+//    exceed 1. At the end, l <= 2^96 and a finite O show that every p stayed far inside the
+//    bf16/fp32 range, so the result is the max-subtracted softmax to rounding (fp32/bf16 relative
+//    precision does not depend on scale). Otherwise the work item is flagged in the workspace and
+//    icl_fwd_kernel, launched right after on the same stream, recomputes exactly those items.
+//  * per 32-key half tile a wave runs 16 MFMAs (S of the next half, PV of the previous half), each
+//    followed by the VALU work of two probabilities of the current half (fma, exp2, convert, dot2
+//    row sum), in one basic block ordered with sched_barrier.
+// ---------------------------------------------------------------------------------------------
+constexpr int IP_NW = 4;
+constexpr int IP_QW = 64;
+constexpr int IP_NBUF = 4;
+constexpr int IP_TILE = 2 * ICL_KT * ICL_D;  // bf16 elements per buffer: K tile then V tile (16 KB)
+constexpr float IP_L_HI = 0x1p96f;
+
+// 16-byte chunk swizzle of a 128-byte tile row: a bijection on key % 8 that keeps (a) any 8
+// consecutive rows at one chunk and (b) the chunk pairs {c, c^1} of 4 consecutive rows on distinct
+// banks.
+__device__ __forceinline__ int ip_swz(int key) { return ((key & 3) << 1) | ((key >> 2) & 1); }
+
+struct IpState {
+  bf16x8 qop[2][4];
+  f32x16 o[2][2];
+  float nm[2];  // -m (log2 units) of this lane's query in column block qc
+  float l[2];   // this lane's share of the row sums
+};
+
+// Queue the copy of the tile at key k0 into the buffer at LDS byte address buf: wave w copies K
+// rows 16w..16w+15 and V rows 16w..16w+15, 8 rows (1 KB) per instruction; rows past `valid` are
+// read from row valid-1 (in bounds, and finite whenever the visible rows are).
+__device__ __forceinline__ void ip_issue(const bf16* kbase, const bf16* vbase, int64_t k_st, int64_t v_st,
+                                         uint32_t buf, int k0, int valid, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 8 * (i & 1) + (lane >> 3);
+    const int c = (lane & 7) ^ ip_swz(row);
+    const int64_t key = min(k0 + row, valid - 1);
+    const bf16* src = (i < 2 ? kbase + key * k_st : vbase + key * v_st) + c * 8;
+    lds_dma16(src, buf + (i < 2 ? 0 : ICL_KT * ICL_D * 2) + (16 * wave + 8 * (i & 1)) * ICL_D * 2);
+  }
+}
+
+// K operand of the S product: d-slice sl of rows kr..kr+31 of the K tile.
+__device__ __forceinline__ bf16x8 ip_kop(const bf16* lk, int kr, int sl, int lr, int hh) {
+  const int row = kr + lr;
+  return *(const bf16x8*)(lk + row * ICL_D + (((2 * sl + hh) ^ ip_swz(row)) << 3));
+}
+
+// V^T operand of one PV MFMA (d-block db, keys kr + 16m .. kr + 16m + 15): two transposed reads.
+// Lane l holds V[key][32 db + l % 32] for the keys of k-slots 8 (l / 32) .. +7, in the order the
+// S^T accumulator puts the probabilities: keys 4 hh + j and 8 + 4 hh + j (j = 0..3).
+__device__ __forceinline__ bf16x8 ip_vop(const bf16* lv, int kr, int m, int db, int lane) {
+  const int g = lane >> 4;
+  const int key = kr + 16 * m + 4 * (g >> 1) + ((lane & 15) >> 2);
+  const int lc = 4 * db + 2 * (g & 1) + ((lane & 3) >> 1);
+  const int half = (lane & 1) * 4;
+  const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(lv + key * ICL_D + ((lc ^ ip_swz(key)) << 3) + half));
+  const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(lv + (key + 8) * ICL_D + ((lc ^ ip_swz(key + 8)) << 3) + half));
+  // reassembled through whole-vector bit casts (per-element casts of a transposed-read result are
+  // folded to element 0 by this compiler)
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+  const u32x2 xw = __builtin_bit_cast(u32x2, x);
+  const u32x2 yw = __builtin_bit_cast(u32x2, y);
+  const u32x4v w = {xw[0], xw[1], yw[0], yw[1]};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// S^T of keys kr..kr+31 of the K tile for both column blocks.
+__device__ __forceinline__ void ip_s(f32x16 (&s)[2], const IpState& st, const bf16* lk, int kr, int lr, int hh) {
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[qc][r] = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl) {
+    const bf16x8 a = ip_kop(lk, kr, sl, lr, hh);
+#pragma unroll
+    for (int qc = 0; qc < 2; ++qc) s[qc] = mfma32x32x16(a, st.qop[qc][sl], s[qc]);
+  }
+}
+
+// O^T += V^T P^T for keys kr..kr+31 of the V tile.
+__device__ __forceinline__ void ip_pv(IpState& st, const bf16x8 (&pop)[2][2], const bf16* lv, int kr, int lane) {
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const bf16x8 a = ip_vop(lv, kr, m, db, lane);
+#pragma unroll
+      for (int qc = 0; qc < 2; ++qc) st.o[qc][db] = mfma32x32x16(a, pop[qc][m], st.o[qc][db]);
+    }
+}
+
+// Keys at or past `valid` out of S^T (keys k0 + 8(r/4) + 4hh + r%4).
+__device__ __forceinline__ void ip_mask(f32x16 (&s)[2], int k0, int valid, int hh) {
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (k0 + 8 * (r >> 2) + 4 * hh + (r & 3) >= valid) s[qc][r] = TA_NEG_INF;
+}
+
+// Probabilities 2k, 2k+1 of column block qc: exp2(s sc - m), one packed convert, row sum by v_dot2
+// over the bf16 values the PV product uses.
+__device__ __forceinline__ void ip_exp2(const f32x16 (&s)[2], const IpState& st, float sc, bf16x8 (&pop)[2][2],
+                                        float (&ls)[2], int qc, int k) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qc][2 * k], sc, st.nm[qc]));
+  const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qc][2 * k + 1], sc, st.nm[qc]));
+  const bf16x2 pr = {(bf16)p0, (bf16)p1};
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+  ls[qc] = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls[qc], false);
+  pop[qc][k >> 2][(2 * k) & 7] = pr[0];
+  pop[qc][k >> 2][(2 * k + 1) & 7] = pr[1];
+}
+
+// One half-tile phase: probabilities of `cur` (keys k0..k0+31) into `pcur`; if DO_S, S^T of the
+// next half tile (rows kr_next.. of lk_next) into `nxt`; if DO_PV, the PV product of the previous
+// half tile's probabilities `pprev` (rows kr_prev.. of lv_prev). Eight steps of up to two MFMAs,
+// each MFMA followed by two probabilities; operands are read from LDS two steps ahead.
+template <bool MASK, bool DO_S, bool DO_PV>
+__device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pcur)[2][2],
+                                         const bf16x8 (&pprev)[2][2], const bf16* lk_next, int kr_next,
+                                         const bf16* lv_prev, int kr_prev, int k0, int valid, float sc,
+                                         int lane) {
+  const int lr = lane & 31, hh = lane >> 5;
+  if (MASK) ip_mask(cur, k0, valid, hh);
+  constexpr int I0 = DO_S ? 0 : 4, I1 = DO_PV ? 8 : 4;  // operand steps [I0, I1)
+  auto read_op = [&](int i) -> bf16x8 {
+    if (i < 4) return ip_kop(lk_next, kr_next, i, lr, hh);
+    const int j = i - 4;  // (db, m) = (j >> 1, j & 1)
+    return ip_vop(lv_prev, kr_prev, j & 1, j >> 1, lane);
+  };
+  if (DO_S) {
+#pragma unroll
+    for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) nxt[qc][r] = 0.f;
+  }
+  float ls[2] = {0.f, 0.f};
+  bf16x8 op[8];
+  if (I0 < I1) op[I0] = read_op(I0);
+  if (I0 + 1 < I1) op[I0 + 1] = read_op(I0 + 1);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i < I0 || i >= I1) {
+      ip_exp2(cur, st, sc, pcur, ls, (2 * i) >> 3, (2 * i) & 7);
+      ip_exp2(cur, st, sc, pcur, ls, (2 * i + 1) >> 3, (2 * i + 1) & 7);
+      continue;
+    }
+    if (i + 2 < I1) op[i + 2] = read_op(i + 2);
+#pragma unroll
+    for (int qc = 0; qc < 2; ++qc) {
+      if (i < 4) {
+        nxt[qc] = mfma32x32x16(op[i], st.qop[qc][i], nxt[qc]);
+      } else {
+        const int j = i - 4;
+        st.o[qc][j >> 1] = mfma32x32x16(op[i], pprev[qc][j & 1], st.o[qc][j >> 1]);
+      }
+      const int step = 2 * i + qc;  // 0..15, two probabilities each
+      ip_exp2(cur, st, sc, pcur, ls, step >> 3, step & 7);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  st.l[0] += ls[0];
+  st.l[1] += ls[1];
+}
+
+struct IpCtx {
+  const bf16* kbase;
+  const bf16* vbase;
+  int64_t k_st, v_st;
+  uint32_t lds0;
+  int t0, nt, valid, wave, lane;
+  float sc;
+};
+
+// Sweep iteration t (tile t0 + t, buffer t % IP_NBUF): phase A = softmax of its first half, S of
+// its second half, PV of the previous tile's second half; join (tile t + 1 landed, tile t - 1
+// retired); queue tile t + IP_NBUF - 1 into tile t - 1's buffer; phase B = softmax of the second
+// half, S of the next tile's first half, PV of this tile's first half.
+template <bool FIRST, bool LAST, bool MASK>
+__device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&sB)[2], bf16x8 (&pA)[2][2],
+                                        bf16x8 (&pB)[2][2], bf16 (*lds)[IP_TILE], const IpCtx& c, int t) {
+  const bf16* lk = lds[t % IP_NBUF];
+  const bf16* lv = lk + ICL_KT * ICL_D;
+  const bf16* lvp = lds[(t + IP_NBUF - 1) % IP_NBUF] + ICL_KT * ICL_D;
+  const bf16* lkn = lds[(t + 1) % IP_NBUF];
+  const int k0 = (c.t0 + t) * ICL_KT;
+  ip_phase<MASK, true, !FIRST>(st, sA, sB, pA, pB, lk, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
+  static_assert(IP_NBUF == 4, "one tile (4 copies per wave) may stay in flight below");
+  TA_WAIT_JOIN(4);
+  ip_issue(c.kbase, c.vbase, c.k_st, c.v_st, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
+           min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT, c.valid, c.wave, c.lane);
+  ip_phase<MASK, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
+}
+
+__global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
+  __shared__ __attribute__((aligned(1024))) bf16 lds[IP_NBUF][IP_TILE];
+  __shared__ int wg_bad;
+
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int qb = work % p.nqb;
+  const int rest = work / p.nqb;
+  const int split = rest % p.nsplit;
+  const int nh = rest / p.nsplit;
+  const int h = nh % p.H, n = nh / p.H;
+
+  int valid = p.Tkv;
+  if (p.valid) {
+    valid = p.valid[p.valid_n == 1 ? 0 : n];
+    valid = valid < 0 ? 0 : (valid > p.Tkv ? p.Tkv : valid);
+  }
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int qw0 = qb * (IP_QW * IP_NW) + wave * IP_QW;
+
+  const bf16* qbase = (const bf16*)p.q + n * p.q_sn + h * p.q_sh;
+  IpState st;
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc) {
+    const int qi = qw0 + qc * 32 + lr;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8 z = {};
+      st.qop[qc][s] = qi < p.Tq ? *(const bf16x8*)(qbase + (int64_t)qi * p.q_st + 16 * s + 8 * hh) : z;
+    }
+    st.nm[qc] = 0.f;
+    st.l[qc] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.o[qc][db][r] = 0.f;
+  }
+  if (threadIdx.x == 0) wg_bad = 0;
+  __syncthreads();
+
+  // this split's tiles [t0, t1) of the ceil(valid / KT) key tiles (as icl_fwd_kernel)
+  const int ntiles = (valid + ICL_KT - 1) / ICL_KT;
+  const int per = (ntiles + p.nsplit - 1) / p.nsplit;
+  const int t0 = min(split * per, ntiles), t1 = min(t0 + per, ntiles);
+  const int nt = t1 - t0;
+  if (nt > 0) {
+    IpCtx c;
+    c.kbase = (const bf16*)p.k + n * p.k_sn + h * p.k_sh;
+    c.vbase = (const bf16*)p.v + n * p.v_sn + h * p.v_sh;
+    c.k_st = p.k_st;
+    c.v_st = p.v_st;
+    c.lds0 = lds_addr(&lds[0][0]);
+    c.t0 = t0;
+    c.nt = nt;
+    c.valid = valid;
+    c.wave = wave;
+    c.lane = lane;
+    c.sc = p.sc;
+#pragma unroll
+    for (int i = 0; i < IP_NBUF - 1; ++i)
+      ip_issue(c.kbase, c.vbase, c.k_st, c.v_st, c.lds0 + i * IP_TILE * 2, min(t0 + i, t1 - 1) * ICL_KT, valid,
+               wave, lane);
+    TA_WAIT_JOIN(8);  // tile t0 landed, two more tiles (8 copies) in flight
+
+    // reference m: ceiled maximum over the first 32 keys of the range
+    f32x16 sA[2], sB[2];
+    bf16x8 pA[2][2], pB[2][2];
+    ip_s(sA, st, lds[0], 0, lr, hh);
+    if (t0 == ntiles - 1) ip_mask(sA, t0 * ICL_KT, valid, hh);
+#pragma unroll
+    for (int qc = 0; qc < 2; ++qc) {
+      float mx = sA[qc][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sA[qc][r]);
+      mx = lane_pair_max(mx) * c.sc;
+      st.nm[qc] = mx > -1e4f ? -fminf(ceilf(mx), 1e4f) : 0.f;
+    }
+
+    const bool masked = t1 == ntiles;
+    if (nt == 1) {
+      if (masked)
+        ip_iter<true, true, true>(st, sA, sB, pA, pB, lds, c, 0);
+      else
+        ip_iter<true, true, false>(st, sA, sB, pA, pB, lds, c, 0);
+    } else {
+      ip_iter<true, false, false>(st, sA, sB, pA, pB, lds, c, 0);
+      for (int t = 1; t + 1 < nt; ++t) ip_iter<false, false, false>(st, sA, sB, pA, pB, lds, c, t);
+      if (masked)
+        ip_iter<false, true, true>(st, sA, sB, pA, pB, lds, c, nt - 1);
+      else
+        ip_iter<false, true, false>(st, sA, sB, pA, pB, lds, c, nt - 1);
+    }
+    ip_pv(st, pB, lds[(nt - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
+    TA_WAIT_JOIN(0);  // no copy into this workgroup's LDS may outlive it
+  }
+
+  // trust test of the fixed reference; any failing lane flags the work item for exact recompute
+  float lt[2];
+  bool bad = false;
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc) {
+    lt[qc] = lane_pair_sum(st.l[qc]);
+    bad |= !(lt[qc] <= IP_L_HI);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bad |= !(__builtin_fabsf(st.o[qc][db][r]) <= 0x1p127f);
+  }
+  if (wave_any(bad)) wg_bad = 1;
+  __syncthreads();
+  if (threadIdx.x == 0) p.flags[work] = wg_bad;
+
+  if (p.nsplit > 1) {
+#pragma unroll
+    for (int qc = 0; qc < 2; ++qc) {
+      const int qi = qw0 + qc * 32 + lr;
+      if (qi < p.Tq) {
+        const int64_t row = ((int64_t)split * p.N * p.H + nh) * p.Tq + qi;
+        float* orow = p.ws_o + row * ICL_D;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float4 ov = make_float4(st.o[qc][db][4 * j], st.o[qc][db][4 * j + 1], st.o[qc][db][4 * j + 2],
+                                    st.o[qc][db][4 * j + 3]);
+            *(float4*)(orow + 32 * db + 8 * j + 4 * hh) = ov;
+          }
+        if (hh == 0) *(float2*)(p.ws_ml + row * 2) = make_float2(-st.nm[qc], lt[qc]);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc) {
+    const float inv = lt[qc] > 0.f ? 1.f / lt[qc] : 0.f;
+    const int qi = qw0 + qc * 32 + lr;
+    if (qi < p.Tq) {
+      bf16* orow = (bf16*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bf16x4 ov;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ov[r] = (bf16)(st.o[qc][db][4 * j + r] * inv);
+          *(bf16x4*)(orow + 32 * db + 8 * j + 4 * hh) = ov;
+        }
+    }
+  }
+}
+
+// Resident workgroups per CU of the kernel that carries the work (the pipelined one for bf16).
 template <typename T, int NW, int QC>
 int blocks_per_cu() {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC>, NW * 64, 0) != hipSuccess)
-    return 1;
-  return n > 0 ? n : 1;
+  const hipError_t e =
+      sizeof(T) == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel, IP_NW * 64, 0)
+                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC>, NW * 64, 0);
+  return e == hipSuccess && n > 0 ? n : 1;
 }
 
 // Number of key splits that best fills whole rounds of resident workgroups:
@@ -416,23 +783,46 @@ int pick_splits(int64_t items, int64_t Tkv) {
   return best;
 }
 
+// Workspace layout: [per-work-item flags, bf16 only, 256-byte aligned][split partials: O fp32
+// [nsplit][rows][64], (m, l) [nsplit][rows][2]].
+int64_t flag_bytes(int64_t nblk) { return (nblk * 4 + 255) / 256 * 256; }
+int64_t part_bytes(int nsplit, int64_t rows) { return nsplit > 1 ? (int64_t)nsplit * rows * (ICL_D + 2) * 4 : 0; }
+
 template <typename T, int NW, int QC>
 int64_t workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv) {
   const int64_t nqb = (Tq + 32 * QC * NW - 1) / (32 * QC * NW);
   const int s = pick_splits<T, NW, QC>(N * H * nqb, Tkv);
-  return s > 1 ? (int64_t)s * N * H * Tq * (ICL_D + 2) * (int64_t)sizeof(float) : 0;
+  return (sizeof(T) == 2 ? flag_bytes(N * H * nqb * s) : 0) + part_bytes(s, N * H * Tq);
 }
 
+// bf16 with a large enough workspace: pipelined kernel, then icl_fwd_kernel on the work items it
+// flagged, then the split merge. Otherwise icl_fwd_kernel alone (splitting only if the workspace
+// holds the partials).
 template <typename T, int NW, int QC>
 void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
   IclParams p = p0;
   p.nqb = (p.Tq + 32 * QC * NW - 1) / (32 * QC * NW);
   const int64_t rows = (int64_t)p.N * p.H * p.Tq;
-  p.nsplit = pick_splits<T, NW, QC>((int64_t)p.N * p.H * p.nqb, p.Tkv);
-  if (p.nsplit > 1 && (ws == nullptr || ws_bytes < (int64_t)p.nsplit * rows * (ICL_D + 2) * 4)) p.nsplit = 1;
-  p.ws_o = (float*)ws;
+  const int64_t items = (int64_t)p.N * p.H * p.nqb;
+  p.nsplit = pick_splits<T, NW, QC>(items, p.Tkv);
+  const int64_t have = ws ? ws_bytes : 0;
+  bool fast = false;
+  int64_t fb = 0;
+  if (sizeof(T) == 2) {
+    if (have < flag_bytes(items * p.nsplit) + part_bytes(p.nsplit, rows)) p.nsplit = 1;
+    fb = flag_bytes(items * p.nsplit);
+    fast = have >= fb + part_bytes(p.nsplit, rows);
+  }
+  if (!fast) {
+    fb = 0;
+    if (have < part_bytes(p.nsplit, rows)) p.nsplit = 1;
+  }
+  p.flags = fast ? (int*)ws : nullptr;
+  p.ws_o = (float*)((char*)ws + fb);
   p.ws_ml = p.ws_o + (p.nsplit > 1 ? (int64_t)p.nsplit * rows * ICL_D : 0);
-  const int64_t nblk = (int64_t)p.N * p.H * p.nsplit * p.nqb;
+  const int64_t nblk = items * p.nsplit;
+  if (fast)
+    hipLaunchKernelGGL(icl_pipe_kernel, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
   hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
   if (p.nsplit > 1) {
     const int64_t threads = rows * (ICL_D / 4);
@@ -463,7 +853,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.v_sn = v_sn; p.v_sh = v_sh; p.v_st = v_st;
   p.o_sn = o_sn; p.o_sh = o_sh; p.o_st = o_st;
   p.sc = scale * TA_LOG2E;
-  p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr;
+  p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr; p.flags = nullptr;
   if (dtype == 0)
     launch<bf16, 4, 2>(p, ws, ws_bytes, stream);
   else

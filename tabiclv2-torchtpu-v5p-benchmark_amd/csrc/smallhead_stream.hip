@@ -77,28 +77,15 @@ struct SsParams {
 __device__ __forceinline__ int ss_swz(int r) { return ((2 * (r & 7)) | ((r >> 2) & 1)) ^ ((r >> 3) & 1); }
 static_assert(SS_CPR == 16, "swizzle above is for 16 chunks per row");
 
-// One 16-byte global -> LDS copy per lane: LDS[lds_addr + 16 * lane] = *src (lds_addr wave-uniform).
-// Issued as inline assembly so that the compiler does not wait for it before unrelated LDS reads;
-// the kernel waits with explicit vmcnt counts. M0 holds nothing else in this kernel.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void ss_dma(const void* src, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // Every sweep iteration issues exactly one copy per wave (past the end of the range the last tile
 // is copied again into a buffer nobody reads), so the wait for tile t is always "all but the
 // SS_NBUF - 2 newest copies". The join also waits for this wave's LDS operations (the restart flag).
 __device__ __forceinline__ void ss_wait_join() {
   static_assert(SS_NBUF - 2 == 6, "vmcnt below");
-  asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  TA_WAIT_JOIN(6);
 }
 __device__ __forceinline__ void ss_drain_join() {
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  TA_WAIT_JOIN(0);
 }
 
 // Per-lane source of the tile copies: lane (row r = 4 * wave + lane / 16, physical chunk lane % 16)
@@ -125,7 +112,7 @@ __device__ __forceinline__ SsSrc ss_src(const SsParams& p, int b, int hg, int wa
 // Copy the tile starting at key k0 (rows clamped to lk - 1: no key past the valid length is read).
 __device__ __forceinline__ void ss_issue(const SsSrc& s, uint32_t buf, int k0, int lk, int wave) {
   const uint32_t key = (uint32_t)min(k0 + s.row, lk - 1);
-  ss_dma(s.base + (uint64_t)key * s.stride, buf + 1024 * wave);
+  lds_dma16(s.base + (uint64_t)key * s.stride, buf + 1024 * wave);
 }
 
 // Scores x = K (q log2e) - m of one 16-query block over a 32-key tile. Lane (l16, G) holds keys
@@ -253,7 +240,7 @@ __device__ __forceinline__ void ss_step(SsState& st, char* lds, uint32_t lds0, c
 template <bool EXACT>
 __device__ __forceinline__ void ss_sweep(SsState& st, char* lds, const SsSrc& src, int t0, int nt, int lk,
                                          int koff, int voff, int wave, int G) {
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+  const uint32_t lds0 = lds_addr(lds);
   const int tlast = t0 + nt - 1;
 #pragma unroll
   for (int i = 0; i < SS_NBUF - 1; ++i) ss_issue(src, lds0 + i * SS_TILE, min(t0 + i, tlast) * SS_KT, lk, wave);
@@ -322,7 +309,7 @@ __global__ __launch_bounds__(SS_NW * 64, 2) void ss_stream_kernel(SsParams p) {
   const int voff =
       vrow * SS_ROW + (((SS_CPR / 2 + 2 * gl + (c4 >> 1)) ^ ss_swz(vrow)) << 4) + 8 * (c4 & 1);
   const SsSrc src = ss_src(p, b, hg, wave, lane);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+  const uint32_t lds0 = lds_addr(lds);
 
   if (nt > 0) {
     // reference m: ceiled maximum over the split's first tile

@@ -147,3 +147,40 @@ def test_icl_full_c4_slice(dev):
         ref = O.splash_sdpa_torch(q[n:n + 1, h:h + 1, rows], k[n:n + 1, h:h + 1], v[n:n + 1, h:h + 1])
         err = float((out[n, h, rows].float().cpu() - ref[0, 0]).abs().max())
         assert err <= 2e-2, err
+
+
+def _native_icl(q, k, v, valid, ws):
+    import tabicl_mi355_native as nat
+    out = torch.empty_like(q)
+    N, H, Tq, D = q.shape
+    nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), valid.data_ptr(), valid.numel(),
+             out.data_ptr(), N, H, Tq, k.shape[2], D, *q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
+             *out.stride()[:3], D ** -0.5, 0, ws.data_ptr(), ws.numel(), nat.stream_of(q))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("name,qscale,expect_flag", [
+    ("ordinary_scores", 1.0, False),
+    ("scores_far_above_first_keys", 80.0, True),  # ~120 nats above the first 32 keys' maximum
+])
+def test_icl_fixed_reference_and_exact_recompute(dev, name, qscale, expect_flag):
+    # bf16 with a workspace runs the pipelined kernel with a fixed softmax reference; work items
+    # whose scores leave its range are flagged (first 256 workspace bytes) and recomputed exactly
+    import tabicl_mi355_native as nat
+    g = torch.Generator().manual_seed(13)
+    N, H, Tq, Tkv, D = 2, 2, 300, 4000, 64
+    q = (torch.randn(N, H, Tq, D, generator=g) * qscale).to(torch.bfloat16)
+    k = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16)
+    valid = torch.tensor([3900, 2500], dtype=torch.int32)
+    nbytes = int(nat.load().tabicl_icl_workspace_bytes(N, H, Tq, Tkv, D, 0))
+    assert nbytes >= 256
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    print(f"[icl] {name}", flush=True)
+    out = _native_icl(q.to(dev), k.to(dev), v.to(dev), valid.to(dev), ws)
+    flags = ws[:256].view(torch.int32).cpu()
+    assert bool((flags != 0).any()) == expect_flag, flags
+    assert torch.isfinite(out.float()).all()
+    ref = O.splash_sdpa_ref(q, k, v, valid.numpy())
+    assert _err(out, ref) <= 2e-2
