@@ -581,11 +581,12 @@ struct IpCtx {
   float sc;
 };
 
-// Sweep iteration t (tile t0 + t, buffer t % IP_NBUF): phase A = softmax of its first half, S of
-// its second half, PV of the previous tile's second half; join (tile t + 1 landed, tile t - 1
-// retired); queue tile t + IP_NBUF - 1 into tile t - 1's buffer; phase B = softmax of the second
-// half, S of the next tile's first half, PV of this tile's first half.
-template <bool FIRST, bool LAST, bool MASK>
+// Sweep iteration t (tile t0 + t, buffer t % IP_NBUF, no key past `valid`): phase A = softmax of
+// its first half, S of its second half, PV of the previous tile's second half; join (tile t + 1
+// landed, tile t - 1 retired); queue tile t + IP_NBUF - 1 into tile t - 1's buffer; phase B =
+// softmax of the second half, S of the next tile's first half (unless LAST), PV of this tile's first
+// half.
+template <bool FIRST, bool LAST>
 __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&sB)[2], bf16x8 (&pA)[2][2],
                                         bf16x8 (&pB)[2][2], bf16 (*lds)[IP_TILE], const IpCtx& c, int t) {
   const bf16* lk = lds[t % IP_NBUF];
@@ -593,12 +594,32 @@ __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&s
   const bf16* lvp = lds[(t + IP_NBUF - 1) % IP_NBUF] + ICL_KT * ICL_D;
   const bf16* lkn = lds[(t + 1) % IP_NBUF];
   const int k0 = (c.t0 + t) * ICL_KT;
-  ip_phase<MASK, true, !FIRST>(st, sA, sB, pA, pB, lk, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
+  ip_phase<false, true, !FIRST>(st, sA, sB, pA, pB, lk, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
   static_assert(IP_NBUF == 4, "one tile (4 copies per wave) may stay in flight below");
   TA_WAIT_JOIN(4);
   ip_issue(c.kbase, c.vbase, c.k_st, c.v_st, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
            min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT, c.valid, c.wave, c.lane);
-  ip_phase<MASK, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
+  ip_phase<false, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
+}
+
+// The tile that crosses `valid` (buffer b, keys k0..): S, mask, probabilities and PV per half,
+// without the MFMA/VALU interleave (once per work item at most).
+__device__ __forceinline__ void ip_tail(IpState& st, const bf16* lk, const bf16* lv, int k0, int valid, float sc,
+                                        int lane) {
+  const int lr = lane & 31, hh = lane >> 5;
+#pragma unroll 1
+  for (int half = 0; half < 2; ++half) {
+    f32x16 sT[2];
+    bf16x8 pT[2][2];
+    ip_s(sT, st, lk, 32 * half, lr, hh);
+    ip_mask(sT, k0 + 32 * half, valid, hh);
+    float ls[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ip_exp2(sT, st, sc, pT, ls, j >> 3, j & 7);
+    st.l[0] += ls[0];
+    st.l[1] += ls[1];
+    ip_pv(st, pT, lv, 32 * half, lane);
+  }
 }
 
 __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
@@ -639,6 +660,12 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) st.o[qc][db][r] = 0.f;
   }
+  // Consume the q loads here: a load the compiler still tracks inside the sweep would make it wait
+  // with s_waitcnt vmcnt(n), which also counts (and so waits for) the tile copies in flight.
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) asm volatile("" ::"v"(st.qop[qc][s]));
   if (threadIdx.x == 0) wg_bad = 0;
   __syncthreads();
 
@@ -680,21 +707,21 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       st.nm[qc] = mx > -1e4f ? -fminf(ceilf(mx), 1e4f) : 0.f;
     }
 
-    const bool masked = t1 == ntiles;
-    if (nt == 1) {
-      if (masked)
-        ip_iter<true, true, true>(st, sA, sB, pA, pB, lds, c, 0);
-      else
-        ip_iter<true, true, false>(st, sA, sB, pA, pB, lds, c, 0);
-    } else {
-      ip_iter<true, false, false>(st, sA, sB, pA, pB, lds, c, 0);
-      for (int t = 1; t + 1 < nt; ++t) ip_iter<false, false, false>(st, sA, sB, pA, pB, lds, c, t);
-      if (masked)
-        ip_iter<false, true, true>(st, sA, sB, pA, pB, lds, c, nt - 1);
-      else
-        ip_iter<false, true, false>(st, sA, sB, pA, pB, lds, c, nt - 1);
+    // tiles entirely below `valid` through the pipelined sweep, the crossing one (if any) after it
+    const int nfull = (t1 == ntiles && valid % ICL_KT != 0) ? nt - 1 : nt;
+    if (nfull == 1) {
+      ip_iter<true, true>(st, sA, sB, pA, pB, lds, c, 0);
+    } else if (nfull > 1) {
+      ip_iter<true, false>(st, sA, sB, pA, pB, lds, c, 0);
+      for (int t = 1; t + 1 < nfull; ++t) ip_iter<false, false>(st, sA, sB, pA, pB, lds, c, t);
+      ip_iter<false, true>(st, sA, sB, pA, pB, lds, c, nfull - 1);
     }
-    ip_pv(st, pB, lds[(nt - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
+    if (nfull > 0) ip_pv(st, pB, lds[(nfull - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
+    if (nfull < nt) {
+      // the crossing tile landed at the last join (or before the sweep when it is the only tile)
+      const bf16* lk = lds[nfull % IP_NBUF];
+      ip_tail(st, lk, lk + ICL_KT * ICL_D, (t0 + nfull) * ICL_KT, valid, c.sc, lane);
+    }
     TA_WAIT_JOIN(0);  // no copy into this workgroup's LDS may outlive it
   }
 
