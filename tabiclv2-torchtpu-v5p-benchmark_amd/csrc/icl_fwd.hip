@@ -4,21 +4,23 @@
 //   O = softmax(scale * Q K^T + mask) V,  mask[j] = -inf for key j >= valid,
 // fp32 scores and softmax, probabilities cast to the value dtype before the PV product.
 //
-// Work decomposition: one workgroup = (n, h, block of NW * QW queries); each wave owns QW = 32 * QC
-// queries (QC column blocks of 32). Keys stream through LDS in tiles of KT = 64, double buffered:
-// the global loads of tile t+1 are issued into registers before tile t is computed and written to
-// the other LDS buffer afterwards, so one barrier per tile suffices and the load latency hides
-// behind the MFMA/softmax work. K is stored row-major [key][d], V transposed [d][key] with the key
-// order permuted inside each 16-key group so that every MFMA operand is one 16-byte LDS read.
-// Per tile and wave:
-//   S^T (keys x queries) = K Q^T      v_mfma_f32_32x32x16_bf16, 2 key blocks x 4 d-slices x QC
-//   online softmax in registers       lane l owns query l%32 of each column block; the two lanes
-//                                     l, l^32 holding a query are combined with v_permlane32_swap
-//   O^T (d x queries)   += V^T P^T    2 d-blocks x 4 key-slices x QC; P^T is the S^T accumulator
-//                                     layout converted to bf16 in place (no shuffles)
-// The running max is updated lazily: the accumulators are rescaled only when the tile max exceeds
-// the running max by more than 2^8 (so p <= 256 otherwise); exact because O and l always share
-// the same reference max.
+// Work decomposition (both kernels): one workgroup = (n, h, key split, block of NW * QW queries);
+// each wave owns QW = 32 * QC queries (QC column blocks of 32). Two kernels share it:
+//  * icl_pipe_kernel (bf16, when the caller gives a workspace): tiles copied global -> LDS by the
+//    load unit several tiles ahead, a softmax reference fixed per query, MFMA and softmax VALU
+//    interleaved per half tile; it flags the work items whose scores leave the reference's range.
+//  * icl_fwd_kernel (fp32; bf16 without a workspace; the flagged bf16 items): keys stream through
+//    LDS in tiles of KT = 64, double buffered (the global loads of tile t+1 are issued into
+//    registers before tile t is computed and written to the other LDS buffer afterwards), K
+//    row-major, V transposed with the key order permuted inside each 16-key group so that every
+//    MFMA operand is one 16-byte LDS read; per tile and wave
+//      S^T (keys x queries) = K Q^T      v_mfma_f32_32x32x16_bf16, 2 key blocks x 4 d-slices x QC
+//      online softmax in registers       lane l owns query l%32 of each column block; the two lanes
+//                                        l, l^32 holding a query are combined with v_permlane32_swap
+//      O^T (d x queries)   += V^T P^T    2 d-blocks x 4 key-slices x QC; P^T is the S^T accumulator
+//                                        layout converted to bf16 in place (no shuffles)
+//    with the running max updated lazily (accumulators rescaled only when the tile max exceeds the
+//    running max by more than 2^8; exact because O and l always share the same reference max).
 #include "common.h"
 
 namespace {
