@@ -170,6 +170,111 @@ def bench_smallhead(configs: set, steps: int, warmup: int) -> list:
     return recs
 
 
+C5_BUCKETS = (1024, 2048, 4096, 8192, 16384)
+
+
+def c5_tables(seed: int = 4):
+    """64 tables, n_train log-uniform in [500, 10000], n_test = 10% of it."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    n_train = np.round(np.exp(rng.uniform(np.log(500), np.log(10000), 64))).astype(int)
+    n_test = np.round(0.1 * n_train).astype(int)
+    return n_train, n_test
+
+
+def c5_bucket(n: int) -> int:
+    for b in C5_BUCKETS:
+        if b >= n:
+            return b
+    raise ValueError(n)
+
+
+def bench_c5(steps: int, warmup: int) -> list:
+    """BASELINE config 5 (ragged, shape-bucketed mixed batch, bf16): per row bucket, the column
+    ISAB pair (hxq over the bucket's rows with valid = n_train per table, then pk_cross of all rows
+    over 128 inducing keys) for 8 estimators x 100 features per table, and the cached-KV ICL
+    attention (8 estimators x 8 heads, test rows padded to the 1k bucket over the train bucket,
+    valid = n_train per table) for 12 blocks. Each (bucket, kernel) is timed on its own inputs (so
+    only one bucket's tensors are resident); the step time is the sum. TFLOP/s on the real
+    (unpadded) sizes; padding efficiency = real / processed FLOPs (the kernels never visit keys
+    past valid, so only padded query rows cost work)."""
+    import torch
+
+    import tabicl_mi355_attn as pk
+    import tabicl_mi355_icl as icl
+
+    dev = torch.device("cuda", 0)
+    E, H, EST_, FEAT, IND = 128, 8, 8, 100, 128
+    n_train, n_test = c5_tables()
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    parts = {"isab1": [0.0, 0.0, 0.0], "isab2": [0.0, 0.0, 0.0], "icl": [0.0, 0.0, 0.0]}  # ms, real, padded FLOPs
+    groups = {}
+    for i in range(64):
+        groups.setdefault(("isab", c5_bucket(int(n_train[i] + n_test[i]))), []).append(i)
+        groups.setdefault(("icl", c5_bucket(int(n_train[i]))), []).append(i)
+    for (kind, L), tabs in sorted(groups.items()):
+        nt = torch.tensor([int(n_train[i]) for i in tabs], dtype=torch.int32)
+        ns = [int(n_test[i]) for i in tabs]
+        if kind == "isab":
+            B = len(tabs) * EST_ * FEAT
+            valid = nt.repeat_interleave(EST_ * FEAT).to(dev)
+            q = torch.randn(B, IND, E, generator=g, device=dev, dtype=torch.bfloat16) * 0.25
+            kv = torch.randn(B, L, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
+            ms = _time(lambda: pk.hxq_attention(q, kv, valid, H), steps, warmup)
+            real = sum(4.0 * IND * int(n) * 16 * H * EST_ * FEAT for n in nt)
+            parts["isab1"][0] += ms
+            parts["isab1"][1] += real
+            parts["isab1"][2] += real  # keys past valid are never visited: no padded work
+            del q, kv
+            q2 = torch.randn(B, L, E, generator=g, device=dev, dtype=torch.bfloat16)
+            kv2 = torch.randn(B, IND, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
+            ms = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25), steps, warmup)
+            parts["isab2"][0] += ms
+            parts["isab2"][1] += sum(4.0 * (int(n) + m) * IND * 16 * H * EST_ * FEAT for n, m in zip(nt, ns))
+            parts["isab2"][2] += 4.0 * L * IND * 16 * H * B
+            del q2, kv2
+        else:
+            N, Tq = len(tabs) * EST_, C5_BUCKETS[0]
+            valid = nt.repeat_interleave(EST_).to(dev)
+            k = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
+            q = torch.randn(N, H, Tq, 64, generator=g, device=dev, dtype=torch.bfloat16)
+            out = torch.empty_like(q)
+
+            def step():
+                for _ in range(BLOCKS):  # one block's cache stands for each of the 12 blocks
+                    icl.ICL_FWD_OUT(q, k, v, valid, 64 ** -0.5, out)
+
+            ms = _time(step, steps, warmup)
+            parts["icl"][0] += ms
+            parts["icl"][1] += BLOCKS * sum(4.0 * m * int(n) * 64 * H * EST_ for n, m in zip(nt, ns))
+            # keys past valid are never visited; the padded query rows are
+            parts["icl"][2] += BLOCKS * sum(4.0 * Tq * int(n) * 64 * H * EST_ for n in nt)
+            del k, v, q, out
+        torch.cuda.empty_cache()
+    recs = []
+    names = {"isab1": "C5 column ISAB-1 (hxq, ragged valid)", "isab2": "C5 column ISAB-2 (pk_cross)",
+             "icl": "C5 cached-KV ICL (12 blocks, per-table valid)"}
+    total = 0.0
+    for key, (ms, real, padded) in parts.items():
+        total += ms
+        tf = real / (ms * 1e-3) / 1e12
+        recs.append({"metric": f"ms per {names[key]} step", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+                     "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": "bf16",
+                     "data": "synthetic N(0,1), seed 4", "config": {"workload": "C5: 64 tables, buckets 1k-16k"},
+                     "attn_tflops_real": round(tf, 2), "padding_efficiency": round(real / padded, 4),
+                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
+    recs.append({"metric": "ms per C5 ragged mixed-batch step (ISAB pair + ICL)", "value": round(total, 4),
+                 "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
+                 "dtype": "bf16", "data": "synthetic N(0,1), seed 4",
+                 "config": {"workload": "C5: 64 tables, n_train log-uniform [500, 10000], n_test 10%, 8 est, "
+                                        "100 features, row buckets 1k-16k"}})
+    return recs
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -177,8 +282,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3 (comma-separated) or all print the "
-                         "d=16 kernel lines")
+                    help="c4 (default) is the headline line; c1, c2, c3, c5 (comma-separated) or all print "
+                         "the other BASELINE configs' lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -188,11 +293,14 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
-        for rec in bench_smallhead(configs, args.steps, args.warmup):
+        recs = bench_smallhead(configs, args.steps, args.warmup)
+        if configs & {"c5", "all"}:
+            recs += bench_c5(args.steps, args.warmup)
+        for rec in recs:
             print(json.dumps(rec), flush=True)
         return 0
 

@@ -13,6 +13,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define TA_LOG2E 1.4426950408889634f
 #define TA_NEG_INF (-__builtin_inff())
+// word 3 of a raw (stride 0) buffer resource on gfx9-family parts: 32-bit data format, no swizzle;
+// accesses at byte offsets >= num_records are dropped (stores) or return 0 (loads)
+#define TA_BUF_WORD3 0x00020000
 
 // Operand vectors: N consecutive k-values of one row held by one lane.
 template <typename T, int N> struct OpVec;

@@ -51,6 +51,7 @@ struct ShParams {
   float scale;
   int B, Lq, Lk;
   int nqb, qbpw, nwg_b;
+  int exact_scale;  // scale is a power of two: bf16(q * scale) needs no rounding
 };
 
 template <typename T, int KT> struct ShLds {
@@ -312,21 +313,23 @@ __global__ __launch_bounds__(SH_NW * 64) void smallhead_fwd_kernel(ShParams p) {
 
 // ---------------------------------------------------------------------------------------------
 // Resident-keys kernel (bf16, Lk <= 128: row self attention over 104 tokens, CLS, ISAB-2 over the
-// 128 inducing points, hxq over short key sets). The workgroup loads all keys of its batch element
-// once (K with RoPE, row-major V, per-key additive term b2 = bias*log2e, 0 without bias, -inf past
-// the valid length) and then walks query blocks of 16 * NW; each wave takes 16 queries and runs the
-// 8 heads one after the other, each head one pass over all keys:
+// 128 inducing points, hxq over short key sets). A workgroup of 8 waves takes one batch element and a
+// run of 16-query blocks. It loads all keys once into LDS (K with RoPE, row-major V, per-key additive
+// term b2 = bias*log2e, 0 without bias, -inf past the valid length); wave g then copies head g's K
+// and V^T MFMA operands into registers and walks the run's query blocks, each one pass over all keys:
 //   x = K (q' log2e) + b2         16x16x32 MFMAs: q' log2e as a bf16 high part and the bf16
-//                                 remainder in the two k-halves, b2 as the accumulator input
+//                                 remainder in the two k-halves, b2 as the accumulator input (a zero
+//                                 accumulator for key groups that need no b2)
 //   p = bf16(exp2(x)), l = 1 p    (ones-operand MFMA)
-//   O^T = V^T P^T / l             V^T from ds_read_b64_tr_b16 on the row-major V tile
+//   O^T = V^T P^T / l             V^T read once with ds_read_b64_tr_b16 from the row-major V tile
+// q is read with buffer loads two blocks ahead of its use and O written with range-checked buffer
+// stores, so the main loop reads no LDS except b2 of masked groups.
 // exp2 takes x without the row maximum subtracted; only when l falls outside [2^-64, 2^64] (or is
-// not finite) is the head recomputed with the exact maximum subtracted. Otherwise every p lies
+// not finite) is the block recomputed with the exact maximum subtracted. Otherwise every p lies
 // below 2^64 and every p that matters above the fp32 floor, and fp32 / bf16 relative precision does
 // not depend on scale, so both give the softmax to rounding.
 // ---------------------------------------------------------------------------------------------
 constexpr int RS_LK = 128;
-constexpr int RS_NG = RS_LK / 32;   // 32-key groups
 constexpr int RS_KSTR = SH_E + 8;   // K rows of 272 B: a 16-row b128 operand read covers all banks
 constexpr int RS_VSTR = SH_E + 16;  // V rows of 288 B: the transposed reads of 8 rows cover all banks
 constexpr float RS_L_HI = 0x1p64f;
@@ -359,68 +362,60 @@ __device__ __forceinline__ f32x4 rope4_bf16(const bf16* row, const float* cs, co
   return y;
 }
 
-// q' log2e operand of one (query, head): dims d0..d0+7 as the bf16 high part (G < 2) or the bf16
-// remainder (G >= 2), q' = bf16(rope(q) * scale) as in the reference's packed kernels (:498-502).
-__device__ __forceinline__ bf16x8 rs_qop(const ShParams& p, const bf16* qrow, int qi, int d0, int G) {
-  float f[8];
-  if (p.rope) {
-    const float* cs = p.cq + (int64_t)qi * SH_E;
-    const float* sn = p.sq + (int64_t)qi * SH_E;
-    const f32x4 y0 = rope4_bf16(qrow, cs, sn, d0, p.rope, p.half, p.rot);
-    const f32x4 y1 = rope4_bf16(qrow, cs, sn, d0 + 4, p.rope, p.half, p.rot);
+// This lane's 4 dims of q at byte offset off of the workgroup's q rows: lanes l and l ^ 32 (G and
+// G ^ 2) share the 8 dims d8..d8+7 of the MFMA operand, G < 2 takes d8..d8+3 and G >= 2 d8+4..d8+7.
+// A buffer load: rows past Lq lie outside the resource and read as zero, and the compiler keeps a
+// load issued ahead of its use where it is (it does not merge these into the loop's phi).
+__device__ __forceinline__ bf16x4 rs_qraw(__amdgpu_buffer_rsrc_t qrsrc, int off) {
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(qrsrc, off, 0, 0));
+}
+
+// q' log2e operand from this lane's 4 values of q' = bf16(rope(q) * scale) (the reference's packed
+// kernels, :498-502), held as floats. Each lane splits its 4 into bf16 high parts and bf16
+// remainders and swaps with lane l ^ 32 the half the other needs (v_permlane32_swap), so G < 2 ends
+// with the 8 high parts and G >= 2 with the 8 remainders of the shared dims.
+__device__ __forceinline__ bf16x8 rs_qsplit(f32x4 qs, int G) {
+  const bool low = G < 2;  // lanes 0..31
+  bf16x4 keep, send;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      f[r] = y0[r];
-      f[4 + r] = y1[r];
-    }
-  } else {
-    const bf16x8 raw = *(const bf16x8*)(qrow + d0);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = (float)raw[j];
+  for (int j = 0; j < 4; ++j) {
+    const float x = qs[j] * TA_LOG2E;
+    const bf16 hi = (bf16)x;
+    const bf16 lo = (bf16)(x - (float)hi);
+    keep[j] = low ? hi : lo;
+    send[j] = low ? lo : hi;
   }
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 sw = __builtin_bit_cast(u32x2, send);
+  u32x2 rw;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const auto r = __builtin_amdgcn_permlane32_swap(sw[w], sw[w], false, false);
+    rw[w] = low ? r[1] : r[0];
+  }
+  const bf16x4 recv = __builtin_bit_cast(bf16x4, rw);
   bf16x8 op;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float x = (float)(bf16)(f[j] * p.scale) * TA_LOG2E;
-    const bf16 hi = (bf16)x;
-    op[j] = G < 2 ? hi : (bf16)(x - (float)hi);
+  for (int j = 0; j < 4; ++j) {
+    op[j] = low ? keep[j] : recv[j];
+    op[4 + j] = low ? recv[j] : keep[j];
   }
   return op;
 }
 
-// p = bf16(exp2(x - sub)) over the 32-key group kg: lane (l16, G) holds keys 32kg + 4G + r and
-// 32kg + 16 + 4G + r of query l16 (the k-slot order 8G + j of the 16x16x32 B operand).
-template <bool SUB>
-__device__ __forceinline__ bf16x8 rs_probs(const bf16* lds_k, const float* lds_b2, bf16x8 qop, int kg,
-                                           int kcol, int l16, int G, float sub) {
-  const bf16x8 ka0 = *(const bf16x8*)(lds_k + (32 * kg + l16) * RS_KSTR + kcol);
-  const bf16x8 ka1 = *(const bf16x8*)(lds_k + (32 * kg + 16 + l16) * RS_KSTR + kcol);
-  const f32x4 c0 = *(const f32x4*)(lds_b2 + 32 * kg + 4 * G);
-  const f32x4 c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
-  const f32x4 x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qop, c0, 0, 0, 0);
-  const f32x4 x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
-  bf16x8 pv;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    pv[r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x0[r] - sub : x0[r]);
-    pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
+// Scores of the 32-key group kg, x = K (q' log2e) + b2: lane (l16, G) holds keys 32kg + 4G + r (x0)
+// and 32kg + 16 + 4G + r (x1) of query l16 (the k-slot order 8G + j of the 16x16x32 B operand).
+// Groups below MF have b2 = 0 for every key (no bias, all keys valid): a zero accumulator.
+template <int MF>
+__device__ __forceinline__ void rs_scores(bf16x8 ka0, bf16x8 ka1, bf16x8 qop, const float* lds_b2, int kg,
+                                          int G, f32x4& x0, f32x4& x1) {
+  f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+  if (kg >= MF) {
+    c0 = *(const f32x4*)(lds_b2 + 32 * kg + 4 * G);
+    c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
   }
-  return pv;
-}
-
-// Largest x over the 32-key group kg (keys past the valid length hold -inf).
-__device__ __forceinline__ float rs_max(const bf16* lds_k, const float* lds_b2, bf16x8 qop, int kg, int kcol,
-                                        int l16, int G) {
-  const bf16x8 ka0 = *(const bf16x8*)(lds_k + (32 * kg + l16) * RS_KSTR + kcol);
-  const bf16x8 ka1 = *(const bf16x8*)(lds_k + (32 * kg + 16 + l16) * RS_KSTR + kcol);
-  const f32x4 c0 = *(const f32x4*)(lds_b2 + 32 * kg + 4 * G);
-  const f32x4 c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
-  const f32x4 x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qop, c0, 0, 0, 0);
-  const f32x4 x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
-  float m = TA_NEG_INF;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(x0[r], x1[r]));
-  return m;
+  x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qop, c0, 0, 0, 0);
+  x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
 }
 
 __device__ __forceinline__ float rs_sum(bf16x8 pv) {
@@ -430,8 +425,89 @@ __device__ __forceinline__ float rs_sum(bf16x8 pv) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pv, zero, 0, 0, 0)[0];
 }
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64, 2) void sh_resident_kernel(ShParams p) {
+// One (16 queries, head) unit over all keys: p = bf16(exp2(x - sub)), l = sum p (ones-operand
+// MFMA), o = V^T p^T, accumulated group by group in key order.
+template <int NG, int MF, bool SUB>
+__device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG], bf16x8 qop,
+                                        const float* lds_b2, int G, float sub, f32x4& o, float& l) {
+  o = f32x4{0.f, 0.f, 0.f, 0.f};
+  l = 0.f;
+#pragma unroll
+  for (int kg = 0; kg < NG; ++kg) {
+    f32x4 x0, x1;
+    rs_scores<MF>(ka[kg][0], ka[kg][1], qop, lds_b2, kg, G, x0, x1);
+    bf16x8 pv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pv[r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x0[r] - sub : x0[r]);
+      pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
+    }
+    l += rs_sum(pv);
+    o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kg], pv, o, 0, 0, 0);
+    // keep the groups apart: hoisting every group's scores first costs registers
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Largest x of query l16 over all keys (keys past the valid length hold -inf).
+template <int NG, int MF>
+__device__ __forceinline__ float rs_max(const bf16x8 (&ka)[NG][2], bf16x8 qop, const float* lds_b2, int G) {
+  float m = TA_NEG_INF;
+#pragma unroll
+  for (int kg = 0; kg < NG; ++kg) {
+    f32x4 x0, x1;
+    rs_scores<MF>(ka[kg][0], ka[kg][1], qop, lds_b2, kg, G, x0, x1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(x0[r], x1[r]));
+  }
+  return quad_max(m);
+}
+
+// One 16-query block of head g: q' operand from the raw q (or RoPE of the q row), one sweep over
+// all keys, the exact-maximum recompute when l is out of range, and the normalised output.
+template <int NG, int MF, bool ROPE>
+__device__ __forceinline__ void rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
+                                         const float* lds_b2, const bf16* qbase, __amdgpu_buffer_rsrc_t orsrc,
+                                         int orow, bf16x4 qr, int qi, int d4, int g, int G) {
+  f32x4 qs = {0.f, 0.f, 0.f, 0.f};
+  if (!ROPE) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f = (float)qr[j] * p.scale;
+      qs[j] = p.exact_scale ? f : (float)(bf16)f;
+    }
+  } else if (qi < p.Lq) {
+    const f32x4 y = rope4_bf16(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E,
+                               d4, p.rope, p.half, p.rot);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
+  }
+  const bf16x8 qop = rs_qsplit(qs, G);
+  f32x4 o;
+  float l;
+  rs_unit<NG, MF, false>(ka, va, qop, lds_b2, G, 0.f, o, l);
+  if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
+    // rare: recompute with the exact maximum subtracted (queries in range keep theirs)
+    const float mx = rs_max<NG, MF>(ka, qop, lds_b2, G);
+    const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
+    rs_unit<NG, MF, true>(ka, va, qop, lds_b2, G, sub, o, l);
+  }
+  // every lane stores: the buffer range check drops rows past Lq, and an unconditional store keeps
+  // the wait for the next block's q from also waiting for this store
+  const float inv = l == 0.f ? 0.f : __builtin_amdgcn_rcpf(l);
+  bf16x4 ov;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ov), orsrc,
+                                        ((qi - orow) * p.o_sr + g * SH_D + 4 * G) * 2, 0, 0);
+}
+
+// NG = 32-key groups swept (ceil(Lk / 32)); b2 is read from LDS for groups kg >= MF only; ROPE:
+// q and k take the rotary embedding.
+template <int NG, int MF, bool ROPE>
+__global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
+  constexpr int NT = SH_H * 64;
   __shared__ __attribute__((aligned(16))) bf16 lds_k[RS_LK * RS_KSTR];
   __shared__ __attribute__((aligned(16))) bf16 lds_v[RS_LK * RS_VSTR];
   __shared__ __attribute__((aligned(16))) float lds_b2[RS_LK];
@@ -444,21 +520,20 @@ __global__ __launch_bounds__(NW * 64, 2) void sh_resident_kernel(ShParams p) {
     const int vl = p.valid[p.valid_n == 1 ? 0 : b];
     lk = vl < 0 ? 0 : (vl < lk ? vl : lk);
   }
-  const int ng = (lk + 31) / 32;
   const int tid = threadIdx.x;
 
   // fill: K rows with RoPE (fp32 math, cast), V rows as they are, b2 per key; keys past lk (up to
-  // the 32-key group boundary) get zero K/V and b2 = -inf
+  // NG 32-key groups) get zero K/V and b2 = -inf
   {
     const bf16* kbase = (const bf16*)p.k + b * p.k_sb;
     const bf16* vbase = (const bf16*)p.v + b * p.v_sb;
-    const int nk = ng * 32;
-    for (int u = tid; u < nk * (SH_E / 4); u += NW * 64) {
+    const int nk = NG * 32;
+    for (int u = tid; u < nk * (SH_E / 4); u += NT) {
       const int key = u >> 5, d0 = (u & 31) * 4;
       bf16x4 val = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
       if (key < lk) {
         const bf16* src = kbase + (int64_t)key * p.k_sr;
-        if (p.rope) {
+        if (ROPE) {
           const f32x4 y = rope4_bf16(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0, p.rope,
                                      p.half, p.rot);
 #pragma unroll
@@ -469,12 +544,12 @@ __global__ __launch_bounds__(NW * 64, 2) void sh_resident_kernel(ShParams p) {
       }
       *(bf16x4*)(lds_k + key * RS_KSTR + d0) = val;
     }
-    for (int u = tid; u < nk * (SH_E / 8); u += NW * 64) {
+    for (int u = tid; u < nk * (SH_E / 8); u += NT) {
       const int key = u >> 4, c8 = (u & 15) * 8;
       const uint4 val = key < lk ? ldg16(vbase + (int64_t)key * p.v_sr + c8) : make_uint4(0, 0, 0, 0);
       *(uint4*)(lds_v + key * RS_VSTR + c8) = val;
     }
-    for (int j = tid; j < nk; j += NW * 64) {
+    for (int j = tid; j < nk; j += NT) {
       float b2 = TA_NEG_INF;
       if (j < lk) b2 = p.bias ? fmaxf(p.bias[b * p.bias_sb + j] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
       lds_b2[j] = b2;
@@ -482,76 +557,78 @@ __global__ __launch_bounds__(NW * 64, 2) void sh_resident_kernel(ShParams p) {
   }
   __syncthreads();
 
-  const int lane = tid & 63, wave = tid >> 6;
+  // wave g owns head g: its K operands (the 16 dims twice, for the high and remainder halves of q)
+  // and V^T operands stay in registers for the whole query range
+  const int lane = tid & 63, g = tid >> 6;
   const int l16 = lane & 15, G = lane >> 4;
-  const bf16* qbase = (const bf16*)p.q + b * p.q_sb;
-  bf16* obase = (bf16*)p.o + b * p.o_sb;
+  const int kcol = g * SH_D + 8 * (G & 1);
   // transposed-read lane roles: lane 4j + c of group G points at key 4G + j, dims 4c..4c+3
   const int tr_key = 4 * G + (l16 >> 2), tr_col = 4 * (l16 & 3);
-
-  for (int qbi = 0; qbi < p.qbpw; ++qbi) {
-    const int qb = qb0 + qbi;
-    if (qb >= p.nqb) break;
-    const int qw0 = qb * 16 * NW + wave * 16;
-    if (qw0 >= p.Lq) break;  // no barrier below: waves leave independently
-    const int qi = qw0 + l16;
-    const bool qok = qi < p.Lq;
-    const bf16* qrow = qbase + (int64_t)qi * p.q_sr;
-#pragma unroll 1
-    for (int g = 0; g < SH_H; ++g) {
-      const int kcol = g * SH_D + 8 * (G & 1);
-      bf16x8 qop;
+  bf16x8 ka[NG][2], va[NG];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qop[j] = (bf16)0.f;
-      if (qok) qop = rs_qop(p, qrow, qi, kcol, G);
-      bf16x8 pv[RS_NG];
-      float l = 0.f;
-#pragma unroll
-      for (int kg = 0; kg < RS_NG; ++kg) {
-        if (kg < ng) {
-          pv[kg] = rs_probs<false>(lds_k, lds_b2, qop, kg, kcol, l16, G, 0.f);
-          l += rs_sum(pv[kg]);
-        }
-      }
-      if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
-        // rare: recompute this head with the exact maximum subtracted (lanes in range keep theirs)
-        float mx = TA_NEG_INF;
-#pragma unroll
-        for (int kg = 0; kg < RS_NG; ++kg)
-          if (kg < ng) mx = fmaxf(mx, rs_max(lds_k, lds_b2, qop, kg, kcol, l16, G));
-        mx = quad_max(mx);
-        const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
-        l = 0.f;
-#pragma unroll
-        for (int kg = 0; kg < RS_NG; ++kg) {
-          if (kg < ng) {
-            pv[kg] = rs_probs<true>(lds_k, lds_b2, qop, kg, kcol, l16, G, sub);
-            l += rs_sum(pv[kg]);
-          }
-        }
-      }
-      f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kg = 0; kg < RS_NG; ++kg) {
-        if (kg < ng) {
-          const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(lds_v + (32 * kg + tr_key) * RS_VSTR + g * SH_D + tr_col));
-          const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(lds_v + (32 * kg + 16 + tr_key) * RS_VSTR + g * SH_D + tr_col));
-          const bf16x4 a0 = __builtin_bit_cast(bf16x4, t0), a1 = __builtin_bit_cast(bf16x4, t1);
-          const bf16x8 va = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-          o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pv[kg], o, 0, 0, 0);
-        }
-      }
-      if (qok) {
-        const float inv = l == 0.f ? 0.f : 1.f / l;
-        bf16x4 ov;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
-        *(bf16x4*)(obase + (int64_t)qi * p.o_sr + g * SH_D + 4 * G) = ov;
-      }
-    }
+  for (int kg = 0; kg < NG; ++kg) {
+    ka[kg][0] = *(const bf16x8*)(lds_k + (32 * kg + l16) * RS_KSTR + kcol);
+    ka[kg][1] = *(const bf16x8*)(lds_k + (32 * kg + 16 + l16) * RS_KSTR + kcol);
+    const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(lds_v + (32 * kg + tr_key) * RS_VSTR + g * SH_D + tr_col));
+    const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(lds_v + (32 * kg + 16 + tr_key) * RS_VSTR + g * SH_D + tr_col));
+    const bf16x4 a0 = __builtin_bit_cast(bf16x4, t0), a1 = __builtin_bit_cast(bf16x4, t1);
+    va[kg] = bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
   }
+
+  const bf16* qbase = (const bf16*)p.q + b * p.q_sb;
+  const int nb = p.nqb - qb0 < p.qbpw ? p.nqb - qb0 : p.qbpw;  // 16-query blocks of this workgroup
+  // output rows orow .. orow + nrow - 1 as a buffer resource (byte offsets, range checked)
+  const int orow = qb0 * 16;
+  const int nrow = nb * 16 < p.Lq - orow ? nb * 16 : p.Lq - orow;
+  const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (bf16*)p.o + b * p.o_sb + (int64_t)orow * p.o_sr, 0, nrow * p.o_sr * 2, TA_BUF_WORD3);
+  const int d4 = kcol + 4 * (G >> 1);  // this lane's 4 dims of q
+  // q rows orow .. orow + nrow - 1 likewise; two q buffers, each loaded two blocks ahead of its use
+  const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (bf16*)qbase + (int64_t)orow * p.q_sr, 0, nrow * p.q_sr * 2, TA_BUF_WORD3);
+  const int qoff = (l16 * p.q_sr + d4) * 2, qstep = 16 * p.q_sr * 2;
+  bf16x4 qa = rs_qraw(qrsrc, qoff), qb = rs_qraw(qrsrc, qoff + qstep);
+  int i = 0;
+#pragma unroll 1
+  for (; i + 1 < nb; i += 2) {
+    rs_block<NG, MF, ROPE>(p, ka, va, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
+    qa = rs_qraw(qrsrc, qoff + (i + 2) * qstep);
+    rs_block<NG, MF, ROPE>(p, ka, va, lds_b2, qbase, orsrc, orow, qb, orow + (i + 1) * 16 + l16, d4, g, G);
+    qb = rs_qraw(qrsrc, qoff + (i + 3) * qstep);
+  }
+  if (i < nb) rs_block<NG, MF, ROPE>(p, ka, va, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
+}
+
+// mode 0: b2 read for every group (key bias or per-batch valid lengths); 1: last group only (Lk not
+// a multiple of 32); 2: none
+template <int NG, bool ROPE>
+void launch_resident_ng(const ShParams& p, int mode, int64_t nblk, hipStream_t stream) {
+  const dim3 grid((unsigned)nblk), block(SH_H * 64);
+  if (mode == 0)
+    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE>), grid, block, 0, stream, p);
+  else if (mode == 1)
+    hipLaunchKernelGGL((sh_resident_kernel<NG, NG - 1, ROPE>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((sh_resident_kernel<NG, NG, ROPE>), grid, block, 0, stream, p);
+}
+
+template <bool ROPE>
+void launch_resident_rope(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStream_t stream) {
+  switch (ngrp) {
+    case 1: launch_resident_ng<1, ROPE>(p, mode, nblk, stream); break;
+    case 2: launch_resident_ng<2, ROPE>(p, mode, nblk, stream); break;
+    case 3: launch_resident_ng<3, ROPE>(p, mode, nblk, stream); break;
+    default: launch_resident_ng<4, ROPE>(p, mode, nblk, stream); break;
+  }
+}
+
+void launch_resident(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStream_t stream) {
+  if (p.rope)
+    launch_resident_rope<true>(p, ngrp, mode, nblk, stream);
+  else
+    launch_resident_rope<false>(p, ngrp, mode, nblk, stream);
 }
 
 }  // namespace
@@ -576,24 +653,24 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   p.cq = cq; p.sq = sq; p.ck = ck; p.sk = sk;
   p.rope = rope; p.half = half; p.rot = rot;
   p.scale = scale;
+  {
+    int e = 0;
+    p.exact_scale = scale > 0.f && frexpf(scale, &e) == 0.5f;
+  }
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   if (dtype == 0 && Lk <= RS_LK) {
-    // all keys resident in LDS: one (16 queries, head) unit at a time, no online softmax;
-    // 8 waves for long query sets, 4 when a batch element has at most 64 queries
-    const int nw = Lq > 64 ? 8 : 4;
-    p.nqb = (int)((Lq + 16 * nw - 1) / (16 * nw));
-    // enough query blocks per workgroup to amortise the key fill, while keeping >= ~8 workgroups
-    // per CU for the whole grid
-    const int64_t target_wgs = 256 * 8;
+    // all keys resident: one workgroup per (batch element, run of 16-query blocks), one head per wave
+    p.nqb = (int)((Lq + 15) / 16);
+    // long enough runs to amortise the key fill, while keeping >= ~32 workgroups per CU for the grid
+    const int64_t target_wgs = 256 * 32;
     int64_t qbpw = (B * (int64_t)p.nqb + target_wgs - 1) / target_wgs;
-    qbpw = qbpw < 1 ? 1 : (qbpw > 16 ? 16 : qbpw);
+    qbpw = qbpw < 1 ? 1 : (qbpw > 64 ? 64 : qbpw);
     p.qbpw = (int)(qbpw > p.nqb ? p.nqb : qbpw);
     p.nwg_b = (p.nqb + p.qbpw - 1) / p.qbpw;
     const int64_t nblk = B * (int64_t)p.nwg_b;
-    if (nw == 8)
-      hipLaunchKernelGGL((sh_resident_kernel<8>), dim3((unsigned)nblk), dim3(8 * 64), 0, stream, p);
-    else
-      hipLaunchKernelGGL((sh_resident_kernel<4>), dim3((unsigned)nblk), dim3(4 * 64), 0, stream, p);
+    const int ngrp = (int)((Lk + 31) / 32);  // 32-key groups every batch element sweeps
+    const int mode = (bias || valid) ? 0 : (Lk == 32 * ngrp ? 2 : 1);
+    launch_resident(p, ngrp, mode, nblk, stream);
     return (int)hipGetLastError();
   }
   p.nqb = (int)((Lq + SH_QB - 1) / SH_QB);

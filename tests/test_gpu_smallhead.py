@@ -289,3 +289,106 @@ def test_stream_split_matches_unsplit(dev):
     ref = O.hxq_ref(q[:, :16].cpu(), kv.cpu(), valid.cpu().numpy(), H)
     assert _err(split[:, :16], ref) <= 2e-2
     assert _err(one[:, :16], ref) <= 2e-2
+
+
+def test_c5_style_bucket_group(dev):
+    # BASELINE config 5 in miniature: tables of different train sizes padded to one row bucket,
+    # several sequences per table, hxq with valid = n_train per sequence, then pk_cross of all rows
+    pk = _attn()
+    g = _gen(14)
+    L, per = 2048, 3
+    n_train = [1100, 1900, 1337]
+    B = per * len(n_train)
+    valid = torch.tensor(n_train, dtype=torch.int32).repeat_interleave(per)
+    q = (torch.randn(B, 128, E, generator=g) * 0.25).to(torch.bfloat16)
+    kv = torch.randn(B, L, 2 * E, generator=g).to(torch.bfloat16)
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), valid.to(dev), H)
+    assert _err(out, O.hxq_ref(q, kv, valid.numpy(), H)) <= 2e-2
+    rows = torch.randn(B, L, E, generator=g).to(torch.bfloat16)
+    ind = torch.randn(B, 128, 2 * E, generator=g).to(torch.bfloat16)
+    out2 = pk.pk_cross_attention(rows.to(dev), ind.to(dev), H, None, None, 0.25)
+    sub = slice(0, 300)
+    assert _err(out2[:, sub], O.pk_cross_ref(rows[:, sub], ind, H, None, None, None, 0.25)) <= 2e-2
+
+
+# --- resident kernel (bf16, Lk <= 128): key-group counts, masking modes, recompute, long runs ---
+
+@pytest.mark.parametrize("name,B,Lq,Lk,bias", [
+    ("one_key", 3, 40, 1, False),                 # one 32-key group, keys past Lk masked
+    ("one_group_full", 3, 40, 32, False),         # no masking at all
+    ("two_groups_ragged", 3, 40, 50, False),
+    ("three_groups_full", 3, 40, 96, False),
+    ("four_groups_key_bias", 4, 104, 104, True),  # key bias: the additive term on every group
+])
+def test_resident_key_groups(dev, name, B, Lq, Lk, bias):
+    pk = _attn()
+    g = _gen(15)
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16)
+    k = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
+    kb = None
+    if bias:
+        kb = torch.randn(B, Lk, generator=g) * 2.0
+        kb[:, Lk - 5:] = -1e30
+    print(f"[resident] {name}", flush=True)
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, None if kb is None else kb.to(dev))
+    assert _err(out, O.hx_ref(q, k, v, H, kb)) <= 2e-2
+
+
+def test_resident_sums_out_of_range(dev):
+    # rows whose exp2 sums leave [2^-64, 2^64] are recomputed with the row maximum subtracted:
+    # batch 0 has every key at bias -60 (sums underflow), batch 1 has every other query scaled
+    # x120 (sums overflow, waves mix recomputed and kept rows), batch 2 stays in range
+    pk = _attn()
+    g = _gen(16)
+    B, Lq, Lk = 3, 80, 128
+    q = torch.randn(B, Lq, E, generator=g) * 0.25
+    q[1, 0::2] *= 120.0
+    q = q.to(torch.bfloat16)
+    k = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
+    kb = torch.zeros(B, Lk)
+    kb[0] = -60.0
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev))
+    assert torch.isfinite(out.float()).all()
+    assert _err(out, O.hx_ref(q, k, v, H, kb)) <= 2e-2
+
+
+def test_resident_all_keys_masked_bf16_is_uniform(dev):
+    pk = _attn()
+    g = _gen(17)
+    q = (torch.randn(2, 24, E, generator=g) * 0.25).to(torch.bfloat16)
+    k = torch.randn(2, 20, E, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 20, E, generator=g).to(torch.bfloat16)
+    kb = torch.full((2, 20), -1e30)
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev))
+    want = v.double().mean(dim=1, keepdim=True).expand(2, 24, E).numpy()
+    assert _err(out, want) <= 2e-2
+
+
+def test_resident_long_query_runs(dev):
+    # enough 16-query blocks that each workgroup walks several (two-buffer loop, odd tail block,
+    # a partial last block of 6 rows)
+    pk = _attn()
+    g = _gen(18)
+    B, Lq, Lk = 80, 3990, 128
+    x = torch.randn(B, Lq, E, generator=g).to(torch.bfloat16)
+    y = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
+    out = pk.pk_cross_attention(x.to(dev), y.to(dev), H, None, None, 0.25).cpu()
+    for b in (0, 41, 79):
+        ref = O.pk_cross_ref(x[b:b + 1], y[b:b + 1], H, None, None, None, 0.25)
+        assert _err(out[b:b + 1], ref) <= 2e-2
+
+
+def test_resident_long_runs_rope(dev):
+    # C2-like row attention with RoPE, several 16-query blocks per workgroup
+    pk = _attn()
+    g = _gen(19)
+    B, L = 2048, 104
+    x = torch.randn(B, L, 3 * E, generator=g).to(torch.bfloat16)
+    rope = _Rope(interleaved=False)
+    out = pk.pk_self_attention(x.to(dev), H, None, rope, 16 ** -0.5).cpu()
+    tabs = _rope_np(rope, L)
+    for b in (0, 1023, 2047):
+        ref = O.pk_self_ref(x[b:b + 1], H, None, tabs, 16 ** -0.5)
+        assert _err(out[b:b + 1], ref) <= 2e-2
