@@ -362,12 +362,47 @@ __device__ __forceinline__ f32x4 rope4_bf16(const bf16* row, const float* cs, co
   return y;
 }
 
-// This lane's 4 dims of q at byte offset off of the workgroup's q rows: lanes l and l ^ 32 (G and
-// G ^ 2) share the 8 dims d8..d8+7 of the MFMA operand, G < 2 takes d8..d8+3 and G >= 2 d8+4..d8+7.
-// A buffer load: rows past Lq lie outside the resource and read as zero, and the compiler keeps a
-// load issued ahead of its use where it is (it does not merge these into the loop's phi).
-__device__ __forceinline__ bf16x4 rs_qraw(__amdgpu_buffer_rsrc_t qrsrc, int off) {
-  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(qrsrc, off, 0, 0));
+// This lane's 8 dims of q (those of its B-operand k-slots) at byte offset off of the workgroup's q
+// rows. A buffer load: rows past Lq lie outside the resource and read as zero, and the compiler
+// keeps a load issued ahead of its use where it is (it does not merge these into the loop's phi).
+__device__ __forceinline__ bf16x8 rs_qraw(__amdgpu_buffer_rsrc_t qrsrc, int off) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qrsrc, off, 0, 0));
+}
+
+// Lanes l and l ^ 32 (G and G ^ 2) share the 8 dims d8..d8+7 of their operand k-slots; each has
+// computed 4 of them (G < 2: d8..d8+3, G >= 2: d8+4..d8+7) and the two swap (v_permlane32_swap).
+__device__ __forceinline__ bf16x8 rs_pair8(bf16x4 mine, int G) {
+  const bool low = G < 2;  // lanes 0..31
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 sw = __builtin_bit_cast(u32x2, mine);
+  u32x2 rw;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const auto r = __builtin_amdgcn_permlane32_swap(sw[w], sw[w], false, false);
+    rw[w] = low ? r[1] : r[0];
+  }
+  const bf16x4 recv = __builtin_bit_cast(bf16x4, rw);
+  bf16x8 op;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    op[j] = low ? mine[j] : recv[j];
+    op[4 + j] = low ? recv[j] : mine[j];
+  }
+  return op;
+}
+
+// K operand with c = scale * log2e folded in: k c as a bf16 high part (G < 2, k-slots 0..15) and
+// the bf16 remainder (G >= 2, k-slots 16..31), so that a raw q' operand in both halves gives
+// x = q' k c to ~2^-17 relative.
+__device__ __forceinline__ bf16x8 rs_ksplit(bf16x8 k, float c, int G) {
+  bf16x8 op;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x = (float)k[j] * c;
+    const bf16 hi = (bf16)x;
+    op[j] = G < 2 ? hi : (bf16)(x - (float)hi);
+  }
+  return op;
 }
 
 // q' log2e operand from this lane's 4 values of q' = bf16(rope(q) * scale) (the reference's packed
@@ -418,9 +453,7 @@ __device__ __forceinline__ void rs_scores(bf16x8 ka0, bf16x8 ka1, bf16x8 qop, co
   x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
 }
 
-__device__ __forceinline__ float rs_sum(bf16x8 pv) {
-  const bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f,
-                       (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+__device__ __forceinline__ float rs_sum(bf16x8 ones, bf16x8 pv) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pv, zero, 0, 0, 0)[0];
 }
@@ -428,8 +461,8 @@ __device__ __forceinline__ float rs_sum(bf16x8 pv) {
 // One (16 queries, head) unit over all keys: p = bf16(exp2(x - sub)), l = sum p (ones-operand
 // MFMA), o = V^T p^T, accumulated group by group in key order.
 template <int NG, int MF, bool SUB>
-__device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG], bf16x8 qop,
-                                        const float* lds_b2, int G, float sub, f32x4& o, float& l) {
+__device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG], bf16x8 ones,
+                                        bf16x8 qop, const float* lds_b2, int G, float sub, f32x4& o, float& l) {
   o = f32x4{0.f, 0.f, 0.f, 0.f};
   l = 0.f;
 #pragma unroll
@@ -442,7 +475,7 @@ __device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 
       pv[r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x0[r] - sub : x0[r]);
       pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
     }
-    l += rs_sum(pv);
+    l += rs_sum(ones, pv);
     o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kg], pv, o, 0, 0, 0);
     // keep the groups apart: hoisting every group's scores first costs registers
     __builtin_amdgcn_sched_barrier(0);
@@ -465,32 +498,44 @@ __device__ __forceinline__ float rs_max(const bf16x8 (&ka)[NG][2], bf16x8 qop, c
 
 // One 16-query block of head g: q' operand from the raw q (or RoPE of the q row), one sweep over
 // all keys, the exact-maximum recompute when l is out of range, and the normalised output.
-template <int NG, int MF, bool ROPE>
+template <int NG, int MF, bool ROPE, bool EXACT>
 __device__ __forceinline__ void rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
-                                         const float* lds_b2, const bf16* qbase, __amdgpu_buffer_rsrc_t orsrc,
-                                         int orow, bf16x4 qr, int qi, int d4, int g, int G) {
-  f32x4 qs = {0.f, 0.f, 0.f, 0.f};
-  if (!ROPE) {
+                                         bf16x8 ones, const float* lds_b2, const bf16* qbase, __amdgpu_buffer_rsrc_t orsrc,
+                                         int orow, bf16x8 qr, int qi, int d4, int g, int G) {
+  bf16x8 qop;
+  if (EXACT && !ROPE) {
+    qop = qr;  // q' = q scale exactly: scale and log2e ride on the K operand
+  } else if (EXACT) {
+    bf16x4 y4 = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+    if (qi < p.Lq) {
+      const f32x4 y = rope4_bf16(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
+                                 p.sq + (int64_t)qi * SH_E, d4, p.rope, p.half, p.rot);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float f = (float)qr[j] * p.scale;
-      qs[j] = p.exact_scale ? f : (float)(bf16)f;
+      for (int j = 0; j < 4; ++j) y4[j] = (bf16)y[j];  // bf16(rope(q) scale) = bf16(rope(q)) scale
     }
-  } else if (qi < p.Lq) {
-    const f32x4 y = rope4_bf16(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E,
-                               d4, p.rope, p.half, p.rot);
+    qop = rs_pair8(y4, G);
+  } else {
+    // other scales: q' = bf16(q scale) rounded here, log2e split over the two k-halves
+    f32x4 qs = {0.f, 0.f, 0.f, 0.f};
+    if (!ROPE) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
+      for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)((float)qr[(G >> 1) * 4 + j] * p.scale);
+    } else if (qi < p.Lq) {
+      const f32x4 y = rope4_bf16(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
+                                 p.sq + (int64_t)qi * SH_E, d4, p.rope, p.half, p.rot);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
+    }
+    qop = rs_qsplit(qs, G);
   }
-  const bf16x8 qop = rs_qsplit(qs, G);
   f32x4 o;
   float l;
-  rs_unit<NG, MF, false>(ka, va, qop, lds_b2, G, 0.f, o, l);
+  rs_unit<NG, MF, false>(ka, va, ones, qop, lds_b2, G, 0.f, o, l);
   if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
     // rare: recompute with the exact maximum subtracted (queries in range keep theirs)
     const float mx = rs_max<NG, MF>(ka, qop, lds_b2, G);
     const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
-    rs_unit<NG, MF, true>(ka, va, qop, lds_b2, G, sub, o, l);
+    rs_unit<NG, MF, true>(ka, va, ones, qop, lds_b2, G, sub, o, l);
   }
   // every lane stores: the buffer range check drops rows past Lq, and an unconditional store keeps
   // the wait for the next block's q from also waiting for this store
@@ -504,8 +549,9 @@ __device__ __forceinline__ void rs_block(const ShParams& p, const bf16x8 (&ka)[N
 }
 
 // NG = 32-key groups swept (ceil(Lk / 32)); b2 is read from LDS for groups kg >= MF only; ROPE:
-// q and k take the rotary embedding.
-template <int NG, int MF, bool ROPE>
+// q and k take the rotary embedding; EXACT: the scale is a power of two (scale and log2e folded
+// into the K operand, raw q as the B operand).
+template <int NG, int MF, bool ROPE, bool EXACT>
 __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   constexpr int NT = SH_H * 64;
   __shared__ __attribute__((aligned(16))) bf16 lds_k[RS_LK * RS_KSTR];
@@ -569,6 +615,10 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   for (int kg = 0; kg < NG; ++kg) {
     ka[kg][0] = *(const bf16x8*)(lds_k + (32 * kg + l16) * RS_KSTR + kcol);
     ka[kg][1] = *(const bf16x8*)(lds_k + (32 * kg + 16 + l16) * RS_KSTR + kcol);
+    if (EXACT) {
+      ka[kg][0] = rs_ksplit(ka[kg][0], p.scale * TA_LOG2E, G);
+      ka[kg][1] = rs_ksplit(ka[kg][1], p.scale * TA_LOG2E, G);
+    }
     const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_s16x4*)(lds_v + (32 * kg + tr_key) * RS_VSTR + g * SH_D + tr_col));
     const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -588,30 +638,42 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   // q rows orow .. orow + nrow - 1 likewise; two q buffers, each loaded two blocks ahead of its use
   const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
       (bf16*)qbase + (int64_t)orow * p.q_sr, 0, nrow * p.q_sr * 2, TA_BUF_WORD3);
-  const int qoff = (l16 * p.q_sr + d4) * 2, qstep = 16 * p.q_sr * 2;
-  bf16x4 qa = rs_qraw(qrsrc, qoff), qb = rs_qraw(qrsrc, qoff + qstep);
+  const int qoff = (l16 * p.q_sr + kcol) * 2, qstep = 16 * p.q_sr * 2;
+  // the ones operand of the row-sum MFMA, kept in registers (not rebuilt per key group)
+  bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  asm volatile("" : "+v"(ones));
+  bf16x8 qa = rs_qraw(qrsrc, qoff);
+  // a zero store to block 0's output (its unit rewrites it later, in order, from this wave) between
+  // the two q loads: the loop is then entered with the pending memory operations in the same order
+  // as at its back edge (q, store, q), and the wait for one buffer's q leaves the last store and the
+  // other buffer's q in flight
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, orsrc, (l16 * p.o_sr + g * SH_D + 4 * G) * 2, 0, 0);
+  bf16x8 qb = rs_qraw(qrsrc, qoff + qstep);
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < nb; i += 2) {
-    rs_block<NG, MF, ROPE>(p, ka, va, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
+    rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
     qa = rs_qraw(qrsrc, qoff + (i + 2) * qstep);
-    rs_block<NG, MF, ROPE>(p, ka, va, lds_b2, qbase, orsrc, orow, qb, orow + (i + 1) * 16 + l16, d4, g, G);
+    rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, orsrc, orow, qb, orow + (i + 1) * 16 + l16, d4, g, G);
     qb = rs_qraw(qrsrc, qoff + (i + 3) * qstep);
   }
-  if (i < nb) rs_block<NG, MF, ROPE>(p, ka, va, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
+  if (i < nb) rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
 }
 
 // mode 0: b2 read for every group (key bias or per-batch valid lengths); 1: last group only (Lk not
-// a multiple of 32); 2: none
+// a multiple of 32); 2: none. Scales other than powers of two take mode 0.
 template <int NG, bool ROPE>
 void launch_resident_ng(const ShParams& p, int mode, int64_t nblk, hipStream_t stream) {
   const dim3 grid((unsigned)nblk), block(SH_H * 64);
-  if (mode == 0)
-    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE>), grid, block, 0, stream, p);
+  if (!p.exact_scale)
+    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, false>), grid, block, 0, stream, p);
+  else if (mode == 0)
+    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, true>), grid, block, 0, stream, p);
   else if (mode == 1)
-    hipLaunchKernelGGL((sh_resident_kernel<NG, NG - 1, ROPE>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((sh_resident_kernel<NG, NG - 1, ROPE, true>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((sh_resident_kernel<NG, NG, ROPE>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((sh_resident_kernel<NG, NG, ROPE, true>), grid, block, 0, stream, p);
 }
 
 template <bool ROPE>
