@@ -496,12 +496,15 @@ __device__ __forceinline__ float rs_max(const bf16x8 (&ka)[NG][2], bf16x8 qop, c
   return quad_max(m);
 }
 
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
 // One 16-query block of head g: q' operand from the raw q (or RoPE of the q row), one sweep over
-// all keys, the exact-maximum recompute when l is out of range, and the normalised output.
+// all keys, the exact-maximum recompute when l is out of range; returns the normalised output (this
+// lane's 4 dims, bf16).
 template <int NG, int MF, bool ROPE, bool EXACT>
-__device__ __forceinline__ void rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
-                                         bf16x8 ones, const float* lds_b2, const bf16* qbase, __amdgpu_buffer_rsrc_t orsrc,
-                                         int orow, bf16x8 qr, int qi, int d4, int g, int G) {
+__device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
+                                         bf16x8 ones, const float* lds_b2, const bf16* qbase, bf16x8 qr, int qi,
+                                         int d4, int G) {
   bf16x8 qop;
   if (EXACT && !ROPE) {
     qop = qr;  // q' = q scale exactly: scale and log2e ride on the K operand
@@ -537,15 +540,17 @@ __device__ __forceinline__ void rs_block(const ShParams& p, const bf16x8 (&ka)[N
     const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
     rs_unit<NG, MF, true>(ka, va, ones, qop, lds_b2, G, sub, o, l);
   }
-  // every lane stores: the buffer range check drops rows past Lq, and an unconditional store keeps
-  // the wait for the next block's q from also waiting for this store
   const float inv = l == 0.f ? 0.f : __builtin_amdgcn_rcpf(l);
   bf16x4 ov;
 #pragma unroll
   for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
-  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ov), orsrc,
-                                        ((qi - orow) * p.o_sr + g * SH_D + 4 * G) * 2, 0, 0);
+  return __builtin_bit_cast(u32x2, ov);
+}
+
+// Every lane stores (the buffer range check drops rows past Lq): an unconditional store keeps the
+// compiler's count of pending memory operations exact, so the waits for q stay partial.
+__device__ __forceinline__ void rs_store(__amdgpu_buffer_rsrc_t orsrc, u32x2 ov, int off) {
+  __builtin_amdgcn_raw_buffer_store_b64(ov, orsrc, off, 0, 0);
 }
 
 // NG = 32-key groups swept (ceil(Lk / 32)); b2 is read from LDS for groups kg >= MF only; ROPE:
@@ -642,23 +647,29 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   // the ones operand of the row-sum MFMA, kept in registers (not rebuilt per key group)
   bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
   asm volatile("" : "+v"(ones));
+  // q loads are issued before the previous block's store and waited for one block later, and the
+  // loop is entered with the pending memory operations in the order of its back edge (q, store, q,
+  // store): each wait for q then leaves the younger stores and q loads in flight. The two zero
+  // stores go to blocks 0 and 1, which their units rewrite later, in order, from this wave (block 1
+  // lies outside the resource when the run has one block, and that store is dropped).
+  const int ooff = (l16 * p.o_sr + g * SH_D + 4 * G) * 2, ostep = 16 * p.o_sr * 2;
   bf16x8 qa = rs_qraw(qrsrc, qoff);
-  // a zero store to block 0's output (its unit rewrites it later, in order, from this wave) between
-  // the two q loads: the loop is then entered with the pending memory operations in the same order
-  // as at its back edge (q, store, q), and the wait for one buffer's q leaves the last store and the
-  // other buffer's q in flight
-  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, orsrc, (l16 * p.o_sr + g * SH_D + 4 * G) * 2, 0, 0);
+  rs_store(orsrc, u32x2{0u, 0u}, ooff);
   bf16x8 qb = rs_qraw(qrsrc, qoff + qstep);
+  rs_store(orsrc, u32x2{0u, 0u}, ooff + ostep);
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < nb; i += 2) {
-    rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
+    u32x2 ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, orow + i * 16 + l16, d4, G);
     qa = rs_qraw(qrsrc, qoff + (i + 2) * qstep);
-    rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, orsrc, orow, qb, orow + (i + 1) * 16 + l16, d4, g, G);
+    rs_store(orsrc, ov, ooff + i * ostep);
+    ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qb, orow + (i + 1) * 16 + l16, d4, G);
     qb = rs_qraw(qrsrc, qoff + (i + 3) * qstep);
+    rs_store(orsrc, ov, ooff + (i + 1) * ostep);
   }
-  if (i < nb) rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, orsrc, orow, qa, orow + i * 16 + l16, d4, g, G);
+  if (i < nb)
+    rs_store(orsrc, rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, orow + i * 16 + l16, d4, G),
+             ooff + i * ostep);
 }
 
 // mode 0: b2 read for every group (key bias or per-batch valid lengths); 1: last group only (Lk not
