@@ -94,6 +94,48 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
                         int32_t dtype, void* stream);
 
 /*
+ * Backward of the small-head ops (training). Inputs as the forward, plus the forward output o and
+ * its gradient dout (both [B, Lq, E], contiguous). P is recomputed in fp32, dS = P (dP - D) with
+ * D = sum over the head's dims of dout * o is cast to the input dtype, dq/dk/dv accumulate in fp32
+ * and are written in the input dtype; the bias gets no gradient. Keys and queries of any length
+ * (the reference stops at 1024 keys).
+ * workspace: at least tabicl_smallhead_bwd_workspace_bytes(B, Lq, E, h) bytes of device memory
+ * (per-query softmax statistics and D, written and read by the two kernels of one call on `stream`);
+ * calls that overlap on the GPU must not share it.
+ */
+int64_t tabicl_smallhead_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t E, int32_t h);
+
+/*
+ * dq, dk, dv [B, L, E] of hx. Replaces tabicl_pk::hx_bwd (reference
+ * scripts/tabicl_tpu_pallas_attn.py:87-122, 185-188, 202-205).
+ */
+int tabicl_hx_bwd(const void* q, const void* k, const void* v, const float* bias, int64_t bias_b,
+                  const void* o, const void* dout, void* dq, void* dk, void* dv, int64_t B, int64_t Lq,
+                  int64_t Lk, int64_t E, int32_t h, int32_t dtype, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/*
+ * d(qkv) [B, L, 3E] packed like qkv: dq = rope_bwd(dq' scale), dk = rope_bwd(dk'), dv, with
+ * rope_bwd(y) = y cos - R(y sin). Replaces tabicl_pk::pk_self_bwd (reference
+ * scripts/tabicl_tpu_pallas_attn.py:512-531, 554-560, 618-621, 654-657).
+ */
+int tabicl_pk_self_bwd(const void* qkv, const float* bias, int64_t bias_b, const float* cos_t,
+                       const float* sin_t, const void* o, const void* dout, void* dqkv, int64_t B, int64_t L,
+                       int64_t E, int32_t h, int32_t rope, int32_t half, int32_t rot, float scale,
+                       int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * dq [B, Lq, E] and d(kv) [B, Lk, 2E] packed like kv. With q_b = 1 (one query set broadcast over
+ * the batch) dq still holds one gradient per batch element; the caller sums them. Replaces
+ * tabicl_pk::pk_cross_bwd (reference scripts/tabicl_tpu_pallas_attn.py:512-553, 633-637, 664-667).
+ */
+int tabicl_pk_cross_bwd(const void* q, int64_t q_b, const void* kv, const float* bias, int64_t bias_b,
+                        const float* cq, const float* sq, const float* ck, const float* sk, const void* o,
+                        const void* dout, void* dq, void* dkv, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                        int32_t h, int32_t rope, int32_t half, int32_t rot, float scale, int32_t dtype,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Dataset-wise in-context attention over cached train-row K/V (head_dim 64).
  * Replaces the Splash hook _tpu_pallas_splash_sdpa / tabicl::tpu_splash_sdpa_{seg,full}
  * (reference results/tpu_patch.diff:95-155; scripts/tabicl_tpu_bucketed.py:221-246).

@@ -14,11 +14,15 @@ It restates, in plain numpy (float64) and CPU torch (float32), the arithmetic of
   splash_sdpa_ref         results/tpu_patch.diff:123-155 (q * D^-0.5, keys >= valid masked)
   tiled_online_sdpa_ref   results/tpu_patch.diff:158-193 (online-softmax recurrence)
   combined_mask_ref       scripts/tabicl_tpu_mha.py:251-290 (additive mask normalisation)
+  attention_bwd_f64       scripts/tabicl_tpu_pallas_attn.py:87-122 (P, dP, D, dS; dq, dk, dv)
+  rope_bwd_ref            pallas_attn.py:446-447, 476-477 (y cos - R(y sin))
+  hx/pk_self/pk_cross_bwd_ref  pallas_attn.py:185-188, 512-560, 618-637 (packed gradients)
 
 Pinning (tests/test_oracle.py): every function is checked against closed forms, invariants and
 brute force (two-key sigmoid, one key, key permutation, row shift, masked keys, q = 0 mean, convex
 hull, valid_len == slicing, chunked == one-shot, RoPE rotation closed form / norm / relative
-position). Parity unpinned: the reference's RotaryEmbedding.freqs initialisation lives in upstream
+position); the backward restatements against torch.autograd of the forward definitions and central
+finite differences. Parity unpinned: the reference's RotaryEmbedding.freqs initialisation lives in upstream
 tabicl (absent here); rope_tables_ref takes the frequencies as an input, and the textbook
 inv_freq_i = base^(-2i/rot) used by tests and bench is an assumption, not a reference fact.
 """
@@ -206,6 +210,97 @@ def pk_cross_ref(q, kv, h, bias, rope_q, rope_k, scale):
     if q.shape[0] != k.shape[0]:
         q = np.broadcast_to(q, (k.shape[0],) + q.shape[1:])
     return attention_f64(q * scale, k, v, h, None if bias is None else _f64(bias))
+
+
+# -------------------------------------------------------------------------------------------
+# backward (training): the reference's bwd kernels, scripts/tabicl_tpu_pallas_attn.py:87-122 (hx)
+# and :512-560 (packed: RoPE and scale on q / k)
+# -------------------------------------------------------------------------------------------
+def attention_bwd_f64(q, k, v, h: int, do, bias=None, o=None):
+    """(dq, dk, dv) of per-head softmax(q k^T + bias) v in merged layout, float64, as the reference's
+    kernels form them: P recomputed; dP = dO V^T; D_g = sum over head g's dims of dO * O (O = the
+    forward output `o` when given, else the exact one); dS = P (dP - D_g); dq = dS K, dk = dS^T Q,
+    dv = P^T dO (pallas_attn.py:104-115). q [B, Lq, E], k/v [B, Lk, E], do [B, Lq, E], bias [1|B, Lk]."""
+    q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
+    B, Lq, E = q.shape
+    Lk = k.shape[1]
+    d = E // h
+    if o is None:
+        o = attention_f64(q, k, v, h, bias)
+    o = _f64(o)
+    bb = None if bias is None else _f64(bias).reshape(-1, Lk)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    for b in range(B):
+        for g in range(h):
+            sl = slice(g * d, (g + 1) * d)
+            s = q[b, :, sl] @ k[b, :, sl].T
+            if bb is not None:
+                s = s + bb[0 if bb.shape[0] == 1 else b][None, :]
+            s = s - s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=1, keepdims=True)
+            dp = do[b, :, sl] @ v[b, :, sl].T
+            dg = (do[b, :, sl] * o[b, :, sl]).sum(axis=1, keepdims=True)
+            ds = p * (dp - dg)
+            dq[b, :, sl] = ds @ k[b, :, sl]
+            dk[b, :, sl] = ds.T @ q[b, :, sl]
+            dv[b, :, sl] = p.T @ do[b, :, sl]
+    return dq, dk, dv
+
+
+def rope_bwd_ref(y, cos, sin, h: int, code: int, half: int, rot: int):
+    """Gradient through x -> x cos + R(x) sin: y cos - R(y sin), since R^T = -R
+    (scripts/tabicl_tpu_pallas_attn.py:446-447, 476-477)."""
+    y = np.asarray(y, np.float64)
+    if code == 0:
+        return y
+    return y * cos - rotate_merged(y * sin, h, code, half, rot)
+
+
+def hx_bwd_ref(q, k, v, h, do, bias=None, o=None):
+    """tabicl_pk::hx_bwd (reference :87-122, 185-188): q pre-scaled, no RoPE."""
+    return attention_bwd_f64(q, k, v, h, do, bias, o)
+
+
+def pk_self_bwd_ref(qkv, h, bias, rope, scale, do, o=None):
+    """tabicl_pk::pk_self_bwd (reference :512-531, 554-560): d(qkv) [B, L, 3E] packed like qkv."""
+    x = _f64(qkv)
+    E = x.shape[-1] // 3
+    q, k, v = x[..., :E], x[..., E:2 * E], x[..., 2 * E:]
+    if rope is not None:
+        cos, sin, code, half, rot = _f64(rope[0]), _f64(rope[1]), rope[2], rope[3], rope[4]
+        q = rope_merged_ref(q, cos, sin, h, code, half, rot)
+        k = rope_merged_ref(k, cos, sin, h, code, half, rot)
+    dq, dk, dv = attention_bwd_f64(q * scale, k, v, h, do, bias, o)
+    dq = dq * scale
+    if rope is not None:
+        dq = rope_bwd_ref(dq, cos, sin, h, code, half, rot)
+        dk = rope_bwd_ref(dk, cos, sin, h, code, half, rot)
+    return np.concatenate([dq, dk, dv], axis=-1)
+
+
+def pk_cross_bwd_ref(q, kv, h, bias, rope_q, rope_k, scale, do, o=None):
+    """tabicl_pk::pk_cross_bwd (reference :512-553): (dq, d(kv) packed like kv). A q with one
+    leading element broadcast over kv's batch gets the sum of the per-element gradients."""
+    q = _f64(q)
+    kv = _f64(kv)
+    E = q.shape[-1]
+    k, v = kv[..., :E], kv[..., E:]
+    if rope_q is not None:
+        cq, sq = _f64(rope_q[0]), _f64(rope_q[1])
+        ck, sk = _f64(rope_k[0]), _f64(rope_k[1])
+        q = rope_merged_ref(q, cq, sq, h, *rope_q[2:])
+        k = rope_merged_ref(k, ck, sk, h, *rope_k[2:])
+    shared = q.shape[0] != k.shape[0]
+    qb = np.broadcast_to(q, (k.shape[0],) + q.shape[1:]) if shared else q
+    dq, dk, dv = attention_bwd_f64(qb * scale, k, v, h, do, bias, o)
+    dq = dq * scale
+    if rope_q is not None:
+        dq = rope_bwd_ref(dq, cq, sq, h, *rope_q[2:])
+        dk = rope_bwd_ref(dk, ck, sk, h, *rope_k[2:])
+    if shared:
+        dq = dq.sum(axis=0, keepdims=True)
+    return dq, np.concatenate([dk, dv], axis=-1)
 
 
 def splash_sdpa_ref(q, k, v, valid=None):

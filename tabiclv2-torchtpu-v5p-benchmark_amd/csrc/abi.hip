@@ -75,6 +75,22 @@ __global__ void cache_append_kernel(T* kc, T* vc, int64_t dst_sn, int64_t dst_sh
   }
 }
 
+// Checks shared by the three backward entry points.
+int bwd_common(const char* op, int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h, int32_t dtype,
+               const float* bias, int64_t bias_b, const void* o, const void* dout, void* ws, int64_t ws_bytes) {
+  int st = smallhead_shape(op, B, Lq, Lk, E, h, dtype);
+  if (st) return st;
+  if (bias && bias_b != 1 && bias_b != B)
+    return fail(1, "%s: bias batch %lld must be 1 or B=%lld", op, (long long)bias_b, (long long)B);
+  if (!o || !dout || !aligned16(o) || !aligned16(dout))
+    return fail(1, "%s: o and dout must be 16-byte aligned device pointers", op);
+  if (B > 0 && Lq > 0 && (!ws || !aligned16(ws) || ws_bytes < tabicl_launch_smallhead_bwd_ws_bytes(B, Lq)))
+    return fail(1, "%s: workspace of %lld bytes (16-byte aligned) required", op,
+                (long long)tabicl_launch_smallhead_bwd_ws_bytes(B, Lq));
+  if (B * ((Lq + 127) / 128 + (Lk + 127) / 128) * 8 > (1LL << 31) - 1) return fail(1, "%s: grid too large", op);
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -192,6 +208,76 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
                               bias && bias_b == B ? Lk : 0, nullptr, 0, cq, sq, ck, sk, rope, half,
                               rot, scale, B, Lq, Lk, dtype, nullptr, 0, (hipStream_t)stream),
       "pk_cross_fwd");
+}
+
+int64_t tabicl_smallhead_bwd_workspace_bytes(int64_t B, int64_t Lq, int64_t E, int32_t h) {
+  if (E != 128 || h != 8 || B < 0 || Lq < 0) return fail(-1, "smallhead_bwd_workspace_bytes: bad arguments");
+  return tabicl_launch_smallhead_bwd_ws_bytes(B, Lq);
+}
+
+int tabicl_hx_bwd(const void* q, const void* k, const void* v, const float* bias, int64_t bias_b,
+                  const void* o, const void* dout, void* dq, void* dk, void* dv, int64_t B, int64_t Lq,
+                  int64_t Lk, int64_t E, int32_t h, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                  void* stream) {
+  int st = bwd_common("hx_bwd", B, Lq, Lk, E, h, dtype, bias, bias_b, o, dout, workspace, workspace_bytes);
+  if (st) return st;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return fail(1, "hx_bwd: pointers must be 16-byte aligned");
+  if (B == 0) return 0;
+  return launch_status(
+      tabicl_launch_smallhead_bwd(q, Lq * E, E, k, Lk * E, E, v, Lk * E, E, o, dout, dq, Lq * E, E, dk, Lk * E, E,
+                                  dv, Lk * E, E, bias, bias && bias_b == B ? Lk : 0, nullptr, nullptr, nullptr,
+                                  nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype, workspace, workspace_bytes,
+                                  (hipStream_t)stream),
+      "hx_bwd");
+}
+
+int tabicl_pk_self_bwd(const void* qkv, const float* bias, int64_t bias_b, const float* cos_t,
+                       const float* sin_t, const void* o, const void* dout, void* dqkv, int64_t B, int64_t L,
+                       int64_t E, int32_t h, int32_t rope, int32_t half, int32_t rot, float scale, int32_t dtype,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
+  int st = bwd_common("pk_self_bwd", B, L, L, E, h, dtype, bias, bias_b, o, dout, workspace, workspace_bytes);
+  if (st) return st;
+  if ((st = rope_args("pk_self_bwd", rope, half, rot))) return st;
+  if (rope && (!cos_t || !sin_t)) return fail(1, "pk_self_bwd: rope tables missing");
+  if (!aligned16(qkv) || !aligned16(dqkv) || (rope && (!aligned16(cos_t) || !aligned16(sin_t))))
+    return fail(1, "pk_self_bwd: pointers must be 16-byte aligned");
+  if (B == 0 || L == 0) return 0;
+  const char* base = (const char*)qkv;
+  char* dbase = (char*)dqkv;
+  const size_t es = esize(dtype);
+  return launch_status(
+      tabicl_launch_smallhead_bwd(base, L * 3 * E, 3 * E, base + E * es, L * 3 * E, 3 * E, base + 2 * E * es,
+                                  L * 3 * E, 3 * E, o, dout, dbase, L * 3 * E, 3 * E, dbase + E * es, L * 3 * E,
+                                  3 * E, dbase + 2 * E * es, L * 3 * E, 3 * E, bias, bias && bias_b == B ? L : 0,
+                                  cos_t, sin_t, cos_t, sin_t, rope, half, rot, scale, B, L, L, dtype, workspace,
+                                  workspace_bytes, (hipStream_t)stream),
+      "pk_self_bwd");
+}
+
+int tabicl_pk_cross_bwd(const void* q, int64_t q_b, const void* kv, const float* bias, int64_t bias_b,
+                        const float* cq, const float* sq, const float* ck, const float* sk, const void* o,
+                        const void* dout, void* dq, void* dkv, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                        int32_t h, int32_t rope, int32_t half, int32_t rot, float scale, int32_t dtype,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
+  int st = bwd_common("pk_cross_bwd", B, Lq, Lk, E, h, dtype, bias, bias_b, o, dout, workspace, workspace_bytes);
+  if (st) return st;
+  if ((st = rope_args("pk_cross_bwd", rope, half, rot))) return st;
+  if (rope && (!cq || !sq || !ck || !sk)) return fail(1, "pk_cross_bwd: rope tables missing");
+  if (q_b != 1 && q_b != B) return fail(1, "pk_cross_bwd: q batch must be 1 or B");
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(dq) || !aligned16(dkv))
+    return fail(1, "pk_cross_bwd: pointers must be 16-byte aligned");
+  if (B == 0) return 0;
+  const char* kvb = (const char*)kv;
+  char* dkvb = (char*)dkv;
+  const size_t es = esize(dtype);
+  return launch_status(
+      tabicl_launch_smallhead_bwd(q, q_b == 1 && B > 1 ? 0 : Lq * E, E, kvb, Lk * 2 * E, 2 * E, kvb + E * es,
+                                  Lk * 2 * E, 2 * E, o, dout, dq, Lq * E, E, dkvb, Lk * 2 * E, 2 * E,
+                                  dkvb + E * es, Lk * 2 * E, 2 * E, bias, bias && bias_b == B ? Lk : 0, cq, sq,
+                                  ck, sk, rope, half, rot, scale, B, Lq, Lk, dtype, workspace, workspace_bytes,
+                                  (hipStream_t)stream),
+      "pk_cross_bwd");
 }
 
 int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,

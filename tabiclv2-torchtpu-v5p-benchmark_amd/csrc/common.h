@@ -90,6 +90,50 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblk) {
 }
 
 struct u32x4 { uint32_t x, y, z, w; };
+
+// RoPE partner of dim jd (0..15) of a head: R(x)_jd = sign * x[partner]
+// (reference: x*cos + R(x)*sin, R = signed rotate-half per head, pairs or halves, zero past rot;
+// scripts/tabicl_tpu_pallas_attn.py:465-473).
+__device__ __forceinline__ void rope_partner(int jd, int rope, int half, int rot, int* partner,
+                                             float* sign) {
+  if (rope == 1) {
+    *partner = jd ^ 1;
+    *sign = (jd & 1) ? 1.f : -1.f;
+  } else if (jd < half) {
+    *partner = jd + half;
+    *sign = -1.f;
+  } else {
+    *partner = jd - half;
+    *sign = 1.f;
+  }
+  if (jd >= rot) {
+    *partner = jd;
+    *sign = 0.f;
+  }
+}
+
+// Four consecutive dims d0..d0+3 (d0 % 4 == 0) of one row after RoPE, in fp32.
+template <typename T>
+__device__ __forceinline__ f32x4 rope4(const T* row, const float* cs, const float* sn, int d0,
+                                       int rope, int half, int rot) {
+  const int hb = d0 & ~15;
+  const float4 c = *(const float4*)(cs + d0);
+  const float4 s = *(const float4*)(sn + d0);
+  const float cv[4] = {c.x, c.y, c.z, c.w};
+  const float sv[4] = {s.x, s.y, s.z, s.w};
+  f32x4 y;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    int pt;
+    float sg;
+    rope_partner((d0 & 15) + r, rope, half, rot, &pt, &sg);
+    const float x = to_f32<T>(row[d0 + r]);
+    const float xp = to_f32<T>(row[hb + pt]);
+    y[r] = x * cv[r] + sg * xp * sv[r];
+  }
+  return y;
+}
+
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *(const uint4*)p; }
 
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): LDS[lds_addr + 16 * lane] =

@@ -31,3 +31,16 @@ int tabicl_launch_ss(const void* q, int64_t q_sb, int64_t q_sr, const void* k, i
                      const int32_t* valid, int64_t valid_n, float scale, int64_t B, int64_t Lq,
                      int64_t Lk, void* ws, int64_t ws_bytes, hipStream_t stream);
 int64_t tabicl_launch_ss_ws_bytes(int64_t B, int64_t Lq, int64_t Lk);
+
+// Backward of the small-head attention (smallhead_bwd.hip): dq, dk, dv (element strides as the
+// inputs) from q, k, v, the forward output o and its gradient dout ([B, Lq, E] contiguous both).
+// ws: tabicl_launch_smallhead_bwd_ws_bytes(B, Lq) bytes (per-query softmax statistics and D).
+int tabicl_launch_smallhead_bwd(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
+                                int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, const void* o,
+                                const void* dout, void* dq, int64_t dq_sb, int64_t dq_sr, void* dk,
+                                int64_t dk_sb, int64_t dk_sr, void* dv, int64_t dv_sb, int64_t dv_sr,
+                                const float* bias, int64_t bias_sb, const float* cq, const float* sq,
+                                const float* ck, const float* sk, int rope, int half, int rot, float scale,
+                                int64_t B, int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
+                                hipStream_t stream);
+int64_t tabicl_launch_smallhead_bwd_ws_bytes(int64_t B, int64_t Lq);

@@ -1,0 +1,429 @@
+// Backward of the small-head attention (8 heads x 16 dims, merged width E = 128) for gfx950.
+//
+// Gradients of O = softmax(q' k'^T + bias) V per head, q' = cast(rope(q) scale), k' = cast(rope(k)),
+// as the reference's training kernels compute them (scripts/tabicl_tpu_pallas_attn.py:87-122 for
+// hx, :512-560 for the packed kernels):
+//   P  = softmax, recomputed in fp32           dP = dO V^T (fp32)
+//   D  = sum over the head's 16 dims of dO * O (the stored forward output)
+//   dS = P * (dP - D), cast to the input dtype
+//   dq' = dS k',  dk' = dS^T q',  dv = cast(P)^T dO   (fp32 accumulation)
+//   dq = rope_bwd(dq' scale), dk = rope_bwd(dk'),  rope_bwd(y) = y cos - R(y sin)
+// The reference keeps all keys of a batch element on chip (at most 1024). Here keys and queries are
+// tiled, so any length works:
+//   sb_dq_kernel   workgroup = (batch element, 128 queries, head); wave = 16 queries. Sweep 1 over
+//                  the key tiles: per-query softmax statistics (row maximum and log2 of the sum, in
+//                  log2 units) and D, written to the workspace; sweep 2: P, dP, dS and dq'.
+//   sb_dkdv_kernel workgroup = (batch element, 128 keys, head); wave = 16 keys. Walks the query
+//                  tiles with the workspace's statistics and D: P, dP, dS, dk' and dv.
+// No atomics, no cross-workgroup reduction: each gradient element is written once.
+// MFMA 16x16x16 (bf16) or 4 x 16x16x4 (fp32), lane layout of mfma16x16x16 in common.h.
+#include "common.h"
+#include "launch.h"
+
+namespace {
+
+constexpr int SB_E = 128;
+constexpr int SB_H = 8;
+constexpr int SB_D = 16;
+constexpr int SB_NW = 8;             // waves per workgroup
+constexpr int SB_QB = 16 * SB_NW;    // queries per dq workgroup
+constexpr int SB_KB = 16 * SB_NW;    // keys per dk/dv workgroup
+constexpr int SB_KT = 128;           // key tile of the dq kernel
+constexpr int SB_QT = 128;           // query tile of the dk/dv kernel
+constexpr float SB_BIAS_FLOOR = -1e37f;
+
+struct SbParams {
+  const void* q;
+  int64_t q_sb, q_sr;
+  const void* k;
+  int64_t k_sb, k_sr;
+  const void* v;
+  int64_t v_sb, v_sr;
+  const void* o;     // [B, Lq, E]
+  const void* dout;  // [B, Lq, E]
+  void* dq;
+  int64_t dq_sb, dq_sr;
+  void* dk;
+  int64_t dk_sb, dk_sr;
+  void* dv;
+  int64_t dv_sb, dv_sr;
+  const float* bias;
+  int64_t bias_sb;
+  const float* cq;
+  const float* sq;
+  const float* ck;
+  const float* sk;
+  int rope, half, rot;
+  float scale;
+  int B, Lq, Lk;
+  // per (batch, head, query), [B][H][Lq] each: the row maximum m of the log2-domain scores and
+  // log2 of the sum of exp2(x - m) (kept apart: with every key at the bias floor, m + log2(l)
+  // would round back to m), and D
+  float* mx;
+  float* ll;
+  float* dd;
+};
+
+template <typename T> struct SbTile {
+  static constexpr int PAD = 16 / sizeof(T);
+  static constexpr int RSTR = SB_D + PAD;   // row-major tile: 16 dims per row
+  static constexpr int TSTR = 128 + PAD;    // transposed tile: 128 rows (keys or queries) per dim
+};
+
+// Per-key additive term in log2 units (reference: bias added to the fp32 scores; -1e30 stays
+// finite, so a row with every key masked is uniform).
+__device__ __forceinline__ float sb_b2(const SbParams& p, int b, int key) {
+  if (key >= p.Lk) return TA_NEG_INF;
+  return p.bias ? fmaxf(p.bias[b * p.bias_sb + key] * TA_LOG2E, SB_BIAS_FLOOR) : 0.f;
+}
+
+// Dims d0..d0+3 of q' (rope, scale, cast) or of k' (rope, cast; scale = 1) of one row.
+template <typename T>
+__device__ __forceinline__ typename OpVec<T, 4>::type sb_prep4(const T* row, const float* cs, const float* sn,
+                                                              int d0, const SbParams& p, float scale) {
+  typedef typename OpVec<T, 4>::type Op4;
+  Op4 r;
+  if (p.rope) {
+    const f32x4 y = rope4<T>(row, cs, sn, d0, p.rope, p.half, p.rot);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = from_f32<T>(y[j] * scale);
+  } else {
+    const Op4 raw = *(const Op4*)(row + d0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = scale == 1.f ? raw[j] : from_f32<T>(to_f32<T>(raw[j]) * scale);
+  }
+  return r;
+}
+
+// rope_bwd of one 16-dim head row held as 4 dims per lane (lane (l16, kap): dims 4 kap .. 4 kap + 3
+// of row l16), exchanged through this wave's LDS scratch [16][17]; cs / sn at the row's position
+// (dims of head g), or null rows for no RoPE.
+__device__ __forceinline__ f32x4 sb_rope_bwd(f32x4 y, float* scr, int l16, int kap, const float* cs,
+                                            const float* sn, int g, const SbParams& p) {
+  if (!p.rope) return y;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) scr[l16 * 17 + 4 * kap + r] = y[r];
+  __builtin_amdgcn_wave_barrier();
+  f32x4 out;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int jd = 4 * kap + r;
+    int pt;
+    float sg;
+    rope_partner(jd, p.rope, p.half, p.rot, &pt, &sg);
+    const float yp = scr[l16 * 17 + pt];
+    out[r] = y[r] * cs[g * SB_D + jd] - sg * yp * sn[g * SB_D + pt];
+  }
+  __builtin_amdgcn_wave_barrier();
+  return out;
+}
+
+// ---------------------------------------------------------------------------------------------
+// dq (and the per-query log-sum-exp and D)
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void sb_fill_keys(const SbParams& p, T* lk, T* lkt, T* lv, float* lb2, int b, int g,
+                                             int k0) {
+  typedef SbTile<T> L;
+  typedef typename OpVec<T, 4>::type Op4;
+  const int tid = threadIdx.x;
+  const T* kbase = (const T*)p.k + b * p.k_sb;
+  const T* vbase = (const T*)p.v + b * p.v_sb;
+  // unit = (key, 4 dims): 128 keys x 4 = 512 units, one per thread
+  for (int u = tid; u < SB_KT * 4; u += SB_NW * 64) {
+    const int row = u >> 2, d4 = (u & 3) * 4, key = k0 + row;
+    Op4 kk, vv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { kk[j] = from_f32<T>(0.f); vv[j] = from_f32<T>(0.f); }
+    if (key < p.Lk) {
+      kk = sb_prep4<T>(kbase + (int64_t)key * p.k_sr, p.ck + (int64_t)key * SB_E, p.sk + (int64_t)key * SB_E,
+                       g * SB_D + d4, p, 1.f);
+      vv = *(const Op4*)(vbase + (int64_t)key * p.v_sr + g * SB_D + d4);
+    }
+    *(Op4*)(lk + row * L::RSTR + d4) = kk;
+    *(Op4*)(lv + row * L::RSTR + d4) = vv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lkt[(d4 + j) * L::TSTR + row] = kk[j];
+  }
+  for (int j = tid; j < SB_KT; j += SB_NW * 64) lb2[j] = sb_b2(p, b, k0 + j);
+}
+
+template <typename T>
+__global__ __launch_bounds__(SB_NW * 64) void sb_dq_kernel(SbParams p) {
+  typedef SbTile<T> L;
+  typedef typename OpVec<T, 4>::type Op4;
+  __shared__ __attribute__((aligned(16))) T lk[SB_KT * L::RSTR];
+  __shared__ __attribute__((aligned(16))) T lkt[SB_D * L::TSTR];
+  __shared__ __attribute__((aligned(16))) T lv[SB_KT * L::RSTR];
+  __shared__ __attribute__((aligned(16))) float lb2[SB_KT];
+  __shared__ float scr[SB_NW][16 * 17];
+
+  const int nqb = (p.Lq + SB_QB - 1) / SB_QB;
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int g = work % SB_H, qb = (work / SB_H) % nqb, b = work / (SB_H * nqb);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, kap = lane >> 4;
+  const int qi = qb * SB_QB + wave * 16 + l16;
+  const bool qok = qi < p.Lq;
+  const int d0 = g * SB_D + 4 * kap;
+
+  // q' and dO operands of query qi (B operands of S^T = K' Q'^T and dP^T = V dO^T), D
+  Op4 qop, dop;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { qop[j] = from_f32<T>(0.f); dop[j] = from_f32<T>(0.f); }
+  float dsum = 0.f;
+  if (qok) {
+    qop = sb_prep4<T>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SB_E,
+                      p.sq + (int64_t)qi * SB_E, d0, p, p.scale);
+    const int64_t orow = ((int64_t)b * p.Lq + qi) * SB_E + d0;
+    dop = *(const Op4*)((const T*)p.dout + orow);
+    const Op4 ov = *(const Op4*)((const T*)p.o + orow);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dsum += to_f32<T>(dop[j]) * to_f32<T>(ov[j]);
+  }
+  dsum = xor_sum(dsum, 16);
+  dsum = xor_sum(dsum, 32);
+
+  const int ntiles = (p.Lk + SB_KT - 1) / SB_KT;
+  // sweep 1: log-sum-exp over this lane's keys (4 per 16-key block), merged over the lane quad
+  float m = TA_NEG_INF, l = 0.f;
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
+    __syncthreads();
+    f32x4 x[SB_KT / 16];
+    float tm = TA_NEG_INF;
+#pragma unroll
+    for (int kt = 0; kt < SB_KT / 16; ++kt) {
+      const Op4 a = *(const Op4*)(lk + (16 * kt + l16) * L::RSTR + 4 * kap);
+      x[kt] = mfma16x16x16(a, qop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[kt][r] = fmaf(x[kt][r], TA_LOG2E, b2[r]);
+        tm = fmaxf(tm, x[kt][r]);
+      }
+    }
+    if (tm > TA_NEG_INF) {
+      const float mn = fmaxf(m, tm);
+      float s = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < SB_KT / 16; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s += __builtin_amdgcn_exp2f(x[kt][r] - mn);
+      l = l * __builtin_amdgcn_exp2f(m - mn) + s;
+      m = mn;
+    }
+  }
+  const float mq = quad_max(m);
+  const float lq = quad_sum(m > TA_NEG_INF ? l * __builtin_amdgcn_exp2f(m - mq) : 0.f);
+  const float lgl = __builtin_amdgcn_logf(lq);  // log2; the row has at least one key, so l >= 1
+  if (qok && kap == 0) {
+    const int64_t s = ((int64_t)b * SB_H + g) * p.Lq + qi;
+    p.mx[s] = mq;
+    p.ll[s] = lgl;
+    p.dd[s] = dsum;
+  }
+
+  // sweep 2: dq' = sum over keys of dS k'
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < ntiles; ++t) {
+    if (ntiles > 1) {
+      __syncthreads();
+      sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
+      __syncthreads();
+    }
+#pragma unroll 2
+    for (int kt = 0; kt < SB_KT / 16; ++kt) {
+      const Op4 a = *(const Op4*)(lk + (16 * kt + l16) * L::RSTR + 4 * kap);
+      const f32x4 s = mfma16x16x16(a, qop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const Op4 av = *(const Op4*)(lv + (16 * kt + l16) * L::RSTR + 4 * kap);
+      const f32x4 dp = mfma16x16x16(av, dop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
+      Op4 ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2[r]) - mq) - lgl);
+        ds[r] = from_f32<T>(pr * (dp[r] - dsum));
+      }
+      const Op4 at = *(const Op4*)(lkt + l16 * L::TSTR + 16 * kt + 4 * kap);
+      acc = mfma16x16x16(at, ds, acc);
+    }
+  }
+
+  // dq = rope_bwd(dq' scale), lane: dims 4 kap .. 4 kap + 3 of head g, query qi
+  f32x4 y;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
+  const int qc = qok ? qi : 0;
+  y = sb_rope_bwd(y, scr[wave], l16, kap, p.cq + (int64_t)qc * SB_E, p.sq + (int64_t)qc * SB_E, g, p);
+  if (qok) {
+    Op4 out;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[r] = from_f32<T>(y[r]);
+    *(Op4*)((T*)p.dq + b * p.dq_sb + (int64_t)qi * p.dq_sr + d0) = out;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// dk, dv
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt, T* ld, T* ldt, float* lmx,
+                                                float* lll, float* ldd, int b, int g, int q0) {
+  typedef SbTile<T> L;
+  typedef typename OpVec<T, 4>::type Op4;
+  const int tid = threadIdx.x;
+  for (int u = tid; u < SB_QT * 4; u += SB_NW * 64) {
+    const int row = u >> 2, d4 = (u & 3) * 4, qi = q0 + row;
+    Op4 qq, dd;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { qq[j] = from_f32<T>(0.f); dd[j] = from_f32<T>(0.f); }
+    if (qi < p.Lq) {
+      qq = sb_prep4<T>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SB_E,
+                       p.sq + (int64_t)qi * SB_E, g * SB_D + d4, p, p.scale);
+      dd = *(const Op4*)((const T*)p.dout + ((int64_t)b * p.Lq + qi) * SB_E + g * SB_D + d4);
+    }
+    *(Op4*)(lq + row * L::RSTR + d4) = qq;
+    *(Op4*)(ld + row * L::RSTR + d4) = dd;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lqt[(d4 + j) * L::TSTR + row] = qq[j];
+      ldt[(d4 + j) * L::TSTR + row] = dd[j];
+    }
+  }
+  for (int j = tid; j < SB_QT; j += SB_NW * 64) {
+    const int qi = q0 + j;
+    const int64_t s = ((int64_t)b * SB_H + g) * p.Lq + qi;
+    // queries past Lq: m = +inf gives P = 0
+    lmx[j] = qi < p.Lq ? p.mx[s] : __builtin_inff();
+    lll[j] = qi < p.Lq ? p.ll[s] : 0.f;
+    ldd[j] = qi < p.Lq ? p.dd[s] : 0.f;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
+  typedef SbTile<T> L;
+  typedef typename OpVec<T, 4>::type Op4;
+  __shared__ __attribute__((aligned(16))) T lq[SB_QT * L::RSTR];
+  __shared__ __attribute__((aligned(16))) T lqt[SB_D * L::TSTR];
+  __shared__ __attribute__((aligned(16))) T ld[SB_QT * L::RSTR];
+  __shared__ __attribute__((aligned(16))) T ldt[SB_D * L::TSTR];
+  __shared__ __attribute__((aligned(16))) float lmx[SB_QT];
+  __shared__ __attribute__((aligned(16))) float lll[SB_QT];
+  __shared__ __attribute__((aligned(16))) float ldd[SB_QT];
+  __shared__ float scr[SB_NW][16 * 17];
+
+  const int nkb = (p.Lk + SB_KB - 1) / SB_KB;
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int g = work % SB_H, kb = (work / SB_H) % nkb, b = work / (SB_H * nkb);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, kap = lane >> 4;
+  const int kj = kb * SB_KB + wave * 16 + l16;
+  const bool kok = kj < p.Lk;
+  const int d0 = g * SB_D + 4 * kap;
+
+  // k' and V operands of key kj (B operands of S = Q' K'^T and dP = dO V^T) and its b2
+  Op4 kop, vop;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { kop[j] = from_f32<T>(0.f); vop[j] = from_f32<T>(0.f); }
+  if (kok) {
+    kop = sb_prep4<T>((const T*)p.k + b * p.k_sb + (int64_t)kj * p.k_sr, p.ck + (int64_t)kj * SB_E,
+                      p.sk + (int64_t)kj * SB_E, d0, p, 1.f);
+    vop = *(const Op4*)((const T*)p.v + b * p.v_sb + (int64_t)kj * p.v_sr + d0);
+  }
+  const float b2 = sb_b2(p, b, kj);
+
+  f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
+  const int ntiles = (p.Lq + SB_QT - 1) / SB_QT;
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    sb_fill_queries<T>(p, lq, lqt, ld, ldt, lmx, lll, ldd, b, g, t * SB_QT);
+    __syncthreads();
+#pragma unroll 2
+    for (int qs = 0; qs < SB_QT / 16; ++qs) {
+      // S[query 16 qs + 4 kap + r][key kj], dP likewise
+      const Op4 aq = *(const Op4*)(lq + (16 * qs + l16) * L::RSTR + 4 * kap);
+      const f32x4 s = mfma16x16x16(aq, kop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const Op4 ad = *(const Op4*)(ld + (16 * qs + l16) * L::RSTR + 4 * kap);
+      const f32x4 dp = mfma16x16x16(ad, vop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 ms = *(const f32x4*)(lmx + 16 * qs + 4 * kap);
+      const f32x4 ls = *(const f32x4*)(lll + 16 * qs + 4 * kap);
+      const f32x4 dq = *(const f32x4*)(ldd + 16 * qs + 4 * kap);
+      Op4 pt, ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2) - ms[r]) - ls[r]);
+        pt[r] = from_f32<T>(pr);
+        ds[r] = from_f32<T>(pr * (dp[r] - dq[r]));
+      }
+      const Op4 adt = *(const Op4*)(ldt + l16 * L::TSTR + 16 * qs + 4 * kap);
+      dv = mfma16x16x16(adt, pt, dv);
+      const Op4 aqt = *(const Op4*)(lqt + l16 * L::TSTR + 16 * qs + 4 * kap);
+      dk = mfma16x16x16(aqt, ds, dk);
+    }
+  }
+
+  const int kc = kok ? kj : 0;
+  const f32x4 y = sb_rope_bwd(dk, scr[wave], l16, kap, p.ck + (int64_t)kc * SB_E, p.sk + (int64_t)kc * SB_E, g, p);
+  if (kok) {
+    Op4 ok, ov;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ok[r] = from_f32<T>(y[r]);
+      ov[r] = from_f32<T>(dv[r]);
+    }
+    *(Op4*)((T*)p.dk + b * p.dk_sb + (int64_t)kj * p.dk_sr + d0) = ok;
+    *(Op4*)((T*)p.dv + b * p.dv_sb + (int64_t)kj * p.dv_sr + d0) = ov;
+  }
+}
+
+template <typename T>
+void launch_bwd(const SbParams& p, hipStream_t stream) {
+  const int64_t nqb = (p.Lq + SB_QB - 1) / SB_QB, nkb = (p.Lk + SB_KB - 1) / SB_KB;
+  // no query (Lq = 0): only the dk/dv kernel runs, and writes zeros
+  if (nqb > 0)
+    hipLaunchKernelGGL((sb_dq_kernel<T>), dim3((unsigned)(p.B * nqb * SB_H)), dim3(SB_NW * 64), 0, stream, p);
+  hipLaunchKernelGGL((sb_dkdv_kernel<T>), dim3((unsigned)(p.B * nkb * SB_H)), dim3(SB_NW * 64), 0, stream, p);
+}
+
+}  // namespace
+
+int64_t tabicl_launch_smallhead_bwd_ws_bytes(int64_t B, int64_t Lq) {
+  const int64_t n = B * SB_H * Lq;
+  return 3 * ((n * 4 + 255) / 256 * 256);
+}
+
+int tabicl_launch_smallhead_bwd(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
+                                int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, const void* o,
+                                const void* dout, void* dq, int64_t dq_sb, int64_t dq_sr, void* dk,
+                                int64_t dk_sb, int64_t dk_sr, void* dv, int64_t dv_sb, int64_t dv_sr,
+                                const float* bias, int64_t bias_sb, const float* cq, const float* sq,
+                                const float* ck, const float* sk, int rope, int half, int rot, float scale,
+                                int64_t B, int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
+                                hipStream_t stream) {
+  if (ws_bytes < tabicl_launch_smallhead_bwd_ws_bytes(B, Lq)) return (int)hipErrorInvalidValue;
+  SbParams p;
+  p.q = q; p.q_sb = q_sb; p.q_sr = q_sr;
+  p.k = k; p.k_sb = k_sb; p.k_sr = k_sr;
+  p.v = v; p.v_sb = v_sb; p.v_sr = v_sr;
+  p.o = o; p.dout = dout;
+  p.dq = dq; p.dq_sb = dq_sb; p.dq_sr = dq_sr;
+  p.dk = dk; p.dk_sb = dk_sb; p.dk_sr = dk_sr;
+  p.dv = dv; p.dv_sb = dv_sb; p.dv_sr = dv_sr;
+  p.bias = bias; p.bias_sb = bias_sb;
+  p.cq = cq; p.sq = sq; p.ck = ck; p.sk = sk;
+  p.rope = rope; p.half = half; p.rot = rot;
+  p.scale = scale;
+  p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
+  const int64_t part = tabicl_launch_smallhead_bwd_ws_bytes(B, Lq) / 3;
+  p.mx = (float*)ws;
+  p.ll = (float*)((char*)ws + part);
+  p.dd = (float*)((char*)ws + 2 * part);
+  if (dtype == 0)
+    launch_bwd<bf16>(p, stream);
+  else
+    launch_bwd<float>(p, stream);
+  return (int)hipGetLastError();
+}

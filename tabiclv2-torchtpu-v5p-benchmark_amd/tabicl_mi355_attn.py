@@ -231,11 +231,143 @@ def _(q, kv, bias, cq, sq, ck, sk, h, lkp, bq, rope, half, rot, prec, scale):  #
     return q.new_empty(kv.shape[0], q.shape[1], q.shape[2])
 
 
+# ---------------------------------------------------------------------------------------------
+# backward ops and autograd (reference scripts/tabicl_tpu_pallas_attn.py:185-207, 618-671)
+# ---------------------------------------------------------------------------------------------
+_BWD_WS_BYTES: dict = {}
+
+
+def _bwd_workspace(B: int, Lq: int, E: int, h: int, device) -> Tensor:
+    """Scratch of one backward call (per-query softmax statistics and D), from torch's caching allocator."""
+    key = (B, Lq, E, h)
+    nbytes = _BWD_WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = int(_nat.load().tabicl_smallhead_bwd_workspace_bytes(B, Lq, E, h))
+        if nbytes < 0:
+            _nat.check(1, "tabicl_smallhead_bwd_workspace_bytes")
+        _BWD_WS_BYTES[key] = nbytes
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+@torch.library.custom_op("tabicl_pk::hx_bwd", mutates_args=())
+def _hx_bwd(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, o: Tensor, do: Tensor, h: int, lkp: int, bq: int,
+            prec: int) -> tuple[Tensor, Tensor, Tensor]:
+    _nat.require_device(q, k, v, bias, o, do)
+    _contig(q, k, v, bias, o, do)
+    B, Lq, E = q.shape
+    Lk = k.shape[1]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = _bwd_workspace(B, Lq, E, h, q.device)
+    _nat.call("tabicl_hx_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), bias.shape[0],
+              o.data_ptr(), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Lq, Lk, E, h,
+              _nat.dtype_code(q.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(q))
+    return dq, dk, dv
+
+
+@_hx_bwd.register_fake
+def _(q, k, v, bias, o, do, h, lkp, bq, prec):  # noqa: ANN001
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _hx_setup(ctx, inputs, output):  # noqa: ANN001
+    q, k, v, bias, h, lkp, bq, prec = inputs
+    ctx.save_for_backward(q, k, v, bias, output)
+    ctx.cfg = (h, lkp, bq, prec)
+
+
+def _hx_backward(ctx, do):  # noqa: ANN001
+    q, k, v, bias, o = ctx.saved_tensors
+    dq, dk, dv = torch.ops.tabicl_pk.hx_bwd(q, k, v, bias, o, do.to(o.dtype).contiguous(), *ctx.cfg)
+    return dq, dk, dv, None, None, None, None, None
+
+
+_hx_fwd.register_autograd(_hx_backward, setup_context=_hx_setup)
+
+
+@torch.library.custom_op("tabicl_pk::pk_self_bwd", mutates_args=())
+def _pk_self_bwd(qkv: Tensor, bias: Tensor, cos: Tensor, sin: Tensor, o: Tensor, do: Tensor, h: int, lkp: int,
+                 rope: int, half: int, rot: int, prec: int, scale: float) -> Tensor:
+    _nat.require_device(qkv, bias, cos, sin, o, do)
+    _contig(qkv, bias, cos, sin, o, do)
+    B, L, E3 = qkv.shape
+    E = E3 // 3
+    dqkv = torch.empty_like(qkv)
+    ws = _bwd_workspace(B, L, E, h, qkv.device)
+    _nat.call("tabicl_pk_self_bwd", qkv.data_ptr(), bias.data_ptr(), bias.shape[0], cos.data_ptr(),
+              sin.data_ptr(), o.data_ptr(), do.data_ptr(), dqkv.data_ptr(), B, L, E, h, rope, half, rot,
+              float(scale), _nat.dtype_code(qkv.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(qkv))
+    return dqkv
+
+
+@_pk_self_bwd.register_fake
+def _(qkv, bias, cos, sin, o, do, h, lkp, rope, half, rot, prec, scale):  # noqa: ANN001
+    return torch.empty_like(qkv)
+
+
+def _pk_self_setup(ctx, inputs, output):  # noqa: ANN001
+    qkv, bias, cos, sin, *cfg = inputs
+    ctx.save_for_backward(qkv, bias, cos, sin, output)
+    ctx.cfg = tuple(cfg)
+
+
+def _pk_self_backward(ctx, do):  # noqa: ANN001
+    qkv, bias, cos, sin, o = ctx.saved_tensors
+    dqkv = torch.ops.tabicl_pk.pk_self_bwd(qkv, bias, cos, sin, o, do.to(o.dtype).contiguous(), *ctx.cfg)
+    return (dqkv,) + (None,) * (3 + len(ctx.cfg))
+
+
+_pk_self_fwd.register_autograd(_pk_self_backward, setup_context=_pk_self_setup)
+
+
+@torch.library.custom_op("tabicl_pk::pk_cross_bwd", mutates_args=())
+def _pk_cross_bwd(q: Tensor, kv: Tensor, bias: Tensor, cq: Tensor, sq: Tensor, ck: Tensor, sk: Tensor, o: Tensor,
+                  do: Tensor, h: int, lkp: int, bq: int, rope: int, half: int, rot: int, prec: int,
+                  scale: float) -> tuple[Tensor, Tensor]:
+    _nat.require_device(q, kv, bias, cq, sq, ck, sk, o, do)
+    _contig(q, kv, bias, cq, sq, ck, sk, o, do)
+    Bq, Lq, E = q.shape
+    B, Lk, _ = kv.shape
+    dq = torch.empty(B, Lq, E, device=q.device, dtype=q.dtype)
+    dkv = torch.empty_like(kv)
+    ws = _bwd_workspace(B, Lq, E, h, q.device)
+    _nat.call("tabicl_pk_cross_bwd", q.data_ptr(), Bq, kv.data_ptr(), bias.data_ptr(), bias.shape[0],
+              cq.data_ptr(), sq.data_ptr(), ck.data_ptr(), sk.data_ptr(), o.data_ptr(), do.data_ptr(),
+              dq.data_ptr(), dkv.data_ptr(), B, Lq, Lk, E, h, rope, half, rot, float(scale),
+              _nat.dtype_code(q.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(q))
+    if Bq != B:  # one query set broadcast over the batch: its gradient is the sum over the batch
+        dq = dq.float().sum(dim=0, keepdim=True).to(q.dtype)
+    return dq, dkv
+
+
+@_pk_cross_bwd.register_fake
+def _(q, kv, bias, cq, sq, ck, sk, o, do, h, lkp, bq, rope, half, rot, prec, scale):  # noqa: ANN001
+    return torch.empty_like(q), torch.empty_like(kv)
+
+
+def _pk_cross_setup(ctx, inputs, output):  # noqa: ANN001
+    q, kv, bias, cq, sq, ck, sk, *cfg = inputs
+    ctx.save_for_backward(q, kv, bias, cq, sq, ck, sk, output)
+    ctx.cfg = tuple(cfg)
+
+
+def _pk_cross_backward(ctx, do):  # noqa: ANN001
+    q, kv, bias, cq, sq, ck, sk, o = ctx.saved_tensors
+    dq, dkv = torch.ops.tabicl_pk.pk_cross_bwd(q, kv, bias, cq, sq, ck, sk, o, do.to(o.dtype).contiguous(),
+                                               *ctx.cfg)
+    return (dq, dkv) + (None,) * (5 + len(ctx.cfg))
+
+
+_pk_cross_fwd.register_autograd(_pk_cross_backward, setup_context=_pk_cross_setup)
+
+
 HX_FWD = torch.ops.tabicl_pk.hx_fwd
 HXQ_FWD = torch.ops.tabicl_pk.hxq_fwd
 PK_SELF = torch.ops.tabicl_pk.pk_self_fwd
 PK_CROSS = torch.ops.tabicl_pk.pk_cross_fwd
 HXF_FWD = None
+HX_BWD = torch.ops.tabicl_pk.hx_bwd
+PK_SELF_BWD = torch.ops.tabicl_pk.pk_self_bwd
+PK_CROSS_BWD = torch.ops.tabicl_pk.pk_cross_bwd
 
 
 # ---------------------------------------------------------------------------------------------

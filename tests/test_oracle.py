@@ -195,3 +195,132 @@ def test_combined_mask_forms():
     assert O.combined_mask_ref(np.zeros((3, 5), bool), None, (2,), 8, 3, 5) is False
     assert O.combined_mask_ref(np.zeros((4, 5), np.float32), None, (2,), 8, 3, 5) is False
     assert O.combined_mask_ref(None, None, (2,), 8, 3, 5) is None
+
+
+# --- backward restatements -------------------------------------------------------------------
+
+def _attn_torch(q, k, v, h, bias=None):
+    """The forward definition in float64 torch (autograd gives the gradients the restatement must
+    match): per-head softmax(q k^T + bias) v, merged layout."""
+    B, Lq, Em = q.shape
+    d = Em // h
+    qh = q.reshape(B, Lq, h, d).transpose(1, 2)
+    kh = k.reshape(k.shape[0], -1, h, d).transpose(1, 2)
+    vh = v.reshape(v.shape[0], -1, h, d).transpose(1, 2)
+    s = qh @ kh.transpose(-1, -2)
+    if bias is not None:
+        s = s + bias.reshape(bias.shape[0], 1, 1, -1)
+    return (torch.softmax(s, dim=-1) @ vh).transpose(1, 2).reshape(B, Lq, Em)
+
+
+def _rot_matrix(h, code, half, rot):
+    """R as an explicit [E, E] matrix (R(x) = x @ M^T), built column by column from unit vectors."""
+    eye = np.eye(E)
+    return O.rotate_merged(eye, h, code, half, rot).T
+
+
+def _rope_torch(x, cos, sin, M):
+    return x * cos + (x @ M.T) * sin
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_attention_bwd_matches_autograd(with_bias):
+    rng = np.random.default_rng(20)
+    q, k, v = _rand(rng, 2, 6, E, scale=0.25), _rand(rng, 2, 9, E), _rand(rng, 2, 9, E)
+    do = _rand(rng, 2, 6, E)
+    bias = None
+    if with_bias:
+        bias = _rand(rng, 2, 9)
+        bias[:, -2:] = -1e30  # masked keys get zero gradient
+    dq, dk, dv = O.attention_bwd_f64(q, k, v, H, do, bias)
+    qt, kt, vt = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    out = _attn_torch(qt, kt, vt, H, None if bias is None else torch.tensor(bias))
+    out.backward(torch.tensor(do))
+    np.testing.assert_allclose(dq, qt.grad.numpy(), rtol=0, atol=1e-12)
+    np.testing.assert_allclose(dk, kt.grad.numpy(), rtol=0, atol=1e-12)
+    np.testing.assert_allclose(dv, vt.grad.numpy(), rtol=0, atol=1e-12)
+    if with_bias:
+        assert np.abs(dk[:, -2:]).max() == 0 and np.abs(dv[:, -2:]).max() == 0
+
+
+def test_attention_bwd_finite_differences():
+    # central differences of <dO, O> on a tiny case (one head of width 16 so that d = 16 holds)
+    rng = np.random.default_rng(21)
+    q, k, v = _rand(rng, 1, 2, 16, scale=0.5), _rand(rng, 1, 3, 16), _rand(rng, 1, 3, 16)
+    do = _rand(rng, 1, 2, 16)
+    dq, dk, dv = O.attention_bwd_f64(q, k, v, 1, do)
+    f = lambda q_, k_, v_: float((O.attention_loops(q_, k_, v_, 1) * do).sum())  # noqa: E731
+    eps = 1e-6
+    for grad, which in ((dq, 0), (dk, 1), (dv, 2)):
+        for idx in [(0, 0, 0), (0, 1, 5), (0, 0, 15)]:
+            args = [q.copy(), k.copy(), v.copy()]
+            args[which][idx] += eps
+            up = f(*args)
+            args[which][idx] -= 2 * eps
+            dn = f(*args)
+            assert abs((up - dn) / (2 * eps) - grad[idx]) < 1e-6
+
+
+def test_bwd_uses_given_forward_output_for_d():
+    # D comes from the stored output: a perturbed O shifts dq/dk by dS changes, dv not at all
+    rng = np.random.default_rng(22)
+    q, k, v = _rand(rng, 1, 4, E, scale=0.25), _rand(rng, 1, 5, E), _rand(rng, 1, 5, E)
+    do = _rand(rng, 1, 4, E)
+    o = O.attention_f64(q, k, v, H)
+    a = O.attention_bwd_f64(q, k, v, H, do, o=o)
+    b = O.attention_bwd_f64(q, k, v, H, do, o=o + 0.01)
+    np.testing.assert_allclose(a[2], b[2], rtol=0, atol=0)
+    assert np.abs(a[0] - b[0]).max() > 1e-6
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_bwd_is_transpose_of_rope(interleaved):
+    rng = np.random.default_rng(23)
+    L = 7
+    cos, sin, code, half, rot = O.rope_tables_ref(O.textbook_freqs(16, 1e4), L, E, H, interleaved)
+    y = _rand(rng, L, E)
+    x = torch.tensor(_rand(rng, L, E), requires_grad=True)
+    M = torch.tensor(_rot_matrix(H, code, half, rot))
+    _rope_torch(x, torch.tensor(cos), torch.tensor(sin), M).backward(torch.tensor(y))
+    np.testing.assert_allclose(O.rope_bwd_ref(y, cos, sin, H, code, half, rot), x.grad.numpy(), rtol=0,
+                               atol=1e-12)
+
+
+def test_pk_self_bwd_matches_autograd():
+    rng = np.random.default_rng(24)
+    B, L, scale = 2, 6, 0.25
+    rope = O.rope_tables_ref(O.textbook_freqs(16, 1e4), L, E, H, False)
+    cos, sin, code, half, rot = rope
+    x = _rand(rng, B, L, 3 * E)
+    do = _rand(rng, B, L, E)
+    bias = _rand(rng, 1, L)
+    got = O.pk_self_bwd_ref(x, H, bias, rope, scale, do)
+    xt = torch.tensor(x, requires_grad=True)
+    M = torch.tensor(_rot_matrix(H, code, half, rot))
+    c, s_ = torch.tensor(cos), torch.tensor(sin)
+    q, k, v = xt[..., :E], xt[..., E:2 * E], xt[..., 2 * E:]
+    out = _attn_torch(_rope_torch(q, c, s_, M) * scale, _rope_torch(k, c, s_, M), v, H, torch.tensor(bias))
+    out.backward(torch.tensor(do))
+    np.testing.assert_allclose(got, xt.grad.numpy(), rtol=0, atol=1e-11)
+
+
+@pytest.mark.parametrize("shared_q", [False, True])
+def test_pk_cross_bwd_matches_autograd(shared_q):
+    rng = np.random.default_rng(25)
+    B, Lq, Lk, scale = 3, 4, 6, 0.25
+    rq = O.rope_tables_ref(O.textbook_freqs(16, 1e4), Lq, E, H, True)
+    rk = O.rope_tables_ref(O.textbook_freqs(16, 1e4), Lk, E, H, True)
+    q = _rand(rng, 1 if shared_q else B, Lq, E)
+    kv = _rand(rng, B, Lk, 2 * E)
+    do = _rand(rng, B, Lq, E)
+    dq, dkv = O.pk_cross_bwd_ref(q, kv, H, None, rq, rk, scale, do)
+    qt = torch.tensor(q, requires_grad=True)
+    kvt = torch.tensor(kv, requires_grad=True)
+    M = torch.tensor(_rot_matrix(H, *rq[2:]))
+    qr = _rope_torch(qt, torch.tensor(rq[0]), torch.tensor(rq[1]), M)
+    kr = _rope_torch(kvt[..., :E], torch.tensor(rk[0]), torch.tensor(rk[1]), M)
+    out = _attn_torch(qr.expand(B, Lq, E) * scale, kr, kvt[..., E:], H)
+    out.backward(torch.tensor(do))
+    assert dq.shape == q.shape
+    np.testing.assert_allclose(dq, qt.grad.numpy(), rtol=0, atol=1e-11)
+    np.testing.assert_allclose(dkv, kvt.grad.numpy(), rtol=0, atol=1e-11)
