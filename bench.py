@@ -170,6 +170,74 @@ def bench_smallhead(configs: set, steps: int, warmup: int) -> list:
     return recs
 
 
+# The reference's training-block benchmark (scripts/tests/test_pallas_attn.py:80-109, 252-285):
+# loss = out.float().square().mean(), forward + backward per step, bf16. Published fwd+bwd ms on one
+# TPU v5p (APPENDIX.md:21-23): the vs_baseline divisor where one exists.
+TRAIN_SHAPES = (
+    ("column ISAB-2 (hx, 416 x 1024 q over 128 keys)", "hx", 416, 1024, 128, 3.72),
+    ("column ISAB-1 (hx, 416 x 128 q over 576 keys)", "hx", 416, 128, 576, 2.69),
+    ("row interaction (pk_self, RoPE, 4096 x 104 tokens)", "pk_self", 4096, 104, 104, 4.91),
+    ("row interaction (hx, 4096 x 104 tokens)", "hx", 4096, 104, 104, None),
+    ("CLS (hx, 4096 x 4 q over 104 keys)", "hx", 4096, 4, 104, None),
+)
+
+
+def bench_train(steps: int, warmup: int) -> list:
+    """fwd+bwd step of the small-head ops on the reference's training shapes. Algorithmic FLOPs:
+    the forward's 4 Lq Lk d per (sequence, head) times 3.5 (backward = 2.5 forwards: dP, dq, dk, dv
+    and the score recompute)."""
+    import torch
+
+    import tabicl_mi355_attn as pk
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    E, H = 128, 8
+    recs = []
+
+    class _Rope:
+        interleaved = False
+        freqs = 100000.0 ** (-torch.arange(0, 16, 2, dtype=torch.float32) / 16)
+
+        def get_seq_pos(self, n, device=None, dtype=torch.float32):
+            return torch.arange(n, device=device, dtype=dtype)
+
+    for i, (name, op, B, Lq, Lk, published) in enumerate(TRAIN_SHAPES):
+        g.manual_seed(10 + i)
+        if op == "hx":
+            q = (torch.randn(B, Lq, E, generator=g, device=dev) * 0.25).to(torch.bfloat16).requires_grad_(True)
+            k = torch.randn(B, Lk, E, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+            v = torch.randn(B, Lk, E, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+            leaves = (q, k, v)
+
+            def fwd():
+                return pk.hx_attention(q, k, v, H)
+        else:
+            x = torch.randn(B, Lq, 3 * E, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+            leaves = (x,)
+            rope = _Rope()
+
+            def fwd():
+                return pk.pk_self_attention(x, H, None, rope, 16 ** -0.5)
+
+        def step():
+            for t in leaves:
+                t.grad = None
+            fwd().float().square().mean().backward()
+
+        ms = _time(step, steps, warmup)
+        tf = 3.5 * 4.0 * Lq * Lk * 16 * H * B / (ms * 1e-3) / 1e12
+        recs.append({"metric": f"ms per fwd+bwd {name} step", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+                     "steps": steps, "warmup": warmup, "higher_is_better": False,
+                     "vs_baseline": None if published is None else round(ms / published, 4),
+                     "dtype": "bf16", "data": "synthetic N(0,1), q x 0.25", "config": {
+                         "workload": f"{B} x {Lq} q over {Lk} keys, 8x16, loss = out.float().square().mean()"},
+                     "attn_tflops": round(tf, 2),
+                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
+    return recs
+
+
 C5_BUCKETS = (1024, 2048, 4096, 8192, 16384)
 
 
@@ -282,8 +350,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5 (comma-separated) or all print "
-                         "the other BASELINE configs' lines")
+                    help="c4 (default) is the headline line; c1, c2, c3, c5, train (comma-separated) or all "
+                         "print the other BASELINE configs' lines and the fwd+bwd training lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -293,13 +361,15 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
         recs = bench_smallhead(configs, args.steps, args.warmup)
         if configs & {"c5", "all"}:
             recs += bench_c5(args.steps, args.warmup)
+        if configs & {"train", "all"}:
+            recs += bench_train(args.steps, args.warmup)
         for rec in recs:
             print(json.dumps(rec), flush=True)
         return 0
