@@ -10,9 +10,11 @@
 //   dq = rope_bwd(dq' scale), dk = rope_bwd(dk'),  rope_bwd(y) = y cos - R(y sin)
 // The reference keeps all keys of a batch element on chip (at most 1024). Here keys and queries are
 // tiled, so any length works:
-//   sb_dq_kernel   workgroup = (batch element, 128 queries, head); wave = 16 queries. Sweep 1 over
-//                  the key tiles: per-query softmax statistics (row maximum and log2 of the sum, in
-//                  log2 units) and D, written to the workspace; sweep 2: P, dP, dS and dq'.
+//   sb_dq_kernel   workgroup = (batch element, run of 128-query blocks, head); wave = 16 queries.
+//                  Per block: per-query softmax statistics (row maximum and log2 of the sum, in log2
+//                  units) and D, written to the workspace, then P, dP, dS and dq'. Keys in one tile
+//                  (<= 128): one fill per run and one pass per block with the scores in registers;
+//                  longer: two sweeps over the key tiles.
 //   sb_dkdv_kernel workgroup = (batch element, 128 keys, head); wave = 16 keys. Walks the query
 //                  tiles with the workspace's statistics and D: P, dP, dS, dk' and dv.
 // No atomics, no cross-workgroup reduction: each gradient element is written once.
@@ -56,6 +58,7 @@ struct SbParams {
   int rope, half, rot;
   float scale;
   int B, Lq, Lk;
+  int qbpw;  // query blocks per dq workgroup
   // per (batch, head, query), [B][H][Lq] each: the row maximum m of the log2-domain scores and
   // log2 of the sum of exp2(x - m) (kept apart: with every key at the bias floor, m + log2(l)
   // would round back to m), and D
@@ -67,7 +70,8 @@ struct SbParams {
 template <typename T> struct SbTile {
   static constexpr int PAD = 16 / sizeof(T);
   static constexpr int RSTR = SB_D + PAD;   // row-major tile: 16 dims per row
-  static constexpr int TSTR = 128 + PAD;    // transposed tile: 128 rows (keys or queries) per dim
+  static constexpr int TSTR = 128 + PAD;    // transposed copy (fp32 only): 128 rows per dim
+  static constexpr int T_ELEMS = sizeof(T) == 2 ? 4 : SB_D * TSTR;
 };
 
 // Per-key additive term in log2 units (reference: bias added to the fp32 scores; -1e30 stays
@@ -118,8 +122,25 @@ __device__ __forceinline__ f32x4 sb_rope_bwd(f32x4 y, float* scr, int l16, int k
   return out;
 }
 
+// Transposed operand of a 16x16x16 product, A[i][4 kap + j] = tile[row0 + 4 kap + j][i] for lane
+// (i = l16, kap). bf16: straight from the row-major tile with ds_read_b64_tr_b16 (lane 4j + c of a
+// 16-lane group points at row 4 kap + j, columns 4c..4c+3, and receives column l16 of those four
+// rows); fp32: from the transposed copy the fill wrote.
+template <typename T>
+__device__ __forceinline__ typename OpVec<T, 4>::type sb_opT(const T* rows, const T* tcopy, int row0, int l16,
+                                                            int kap) {
+  typedef SbTile<T> L;
+  if constexpr (sizeof(T) == 2) {
+    const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(rows + (row0 + 4 * kap + (l16 >> 2)) * L::RSTR + 4 * (l16 & 3)));
+    return __builtin_bit_cast(bf16x4, t);
+  } else {
+    return *(const f32x4*)(tcopy + l16 * L::TSTR + row0 + 4 * kap);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
-// dq (and the per-query log-sum-exp and D)
+// dq (and the per-query softmax statistics and D)
 // ---------------------------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void sb_fill_keys(const SbParams& p, T* lk, T* lkt, T* lv, float* lb2, int b, int g,
@@ -142,126 +163,177 @@ __device__ __forceinline__ void sb_fill_keys(const SbParams& p, T* lk, T* lkt, T
     }
     *(Op4*)(lk + row * L::RSTR + d4) = kk;
     *(Op4*)(lv + row * L::RSTR + d4) = vv;
+    if constexpr (sizeof(T) == 4) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) lkt[(d4 + j) * L::TSTR + row] = kk[j];
+      for (int j = 0; j < 4; ++j) lkt[(d4 + j) * L::TSTR + row] = kk[j];
+    }
   }
   for (int j = tid; j < SB_KT; j += SB_NW * 64) lb2[j] = sb_b2(p, b, k0 + j);
 }
 
+// Scores of the key tile for this lane's query, log2 units: x[kt][r] for key 16 kt + 4 kap + r.
 template <typename T>
-__global__ __launch_bounds__(SB_NW * 64) void sb_dq_kernel(SbParams p) {
+__device__ __forceinline__ void sb_scores(const T* lk, const float* lb2, typename OpVec<T, 4>::type qop, int l16,
+                                          int kap, f32x4 (&x)[SB_KT / 16]) {
   typedef SbTile<T> L;
   typedef typename OpVec<T, 4>::type Op4;
+#pragma unroll
+  for (int kt = 0; kt < SB_KT / 16; ++kt) {
+    const Op4 a = *(const Op4*)(lk + (16 * kt + l16) * L::RSTR + 4 * kap);
+    x[kt] = mfma16x16x16(a, qop, f32x4{0.f, 0.f, 0.f, 0.f});
+    const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[kt][r] = fmaf(x[kt][r], TA_LOG2E, b2[r]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// dq' += dS k' over the key tile, P = exp2((x - m) - log2 l).
+template <typename T>
+__device__ __forceinline__ void sb_dq_tile(const T* lk, const T* lkt, const T* lv, const f32x4 (&x)[SB_KT / 16],
+                                           typename OpVec<T, 4>::type dop, float mq, float lgl, float dsum, int l16,
+                                           int kap, f32x4& acc) {
+  typedef SbTile<T> L;
+  typedef typename OpVec<T, 4>::type Op4;
+#pragma unroll
+  for (int kt = 0; kt < SB_KT / 16; ++kt) {
+    const Op4 av = *(const Op4*)(lv + (16 * kt + l16) * L::RSTR + 4 * kap);
+    const f32x4 dp = mfma16x16x16(av, dop, f32x4{0.f, 0.f, 0.f, 0.f});
+    Op4 ds;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = __builtin_amdgcn_exp2f((x[kt][r] - mq) - lgl);
+      ds[r] = from_f32<T>(pr * (dp[r] - dsum));
+    }
+    acc = mfma16x16x16(sb_opT<T>(lk, lkt, 16 * kt, l16, kap), ds, acc);
+    // one key block at a time: hoisting every block's dP first costs registers
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ONE_TILE: all keys fit one tile (Lk <= SB_KT).
+template <typename T, bool ONE_TILE>
+__global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
+  typedef SbTile<T> L;
+  typedef typename OpVec<T, 4>::type Op4;
+  constexpr int NKT = SB_KT / 16;
   __shared__ __attribute__((aligned(16))) T lk[SB_KT * L::RSTR];
-  __shared__ __attribute__((aligned(16))) T lkt[SB_D * L::TSTR];
+  __shared__ __attribute__((aligned(16))) T lkt[L::T_ELEMS];
   __shared__ __attribute__((aligned(16))) T lv[SB_KT * L::RSTR];
   __shared__ __attribute__((aligned(16))) float lb2[SB_KT];
   __shared__ float scr[SB_NW][16 * 17];
 
   const int nqb = (p.Lq + SB_QB - 1) / SB_QB;
+  const int nwg_q = (nqb + p.qbpw - 1) / p.qbpw;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int g = work % SB_H, qb = (work / SB_H) % nqb, b = work / (SB_H * nqb);
+  const int g = work % SB_H, qw = (work / SB_H) % nwg_q, b = work / (SB_H * nwg_q);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, kap = lane >> 4;
-  const int qi = qb * SB_QB + wave * 16 + l16;
-  const bool qok = qi < p.Lq;
   const int d0 = g * SB_D + 4 * kap;
-
-  // q' and dO operands of query qi (B operands of S^T = K' Q'^T and dP^T = V dO^T), D
-  Op4 qop, dop;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) { qop[j] = from_f32<T>(0.f); dop[j] = from_f32<T>(0.f); }
-  float dsum = 0.f;
-  if (qok) {
-    qop = sb_prep4<T>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SB_E,
-                      p.sq + (int64_t)qi * SB_E, d0, p, p.scale);
-    const int64_t orow = ((int64_t)b * p.Lq + qi) * SB_E + d0;
-    dop = *(const Op4*)((const T*)p.dout + orow);
-    const Op4 ov = *(const Op4*)((const T*)p.o + orow);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dsum += to_f32<T>(dop[j]) * to_f32<T>(ov[j]);
-  }
-  dsum = xor_sum(dsum, 16);
-  dsum = xor_sum(dsum, 32);
-
   const int ntiles = (p.Lk + SB_KT - 1) / SB_KT;
-  // sweep 1: log-sum-exp over this lane's keys (4 per 16-key block), merged over the lane quad
-  float m = TA_NEG_INF, l = 0.f;
-  for (int t = 0; t < ntiles; ++t) {
+  if (ONE_TILE) {  // fill once for every query block of the run
+    sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, 0);
     __syncthreads();
-    sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
-    __syncthreads();
-    f32x4 x[SB_KT / 16];
-    float tm = TA_NEG_INF;
-#pragma unroll
-    for (int kt = 0; kt < SB_KT / 16; ++kt) {
-      const Op4 a = *(const Op4*)(lk + (16 * kt + l16) * L::RSTR + 4 * kap);
-      x[kt] = mfma16x16x16(a, qop, f32x4{0.f, 0.f, 0.f, 0.f});
-      const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[kt][r] = fmaf(x[kt][r], TA_LOG2E, b2[r]);
-        tm = fmaxf(tm, x[kt][r]);
-      }
-    }
-    if (tm > TA_NEG_INF) {
-      const float mn = fmaxf(m, tm);
-      float s = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < SB_KT / 16; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s += __builtin_amdgcn_exp2f(x[kt][r] - mn);
-      l = l * __builtin_amdgcn_exp2f(m - mn) + s;
-      m = mn;
-    }
-  }
-  const float mq = quad_max(m);
-  const float lq = quad_sum(m > TA_NEG_INF ? l * __builtin_amdgcn_exp2f(m - mq) : 0.f);
-  const float lgl = __builtin_amdgcn_logf(lq);  // log2; the row has at least one key, so l >= 1
-  if (qok && kap == 0) {
-    const int64_t s = ((int64_t)b * SB_H + g) * p.Lq + qi;
-    p.mx[s] = mq;
-    p.ll[s] = lgl;
-    p.dd[s] = dsum;
   }
 
-  // sweep 2: dq' = sum over keys of dS k'
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int t = 0; t < ntiles; ++t) {
-    if (ntiles > 1) {
-      __syncthreads();
-      sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
-      __syncthreads();
-    }
-#pragma unroll 2
-    for (int kt = 0; kt < SB_KT / 16; ++kt) {
-      const Op4 a = *(const Op4*)(lk + (16 * kt + l16) * L::RSTR + 4 * kap);
-      const f32x4 s = mfma16x16x16(a, qop, f32x4{0.f, 0.f, 0.f, 0.f});
-      const Op4 av = *(const Op4*)(lv + (16 * kt + l16) * L::RSTR + 4 * kap);
-      const f32x4 dp = mfma16x16x16(av, dop, f32x4{0.f, 0.f, 0.f, 0.f});
-      const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
-      Op4 ds;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2[r]) - mq) - lgl);
-        ds[r] = from_f32<T>(pr * (dp[r] - dsum));
-      }
-      const Op4 at = *(const Op4*)(lkt + l16 * L::TSTR + 16 * kt + 4 * kap);
-      acc = mfma16x16x16(at, ds, acc);
-    }
-  }
+  for (int qbi = 0; qbi < p.qbpw; ++qbi) {
+    const int qb = qw * p.qbpw + qbi;
+    if (qb >= nqb) break;  // uniform over the workgroup
+    const int qi = qb * SB_QB + wave * 16 + l16;
+    const bool qok = qi < p.Lq;
 
-  // dq = rope_bwd(dq' scale), lane: dims 4 kap .. 4 kap + 3 of head g, query qi
-  f32x4 y;
+    // q' and dO operands of query qi (B operands of S^T = K' Q'^T and dP^T = V dO^T), D
+    Op4 qop, dop;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
-  const int qc = qok ? qi : 0;
-  y = sb_rope_bwd(y, scr[wave], l16, kap, p.cq + (int64_t)qc * SB_E, p.sq + (int64_t)qc * SB_E, g, p);
-  if (qok) {
-    Op4 out;
+    for (int j = 0; j < 4; ++j) { qop[j] = from_f32<T>(0.f); dop[j] = from_f32<T>(0.f); }
+    float dsum = 0.f;
+    if (qok) {
+      qop = sb_prep4<T>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SB_E,
+                        p.sq + (int64_t)qi * SB_E, d0, p, p.scale);
+      const int64_t orow = ((int64_t)b * p.Lq + qi) * SB_E + d0;
+      dop = *(const Op4*)((const T*)p.dout + orow);
+      const Op4 ov = *(const Op4*)((const T*)p.o + orow);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[r] = from_f32<T>(y[r]);
-    *(Op4*)((T*)p.dq + b * p.dq_sb + (int64_t)qi * p.dq_sr + d0) = out;
+      for (int j = 0; j < 4; ++j) dsum += to_f32<T>(dop[j]) * to_f32<T>(ov[j]);
+    }
+    dsum = xor_sum(dsum, 16);
+    dsum = xor_sum(dsum, 32);
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float mq, lgl;
+    if (ONE_TILE) {
+      // one pass: the scores stay in registers between the statistics and dq'
+      f32x4 x[NKT];
+      sb_scores<T>(lk, lb2, qop, l16, kap, x);
+      float tm = TA_NEG_INF;
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tm = fmaxf(tm, x[kt][r]);
+      mq = quad_max(tm);  // finite: the tile holds at least one key
+      float l = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) l += __builtin_amdgcn_exp2f(x[kt][r] - mq);
+      lgl = __builtin_amdgcn_logf(quad_sum(l));  // log2; >= 0
+      sb_dq_tile<T>(lk, lkt, lv, x, dop, mq, lgl, dsum, l16, kap, acc);
+    } else {
+      // sweep 1: statistics over this lane's keys (4 per 16-key block), merged over the lane quad
+      float m = TA_NEG_INF, l = 0.f;
+      for (int t = 0; t < ntiles; ++t) {
+        __syncthreads();
+        sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
+        __syncthreads();
+        f32x4 x[NKT];
+        sb_scores<T>(lk, lb2, qop, l16, kap, x);
+        float tm = TA_NEG_INF;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tm = fmaxf(tm, x[kt][r]);
+        if (tm > TA_NEG_INF) {
+          const float mn = fmaxf(m, tm);
+          float s = 0.f;
+#pragma unroll
+          for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s += __builtin_amdgcn_exp2f(x[kt][r] - mn);
+          l = l * __builtin_amdgcn_exp2f(m - mn) + s;
+          m = mn;
+        }
+      }
+      mq = quad_max(m);
+      lgl = __builtin_amdgcn_logf(quad_sum(m > TA_NEG_INF ? l * __builtin_amdgcn_exp2f(m - mq) : 0.f));
+      // sweep 2: dq'
+      for (int t = 0; t < ntiles; ++t) {
+        __syncthreads();
+        sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
+        __syncthreads();
+        f32x4 x[NKT];
+        sb_scores<T>(lk, lb2, qop, l16, kap, x);
+        sb_dq_tile<T>(lk, lkt, lv, x, dop, mq, lgl, dsum, l16, kap, acc);
+      }
+    }
+    if (qok && kap == 0) {
+      const int64_t s = ((int64_t)b * SB_H + g) * p.Lq + qi;
+      p.mx[s] = mq;
+      p.ll[s] = lgl;
+      p.dd[s] = dsum;
+    }
+
+    // dq = rope_bwd(dq' scale), lane: dims 4 kap .. 4 kap + 3 of head g, query qi
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
+    const int qc = qok ? qi : 0;
+    y = sb_rope_bwd(y, scr[wave], l16, kap, p.cq + (int64_t)qc * SB_E, p.sq + (int64_t)qc * SB_E, g, p);
+    if (qok) {
+      Op4 out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[r] = from_f32<T>(y[r]);
+      *(Op4*)((T*)p.dq + b * p.dq_sb + (int64_t)qi * p.dq_sr + d0) = out;
+    }
   }
 }
 
@@ -286,10 +358,12 @@ __device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt
     }
     *(Op4*)(lq + row * L::RSTR + d4) = qq;
     *(Op4*)(ld + row * L::RSTR + d4) = dd;
+    if constexpr (sizeof(T) == 4) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lqt[(d4 + j) * L::TSTR + row] = qq[j];
-      ldt[(d4 + j) * L::TSTR + row] = dd[j];
+      for (int j = 0; j < 4; ++j) {
+        lqt[(d4 + j) * L::TSTR + row] = qq[j];
+        ldt[(d4 + j) * L::TSTR + row] = dd[j];
+      }
     }
   }
   for (int j = tid; j < SB_QT; j += SB_NW * 64) {
@@ -307,9 +381,9 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
   typedef SbTile<T> L;
   typedef typename OpVec<T, 4>::type Op4;
   __shared__ __attribute__((aligned(16))) T lq[SB_QT * L::RSTR];
-  __shared__ __attribute__((aligned(16))) T lqt[SB_D * L::TSTR];
+  __shared__ __attribute__((aligned(16))) T lqt[L::T_ELEMS];
   __shared__ __attribute__((aligned(16))) T ld[SB_QT * L::RSTR];
-  __shared__ __attribute__((aligned(16))) T ldt[SB_D * L::TSTR];
+  __shared__ __attribute__((aligned(16))) T ldt[L::T_ELEMS];
   __shared__ __attribute__((aligned(16))) float lmx[SB_QT];
   __shared__ __attribute__((aligned(16))) float lll[SB_QT];
   __shared__ __attribute__((aligned(16))) float ldd[SB_QT];
@@ -358,10 +432,8 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
         pt[r] = from_f32<T>(pr);
         ds[r] = from_f32<T>(pr * (dp[r] - dq[r]));
       }
-      const Op4 adt = *(const Op4*)(ldt + l16 * L::TSTR + 16 * qs + 4 * kap);
-      dv = mfma16x16x16(adt, pt, dv);
-      const Op4 aqt = *(const Op4*)(lqt + l16 * L::TSTR + 16 * qs + 4 * kap);
-      dk = mfma16x16x16(aqt, ds, dk);
+      dv = mfma16x16x16(sb_opT<T>(ld, ldt, 16 * qs, l16, kap), pt, dv);
+      dk = mfma16x16x16(sb_opT<T>(lq, lqt, 16 * qs, l16, kap), ds, dk);
     }
   }
 
@@ -380,11 +452,22 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
 }
 
 template <typename T>
-void launch_bwd(const SbParams& p, hipStream_t stream) {
+void launch_bwd(SbParams p, hipStream_t stream) {
   const int64_t nqb = (p.Lq + SB_QB - 1) / SB_QB, nkb = (p.Lk + SB_KB - 1) / SB_KB;
+  // keys in one tile: runs of query blocks per workgroup (one fill each), still >= ~16 workgroups
+  // per CU over the grid
+  int64_t qbpw = 1;
+  if (p.Lk <= SB_KT) {
+    qbpw = (p.B * nqb * SB_H + 4095) / 4096;
+    qbpw = qbpw < 1 ? 1 : (qbpw > nqb ? nqb : qbpw);
+  }
+  p.qbpw = (int)qbpw;
+  const int64_t nwg_q = nqb > 0 ? (nqb + qbpw - 1) / qbpw : 0;
   // no query (Lq = 0): only the dk/dv kernel runs, and writes zeros
-  if (nqb > 0)
-    hipLaunchKernelGGL((sb_dq_kernel<T>), dim3((unsigned)(p.B * nqb * SB_H)), dim3(SB_NW * 64), 0, stream, p);
+  if (nwg_q > 0 && p.Lk <= SB_KT)
+    hipLaunchKernelGGL((sb_dq_kernel<T, true>), dim3((unsigned)(p.B * nwg_q * SB_H)), dim3(SB_NW * 64), 0, stream, p);
+  else if (nwg_q > 0)
+    hipLaunchKernelGGL((sb_dq_kernel<T, false>), dim3((unsigned)(p.B * nwg_q * SB_H)), dim3(SB_NW * 64), 0, stream, p);
   hipLaunchKernelGGL((sb_dkdv_kernel<T>), dim3((unsigned)(p.B * nkb * SB_H)), dim3(SB_NW * 64), 0, stream, p);
 }
 
