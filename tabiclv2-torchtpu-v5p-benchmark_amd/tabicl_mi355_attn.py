@@ -139,6 +139,24 @@ def _contig(*ts: Tensor) -> None:
             raise ValueError("tabicl_pk ops need contiguous inputs")
 
 
+def _bias_ptr(bias: Tensor):
+    """Device pointer of an op's key bias; an empty bias tensor (no rows) stands for no bias, which
+    lets the kernels skip the additive term (a bias of zeros gives the same result, more slowly)."""
+    return bias.data_ptr() if bias.numel() else None
+
+
+def _bias_rows(bias: Tensor) -> int:
+    return bias.shape[0] if bias.numel() else 0
+
+
+def _bias_arg(key_bias: Optional[Tensor], lead, Lk: int, device) -> Tensor:
+    """The op's bias argument for a wrapper's key_bias: _bias3's [1|B, 1, Lk] fp32, or an empty
+    [0, 1, Lk] tensor for no bias."""
+    if key_bias is None:
+        return torch.empty(0, 1, Lk, device=device, dtype=torch.float32)
+    return _bias3(key_bias, lead, Lk, device)
+
+
 @torch.library.custom_op("tabicl_pk::hx_fwd", mutates_args=())
 def _hx_fwd(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, h: int, lkp: int, bq: int, prec: int) -> Tensor:
     _nat.require_device(q, k, v, bias)
@@ -146,7 +164,7 @@ def _hx_fwd(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, h: int, lkp: int, bq:
     B, Lq, E = q.shape
     Lk = k.shape[1]
     out = torch.empty_like(q)
-    _nat.call("tabicl_hx_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), bias.shape[0],
+    _nat.call("tabicl_hx_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), _bias_ptr(bias), _bias_rows(bias),
               out.data_ptr(), B, Lq, Lk, E, h, _nat.dtype_code(q.dtype), _nat.stream_of(q))
     return out
 
@@ -200,7 +218,7 @@ def _pk_self_fwd(qkv: Tensor, bias: Tensor, cos: Tensor, sin: Tensor, h: int, lk
     B, L, E3 = qkv.shape
     E = E3 // 3
     out = torch.empty(B, L, E, device=qkv.device, dtype=qkv.dtype)
-    _nat.call("tabicl_pk_self_fwd", qkv.data_ptr(), bias.data_ptr(), bias.shape[0], cos.data_ptr(), sin.data_ptr(),
+    _nat.call("tabicl_pk_self_fwd", qkv.data_ptr(), _bias_ptr(bias), _bias_rows(bias), cos.data_ptr(), sin.data_ptr(),
               out.data_ptr(), B, L, E, h, rope, half, rot, float(scale), _nat.dtype_code(qkv.dtype),
               _nat.stream_of(qkv))
     return out
@@ -220,7 +238,7 @@ def _pk_cross_fwd(q: Tensor, kv: Tensor, bias: Tensor, cq: Tensor, sq: Tensor, c
     Bq, Lq, E = q.shape
     B, Lk, _ = kv.shape
     out = torch.empty(B, Lq, E, device=q.device, dtype=q.dtype)
-    _nat.call("tabicl_pk_cross_fwd", q.data_ptr(), Bq, kv.data_ptr(), bias.data_ptr(), bias.shape[0],
+    _nat.call("tabicl_pk_cross_fwd", q.data_ptr(), Bq, kv.data_ptr(), _bias_ptr(bias), _bias_rows(bias),
               cq.data_ptr(), sq.data_ptr(), ck.data_ptr(), sk.data_ptr(), out.data_ptr(), B, Lq, Lk, E, h,
               rope, half, rot, float(scale), _nat.dtype_code(q.dtype), _nat.stream_of(q))
     return out
@@ -258,7 +276,7 @@ def _hx_bwd(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, o: Tensor, do: Tensor
     Lk = k.shape[1]
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws = _bwd_workspace(B, Lq, E, h, q.device)
-    _nat.call("tabicl_hx_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), bias.shape[0],
+    _nat.call("tabicl_hx_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), _bias_ptr(bias), _bias_rows(bias),
               o.data_ptr(), do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Lq, Lk, E, h,
               _nat.dtype_code(q.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(q))
     return dq, dk, dv
@@ -293,7 +311,7 @@ def _pk_self_bwd(qkv: Tensor, bias: Tensor, cos: Tensor, sin: Tensor, o: Tensor,
     E = E3 // 3
     dqkv = torch.empty_like(qkv)
     ws = _bwd_workspace(B, L, E, h, qkv.device)
-    _nat.call("tabicl_pk_self_bwd", qkv.data_ptr(), bias.data_ptr(), bias.shape[0], cos.data_ptr(),
+    _nat.call("tabicl_pk_self_bwd", qkv.data_ptr(), _bias_ptr(bias), _bias_rows(bias), cos.data_ptr(),
               sin.data_ptr(), o.data_ptr(), do.data_ptr(), dqkv.data_ptr(), B, L, E, h, rope, half, rot,
               float(scale), _nat.dtype_code(qkv.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(qkv))
     return dqkv
@@ -330,7 +348,7 @@ def _pk_cross_bwd(q: Tensor, kv: Tensor, bias: Tensor, cq: Tensor, sq: Tensor, c
     dq = torch.empty(B, Lq, E, device=q.device, dtype=q.dtype)
     dkv = torch.empty_like(kv)
     ws = _bwd_workspace(B, Lq, E, h, q.device)
-    _nat.call("tabicl_pk_cross_bwd", q.data_ptr(), Bq, kv.data_ptr(), bias.data_ptr(), bias.shape[0],
+    _nat.call("tabicl_pk_cross_bwd", q.data_ptr(), Bq, kv.data_ptr(), _bias_ptr(bias), _bias_rows(bias),
               cq.data_ptr(), sq.data_ptr(), ck.data_ptr(), sk.data_ptr(), o.data_ptr(), do.data_ptr(),
               dq.data_ptr(), dkv.data_ptr(), B, Lq, Lk, E, h, rope, half, rot, float(scale),
               _nat.dtype_code(q.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(q))
@@ -383,7 +401,7 @@ def hx_attention(q: Tensor, k: Tensor, v: Tensor, h: int, key_bias: Optional[Ten
     q3 = q.reshape(-1, Lq, E)
     k3 = k.reshape(-1, Lk, E)
     v3 = v.reshape(-1, Lk, E)
-    bias = _bias3(key_bias, lead, Lk, q.device)
+    bias = _bias_arg(key_bias, lead, Lk, q.device)
     prec = _fp32_prec_code() if q.dtype == torch.float32 else 0
     out = HX_FWD(q3.contiguous(), k3.contiguous(), v3.contiguous(), bias, h, lkp, _pick_bq(Lq, lkp), prec)
     return out.reshape(*lead, Lq, E)
@@ -415,7 +433,7 @@ def pk_self_attention(qkv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,
     lkp = -(-L // 128) * 128
     cos, sin, rc, half, rot = rope_tables(rope_mod, L, E, h, qkv.device)
     prec = _fp32_prec_code() if qkv.dtype == torch.float32 else 0
-    out = PK_SELF(qkv.reshape(-1, L, E3).contiguous(), _bias3(key_bias, lead, L, qkv.device), cos, sin, h, lkp, rc,
+    out = PK_SELF(qkv.reshape(-1, L, E3).contiguous(), _bias_arg(key_bias, lead, L, qkv.device), cos, sin, h, lkp, rc,
                   half, rot, prec, float(scale))
     return out.reshape(*lead, L, E)
 
@@ -440,6 +458,6 @@ def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor]
     elif q3.shape[0] != kv3.shape[0]:
         q3 = q3.expand(kv3.shape[0], Lq, E)
     out_lead = lead if q.shape[:-2].numel() == kv3.shape[0] else kv.shape[:-2]
-    out = PK_CROSS(q3.contiguous(), kv3.contiguous(), _bias3(key_bias, out_lead, Lk, q.device), cq, sq, ck, sk,
+    out = PK_CROSS(q3.contiguous(), kv3.contiguous(), _bias_arg(key_bias, out_lead, Lk, q.device), cq, sq, ck, sk,
                    h, lkp, bq, rc, half, rot, prec, float(scale))
     return out.reshape(*out_lead, Lq, E)
