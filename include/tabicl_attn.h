@@ -94,6 +94,25 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
                         int32_t dtype, void* stream);
 
 /*
+ * Folded first ISAB attention (inference): U = softmax(qf x^T) x, one head of head dim E = 128 over
+ * the raw rows x (K = V = x), qf pre-scaled (no scale applied).
+ * Replaces tabicl_pk::hxf_fwd (reference scripts/tabicl_tpu_pallas_attn.py:345-404, 414-419, 429-442).
+ * qf [q_b, hq, E] with q_b in {1, B} (1: one folded query set shared by every batch element),
+ * x [B, Lk, E], out [B, hq, E], contiguous; valid: device int32 [valid_n], valid_n in {1, B} (keys
+ * >= valid ignored; a row with no valid key is written as 0). workspace: optional, of
+ * tabicl_hxf_workspace_bytes(...) bytes (key splits merged by a second kernel on the same stream).
+ */
+int tabicl_hxf_fwd(const int32_t* valid, int64_t valid_n, const void* qf, int64_t q_b, const void* x, void* out,
+                   int64_t B, int64_t hq, int64_t Lk, int64_t E, int32_t dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes tabicl_hxf_fwd can use for these sizes on the current device (0: no key split).
+ * No counterpart in the reference (its Pallas grid needs no scratch in HBM). <0 on bad arguments.
+ */
+int64_t tabicl_hxf_workspace_bytes(int64_t B, int64_t hq, int64_t Lk, int64_t E, int32_t dtype);
+
+/*
  * Backward of the small-head ops (training). Inputs as the forward, plus the forward output o and
  * its gradient dout (both [B, Lq, E], contiguous). P is recomputed in fp32, dS = P (dP - D) with
  * D = sum over the head's dims of dout * o is cast to the input dtype, dq/dk/dv accumulate in fp32

@@ -17,6 +17,7 @@ It restates, in plain numpy (float64) and CPU torch (float32), the arithmetic of
   attention_bwd_f64       scripts/tabicl_tpu_pallas_attn.py:87-122 (P, dP, D, dS; dq, dk, dv)
   rope_bwd_ref            pallas_attn.py:446-447, 476-477 (y cos - R(y sin))
   hx/pk_self/pk_cross_bwd_ref  pallas_attn.py:185-188, 512-560, 618-637 (packed gradients)
+  hxf_ref, folded_mab1_ref     pallas_attn.py:345-404, 429-442; tests/test_pallas_attn.py:300-318
 
 Pinning (tests/test_oracle.py): every function is checked against closed forms, invariants and
 brute force (two-key sigmoid, one key, key permutation, row shift, masked keys, q = 0 mean, convex
@@ -301,6 +302,31 @@ def pk_cross_bwd_ref(q, kv, h, bias, rope_q, rope_k, scale, do, o=None):
     if shared:
         dq = dq.sum(axis=0, keepdims=True)
     return dq, np.concatenate([dk, dv], axis=-1)
+
+
+def hxf_ref(qf, x, valid):
+    """hxf_attention (reference scripts/tabicl_tpu_pallas_attn.py:345-404, 429-442): U = softmax(qf x^T) x
+    over the keys < valid, one head of width E; qf [1|B, hq, E] (1: shared), x [B, Lk, E]; a row with
+    no valid key -> 0. float64."""
+    qf = _f64(qf)
+    x = _f64(x)
+    if qf.shape[0] != x.shape[0]:
+        qf = np.broadcast_to(qf, (x.shape[0],) + qf.shape[1:])
+    return attention_f64(qf, x, x, 1, valid=np.asarray(valid).astype(np.int64))
+
+
+def folded_mab1_ref(ind, x, valid, h: int, W, b):
+    """The first ISAB attention before its output projection, unfolded: q = ind W_q^T + b_q (pre-scaled by
+    hd^-0.5), K = x W_k^T + b_k, V = x W_v^T + b_v, per-head softmax(q K^T) V over keys < valid
+    (reference check_hxf, scripts/tests/test_pallas_attn.py:300-318). ind [Lq, E], x [B, Lk, E]."""
+    ind, x, W, b = _f64(ind), _f64(x), _f64(W), _f64(b)
+    E = ind.shape[-1]
+    hd = E // h
+    q = (ind @ W[:E].T + b[:E]) * hd ** -0.5
+    k = x @ W[E:2 * E].T + b[E:2 * E]
+    v = x @ W[2 * E:].T + b[2 * E:]
+    q = np.broadcast_to(q, (x.shape[0],) + q.shape)
+    return attention_f64(q, k, v, h, valid=np.asarray(valid).astype(np.int64))
 
 
 def splash_sdpa_ref(q, k, v, valid=None):

@@ -302,7 +302,7 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
   if (N == 0 || H == 0 || Tq == 0) return 0;
   if (N * H * ((Tq + 127) / 128) > (1LL << 31) - 1) return fail(1, "icl_fwd: grid too large");
   return launch_status(
-      tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, q_sn, q_sh,
+      tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, 64, q_sn, q_sh,
                             q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale,
                             dtype, workspace && aligned16(workspace) ? workspace : nullptr,
                             workspace_bytes, (hipStream_t)stream),
@@ -315,7 +315,36 @@ int64_t tabicl_icl_workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv
       Tq < 0 || Tkv < 1)
     return fail(-1, "icl_workspace_bytes: bad arguments");
   if (N == 0 || H == 0 || Tq == 0) return 0;
-  return tabicl_launch_icl_ws_bytes(N, H, Tq, Tkv, dtype);
+  return tabicl_launch_icl_ws_bytes(N, H, Tq, Tkv, 64, dtype);
+}
+
+int tabicl_hxf_fwd(const int32_t* valid, int64_t valid_n, const void* qf, int64_t q_b, const void* x, void* out,
+                   int64_t B, int64_t hq, int64_t Lk, int64_t E, int32_t dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
+    return fail(1, "hxf_fwd: dtype code %d not supported", dtype);
+  if (E != 128) return fail(1, "hxf_fwd: needs E == 128, got %lld", (long long)E);
+  if (B < 0 || hq < 0 || Lk < 1 || B > (1LL << 30) || hq > (1LL << 30) || Lk > (1LL << 30))
+    return fail(1, "hxf_fwd: bad sizes B=%lld hq=%lld Lk=%lld", (long long)B, (long long)hq, (long long)Lk);
+  if (q_b != 1 && q_b != B) return fail(1, "hxf_fwd: qf batch must be 1 or B");
+  if (!valid || (valid_n != 1 && valid_n != B))
+    return fail(1, "hxf_fwd: valid must hold 1 or B=%lld entries", (long long)B);
+  if (!aligned16(qf) || !aligned16(x) || !aligned16(out)) return fail(1, "hxf_fwd: pointers must be 16-byte aligned");
+  if (B == 0 || hq == 0) return 0;
+  if (B * ((hq + 127) / 128) * 4 > (1LL << 31) - 1) return fail(1, "hxf_fwd: grid too large");
+  return launch_status(
+      tabicl_launch_icl_fwd(qf, x, x, valid, valid_n, out, B, 1, hq, Lk, 128, q_b == 1 && B > 1 ? 0 : hq * E, 0, E,
+                            Lk * E, 0, E, Lk * E, 0, E, hq * E, 0, E, 1.0f, dtype,
+                            workspace && aligned16(workspace) ? workspace : nullptr, workspace_bytes,
+                            (hipStream_t)stream),
+      "hxf_fwd");
+}
+
+int64_t tabicl_hxf_workspace_bytes(int64_t B, int64_t hq, int64_t Lk, int64_t E, int32_t dtype) {
+  if ((dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) || E != 128 || B < 0 || hq < 0 || Lk < 1)
+    return fail(-1, "hxf_workspace_bytes: bad arguments");
+  if (B == 0 || hq == 0) return 0;
+  return tabicl_launch_icl_ws_bytes(B, 1, hq, Lk, 128, dtype);
 }
 
 int tabicl_icl_cache_append(void* k_cache, void* v_cache, int64_t dst_sn, int64_t dst_sh,

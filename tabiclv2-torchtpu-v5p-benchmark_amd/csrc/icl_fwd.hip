@@ -47,13 +47,14 @@ struct IclParams {
   int* flags;
 };
 
-template <typename T> struct IclLds {
+// LDS tiles of the generic kernel for head dim D (64: ICL; 128: the folded ISAB-1 attention).
+template <typename T, int D = ICL_D> struct IclLds {
   static constexpr int EPC = 16 / sizeof(T);      // elements per 16-byte chunk
-  static constexpr int CPR = ICL_D / EPC;          // chunks per row
-  static constexpr int KSTR = ICL_D + EPC;         // padded row strides (elements)
+  static constexpr int CPR = D / EPC;              // chunks per row
+  static constexpr int KSTR = D + EPC;             // padded row strides (elements)
   static constexpr int VSTR = ICL_KT + EPC;
   static constexpr int K_ELEMS = ICL_KT * KSTR;
-  static constexpr int V_ELEMS = ICL_D * VSTR;
+  static constexpr int V_ELEMS = D * VSTR;
 };
 
 // Position of key r (0..15) inside its 16-key group in the transposed V tile: bits 2 and 3
@@ -83,8 +84,8 @@ __device__ __forceinline__ int vt_off(int d, int pos, int vstr) {
 // of 16-byte chunks of two consecutive V rows. Rows past `valid` are read from row valid-1 (always
 // in bounds and finite whenever the visible rows are), so the masked keys of the last tile meet
 // p = 0 times a finite value and nothing from the unused cache tail is ever read.
-template <typename T, int NT> struct Stage {
-  static constexpr int EPC = IclLds<T>::EPC, CPR = IclLds<T>::CPR;
+template <typename T, int NT, int D = ICL_D> struct Stage {
+  static constexpr int EPC = IclLds<T, D>::EPC, CPR = IclLds<T, D>::CPR;
   static constexpr int KREP = ICL_KT * CPR / NT;
   static constexpr int VREP = (ICL_KT / 2) * CPR / NT;
   uint4 k[KREP];
@@ -109,7 +110,7 @@ template <typename T, int NT> struct Stage {
   }
 
   __device__ __forceinline__ void store(T* lds_k, T* lds_vt) const {
-    typedef IclLds<T> L;
+    typedef IclLds<T, D> L;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < KREP; ++i) {
@@ -157,18 +158,18 @@ __device__ __forceinline__ float psum8(const f32x8& p, float acc) {
   return acc;
 }
 
-template <typename T, int QC> struct IclState {
+template <typename T, int QC, int D = ICL_D> struct IclState {
   typedef typename OpVec<T, 8>::type Op8;
-  Op8 qop[QC][4];
-  f32x16 o[QC][2];
+  Op8 qop[QC][D / 16];
+  f32x16 o[QC][D / 32];
   float m_run[QC], l_run[QC];
 };
 
 // One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK: the tile crosses `valid`.
-template <typename T, int QC, bool MASK>
-__device__ __forceinline__ void icl_tile(IclState<T, QC>& st, const T* lk, const T* lv, int k0,
+template <typename T, int QC, bool MASK, int D>
+__device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, const T* lv, int k0,
                                          int valid, float sc, int lr, int hh) {
-  typedef IclLds<T> L;
+  typedef IclLds<T, D> L;
   typedef typename OpVec<T, 8>::type Op8;
   f32x16 s[QC][2];
 #pragma unroll
@@ -178,7 +179,7 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC>& st, const T* lk, const
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[qc][kb][r] = 0.f;
 #pragma unroll
-    for (int sl = 0; sl < 4; ++sl) {
+    for (int sl = 0; sl < D / 16; ++sl) {
       const Op8 a = *(const Op8*)(lk + (kb * 32 + lr) * L::KSTR + 16 * sl + 8 * hh);
 #pragma unroll
       for (int qc = 0; qc < QC; ++qc) s[qc][kb] = mfma32x32x16(a, st.qop[qc][sl], s[qc][kb]);
@@ -210,7 +211,7 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC>& st, const T* lk, const
       const float alpha = __builtin_amdgcn_exp2f((st.m_run[qc] - m_new) * sc);
       st.l_run[qc] *= alpha;
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
+      for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) st.o[qc][db][r] *= alpha;
       st.m_run[qc] = m_new;
@@ -230,7 +231,7 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC>& st, const T* lk, const
   }
 
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
+  for (int db = 0; db < D / 32; ++db)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -241,9 +242,9 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC>& st, const T* lk, const
       }
 }
 
-template <typename T, int NW, int QC>
+template <typename T, int NW, int QC, int D = ICL_D>
 __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
-  typedef IclLds<T> L;
+  typedef IclLds<T, D> L;
   typedef typename OpVec<T, 8>::type Op8;
   constexpr int NT = NW * 64;
   constexpr int QW = 32 * QC;
@@ -274,19 +275,19 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   const T* kbase = (const T*)p.k + n * p.k_sn + h * p.k_sh;
   const T* vbase = (const T*)p.v + n * p.v_sn + h * p.v_sh;
 
-  IclState<T, QC> st;
+  IclState<T, QC, D> st;
 #pragma unroll
   for (int qc = 0; qc < QC; ++qc) {
     const int qi = qw0 + qc * 32 + lr;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < D / 16; ++s) {
       Op8 z = {};
       st.qop[qc][s] = qi < p.Tq ? *(const Op8*)(qbase + (int64_t)qi * p.q_st + 16 * s + 8 * hh) : z;
     }
     st.m_run[qc] = TA_NEG_INF;
     st.l_run[qc] = 0.f;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) st.o[qc][db][r] = 0.f;
   }
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   const int per = (ntiles + p.nsplit - 1) / p.nsplit;
   const int t0 = min(split * per, ntiles), t1 = min(t0 + per, ntiles);
   if (t1 > t0) {
-    Stage<T, NT> stg;
+    Stage<T, NT, D> stg;
     stg.load(kbase, vbase, p.k_st, p.v_st, t0 * ICL_KT, valid);
     stg.store(lds_k[0], lds_vt[0]);
     __syncthreads();
@@ -305,15 +306,15 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     for (int t = t0; t + 1 < t1; ++t) {
       const int k0 = t * ICL_KT, buf = (t - t0) & 1;
       stg.load(kbase, vbase, p.k_st, p.v_st, k0 + ICL_KT, valid);
-      icl_tile<T, QC, false>(st, lds_k[buf], lds_vt[buf], k0, valid, sc, lr, hh);
+      icl_tile<T, QC, false, D>(st, lds_k[buf], lds_vt[buf], k0, valid, sc, lr, hh);
       stg.store(lds_k[buf ^ 1], lds_vt[buf ^ 1]);
       __syncthreads();
     }
     const int tl = t1 - 1, bl = (tl - t0) & 1;
     if (t1 == ntiles)
-      icl_tile<T, QC, true>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
+      icl_tile<T, QC, true, D>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
     else
-      icl_tile<T, QC, false>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
+      icl_tile<T, QC, false, D>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
   }
 
   if (p.nsplit > 1) {
@@ -324,9 +325,9 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
       const int qi = qw0 + qc * 32 + lr;
       if (qi < p.Tq) {
         const int64_t row = ((int64_t)split * p.N * p.H + nh) * p.Tq + qi;
-        float* orow = p.ws_o + row * ICL_D;
+        float* orow = p.ws_o + row * D;
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
+        for (int db = 0; db < D / 32; ++db)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float4 ov = make_float4(st.o[qc][db][4 * j], st.o[qc][db][4 * j + 1], st.o[qc][db][4 * j + 2],
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     if (qi < p.Tq) {
       T* orow = (T*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st;
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
+      for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           typename OpVec<T, 4>::type ov;
@@ -361,13 +362,13 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
 
 // Combines the per-split partials (m in log2 units): m* = max_s m_s, w_s = 2^(m_s - m*),
 // O = sum_s w_s O_s / sum_s w_s l_s (0 when no split saw a valid key). One thread per 4 outputs.
-template <typename T>
+template <typename T, int D = ICL_D>
 __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
   const int64_t rows = (int64_t)p.N * p.H * p.Tq;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * (ICL_D / 4)) return;
-  const int64_t row = idx / (ICL_D / 4);
-  const int c4 = (int)(idx % (ICL_D / 4)) * 4;
+  if (idx >= rows * (D / 4)) return;
+  const int64_t row = idx / (D / 4);
+  const int c4 = (int)(idx % (D / 4)) * 4;
   float mstar = TA_NEG_INF;
   for (int s = 0; s < p.nsplit; ++s) {
     const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)s * rows + row) * 2);
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
     const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)s * rows + row) * 2);
     if (!(ml.y > 0.f)) continue;
     const float w = __builtin_amdgcn_exp2f(ml.x - mstar);
-    const float4 o = *(const float4*)(p.ws_o + ((int64_t)s * rows + row) * ICL_D + c4);
+    const float4 o = *(const float4*)(p.ws_o + ((int64_t)s * rows + row) * D + c4);
     acc.x += w * o.x; acc.y += w * o.y; acc.z += w * o.z; acc.w += w * o.w;
     l += w * ml.y;
   }
@@ -782,25 +783,26 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
   }
 }
 
-// Resident workgroups per CU of the kernel that carries the work (the pipelined one for bf16).
-template <typename T, int NW, int QC>
+// Resident workgroups per CU of the kernel that carries the work (the pipelined one for bf16, d = 64).
+template <typename T, int NW, int QC, int D>
 int blocks_per_cu() {
   int n = 0;
   const hipError_t e =
-      sizeof(T) == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel, IP_NW * 64, 0)
-                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC>, NW * 64, 0);
+      sizeof(T) == 2 && D == ICL_D
+          ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel, IP_NW * 64, 0)
+          : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC, D>, NW * 64, 0);
   return e == hipSuccess && n > 0 ? n : 1;
 }
 
 // Number of key splits that best fills whole rounds of resident workgroups:
 // minimises ceil(items * S / slots) / S over S = 1..4, each split keeping >= 8 key tiles.
-template <typename T, int NW, int QC>
+template <typename T, int NW, int QC, int D>
 int pick_splits(int64_t items, int64_t Tkv) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return 1;
-  const int64_t slots = (int64_t)cus * blocks_per_cu<T, NW, QC>();
+  const int64_t slots = (int64_t)cus * blocks_per_cu<T, NW, QC, D>();
   const int64_t tiles = (Tkv + ICL_KT - 1) / ICL_KT;
   int best = 1;
   double best_cost = (double)((items + slots - 1) / slots);
@@ -812,63 +814,65 @@ int pick_splits(int64_t items, int64_t Tkv) {
   return best;
 }
 
-// Workspace layout: [per-work-item flags, bf16 only, 256-byte aligned][split partials: O fp32
-// [nsplit][rows][64], (m, l) [nsplit][rows][2]].
+// Workspace layout: [per-work-item flags, bf16 d = 64 only, 256-byte aligned][split partials: O fp32
+// [nsplit][rows][D], (m, l) [nsplit][rows][2]].
 int64_t flag_bytes(int64_t nblk) { return (nblk * 4 + 255) / 256 * 256; }
-int64_t part_bytes(int nsplit, int64_t rows) { return nsplit > 1 ? (int64_t)nsplit * rows * (ICL_D + 2) * 4 : 0; }
+int64_t part_bytes(int nsplit, int64_t rows, int D) { return nsplit > 1 ? (int64_t)nsplit * rows * (D + 2) * 4 : 0; }
 
-template <typename T, int NW, int QC>
+template <typename T, int NW, int QC, int D>
 int64_t workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv) {
   const int64_t nqb = (Tq + 32 * QC * NW - 1) / (32 * QC * NW);
-  const int s = pick_splits<T, NW, QC>(N * H * nqb, Tkv);
-  return (sizeof(T) == 2 ? flag_bytes(N * H * nqb * s) : 0) + part_bytes(s, N * H * Tq);
+  const int s = pick_splits<T, NW, QC, D>(N * H * nqb, Tkv);
+  return (sizeof(T) == 2 && D == ICL_D ? flag_bytes(N * H * nqb * s) : 0) + part_bytes(s, N * H * Tq, D);
 }
 
-// bf16 with a large enough workspace: pipelined kernel, then icl_fwd_kernel on the work items it
-// flagged, then the split merge. Otherwise icl_fwd_kernel alone (splitting only if the workspace
-// holds the partials).
-template <typename T, int NW, int QC>
+// bf16 d = 64 with a large enough workspace: pipelined kernel, then icl_fwd_kernel on the work
+// items it flagged, then the split merge. Otherwise icl_fwd_kernel alone (splitting only if the
+// workspace holds the partials).
+template <typename T, int NW, int QC, int D>
 void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
   IclParams p = p0;
   p.nqb = (p.Tq + 32 * QC * NW - 1) / (32 * QC * NW);
   const int64_t rows = (int64_t)p.N * p.H * p.Tq;
   const int64_t items = (int64_t)p.N * p.H * p.nqb;
-  p.nsplit = pick_splits<T, NW, QC>(items, p.Tkv);
+  p.nsplit = pick_splits<T, NW, QC, D>(items, p.Tkv);
   const int64_t have = ws ? ws_bytes : 0;
   bool fast = false;
   int64_t fb = 0;
-  if (sizeof(T) == 2) {
-    if (have < flag_bytes(items * p.nsplit) + part_bytes(p.nsplit, rows)) p.nsplit = 1;
+  if (sizeof(T) == 2 && D == ICL_D) {
+    if (have < flag_bytes(items * p.nsplit) + part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
     fb = flag_bytes(items * p.nsplit);
-    fast = have >= fb + part_bytes(p.nsplit, rows);
+    fast = have >= fb + part_bytes(p.nsplit, rows, D);
   }
   if (!fast) {
     fb = 0;
-    if (have < part_bytes(p.nsplit, rows)) p.nsplit = 1;
+    if (have < part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
   }
   p.flags = fast ? (int*)ws : nullptr;
   p.ws_o = (float*)((char*)ws + fb);
-  p.ws_ml = p.ws_o + (p.nsplit > 1 ? (int64_t)p.nsplit * rows * ICL_D : 0);
+  p.ws_ml = p.ws_o + (p.nsplit > 1 ? (int64_t)p.nsplit * rows * D : 0);
   const int64_t nblk = items * p.nsplit;
   if (fast)
     hipLaunchKernelGGL(icl_pipe_kernel, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
-  hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
+  hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC, D>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
   if (p.nsplit > 1) {
-    const int64_t threads = rows * (ICL_D / 4);
-    hipLaunchKernelGGL((icl_merge_kernel<T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
+    const int64_t threads = rows * (D / 4);
+    hipLaunchKernelGGL((icl_merge_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
   }
 }
 
 }  // namespace
 
-// Host launchers (called from the C ABI in abi.hip).
-int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int dtype) {
-  return dtype == 0 ? workspace_bytes<bf16, 4, 2>(N, H, Tq, Tkv) : workspace_bytes<float, 4, 1>(N, H, Tq, Tkv);
+// Host launchers (called from the C ABI in abi.hip). D: head dim, 64 (ICL) or 128 (folded ISAB-1).
+int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype) {
+  if (D == 128)
+    return dtype == 0 ? workspace_bytes<bf16, 4, 1, 128>(N, H, Tq, Tkv) : workspace_bytes<float, 8, 1, 128>(N, H, Tq, Tkv);
+  return dtype == 0 ? workspace_bytes<bf16, 4, 2, 64>(N, H, Tq, Tkv) : workspace_bytes<float, 4, 1, 64>(N, H, Tq, Tkv);
 }
 
 int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
                           int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
-                          int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
+                          int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream) {
@@ -883,9 +887,15 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.o_sn = o_sn; p.o_sh = o_sh; p.o_st = o_st;
   p.sc = scale * TA_LOG2E;
   p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr; p.flags = nullptr;
-  if (dtype == 0)
-    launch<bf16, 4, 2>(p, ws, ws_bytes, stream);
-  else
-    launch<float, 4, 1>(p, ws, ws_bytes, stream);
+  if (D == 128) {
+    if (dtype == 0)
+      launch<bf16, 4, 1, 128>(p, ws, ws_bytes, stream);
+    else
+      launch<float, 8, 1, 128>(p, ws, ws_bytes, stream);
+  } else if (dtype == 0) {
+    launch<bf16, 4, 2, 64>(p, ws, ws_bytes, stream);
+  } else {
+    launch<float, 4, 1, 64>(p, ws, ws_bytes, stream);
+  }
   return (int)hipGetLastError();
 }

@@ -4,14 +4,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// d = 64 cached-KV attention (icl_fwd.hip).
+// Flash attention over [N, H, T, D] views (icl_fwd.hip): D = 64 is the cached-KV ICL attention,
+// D = 128 the folded ISAB-1 attention (one head, K = V = the raw rows).
 int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
                           int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
-                          int64_t Tkv, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
+                          int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream);
-int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int dtype);
+int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
 // Small-head (8 x 16) attention (smallhead_fwd.hip): picks the resident, streaming or general
 // kernel for the shape. ws may be null (no key split).

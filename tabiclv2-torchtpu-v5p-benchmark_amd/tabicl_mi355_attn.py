@@ -124,10 +124,10 @@ def packed_supported(Lq: int, Lk: int, E: int, h: int, self_attn: bool,
     return _dt_ok(dtype) and _nat.supported(op, Lq, Lk, E, h, dtype)
 
 
-def hxf_supported(hq: int, Lk: int, E: int) -> bool:  # noqa: ARG001
-    """Folded first-ISAB kernel (reference :425-426) is not built: always False, so the dispatcher
-    keeps the hxq path (the reference's best preset does not enable hxf either)."""
-    return False
+def hxf_supported(hq: int, Lk: int, E: int) -> bool:
+    """Folded first-ISAB kernel (reference :425-426): E = 128 (the kernel's head dim), hq a multiple of
+    8 and at most 2048 folded queries, any key length >= 1."""
+    return E == 128 and hq % 8 == 0 and 0 < hq <= 2048 and Lk >= 1
 
 
 # ---------------------------------------------------------------------------------------------
@@ -247,6 +247,34 @@ def _pk_cross_fwd(q: Tensor, kv: Tensor, bias: Tensor, cq: Tensor, sq: Tensor, c
 @_pk_cross_fwd.register_fake
 def _(q, kv, bias, cq, sq, ck, sk, h, lkp, bq, rope, half, rot, prec, scale):  # noqa: ANN001
     return q.new_empty(kv.shape[0], q.shape[1], q.shape[2])
+
+
+@torch.library.custom_op("tabicl_pk::hxf_fwd", mutates_args=())
+def _hxf_fwd(valid: Tensor, q: Tensor, x: Tensor, bk: int, prec: int) -> Tensor:
+    _nat.require_device(valid, q, x)
+    _contig(valid, q, x)
+    if valid.dtype != torch.int32:
+        raise ValueError("valid must be int32")
+    Bq, hq, E = q.shape
+    B, Lk, _ = x.shape
+    out = torch.empty(B, hq, E, device=x.device, dtype=x.dtype)
+    code = _nat.dtype_code(x.dtype)
+    key = ("hxf", B, hq, Lk, E, code, x.device.index)
+    nbytes = _HXQ_WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = int(_nat.load().tabicl_hxf_workspace_bytes(B, hq, Lk, E, code))
+        _HXQ_WS_BYTES[key] = max(nbytes, 0)
+        nbytes = _HXQ_WS_BYTES[key]
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+    _nat.call("tabicl_hxf_fwd", valid.data_ptr(), valid.numel(), q.data_ptr(), Bq, x.data_ptr(), out.data_ptr(),
+              B, hq, Lk, E, code, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+              _nat.stream_of(x))
+    return out
+
+
+@_hxf_fwd.register_fake
+def _(valid, q, x, bk, prec):  # noqa: ANN001
+    return x.new_empty(x.shape[0], q.shape[1], q.shape[2])
 
 
 # ---------------------------------------------------------------------------------------------
@@ -382,7 +410,7 @@ HX_FWD = torch.ops.tabicl_pk.hx_fwd
 HXQ_FWD = torch.ops.tabicl_pk.hxq_fwd
 PK_SELF = torch.ops.tabicl_pk.pk_self_fwd
 PK_CROSS = torch.ops.tabicl_pk.pk_cross_fwd
-HXF_FWD = None
+HXF_FWD = torch.ops.tabicl_pk.hxf_fwd
 HX_BWD = torch.ops.tabicl_pk.hx_bwd
 PK_SELF_BWD = torch.ops.tabicl_pk.pk_self_bwd
 PK_CROSS_BWD = torch.ops.tabicl_pk.pk_cross_bwd
@@ -461,3 +489,21 @@ def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor]
     out = PK_CROSS(q3.contiguous(), kv3.contiguous(), _bias_arg(key_bias, out_lead, Lk, q.device), cq, sq, ck, sk,
                    h, lkp, bq, rc, half, rot, prec, float(scale))
     return out.reshape(*out_lead, Lq, E)
+
+
+def hxf_attention(qf: Tensor, x: Tensor, valid_len: Tensor) -> Tensor:
+    """Inference only. qf [hq, E] (shared by every batch element) or [..., hq, E]: folded, pre-scaled
+    queries; x [..., Lk, E]: the raw key/value rows (positions >= valid_len ignored). Returns
+    softmax(qf x^T) x: [..., hq, E] (reference :429-442). valid_len may be a scalar or hold one
+    length per flattened batch element; qf is computed in x's dtype."""
+    lead = x.shape[:-2]
+    Lk, E = x.shape[-2], x.shape[-1]
+    hq = qf.shape[-2]
+    x3 = x.reshape(-1, Lk, E).contiguous()
+    q3 = qf.reshape(-1, hq, E).to(x.dtype)
+    if q3.shape[0] not in (1, x3.shape[0]):
+        q3 = q3.expand(x3.shape[0], hq, E)
+    valid = torch.as_tensor(valid_len, device=x.device).to(dtype=torch.int32).reshape(-1).contiguous()
+    prec = _fp32_prec_code() if x.dtype == torch.float32 else 0
+    out = HXF_FWD(valid, q3.contiguous(), x3, _pick_bk(Lk), prec)
+    return out.reshape(*lead, hq, E)

@@ -6,6 +6,8 @@ patches upstream tabicl's `multi_head_attention_forward` (and `sdpa_with_flatten
 cached-KV ICL attention) so that the attention itself runs in the HIP kernels of
 libtabicl_attn.so (tabicl_mi355_attn / tabicl_mi355_icl), keeping the reference's routing order:
 
+  HXF      inference first-ISAB attention with the K projection folded into the queries
+           (folded_mab1 + hxf_attention; the K/V projection is never formed)   (reference :319-327)
   HXQ      inference first-ISAB attention (few queries over the train rows, keys >= valid ignored):
            q / packed K|V projections, SSMax on q, hxq_attention            (reference :328-342)
   fallback upstream for cached_kv / need_kv / dropout / valid_kv_len / head dim > MAX_HEAD_DIM /
@@ -18,7 +20,7 @@ libtabicl_attn.so (tabicl_mi355_attn / tabicl_mi355_icl), keeping the reference'
 
 Knobs (same names as the reference where they select kernels):
   TABICL_TPU_MHA=hxq|hxk|thl|std|pk|hx|auto|<rules>, TABICL_TPU_MHA_MAX_HEAD_DIM (32),
-  TABICL_TPU_MHA_PROJ=packed|split|views, TABICL_TPU_MHA_HXQ=1, TABICL_TPU_MHA_PACKED=1,
+  TABICL_TPU_MHA_PROJ=packed|split|views, TABICL_TPU_MHA_HXF=1, TABICL_TPU_MHA_HXQ=1, TABICL_TPU_MHA_PACKED=1,
   TABICL_TPU_MHA_ANY_DEVICE=1 (CPU equivalence tests: lets the wrapper's torch layouts run on CPU;
   the HIP kernels themselves never run on CPU tensors).
 """
@@ -36,6 +38,7 @@ _MAX_HEAD_DIM = int(os.environ.get("TABICL_TPU_MHA_MAX_HEAD_DIM", "32") or 32)
 _ANY_DEVICE = os.environ.get("TABICL_TPU_MHA_ANY_DEVICE", "") == "1"
 _PROJ = os.environ.get("TABICL_TPU_MHA_PROJ", "packed").strip().lower()
 _HXQ = os.environ.get("TABICL_TPU_MHA_HXQ", "") == "1"
+_HXF = os.environ.get("TABICL_TPU_MHA_HXF", "") == "1"
 _PACKED = os.environ.get("TABICL_TPU_MHA_PACKED", "") == "1"
 _ICL = os.environ.get("TABICL_MI355_ICL", "1") == "1"
 _PK = None  # tabicl_mi355_attn, imported by install()
@@ -214,10 +217,39 @@ def _combined_mask(attn_mask, key_padding_mask, batch_shape, nh: int, Lq: int, L
     return m
 
 
-def folded_mab1(*args, pk=None, **kwargs) -> Optional[Tensor]:  # noqa: ANN001, ARG001
-    """Folded first-ISAB attention (reference :60-92) needs the hxf kernel, which is not built:
-    always None, so callers take the hxq path."""
-    return None
+def folded_mab1(query: Tensor, key: Tensor, valid_kv_len: Tensor, num_heads: int, in_proj_weight: Tensor,
+                in_proj_bias: Optional[Tensor], ssmax_layer=None, src_len_override=None, pk=None) -> Optional[Tensor]:  # noqa: ANN001
+    """Folded first-ISAB attention (reference scripts/tabicl_tpu_mha.py:60-92): softmax(q_g K_g^T) V_g
+    for every head, merged [..., Lq, E] before the output projection, with K = key W_k^T + b_k and
+    V = key W_v^T + b_v never formed: U = softmax(Qf key^T) key with Qf_g = q_g W_k,g (q pre-scaled;
+    q_g . b_k,g is constant per query row, so softmax drops it), then O_g = U_g W_v,g^T + b_v,g (rows
+    of P sum to 1). None when the kernel does not apply."""
+    pk = pk if pk is not None else _PK
+    E = query.shape[-1]
+    hd = E // num_heads
+    qsrc = query
+    while qsrc.dim() > 2 and qsrc.stride(0) == 0:  # inducing points expanded over the batch: fold once
+        qsrc = qsrc[0]
+    Lq = qsrc.shape[-2]
+    nb_q = qsrc.shape[:-2].numel()
+    nb_k = key.shape[:-2].numel()
+    if pk is None or nb_q not in (1, nb_k) or not pk.hxf_supported(num_heads * Lq, key.shape[-2], E):
+        return None
+    w_q, w_k, w_v = in_proj_weight.split([E, E, E])
+    b_q, _b_k, b_v = (None, None, None) if in_proj_bias is None else in_proj_bias.split([E, E, E])
+    q = F.linear(qsrc, w_q, b_q)
+    if ssmax_layer is not None:
+        q = _ssmax(ssmax_layer, q, num_heads, src_len_override if src_len_override is not None else valid_kv_len)
+    q = q * (hd ** -0.5)
+    # Qf[.., g, i, :] = q[.., i, g, :] @ W_k,g  ([hd] x [hd, E]); batched over heads, right operand contiguous
+    qh = q.unflatten(-1, (num_heads, hd)).transpose(-3, -2)
+    qf = torch.matmul(qh, w_k.reshape(num_heads, hd, E).contiguous())
+    u = pk.hxf_attention(qf.flatten(-3, -2), key, valid_kv_len)  # [*key_lead, h * Lq, E]
+    # O[.., i, g, :] = U[.., g, i, :] @ W_v,g^T
+    uh = u.unflatten(-2, (num_heads, Lq))
+    o = torch.matmul(uh, w_v.reshape(num_heads, hd, E).transpose(-1, -2).contiguous().to(uh.dtype))
+    o = o.transpose(-3, -2).flatten(-2, -1)
+    return o + b_v if b_v is not None else o
 
 
 def _ssmax(ssmax_layer, q: Tensor, num_heads: int, n) -> Tensor:  # noqa: ANN001
@@ -256,6 +288,14 @@ def install(att_module, layers_module=None, mode: Optional[str] = None, proj: Op
         E = query.shape[-1]
         hd = E // num_heads
         on_gpu = query.device.type == _DEVICE
+        if (_HXF and isinstance(valid_kv_len, Tensor) and not torch.is_grad_enabled() and cached_kv is None
+                and not need_kv and key is not None and key is value and rope is None and attn_mask is None
+                and key_padding_mask is None and hd <= _MAX_HEAD_DIM and on_gpu
+                and (not isinstance(src_len_override, Tensor) or src_len_override.numel() == 1)):
+            o = folded_mab1(query, key, valid_kv_len, num_heads, in_proj_weight, in_proj_bias, ssmax_layer,
+                            src_len_override)
+            if o is not None:
+                return F.linear(o, out_proj_weight, out_proj_bias)
         if (_HXQ and isinstance(valid_kv_len, Tensor) and not torch.is_grad_enabled() and cached_kv is None
                 and not need_kv and key is not None and key is value and rope is None and attn_mask is None
                 and key_padding_mask is None and hd <= _MAX_HEAD_DIM and on_gpu

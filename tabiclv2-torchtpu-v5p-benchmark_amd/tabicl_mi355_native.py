@@ -31,6 +31,8 @@ SIGNATURES = {
                            _f32, _i32, _c_p],
     "tabicl_pk_cross_fwd": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
                             _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_p],
+    "tabicl_hxf_fwd": [_c_p, _i64, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _c_p, _i64, _c_p],
+    "tabicl_hxf_workspace_bytes": [_i64, _i64, _i64, _i64, _i32],
     "tabicl_smallhead_bwd_workspace_bytes": [_i64, _i64, _i64, _i32],
     "tabicl_hx_bwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32,
                       _i32, _c_p, _i64, _c_p],
@@ -49,7 +51,7 @@ SIGNATURES = {
 }
 _RESTYPES = {"tabicl_attn_last_error": ctypes.c_char_p, "tabicl_attn_version": ctypes.c_char_p,
              "tabicl_icl_workspace_bytes": ctypes.c_int64, "tabicl_hxq_workspace_bytes": ctypes.c_int64,
-             "tabicl_smallhead_bwd_workspace_bytes": ctypes.c_int64}
+             "tabicl_smallhead_bwd_workspace_bytes": ctypes.c_int64, "tabicl_hxf_workspace_bytes": ctypes.c_int64}
 
 
 class NativeLibraryError(RuntimeError):

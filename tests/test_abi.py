@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     import tabicl_mi355_native as nat
     lib = nat.load()
     names = _declared()
-    assert len(names) == 15, names
+    assert len(names) == 17, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in nat.SIGNATURES, name

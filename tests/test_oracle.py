@@ -324,3 +324,34 @@ def test_pk_cross_bwd_matches_autograd(shared_q):
     assert dq.shape == q.shape
     np.testing.assert_allclose(dq, qt.grad.numpy(), rtol=0, atol=1e-11)
     np.testing.assert_allclose(dkv, kvt.grad.numpy(), rtol=0, atol=1e-11)
+
+
+def test_folding_identity_matches_unfolded_attention():
+    # the algebra the folded first ISAB attention rests on (reference scripts/tabicl_tpu_mha.py:60-92):
+    # softmax(q_g K_g^T) V_g == softmax((q_g W_k,g) x^T) x W_v,g^T + b_v,g  (q_g . b_k,g drops out of
+    # the softmax; rows of P sum to 1)
+    rng = np.random.default_rng(26)
+    B, Lq, Lk, valid, hd = 2, 5, 11, 8, E // H
+    ind = _rand(rng, Lq, E, scale=0.5)
+    x = _rand(rng, B, Lk, E)
+    W = _rand(rng, 3 * E, E, scale=E ** -0.5)
+    b = _rand(rng, 3 * E, scale=0.1)
+    ref = O.folded_mab1_ref(ind, x, valid, H, W, b)
+    q = (ind @ W[:E].T + b[:E]) * hd ** -0.5
+    qf = np.concatenate([q[:, g * hd:(g + 1) * hd] @ W[E + g * hd:E + (g + 1) * hd] for g in range(H)])  # [H*Lq, E]
+    u = O.hxf_ref(qf[None], x, valid)  # [B, H*Lq, E]
+    out = np.zeros((B, Lq, E))
+    for g in range(H):
+        wv = W[2 * E + g * hd:2 * E + (g + 1) * hd]
+        out[..., g * hd:(g + 1) * hd] = u[:, g * Lq:(g + 1) * Lq] @ wv.T + b[2 * E + g * hd:2 * E + (g + 1) * hd]
+    np.testing.assert_allclose(out, ref, rtol=0, atol=1e-10)
+
+
+def test_hxf_ref_valid_and_shared_query():
+    rng = np.random.default_rng(27)
+    qf = _rand(rng, 1, 6, E, scale=0.1)
+    x = _rand(rng, 3, 9, E)
+    got = O.hxf_ref(qf, x, np.array([9, 4, 0]))
+    np.testing.assert_allclose(got[1], O.hxf_ref(qf, x[1:2, :4], 4)[0], rtol=0, atol=1e-12)
+    assert np.abs(got[2]).max() == 0
+    np.testing.assert_allclose(got[0], O.attention_loops(qf, x[:1], x[:1], 1)[0], rtol=0, atol=1e-12)
