@@ -238,6 +238,54 @@ def bench_train(steps: int, warmup: int) -> list:
     return recs
 
 
+def bench_hxf(steps: int, warmup: int) -> list:
+    """The reference's folded first-ISAB benchmark (scripts/tests/test_pallas_attn.py:321-362, shape
+    infer_tile54 :368): folded_mab1 (K projection folded into the 1024 queries, U = softmax(Qf x^T) x,
+    d = 128) against the packed K/V projection + hxq route, forward only, fp32 and bf16."""
+    import torch
+    from torch.nn import functional as F
+
+    import tabicl_mi355_attn as pk
+    import tabicl_mi355_mha as mha
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    E, H, B, Lq, Lk, valid = 128, 8, 54, 128, 53248, 45000
+    recs = []
+    for dt, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        ind = (torch.randn(Lq, E, generator=g, device=dev) * 0.5).to(dt)
+        x = torch.randn(B, Lk, E, generator=g, device=dev).to(dt)
+        W = (torch.randn(3 * E, E, generator=g, device=dev) * E ** -0.5).to(dt)
+        b = (torch.randn(3 * E, generator=g, device=dev) * 0.1).to(dt)
+        vt = torch.tensor(valid, device=dev)
+
+        def folded():
+            return mha.folded_mab1(ind.expand(B, Lq, E), x, vt, H, W, b, None, None, pk=pk)
+
+        def unfolded():
+            q = F.linear(ind, W[:E], b[:E]) * (E // H) ** -0.5
+            kv = F.linear(x, W[E:], b[E:])
+            return pk.hxq_attention(q.expand(B, Lq, E), kv, vt, H)
+
+        with torch.no_grad():
+            ms_f = _time(folded, steps, warmup)
+            ms_u = _time(unfolded, steps, warmup)
+        tf = 4.0 * H * Lq * valid * E * B / (ms_f * 1e-3) / 1e12
+        peak = 157.3 if dt == torch.float32 else PEAK_BF16_TFLOPS
+        for label, ms in (("folded (hxf)", ms_f), ("projection + hxq", ms_u)):
+            rec = {"metric": f"ms per column ISAB-1 {label} pass, {name}", "value": round(ms, 4), "unit": "ms",
+                   "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False, "vs_baseline": None,
+                   "dtype": name, "data": "synthetic (reference _mab1_inputs scales)",
+                   "config": {"workload": "54 x 128 inducing queries over 45000 of 53248 rows, 8x16, E=128"}}
+            if label.startswith("folded"):
+                rec["attn_tflops"] = round(tf, 2)
+                rec["roofline"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+                                   "frac": round(tf / peak, 4)}
+            recs.append(rec)
+        del x
+    return recs
+
+
 C5_BUCKETS = (1024, 2048, 4096, 8192, 16384)
 
 
@@ -350,8 +398,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5, train (comma-separated) or all "
-                         "print the other BASELINE configs' lines and the fwd+bwd training lines")
+                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf (comma-separated) or "
+                         "all print the other BASELINE configs' lines, the fwd+bwd training lines and the folded "
+                         "first-ISAB lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -361,7 +410,7 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
@@ -370,6 +419,8 @@ def main() -> int:
             recs += bench_c5(args.steps, args.warmup)
         if configs & {"train", "all"}:
             recs += bench_train(args.steps, args.warmup)
+        if configs & {"hxf", "all"}:
+            recs += bench_hxf(args.steps, args.warmup)
         for rec in recs:
             print(json.dumps(rec), flush=True)
         return 0
