@@ -134,6 +134,42 @@ __device__ __forceinline__ f32x4 rope4(const T* row, const float* cs, const floa
   return y;
 }
 
+// rope4 with fast paths for the full-width rotations (rot = 16): halves (partner chunk d0 ^ 8) and
+// pairs (partner inside the chunk); other forms through rope4.
+template <typename T>
+__device__ __forceinline__ f32x4 rope4_fast(const T* row, const float* cs, const float* sn, int d0, int rope,
+                                            int half, int rot) {
+  typedef typename OpVec<T, 4>::type Op4;
+  if (rope == 2 && half == 8 && rot == 16) {
+    const Op4 own = *(const Op4*)(row + d0);
+    const Op4 pt = *(const Op4*)(row + (d0 ^ 8));
+    const float4 c = *(const float4*)(cs + d0);
+    const float4 s = *(const float4*)(sn + d0);
+    const float cv[4] = {c.x, c.y, c.z, c.w};
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+    const float sg = (d0 & 8) ? 1.f : -1.f;
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = to_f32<T>(own[r]) * cv[r] + sg * to_f32<T>(pt[r]) * sv[r];
+    return y;
+  }
+  if (rope == 1 && rot == 16) {
+    const Op4 own = *(const Op4*)(row + d0);
+    const float4 c = *(const float4*)(cs + d0);
+    const float4 s = *(const float4*)(sn + d0);
+    const float cv[4] = {c.x, c.y, c.z, c.w};
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float xp = to_f32<T>(own[r ^ 1]);
+      y[r] = to_f32<T>(own[r]) * cv[r] + ((r & 1) ? xp : -xp) * sv[r];
+    }
+    return y;
+  }
+  return rope4<T>(row, cs, sn, d0, rope, half, rot);
+}
+
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *(const uint4*)p; }
 
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): LDS[lds_addr + 16 * lane] =

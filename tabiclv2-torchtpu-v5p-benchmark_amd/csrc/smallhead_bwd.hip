@@ -451,8 +451,302 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Short sequences (1 <= Lq, Lk <= 128, bf16): one fused kernel, workgroup = (batch element, group of
+// 4 heads), wave = (head of the group, parity of the 16-row blocks it takes). The group's 64 merged
+// dims of every query and key row are loaded once, with full-row coalesced reads, into LDS (q', k',
+// V, dO; D per query and head from dO and O on the way). Phase 1: per query block the scores of all
+// keys stay in registers (statistics, P, dP, dS, dq'); the statistics go to LDS. Phase 2: per key
+// block, dk' and dv over all query blocks from those statistics. Two workgroups fit one CU.
+// RM: RoPE form, 0 none, 1 pairs over all 16 dims, 2 halves over all 16 dims (rot = 16).
+// ---------------------------------------------------------------------------------------------
+constexpr int SS_HG = 4;               // heads per workgroup
+constexpr int SS_W = SS_HG * SB_D;     // merged dims per workgroup
+constexpr int SS_STR = SS_W + 4;       // LDS row stride, elements
+constexpr int SS_ROWS = 128;
+constexpr int SS_NT = 8 * 64;          // threads
+
+struct SsLds {
+  bf16 q[SS_ROWS * SS_STR];  // q' = cast(rope(q) scale)
+  bf16 k[SS_ROWS * SS_STR];  // k' = cast(rope(k))
+  bf16 v[SS_ROWS * SS_STR];
+  bf16 d[SS_ROWS * SS_STR];  // dO
+  float mx[SS_HG][SS_ROWS];  // per head and query: row maximum (log2 units), +inf past Lq
+  float lg[SS_HG][SS_ROWS];  // log2 of the row sum
+  float dd[SS_HG][SS_ROWS];  // D
+  float b2[SS_ROWS];         // per key: additive term, log2 units, -inf past Lk
+};
+
+// RoPE of a 4-dim chunk (chunk index c4 = (dim within the head) / 4) in the fill: pairs in-lane,
+// halves from the partner chunk c4 ^ 2, held by lane ^ 2.
+template <int RM>
+__device__ __forceinline__ f32x4 ss_rope_fwd(bf16x4 x, float4 c, float4 s, int c4) {
+  f32x4 y;
+  const float cv[4] = {c.x, c.y, c.z, c.w};
+  const float sv[4] = {s.x, s.y, s.z, s.w};
+  if constexpr (RM == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = (float)x[r];
+  } else if constexpr (RM == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float xp = (float)x[r ^ 1];
+      y[r] = (float)x[r] * cv[r] + ((r & 1) ? xp : -xp) * sv[r];
+    }
+  } else {
+    const uint2 u = __builtin_bit_cast(uint2, x);
+    const uint2 w = {(uint32_t)__shfl_xor((int)u.x, 2, 64), (uint32_t)__shfl_xor((int)u.y, 2, 64)};
+    const bf16x4 xp = __builtin_bit_cast(bf16x4, w);
+    const float sg = (c4 & 2) ? 1.f : -1.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = (float)x[r] * cv[r] + sg * (float)xp[r] * sv[r];
+  }
+  return y;
+}
+
+// rope_bwd of dims 4 kap .. 4 kap + 3 of one head row in the MFMA result layout; cs / sn point at
+// dim 0 of the head in the row's table row. Halves: the partner dims sit in lane ^ 32.
+template <int RM>
+__device__ __forceinline__ f32x4 ss_rope_bwd(f32x4 y, const float* cs, const float* sn, int kap) {
+  if constexpr (RM == 0) return y;
+  const float4 c = *(const float4*)(cs + 4 * kap);
+  const float cv[4] = {c.x, c.y, c.z, c.w};
+  f32x4 out;
+  if constexpr (RM == 1) {
+    const float4 s = *(const float4*)(sn + 4 * kap);
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float sg = (r & 1) ? 1.f : -1.f;
+      out[r] = y[r] * cv[r] - sg * y[r ^ 1] * sv[r ^ 1];
+    }
+  } else {
+    const float4 s = *(const float4*)(sn + 4 * (kap ^ 2));
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+    const float sg = (kap & 2) ? 1.f : -1.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[r] = y[r] * cv[r] - sg * __shfl_xor(y[r], 32, 64) * sv[r];
+  }
+  return out;
+}
+
+// Transposed operand from a row-major LDS tile: A[i][4 kap + j] = tile[row0 + 4 kap + j][col0 + i]
+// for lane (i = l16, kap), with ds_read_b64_tr_b16.
+__device__ __forceinline__ bf16x4 ss_opT(const bf16* tile, int row0, int col0, int l16, int kap) {
+  const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)(tile + (row0 + 4 * kap + (l16 >> 2)) * SS_STR + col0 + 4 * (l16 & 3)));
+  return __builtin_bit_cast(bf16x4, t);
+}
+
+__device__ __forceinline__ bf16x4 ss_row4(const bf16* tile, int row, int col) {
+  return *(const bf16x4*)(tile + row * SS_STR + col);
+}
+
+template <int RM>
+__global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
+  __shared__ __attribute__((aligned(16))) SsLds sh;
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int hg = work % (SB_H / SS_HG), b = work / (SB_H / SS_HG);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nqb = (p.Lq + 15) >> 4, nkb = (p.Lk + 15) >> 4;
+  const int nq16 = nqb * 16, nk16 = nkb * 16;
+
+  // ---- fill: thread = (row of a 32-row pass, 4-dim chunk c); two passes per round for loads in flight
+  {
+    const int c = tid & 15, r0 = tid >> 4;
+    const int dl = 4 * c, dg = hg * SS_W + dl;
+    const bf16* qbase = (const bf16*)p.q + b * p.q_sb + dg;
+    const bf16* kbase = (const bf16*)p.k + b * p.k_sb + dg;
+    const bf16* vbase = (const bf16*)p.v + b * p.v_sb + dg;
+    const bf16* obase = (const bf16*)p.o + (int64_t)b * p.Lq * SB_E + dg;
+    const bf16* dbase = (const bf16*)p.dout + (int64_t)b * p.Lq * SB_E + dg;
+    const int nmax = nq16 > nk16 ? nq16 : nk16;
+    for (int i0 = 0; 32 * i0 < nmax; i0 += 2) {
+      bf16x4 qx[2], ox[2], dx[2], kx[2], vx[2];
+      float4 qc[2], qs[2], kc[2], ks[2];
+      int rq[2], rk[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {  // loads only, clamped to valid rows
+        const int row = r0 + 32 * (i0 + u);
+        rq[u] = row < p.Lq ? row : p.Lq - 1;
+        rk[u] = row < p.Lk ? row : p.Lk - 1;
+        qx[u] = *(const bf16x4*)(qbase + (int64_t)rq[u] * p.q_sr);
+        ox[u] = *(const bf16x4*)(obase + (int64_t)rq[u] * SB_E);
+        dx[u] = *(const bf16x4*)(dbase + (int64_t)rq[u] * SB_E);
+        kx[u] = *(const bf16x4*)(kbase + (int64_t)rk[u] * p.k_sr);
+        vx[u] = *(const bf16x4*)(vbase + (int64_t)rk[u] * p.v_sr);
+        if constexpr (RM != 0) {
+          qc[u] = *(const float4*)(p.cq + (int64_t)rq[u] * SB_E + dg);
+          qs[u] = *(const float4*)(p.sq + (int64_t)rq[u] * SB_E + dg);
+          kc[u] = *(const float4*)(p.ck + (int64_t)rk[u] * SB_E + dg);
+          ks[u] = *(const float4*)(p.sk + (int64_t)rk[u] * SB_E + dg);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int row = r0 + 32 * (i0 + u);
+        const bool qok = row < p.Lq, kok = row < p.Lk;
+        const f32x4 yq = ss_rope_fwd<RM>(qx[u], qc[u], qs[u], c & 3);
+        const f32x4 yk = ss_rope_fwd<RM>(kx[u], kc[u], ks[u], c & 3);
+        bf16x4 qq, kk, vv, dd;
+        float part = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          qq[r] = qok ? (bf16)(yq[r] * p.scale) : (bf16)0.f;
+          dd[r] = qok ? dx[u][r] : (bf16)0.f;
+          kk[r] = kok ? (bf16)yk[r] : (bf16)0.f;
+          vv[r] = kok ? vx[u][r] : (bf16)0.f;
+          part += (float)dd[r] * (qok ? (float)ox[u][r] : 0.f);
+        }
+        part += __shfl_xor(part, 1, 64);  // the 4 chunks of one head: lanes c ^ 1, c ^ 2
+        part += __shfl_xor(part, 2, 64);
+        if (row < nq16) {
+          *(bf16x4*)(sh.q + row * SS_STR + dl) = qq;
+          *(bf16x4*)(sh.d + row * SS_STR + dl) = dd;
+          if ((c & 3) == 0) sh.dd[c >> 2][row] = part;
+        }
+        if (row < nk16) {
+          *(bf16x4*)(sh.k + row * SS_STR + dl) = kk;
+          *(bf16x4*)(sh.v + row * SS_STR + dl) = vv;
+        }
+      }
+    }
+    for (int j = tid; j < nk16; j += SS_NT) sh.b2[j] = sb_b2(p, b, j);
+  }
+  __syncthreads();
+
+  const int gl = wave & (SS_HG - 1), par = wave / SS_HG;  // head within the group, block parity
+  const int l16 = lane & 15, kap = lane >> 4;
+  const int hd = gl * SB_D;                    // the head's first dim in the group
+  const int dglob = hg * SS_W + hd + 4 * kap;  // merged dim of this lane's 4 output dims
+
+  // ---- phase 1: per query block, statistics, dq
+  for (int qb = par; qb < nqb; qb += 2) {
+    const int qr = 16 * qb + l16;
+    const bf16x4 qop = ss_row4(sh.q, qr, hd + 4 * kap);
+    const bf16x4 dop = ss_row4(sh.d, qr, hd + 4 * kap);
+    const float dsum = sh.dd[gl][qr];
+    f32x4 x[8];
+    float tm = TA_NEG_INF;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      if (kt < nkb) {
+        x[kt] = mfma16x16x16(ss_row4(sh.k, 16 * kt + l16, hd + 4 * kap), qop, f32x4{0.f, 0.f, 0.f, 0.f});
+        const f32x4 b2 = *(const f32x4*)(sh.b2 + 16 * kt + 4 * kap);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[kt][r] = fmaf(x[kt][r], TA_LOG2E, b2[r]);
+          tm = fmaxf(tm, x[kt][r]);
+        }
+      }
+    }
+    const float m = quad_max(tm);  // finite: key 0 exists
+    float l = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      if (kt < nkb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[kt][r] = __builtin_amdgcn_exp2f(x[kt][r] - m);
+          l += x[kt][r];
+        }
+      }
+    }
+    l = quad_sum(l);  // >= 1
+    const float inv = __builtin_amdgcn_rcpf(l);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      if (kt < nkb) {
+        const f32x4 dp = mfma16x16x16(ss_row4(sh.v, 16 * kt + l16, hd + 4 * kap), dop, f32x4{0.f, 0.f, 0.f, 0.f});
+        bf16x4 ds;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ds[r] = (bf16)(x[kt][r] * inv * (dp[r] - dsum));
+        acc = mfma16x16x16(ss_opT(sh.k, 16 * kt, hd, l16, kap), ds, acc);
+      }
+    }
+    if (kap == 0) {
+      sh.mx[gl][qr] = qr < p.Lq ? m : __builtin_inff();
+      sh.lg[gl][qr] = __builtin_amdgcn_logf(l);
+    }
+    f32x4 y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
+    const int qc = qr < p.Lq ? qr : 0;
+    y = ss_rope_bwd<RM>(y, p.cq + (int64_t)qc * SB_E + hg * SS_W + hd, p.sq + (int64_t)qc * SB_E + hg * SS_W + hd,
+                        kap);
+    if (qr < p.Lq) {
+      bf16x4 out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[r] = (bf16)y[r];
+      *(bf16x4*)((bf16*)p.dq + b * p.dq_sb + (int64_t)qr * p.dq_sr + dglob) = out;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: per key block, dk and dv over every query block
+  for (int kb = par; kb < nkb; kb += 2) {
+    const int kr = 16 * kb + l16;
+    const bf16x4 kop = ss_row4(sh.k, kr, hd + 4 * kap);
+    const bf16x4 vop = ss_row4(sh.v, kr, hd + 4 * kap);
+    const float b2 = sh.b2[kr];
+    f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
+    for (int qs = 0; qs < nqb; ++qs) {
+      // S[query 16 qs + 4 kap + r][key kr], dP likewise
+      const f32x4 s = mfma16x16x16(ss_row4(sh.q, 16 * qs + l16, hd + 4 * kap), kop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 dp = mfma16x16x16(ss_row4(sh.d, 16 * qs + l16, hd + 4 * kap), vop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 ms = *(const f32x4*)(&sh.mx[gl][16 * qs + 4 * kap]);
+      const f32x4 ls = *(const f32x4*)(&sh.lg[gl][16 * qs + 4 * kap]);
+      const f32x4 dq = *(const f32x4*)(&sh.dd[gl][16 * qs + 4 * kap]);
+      bf16x4 pt, ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2) - ms[r]) - ls[r]);
+        pt[r] = (bf16)pr;
+        ds[r] = (bf16)(pr * (dp[r] - dq[r]));
+      }
+      dv = mfma16x16x16(ss_opT(sh.d, 16 * qs, hd, l16, kap), pt, dv);
+      dk = mfma16x16x16(ss_opT(sh.q, 16 * qs, hd, l16, kap), ds, dk);
+    }
+    const int kc = kr < p.Lk ? kr : 0;
+    const f32x4 y = ss_rope_bwd<RM>(dk, p.ck + (int64_t)kc * SB_E + hg * SS_W + hd,
+                                    p.sk + (int64_t)kc * SB_E + hg * SS_W + hd, kap);
+    if (kr < p.Lk) {
+      bf16x4 ok, ov;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ok[r] = (bf16)y[r];
+        ov[r] = (bf16)dv[r];
+      }
+      *(bf16x4*)((bf16*)p.dk + b * p.dk_sb + (int64_t)kr * p.dk_sr + dglob) = ok;
+      *(bf16x4*)((bf16*)p.dv + b * p.dv_sb + (int64_t)kr * p.dv_sr + dglob) = ov;
+    }
+  }
+}
+
+// The fused short kernel's RoPE form for these parameters, or -1 when it does not cover them.
+int ss_mode(const SbParams& p) {
+  if (p.rope == 0) return 0;
+  if (p.rope == 1 && p.rot == 16) return 1;
+  if (p.rope == 2 && p.half == 8 && p.rot == 16) return 2;
+  return -1;
+}
+
 template <typename T>
 void launch_bwd(SbParams p, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2) {
+    const int rm = ss_mode(p);
+    if (p.Lq >= 1 && p.Lk >= 1 && p.Lq <= SS_ROWS && p.Lk <= SS_ROWS && rm >= 0) {
+      const dim3 grid((unsigned)(p.B * (SB_H / SS_HG)));
+      if (rm == 0)
+        hipLaunchKernelGGL((ss_bwd_kernel<0>), grid, dim3(SS_NT), 0, stream, p);
+      else if (rm == 1)
+        hipLaunchKernelGGL((ss_bwd_kernel<1>), grid, dim3(SS_NT), 0, stream, p);
+      else
+        hipLaunchKernelGGL((ss_bwd_kernel<2>), grid, dim3(SS_NT), 0, stream, p);
+      return;
+    }
+  }
   const int64_t nqb = (p.Lq + SB_QB - 1) / SB_QB, nkb = (p.Lk + SB_KB - 1) / SB_KB;
   // keys in one tile: runs of query blocks per workgroup (one fill each), still >= ~16 workgroups
   // per CU over the grid

@@ -292,33 +292,6 @@ constexpr int RS_VSTR = SH_E + 16;  // V rows of 288 B: the transposed reads of 
 constexpr float RS_L_HI = 0x1p64f;
 constexpr float RS_L_LO = 0x1p-64f;
 
-// RoPE of dims d0..d0+3 of one bf16 row (fp32 math). Fast paths for the full-width rotations
-// (rot = 16): halves (partner chunk d0 ^ 8) and pairs (partner inside the chunk).
-__device__ __forceinline__ f32x4 rope4_bf16(const bf16* row, const float* cs, const float* sn, int d0,
-                                            int rope, int half, int rot) {
-  const bf16x4 own = *(const bf16x4*)(row + d0);
-  const float4 c = *(const float4*)(cs + d0);
-  const float4 s = *(const float4*)(sn + d0);
-  const float cv[4] = {c.x, c.y, c.z, c.w};
-  const float sv[4] = {s.x, s.y, s.z, s.w};
-  f32x4 y;
-  if (rope == 2 && half == 8 && rot == 16) {
-    const bf16x4 pt = *(const bf16x4*)(row + (d0 ^ 8));
-    const float sg = (d0 & 8) ? 1.f : -1.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = (float)own[r] * cv[r] + sg * (float)pt[r] * sv[r];
-  } else if (rope == 1 && rot == 16) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float xp = (float)own[r ^ 1];
-      y[r] = (float)own[r] * cv[r] + ((r & 1) ? xp : -xp) * sv[r];
-    }
-  } else {
-    y = rope4<bf16>(row, cs, sn, d0, rope, half, rot);
-  }
-  return y;
-}
-
 // This lane's 8 dims of q (those of its B-operand k-slots) at byte offset off of the workgroup's q
 // rows. A buffer load: rows past Lq lie outside the resource and read as zero, and the compiler
 // keeps a load issued ahead of its use where it is (it does not merge these into the loop's phi).
@@ -468,7 +441,7 @@ __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[
   } else if (EXACT) {
     bf16x4 y4 = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
     if (qi < p.Lq) {
-      const f32x4 y = rope4_bf16(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
+      const f32x4 y = rope4_fast<bf16>(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
                                  p.sq + (int64_t)qi * SH_E, d4, p.rope, p.half, p.rot);
 #pragma unroll
       for (int j = 0; j < 4; ++j) y4[j] = (bf16)y[j];  // bf16(rope(q) scale) = bf16(rope(q)) scale
@@ -481,7 +454,7 @@ __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[
 #pragma unroll
       for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)((float)qr[(G >> 1) * 4 + j] * p.scale);
     } else if (qi < p.Lq) {
-      const f32x4 y = rope4_bf16(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
+      const f32x4 y = rope4_fast<bf16>(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
                                  p.sq + (int64_t)qi * SH_E, d4, p.rope, p.half, p.rot);
 #pragma unroll
       for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
@@ -542,7 +515,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
       if (key < lk) {
         const bf16* src = kbase + (int64_t)key * p.k_sr;
         if (ROPE) {
-          const f32x4 y = rope4_bf16(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0, p.rope,
+          const f32x4 y = rope4_fast<bf16>(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0, p.rope,
                                      p.half, p.rot);
 #pragma unroll
           for (int r = 0; r < 4; ++r) val[r] = (bf16)y[r];

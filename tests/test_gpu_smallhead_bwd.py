@@ -66,6 +66,11 @@ def _rope_np(rope, L):
     ("cls_bf16", 16, 4, 104, torch.bfloat16, False),
     ("long_keys_bf16", 2, 200, 3000, torch.bfloat16, True),   # past the reference's 1024-key limit
     ("long_keys_fp32", 2, 70, 1500, torch.float32, False),
+    # fused short-sequence kernel (both lengths <= 128, bf16): edges of its range
+    ("short_max_bf16_bias", 5, 128, 128, torch.bfloat16, True),
+    ("short_one_bf16", 3, 1, 1, torch.bfloat16, False),
+    ("short_ragged_bf16_bias", 7, 33, 77, torch.bfloat16, True),
+    ("short_keys_past_128_bf16", 3, 40, 129, torch.bfloat16, False),
 ])
 def test_hx_bwd(dev, name, B, Lq, Lk, dtype, bias):
     pk = _attn()
@@ -94,6 +99,8 @@ def test_hx_bwd(dev, name, B, Lq, Lk, dtype, bias):
     ("self_fp32_rope_halves_bias", 16, 108, torch.float32, False, True),
     ("self_fp32_rope_pairs", 8, 104, torch.float32, True, False),
     ("self_bf16_norope_long", 2, 700, torch.bfloat16, None, False),
+    ("self_bf16_rope_pairs", 8, 104, torch.bfloat16, True, False),
+    ("self_bf16_rope_halves_bias_128", 4, 128, torch.bfloat16, False, True),
 ])
 def test_pk_self_bwd(dev, name, B, L, dtype, interleaved, bias):
     pk = _attn()
@@ -120,6 +127,8 @@ def test_pk_self_bwd(dev, name, B, L, dtype, interleaved, bias):
     ("cross_col2_fp32", 2, 4096, 128, torch.float32, None, False),
     ("cross_shared_q_bf16", 6, 128, 300, torch.bfloat16, None, True),   # ISAB inducing points
     ("cross_shared_q_fp32_rope", 3, 16, 50, torch.float32, True, True),
+    ("cross_shared_q_bf16_short", 6, 128, 100, torch.bfloat16, None, True),
+    ("cross_shared_q_bf16_rope_pairs", 3, 16, 50, torch.bfloat16, True, True),
 ])
 def test_pk_cross_bwd(dev, name, B, Lq, Lk, dtype, interleaved, shared_q):
     pk = _attn()
