@@ -52,6 +52,16 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f32x8 a, f32x8 b, f32x16 c) {
 }
 
 template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+// Four fp32 values to bf16 (round to nearest even), converted in pairs (v_cvt_pk_bf16_f32); built
+// from two packed halves so that the compiler does not convert element by element and repack.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x4 cvt_bf16x4(f32x4 x) {
+  const bf16x2 lo = __builtin_convertvector(f32x2{x[0], x[1]}, bf16x2);
+  const bf16x2 hi = __builtin_convertvector(f32x2{x[2], x[3]}, bf16x2);
+  const uint2 u = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+  return __builtin_bit_cast(bf16x4, u);
+}
 template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
 
 // Max / sum across the lane pairs (l, l^32) and quads (l, l^16, l^32, l^48).

@@ -472,7 +472,7 @@ struct SsLds {
   bf16 v[SS_ROWS * SS_STR];
   bf16 d[SS_ROWS * SS_STR];  // dO
   float mx[SS_HG][SS_ROWS];  // per head and query: row maximum (log2 units), +inf past Lq
-  float lg[SS_HG][SS_ROWS];  // log2 of the row sum
+  float lg[SS_HG][SS_ROWS];  // log2 of the row sum (with a key bias; else mx holds -(m + lg), -inf past Lq)
   float dd[SS_HG][SS_ROWS];  // D
   float b2[SS_ROWS];         // per key: additive term, log2 units, -inf past Lk
 };
@@ -542,7 +542,7 @@ __device__ __forceinline__ bf16x4 ss_row4(const bf16* tile, int row, int col) {
   return *(const bf16x4*)(tile + row * SS_STR + col);
 }
 
-template <int RM>
+template <int RM, bool HB>
 __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
   __shared__ __attribute__((aligned(16))) SsLds sh;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
@@ -551,64 +551,62 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
   const int nqb = (p.Lq + 15) >> 4, nkb = (p.Lk + 15) >> 4;
   const int nq16 = nqb * 16, nk16 = nkb * 16;
 
-  // ---- fill: thread = (row of a 32-row pass, 4-dim chunk c); two passes per round for loads in flight
+  // ---- fill: thread = (row of a 32-row pass, 4-dim chunk c); two passes per round for loads in
+  // flight. Rows past Lq / Lk hold the last valid row (clamped): a padded query gets P = 0 in phase 2
+  // (its statistic is +inf), a padded key gets P = 0 in phase 1 (b2 = -inf) and is not stored, so
+  // their finite values contribute nothing. Buffer loads with 32-bit byte offsets from the batch
+  // element's base (the launcher checks that every offset fits).
   {
     const int c = tid & 15, r0 = tid >> 4;
     const int dl = 4 * c, dg = hg * SS_W + dl;
-    const bf16* qbase = (const bf16*)p.q + b * p.q_sb + dg;
-    const bf16* kbase = (const bf16*)p.k + b * p.k_sb + dg;
-    const bf16* vbase = (const bf16*)p.v + b * p.v_sb + dg;
-    const bf16* obase = (const bf16*)p.o + (int64_t)b * p.Lq * SB_E + dg;
-    const bf16* dbase = (const bf16*)p.dout + (int64_t)b * p.Lq * SB_E + dg;
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.q + b * p.q_sb, 0, p.Lq * (int)p.q_sr * 2, TA_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.k + b * p.k_sb, 0, p.Lk * (int)p.k_sr * 2, TA_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.v + b * p.v_sb, 0, p.Lk * (int)p.v_sr * 2, TA_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.o + (int64_t)b * p.Lq * SB_E, 0, p.Lq * SB_E * 2, TA_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.dout + (int64_t)b * p.Lq * SB_E, 0, p.Lq * SB_E * 2, TA_BUF_WORD3);
     const int nmax = nq16 > nk16 ? nq16 : nk16;
     for (int i0 = 0; 32 * i0 < nmax; i0 += 2) {
       bf16x4 qx[2], ox[2], dx[2], kx[2], vx[2];
       float4 qc[2], qs[2], kc[2], ks[2];
-      int rq[2], rk[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {  // loads only, clamped to valid rows
+      for (int u = 0; u < 2; ++u) {  // loads only
         const int row = r0 + 32 * (i0 + u);
-        rq[u] = row < p.Lq ? row : p.Lq - 1;
-        rk[u] = row < p.Lk ? row : p.Lk - 1;
-        qx[u] = *(const bf16x4*)(qbase + (int64_t)rq[u] * p.q_sr);
-        ox[u] = *(const bf16x4*)(obase + (int64_t)rq[u] * SB_E);
-        dx[u] = *(const bf16x4*)(dbase + (int64_t)rq[u] * SB_E);
-        kx[u] = *(const bf16x4*)(kbase + (int64_t)rk[u] * p.k_sr);
-        vx[u] = *(const bf16x4*)(vbase + (int64_t)rk[u] * p.v_sr);
+        const int rq = row < p.Lq ? row : p.Lq - 1, rk = row < p.Lk ? row : p.Lk - 1;
+        const int oq = (rq * SB_E + dg) * 2;
+        qx[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(qrs, (rq * (int)p.q_sr + dg) * 2, 0, 0));
+        ox[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(ors, oq, 0, 0));
+        dx[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(drs, oq, 0, 0));
+        kx[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(krs, (rk * (int)p.k_sr + dg) * 2, 0, 0));
+        vx[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(vrs, (rk * (int)p.v_sr + dg) * 2, 0, 0));
         if constexpr (RM != 0) {
-          qc[u] = *(const float4*)(p.cq + (int64_t)rq[u] * SB_E + dg);
-          qs[u] = *(const float4*)(p.sq + (int64_t)rq[u] * SB_E + dg);
-          kc[u] = *(const float4*)(p.ck + (int64_t)rk[u] * SB_E + dg);
-          ks[u] = *(const float4*)(p.sk + (int64_t)rk[u] * SB_E + dg);
+          qc[u] = *(const float4*)(p.cq + rq * SB_E + dg);
+          qs[u] = *(const float4*)(p.sq + rq * SB_E + dg);
+          kc[u] = *(const float4*)(p.ck + rk * SB_E + dg);
+          ks[u] = *(const float4*)(p.sk + rk * SB_E + dg);
         }
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int row = r0 + 32 * (i0 + u);
-        const bool qok = row < p.Lq, kok = row < p.Lk;
+        const int row = r0 + 32 * (i0 + u);  // < 128: the loop covers at most 128 rows
         const f32x4 yq = ss_rope_fwd<RM>(qx[u], qc[u], qs[u], c & 3);
-        const f32x4 yk = ss_rope_fwd<RM>(kx[u], kc[u], ks[u], c & 3);
-        bf16x4 qq, kk, vv, dd;
         float part = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          qq[r] = qok ? (bf16)(yq[r] * p.scale) : (bf16)0.f;
-          dd[r] = qok ? dx[u][r] : (bf16)0.f;
-          kk[r] = kok ? (bf16)yk[r] : (bf16)0.f;
-          vv[r] = kok ? vx[u][r] : (bf16)0.f;
-          part += (float)dd[r] * (qok ? (float)ox[u][r] : 0.f);
-        }
+        for (int r = 0; r < 4; ++r) part += (float)dx[u][r] * (float)ox[u][r];
         part += __shfl_xor(part, 1, 64);  // the 4 chunks of one head: lanes c ^ 1, c ^ 2
         part += __shfl_xor(part, 2, 64);
-        if (row < nq16) {
-          *(bf16x4*)(sh.q + row * SS_STR + dl) = qq;
-          *(bf16x4*)(sh.d + row * SS_STR + dl) = dd;
-          if ((c & 3) == 0) sh.dd[c >> 2][row] = part;
-        }
-        if (row < nk16) {
-          *(bf16x4*)(sh.k + row * SS_STR + dl) = kk;
-          *(bf16x4*)(sh.v + row * SS_STR + dl) = vv;
-        }
+        *(bf16x4*)(sh.q + row * SS_STR + dl) = cvt_bf16x4(yq * p.scale);
+        *(bf16x4*)(sh.d + row * SS_STR + dl) = dx[u];
+        if ((c & 3) == 0) sh.dd[c >> 2][row] = part;
+        if constexpr (RM != 0)
+          *(bf16x4*)(sh.k + row * SS_STR + dl) = cvt_bf16x4(ss_rope_fwd<RM>(kx[u], kc[u], ks[u], c & 3));
+        else
+          *(bf16x4*)(sh.k + row * SS_STR + dl) = kx[u];
+        *(bf16x4*)(sh.v + row * SS_STR + dl) = vx[u];
       }
     }
     for (int j = tid; j < nk16; j += SS_NT) sh.b2[j] = sb_b2(p, b, j);
@@ -620,7 +618,8 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
   const int hd = gl * SB_D;                    // the head's first dim in the group
   const int dglob = hg * SS_W + hd + 4 * kap;  // merged dim of this lane's 4 output dims
 
-  // ---- phase 1: per query block, statistics, dq
+  // ---- phase 1: per query block, statistics, dq. Without a key bias the scores are reduced raw
+  // (b2 only masks the padded keys of the last block) and the log2e factor goes into the exponent's fma.
   for (int qb = par; qb < nqb; qb += 2) {
     const int qr = 16 * qb + l16;
     const bf16x4 qop = ss_row4(sh.q, qr, hd + 4 * kap);
@@ -632,42 +631,50 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
     for (int kt = 0; kt < 8; ++kt) {
       if (kt < nkb) {
         x[kt] = mfma16x16x16(ss_row4(sh.k, 16 * kt + l16, hd + 4 * kap), qop, f32x4{0.f, 0.f, 0.f, 0.f});
-        const f32x4 b2 = *(const f32x4*)(sh.b2 + 16 * kt + 4 * kap);
+        if (HB || kt == nkb - 1) {
+          const f32x4 b2 = *(const f32x4*)(sh.b2 + 16 * kt + 4 * kap);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          x[kt][r] = fmaf(x[kt][r], TA_LOG2E, b2[r]);
-          tm = fmaxf(tm, x[kt][r]);
+          for (int r = 0; r < 4; ++r) x[kt][r] = HB ? fmaf(x[kt][r], TA_LOG2E, b2[r]) : x[kt][r] + b2[r];
         }
+        tm = fmaxf(tm, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
       }
     }
-    const float m = quad_max(tm);  // finite: key 0 exists
+    // m: row maximum in log2 units; x -> exp2(x log2e - m) (no bias) or exp2(x - m)
+    const float mraw = quad_max(tm);  // finite: key 0 exists
+    const float m = HB ? mraw : mraw * TA_LOG2E;
     float l = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       if (kt < nkb) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          x[kt][r] = __builtin_amdgcn_exp2f(x[kt][r] - m);
+          x[kt][r] = __builtin_amdgcn_exp2f(HB ? x[kt][r] - m : fmaf(x[kt][r], TA_LOG2E, -m));
           l += x[kt][r];
         }
       }
     }
     l = quad_sum(l);  // >= 1
     const float inv = __builtin_amdgcn_rcpf(l);
+    const float dinv = dsum * inv;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       if (kt < nkb) {
         const f32x4 dp = mfma16x16x16(ss_row4(sh.v, 16 * kt + l16, hd + 4 * kap), dop, f32x4{0.f, 0.f, 0.f, 0.f});
-        bf16x4 ds;
+        f32x4 dsf;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ds[r] = (bf16)(x[kt][r] * inv * (dp[r] - dsum));
-        acc = mfma16x16x16(ss_opT(sh.k, 16 * kt, hd, l16, kap), ds, acc);
+        for (int r = 0; r < 4; ++r) dsf[r] = x[kt][r] * fmaf(dp[r], inv, -dinv);  // P (dP - D)
+        acc = mfma16x16x16(ss_opT(sh.k, 16 * kt, hd, l16, kap), cvt_bf16x4(dsf), acc);
       }
     }
+    const float lg = __builtin_amdgcn_logf(l);
     if (kap == 0) {
-      sh.mx[gl][qr] = qr < p.Lq ? m : __builtin_inff();
-      sh.lg[gl][qr] = __builtin_amdgcn_logf(l);
+      if (HB) {
+        sh.mx[gl][qr] = qr < p.Lq ? m : __builtin_inff();
+        sh.lg[gl][qr] = lg;
+      } else {
+        sh.mx[gl][qr] = qr < p.Lq ? -(m + lg) : TA_NEG_INF;
+      }
     }
     f32x4 y;
 #pragma unroll
@@ -675,51 +682,44 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
     const int qc = qr < p.Lq ? qr : 0;
     y = ss_rope_bwd<RM>(y, p.cq + (int64_t)qc * SB_E + hg * SS_W + hd, p.sq + (int64_t)qc * SB_E + hg * SS_W + hd,
                         kap);
-    if (qr < p.Lq) {
-      bf16x4 out;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) out[r] = (bf16)y[r];
-      *(bf16x4*)((bf16*)p.dq + b * p.dq_sb + (int64_t)qr * p.dq_sr + dglob) = out;
-    }
+    if (qr < p.Lq) *(bf16x4*)((bf16*)p.dq + b * p.dq_sb + (int64_t)qr * p.dq_sr + dglob) = cvt_bf16x4(y);
   }
   __syncthreads();
 
-  // ---- phase 2: per key block, dk and dv over every query block
+  // ---- phase 2: per key block, dk and dv over every query block. P = exp2(s log2e + b2 - m - lg);
+  // without a key bias one fma against -(m + lg) (padded keys: not stored, their P is not used).
   for (int kb = par; kb < nkb; kb += 2) {
     const int kr = 16 * kb + l16;
     const bf16x4 kop = ss_row4(sh.k, kr, hd + 4 * kap);
     const bf16x4 vop = ss_row4(sh.v, kr, hd + 4 * kap);
-    const float b2 = sh.b2[kr];
+    const float b2 = HB ? sh.b2[kr] : 0.f;
     f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
     for (int qs = 0; qs < nqb; ++qs) {
       // S[query 16 qs + 4 kap + r][key kr], dP likewise
       const f32x4 s = mfma16x16x16(ss_row4(sh.q, 16 * qs + l16, hd + 4 * kap), kop, f32x4{0.f, 0.f, 0.f, 0.f});
       const f32x4 dp = mfma16x16x16(ss_row4(sh.d, 16 * qs + l16, hd + 4 * kap), vop, f32x4{0.f, 0.f, 0.f, 0.f});
       const f32x4 ms = *(const f32x4*)(&sh.mx[gl][16 * qs + 4 * kap]);
-      const f32x4 ls = *(const f32x4*)(&sh.lg[gl][16 * qs + 4 * kap]);
       const f32x4 dq = *(const f32x4*)(&sh.dd[gl][16 * qs + 4 * kap]);
-      bf16x4 pt, ds;
+      f32x4 pr, dsf;
+      if constexpr (HB) {
+        const f32x4 ls = *(const f32x4*)(&sh.lg[gl][16 * qs + 4 * kap]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2) - ms[r]) - ls[r]);
-        pt[r] = (bf16)pr;
-        ds[r] = (bf16)(pr * (dp[r] - dq[r]));
+        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2) - ms[r]) - ls[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(fmaf(s[r], TA_LOG2E, ms[r]));
       }
-      dv = mfma16x16x16(ss_opT(sh.d, 16 * qs, hd, l16, kap), pt, dv);
-      dk = mfma16x16x16(ss_opT(sh.q, 16 * qs, hd, l16, kap), ds, dk);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dsf[r] = pr[r] * (dp[r] - dq[r]);
+      dv = mfma16x16x16(ss_opT(sh.d, 16 * qs, hd, l16, kap), cvt_bf16x4(pr), dv);
+      dk = mfma16x16x16(ss_opT(sh.q, 16 * qs, hd, l16, kap), cvt_bf16x4(dsf), dk);
     }
     const int kc = kr < p.Lk ? kr : 0;
     const f32x4 y = ss_rope_bwd<RM>(dk, p.ck + (int64_t)kc * SB_E + hg * SS_W + hd,
                                     p.sk + (int64_t)kc * SB_E + hg * SS_W + hd, kap);
     if (kr < p.Lk) {
-      bf16x4 ok, ov;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ok[r] = (bf16)y[r];
-        ov[r] = (bf16)dv[r];
-      }
-      *(bf16x4*)((bf16*)p.dk + b * p.dk_sb + (int64_t)kr * p.dk_sr + dglob) = ok;
-      *(bf16x4*)((bf16*)p.dv + b * p.dv_sb + (int64_t)kr * p.dv_sr + dglob) = ov;
+      *(bf16x4*)((bf16*)p.dk + b * p.dk_sb + (int64_t)kr * p.dk_sr + dglob) = cvt_bf16x4(y);
+      *(bf16x4*)((bf16*)p.dv + b * p.dv_sb + (int64_t)kr * p.dv_sr + dglob) = cvt_bf16x4(dv);
     }
   }
 }
@@ -736,14 +736,24 @@ template <typename T>
 void launch_bwd(SbParams p, hipStream_t stream) {
   if constexpr (sizeof(T) == 2) {
     const int rm = ss_mode(p);
-    if (p.Lq >= 1 && p.Lk >= 1 && p.Lq <= SS_ROWS && p.Lk <= SS_ROWS && rm >= 0) {
+    // byte offsets within a batch element fit 32 bits (buffer loads)
+    const bool fits = (int64_t)p.Lq * p.q_sr * 2 < INT32_MAX && (int64_t)p.Lk * p.k_sr * 2 < INT32_MAX &&
+                      (int64_t)p.Lk * p.v_sr * 2 < INT32_MAX && p.q_sr >= 0 && p.k_sr >= 0 && p.v_sr >= 0;
+    if (p.Lq >= 1 && p.Lk >= 1 && p.Lq <= SS_ROWS && p.Lk <= SS_ROWS && rm >= 0 && fits) {
       const dim3 grid((unsigned)(p.B * (SB_H / SS_HG)));
-      if (rm == 0)
-        hipLaunchKernelGGL((ss_bwd_kernel<0>), grid, dim3(SS_NT), 0, stream, p);
+      const bool hb = p.bias != nullptr;
+      if (rm == 0 && hb)
+        hipLaunchKernelGGL((ss_bwd_kernel<0, true>), grid, dim3(SS_NT), 0, stream, p);
+      else if (rm == 0)
+        hipLaunchKernelGGL((ss_bwd_kernel<0, false>), grid, dim3(SS_NT), 0, stream, p);
+      else if (rm == 1 && hb)
+        hipLaunchKernelGGL((ss_bwd_kernel<1, true>), grid, dim3(SS_NT), 0, stream, p);
       else if (rm == 1)
-        hipLaunchKernelGGL((ss_bwd_kernel<1>), grid, dim3(SS_NT), 0, stream, p);
+        hipLaunchKernelGGL((ss_bwd_kernel<1, false>), grid, dim3(SS_NT), 0, stream, p);
+      else if (hb)
+        hipLaunchKernelGGL((ss_bwd_kernel<2, true>), grid, dim3(SS_NT), 0, stream, p);
       else
-        hipLaunchKernelGGL((ss_bwd_kernel<2>), grid, dim3(SS_NT), 0, stream, p);
+        hipLaunchKernelGGL((ss_bwd_kernel<2, false>), grid, dim3(SS_NT), 0, stream, p);
       return;
     }
   }
