@@ -8,8 +8,10 @@
 //   dS = P * (dP - D), cast to the input dtype
 //   dq' = dS k',  dk' = dS^T q',  dv = cast(P)^T dO   (fp32 accumulation)
 //   dq = rope_bwd(dq' scale), dk = rope_bwd(dk'),  rope_bwd(y) = y cos - R(y sin)
-// The reference keeps all keys of a batch element on chip (at most 1024). Here keys and queries are
-// tiled, so any length works:
+// The reference keeps all keys of a batch element on chip (at most 1024). Here:
+//   ss_bwd_kernel  bf16 with both lengths <= 128 (row, CLS): one fused kernel per (batch element,
+//                  4 heads) with every row resident in LDS (described above its definition).
+// Otherwise keys and queries are tiled, so any length works:
 //   sb_dq_kernel   workgroup = (batch element, run of 128-query blocks, head); wave = 16 queries.
 //                  Per block: per-query softmax statistics (row maximum and log2 of the sum, in log2
 //                  units) and D, written to the workspace, then P, dP, dS and dq'. Keys in one tile
