@@ -51,7 +51,8 @@ struct ShParams {
   float scale;
   int B, Lq, Lk;
   int nqb, qbpw, nwg_b;
-  int exact_scale;  // scale is a power of two: bf16(q * scale) needs no rounding
+  int exact_scale;  // fold scale and log2e into the K operand: scale is a power of two (bf16(q * scale)
+                    // needs no rounding) and the runs are long enough to amortise the K split
 };
 
 template <typename T, int KT> struct ShLds {
@@ -670,6 +671,9 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     qbpw = qbpw < 1 ? 1 : (qbpw > 64 ? 64 : qbpw);
     p.qbpw = (int)(qbpw > p.nqb ? p.nqb : qbpw);
     p.nwg_b = (p.nqb + p.qbpw - 1) / p.qbpw;
+    // short runs: splitting q' log2e per block (a few VALU per block) costs less than splitting every
+    // key of the head once per workgroup (~320 VALU per wave); same product to ~2^-17 either way
+    if (p.qbpw <= 8) p.exact_scale = 0;
     const int64_t nblk = B * (int64_t)p.nwg_b;
     const int ngrp = (int)((Lk + 31) / 32);  // 32-key groups every batch element sweeps
     const int mode = (bias || valid) ? 0 : (Lk == 32 * ngrp ? 2 : 1);
