@@ -300,6 +300,11 @@ __device__ __forceinline__ bf16x8 rs_qraw(__amdgpu_buffer_rsrc_t qrsrc, int off)
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qrsrc, off, 0, 0));
 }
 
+// Four fp32 table values (cos or sin of 4 dims) at byte offset off, likewise.
+__device__ __forceinline__ f32x4 rs_tab(__amdgpu_buffer_rsrc_t rsrc, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+}
+
 // Lanes l and l ^ 32 (G and G ^ 2) share the 8 dims d8..d8+7 of their operand k-slots; each has
 // computed 4 of them (G < 2: d8..d8+3, G >= 2: d8+4..d8+7) and the two swap (v_permlane32_swap).
 __device__ __forceinline__ bf16x8 rs_pair8(bf16x4 mine, int G) {
@@ -429,38 +434,74 @@ __device__ __forceinline__ float rs_max(const bf16x8 (&ka)[NG][2], bf16x8 qop, c
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-// One 16-query block of head g: q' operand from the raw q (or RoPE of the q row), one sweep over
-// all keys, the exact-maximum recompute when l is out of range; returns the normalised output (this
-// lane's 4 dims, bf16).
+// RoPE of this lane's 4 dims of q (d4..d4+3) from the raw 8 dims qr of its k-slots (the lane's 4 at
+// positions 4 (G >> 1)) and the prefetched cos / sin of those 4 dims, for the two full-width forms
+// (rot = 16) this kernel takes: pairs in-lane; halves with the partner dims d4 ^ 8 from lane l ^ 16,
+// whose qr holds the other 8 dims of the head at the same positions (v_permlane16_swap).
+__device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 cs, f32x4 sn, int G) {
+  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+  typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+  const u32x4v w = __builtin_bit_cast(u32x4v, qr);
+  const bool upper = (G >> 1) != 0;
+  const u32x2v ow = {upper ? w[2] : w[0], upper ? w[3] : w[1]};
+  const bf16x4 own = __builtin_bit_cast(bf16x4, ow);
+  f32x4 y;
+  if (p.rope == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float xp = (float)own[r ^ 1];
+      y[r] = (float)own[r] * cs[r] + ((r & 1) ? xp : -xp) * sn[r];
+    }
+  } else {
+    u32x2v pw;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const auto r = __builtin_amdgcn_permlane16_swap(ow[k], ow[k], false, false);
+      pw[k] = (G & 1) ? r[0] : r[1];
+    }
+    const bf16x4 pt = __builtin_bit_cast(bf16x4, pw);
+    const float sg = (G & 1) ? 1.f : -1.f;  // dims 8..15 of the head: +x[jd - 8]; 0..7: -x[jd + 8]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = (float)own[r] * cs[r] + sg * (float)pt[r] * sn[r];
+  }
+  return y;
+}
+
+// One 16-query block of head g: q' operand from the raw q (and, with RoPE, its prefetched cos / sin),
+// one sweep over all keys, the exact-maximum recompute when l is out of range; returns the
+// normalised output (this lane's 4 dims, bf16).
+// With RoPE, cs / sn hold this block's cos / sin on entry and the next block's (table byte offset
+// cnext) on return: reloaded as soon as the q' operand is built, a block of work ahead of their use.
 template <int NG, int MF, bool ROPE, bool EXACT>
 __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
-                                         bf16x8 ones, const float* lds_b2, const bf16* qbase, bf16x8 qr, int qi,
-                                         int d4, int G) {
+                                         bf16x8 ones, const float* lds_b2, const bf16* qbase, bf16x8 qr, f32x4& cs,
+                                         f32x4& sn, __amdgpu_buffer_rsrc_t crsrc, __amdgpu_buffer_rsrc_t srsrc,
+                                         int cnext, int qi, int d4, int G) {
   bf16x8 qop;
   if (EXACT && !ROPE) {
     qop = qr;  // q' = q scale exactly: scale and log2e ride on the K operand
   } else if (EXACT) {
-    bf16x4 y4 = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
-    if (qi < p.Lq) {
-      const f32x4 y = rope4_fast<bf16>(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
-                                 p.sq + (int64_t)qi * SH_E, d4, p.rope, p.half, p.rot);
+    const f32x4 y = rs_rope_q(p, qr, cs, sn, G);
+    bf16x4 y4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) y4[j] = (bf16)y[j];  // bf16(rope(q) scale) = bf16(rope(q)) scale
-    }
+    for (int j = 0; j < 4; ++j) y4[j] = (bf16)y[j];  // bf16(rope(q) scale) = bf16(rope(q)) scale
     qop = rs_pair8(y4, G);
   } else {
-    // other scales: q' = bf16(q scale) rounded here, log2e split over the two k-halves
-    f32x4 qs = {0.f, 0.f, 0.f, 0.f};
+    // other scales or short runs: q' = bf16(q scale) rounded here, log2e split over the two k-halves
+    f32x4 qs;
     if (!ROPE) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)((float)qr[(G >> 1) * 4 + j] * p.scale);
-    } else if (qi < p.Lq) {
-      const f32x4 y = rope4_fast<bf16>(qbase + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SH_E,
-                                 p.sq + (int64_t)qi * SH_E, d4, p.rope, p.half, p.rot);
+    } else {
+      const f32x4 y = rs_rope_q(p, qr, cs, sn, G);
 #pragma unroll
       for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
     }
     qop = rs_qsplit(qs, G);
+  }
+  if constexpr (ROPE) {
+    cs = rs_tab(crsrc, cnext);
+    sn = rs_tab(srsrc, cnext);
   }
   f32x4 o;
   float l;
@@ -515,9 +556,9 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
       bf16x4 val = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
       if (key < lk) {
         const bf16* src = kbase + (int64_t)key * p.k_sr;
-        if (ROPE) {
+        if (ROPE) {  // full-width forms only (the launcher sends others to smallhead_fwd_kernel)
           const f32x4 y = rope4_fast<bf16>(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0, p.rope,
-                                     p.half, p.rot);
+                                           8, 16);
 #pragma unroll
           for (int r = 0; r < 4; ++r) val[r] = (bf16)y[r];
         } else {
@@ -584,6 +625,17 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   // stores go to blocks 0 and 1, which their units rewrite later, in order, from this wave (block 1
   // lies outside the resource when the run has one block, and that store is dropped).
   const int ooff = (l16 * p.o_sr + g * SH_D + 4 * G) * 2, ostep = 16 * p.o_sr * 2;
+  // RoPE: cos / sin of the lane's 4 dims at its query's position (tables [Lq][E] fp32; rows past Lq
+  // read as zero), one buffer refilled inside each block for the next one
+  __amdgpu_buffer_rsrc_t crsrc, srsrc;
+  const int coff = (l16 * SH_E + d4) * 4, cstep = 16 * SH_E * 4;
+  f32x4 cs = {0.f, 0.f, 0.f, 0.f}, sn = cs;
+  if constexpr (ROPE) {
+    crsrc = __builtin_amdgcn_make_buffer_rsrc((float*)p.cq + (int64_t)orow * SH_E, 0, nrow * SH_E * 4, TA_BUF_WORD3);
+    srsrc = __builtin_amdgcn_make_buffer_rsrc((float*)p.sq + (int64_t)orow * SH_E, 0, nrow * SH_E * 4, TA_BUF_WORD3);
+    cs = rs_tab(crsrc, coff);
+    sn = rs_tab(srsrc, coff);
+  }
   bf16x8 qa = rs_qraw(qrsrc, qoff);
   rs_store(orsrc, u32x2{0u, 0u}, ooff);
   bf16x8 qb = rs_qraw(qrsrc, qoff + qstep);
@@ -591,31 +643,46 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < nb; i += 2) {
-    u32x2 ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, orow + i * 16 + l16, d4, G);
+    u32x2 ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
+                                              coff + (i + 1) * cstep, orow + i * 16 + l16, d4, G);
     qa = rs_qraw(qrsrc, qoff + (i + 2) * qstep);
     rs_store(orsrc, ov, ooff + i * ostep);
-    ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qb, orow + (i + 1) * 16 + l16, d4, G);
+    ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qb, cs, sn, crsrc, srsrc,
+                                       coff + (i + 2) * cstep, orow + (i + 1) * 16 + l16, d4, G);
     qb = rs_qraw(qrsrc, qoff + (i + 3) * qstep);
     rs_store(orsrc, ov, ooff + (i + 1) * ostep);
   }
   if (i < nb)
-    rs_store(orsrc, rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, orow + i * 16 + l16, d4, G),
+    rs_store(orsrc,
+             rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
+                                           coff + (i + 1) * cstep, orow + i * 16 + l16, d4, G),
              ooff + i * ostep);
 }
 
 // mode 0: b2 read for every group (key bias or per-batch valid lengths); 1: last group only (Lk not
-// a multiple of 32); 2: none. Scales other than powers of two take mode 0.
+// a multiple of 32); 2: none.
+template <int NG, bool ROPE, bool EXACT>
+void launch_resident_mode(const ShParams& p, int mode, int64_t nblk, hipStream_t stream) {
+  const dim3 grid((unsigned)nblk), block(SH_H * 64);
+  if (mode == 0)
+    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, EXACT>), grid, block, 0, stream, p);
+  else if (mode == 1)
+    hipLaunchKernelGGL((sh_resident_kernel<NG, NG - 1, ROPE, EXACT>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((sh_resident_kernel<NG, NG, ROPE, EXACT>), grid, block, 0, stream, p);
+}
+
+// The K split (EXACT) serves RoPE-free long runs; with RoPE, and for three key groups (whose K-split
+// build needs more than 128 VGPRs), q carries the split.
 template <int NG, bool ROPE>
 void launch_resident_ng(const ShParams& p, int mode, int64_t nblk, hipStream_t stream) {
-  const dim3 grid((unsigned)nblk), block(SH_H * 64);
-  if (!p.exact_scale)
-    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, false>), grid, block, 0, stream, p);
-  else if (mode == 0)
-    hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, true>), grid, block, 0, stream, p);
-  else if (mode == 1)
-    hipLaunchKernelGGL((sh_resident_kernel<NG, NG - 1, ROPE, true>), grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL((sh_resident_kernel<NG, NG, ROPE, true>), grid, block, 0, stream, p);
+  if constexpr (!ROPE && NG != 3) {
+    if (p.exact_scale) {
+      launch_resident_mode<NG, false, true>(p, mode, nblk, stream);
+      return;
+    }
+  }
+  launch_resident_mode<NG, ROPE, false>(p, mode, nblk, stream);
 }
 
 template <bool ROPE>
@@ -662,7 +729,8 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     p.exact_scale = scale > 0.f && frexpf(scale, &e) == 0.5f;
   }
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
-  if (dtype == 0 && Lk <= RS_LK) {
+  const bool fast_rope = rope == 0 || (rope == 1 && rot == 16) || (rope == 2 && half == 8 && rot == 16);
+  if (dtype == 0 && Lk <= RS_LK && fast_rope) {
     // all keys resident: one workgroup per (batch element, run of 16-query blocks), one head per wave
     p.nqb = (int)((Lq + 15) / 16);
     // long enough runs to amortise the key fill, while keeping >= ~32 workgroups per CU for the grid
@@ -674,6 +742,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     // short runs: splitting q' log2e per block (a few VALU per block) costs less than splitting every
     // key of the head once per workgroup (~320 VALU per wave); same product to ~2^-17 either way
     if (p.qbpw <= 8) p.exact_scale = 0;
+    if (rope) p.exact_scale = 0;
     const int64_t nblk = B * (int64_t)p.nwg_b;
     const int ngrp = (int)((Lk + 31) / 32);  // 32-key groups every batch element sweeps
     const int mode = (bias || valid) ? 0 : (Lk == 32 * ngrp ? 2 : 1);

@@ -169,11 +169,30 @@ def test_pk_self(dev, name, B, L, dtype, interleaved, bias):
     assert _err(out, ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("name,B,L,dtype,interleaved", [
+    ("self_bf16_rot8_halves", 8, 104, torch.bfloat16, False),
+    ("self_bf16_rot8_pairs", 8, 104, torch.bfloat16, True),
+    ("self_fp32_rot8_halves", 4, 108, torch.float32, False),
+])
+def test_pk_self_partial_rotary(dev, name, B, L, dtype, interleaved):
+    # rotary embedding over the first 8 of each head's 16 dims (cos = 1, sin = 0 beyond): the forms
+    # other than full-width pairs / halves take the tiled kernel's generic RoPE
+    pk = _attn()
+    g = _gen(16)
+    x = torch.randn(B, L, 3 * E, generator=g).to(dtype)
+    rope = _Rope(dim=8, interleaved=interleaved)
+    print(f"[pk_self partial rotary] {name}", flush=True)
+    out = pk.pk_self_attention(x.to(dev), H, None, rope, 16 ** -0.5)
+    ref = O.pk_self_ref(x, H, None, _rope_np(rope, L), 16 ** -0.5)
+    assert _err(out, ref) <= TOL[dtype]
+
+
 @pytest.mark.parametrize("name,B,Lq,Lk,dtype,interleaved", [
     ("cross_cls_bf16_rope", 16, 4, 104, torch.bfloat16, False),
     ("cross_col2_bf16", 4, 1024, 128, torch.bfloat16, None),
     ("cross_col1_bf16", 4, 128, 576, torch.bfloat16, None),
     ("cross_col2_fp32", 2, 4096, 128, torch.float32, None),
+    ("cross_cls_bf16_rope_pairs", 16, 4, 104, torch.bfloat16, True),
 ])
 def test_pk_cross(dev, name, B, Lq, Lk, dtype, interleaved):
     pk = _attn()
@@ -391,4 +410,21 @@ def test_resident_long_runs_rope(dev):
     tabs = _rope_np(rope, L)
     for b in (0, 1023, 2047):
         ref = O.pk_self_ref(x[b:b + 1], H, None, tabs, 16 ** -0.5)
+        assert _err(out[b:b + 1], ref) <= 2e-2
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_resident_long_runs_cross_rope(dev, interleaved):
+    # pk_cross with RoPE (positions 0..L-1 on both sides) and runs of several 16-query blocks per
+    # workgroup (the cos / sin buffer refilled block by block), keys not a multiple of 32
+    pk = _attn()
+    g = _gen(20)
+    B, Lq, Lk = 80, 3990, 100
+    x = torch.randn(B, Lq, E, generator=g).to(torch.bfloat16)
+    y = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
+    rope = _Rope(interleaved=interleaved)
+    out = pk.pk_cross_attention(x.to(dev), y.to(dev), H, None, rope, 16 ** -0.5).cpu()
+    rq, rk = _rope_np(rope, Lq), _rope_np(rope, Lk)
+    for b in (0, 41, 79):
+        ref = O.pk_cross_ref(x[b:b + 1], y[b:b + 1], H, None, rq, rk, 16 ** -0.5)
         assert _err(out[b:b + 1], ref) <= 2e-2

@@ -120,6 +120,25 @@ def test_pk_self_bwd(dev, name, B, L, dtype, interleaved, bias):
     _check("dqkv", xr.grad, ref, dtype)
 
 
+@pytest.mark.parametrize("name,B,L,dtype,interleaved", [
+    ("self_bf16_rot8_halves", 8, 104, torch.bfloat16, False),
+    ("self_fp32_rot8_pairs", 4, 100, torch.float32, True),
+])
+def test_pk_self_bwd_partial_rotary(dev, name, B, L, dtype, interleaved):
+    # rotary embedding over the first 8 of each head's 16 dims: the tiled backward's generic RoPE
+    pk = _attn()
+    g = _gen(35)
+    x = torch.randn(B, L, 3 * E, generator=g).to(dtype)
+    rope = _Rope(dim=8, interleaved=interleaved)
+    go = torch.randn(B, L, E, generator=g)
+    print(f"[pk_self_bwd partial rotary] {name}", flush=True)
+    xr = x.to(dev).requires_grad_(True)
+    out = pk.pk_self_attention(xr, H, None, rope, 16 ** -0.5)
+    out.float().backward(go.to(dev))
+    ref = O.pk_self_bwd_ref(x, H, None, _rope_np(rope, L), 16 ** -0.5, go.to(dtype))
+    _check("dqkv", xr.grad, ref, dtype)
+
+
 @pytest.mark.parametrize("name,B,Lq,Lk,dtype,interleaved,shared_q", [
     ("cross_cls_bf16_rope", 16, 4, 104, torch.bfloat16, False, False),
     ("cross_col2_bf16", 4, 1024, 128, torch.bfloat16, None, False),
