@@ -546,33 +546,83 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   const int tid = threadIdx.x;
 
   // fill: K rows with RoPE (fp32 math, cast), V rows as they are, b2 per key; keys past lk (up to
-  // NG 32-key groups) get zero K/V and b2 = -inf
+  // NG 32-key groups) get zero K/V (the buffer loads' range check) and b2 = -inf. Thread units: whole
+  // 16-dim head rows of K (the RoPE partner dims in registers) and 16-byte chunks of V; every load of
+  // the fill is issued before the first LDS store.
   {
-    const bf16* kbase = (const bf16*)p.k + b * p.k_sb;
-    const bf16* vbase = (const bf16*)p.v + b * p.v_sb;
-    const int nk = NG * 32;
-    for (int u = tid; u < nk * (SH_E / 4); u += NT) {
-      const int key = u >> 5, d0 = (u & 31) * 4;
-      bf16x4 val = {(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
-      if (key < lk) {
-        const bf16* src = kbase + (int64_t)key * p.k_sr;
-        if (ROPE) {  // full-width forms only (the launcher sends others to smallhead_fwd_kernel)
-          const f32x4 y = rope4_fast<bf16>(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0, p.rope,
-                                           8, 16);
+    constexpr int NK = NG * 32;
+    constexpr int KU = (NK * SH_H + NT - 1) / NT;  // K head rows per thread
+    constexpr int VU = (NK * 16 + NT - 1) / NT;    // V chunks per thread
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.k + b * p.k_sb, 0, lk * (int)p.k_sr * 2, TA_BUF_WORD3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.v + b * p.v_sb, 0, lk * (int)p.v_sr * 2, TA_BUF_WORD3);
+    __amdgpu_buffer_rsrc_t crs, srs;
+    if constexpr (ROPE) {
+      crs = __builtin_amdgcn_make_buffer_rsrc((float*)p.ck, 0, lk * SH_E * 4, TA_BUF_WORD3);
+      srs = __builtin_amdgcn_make_buffer_rsrc((float*)p.sk, 0, lk * SH_E * 4, TA_BUF_WORD3);
+    }
+    typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+    u32x4v kx[KU][2], vx[VU];
+    f32x4 kc[KU][4], ks[KU][4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) val[r] = (bf16)y[r];
-        } else {
-          val = *(const bf16x4*)(src + d0);
+    for (int j = 0; j < KU; ++j) {
+      const int u = tid + j * NT, key = u >> 3, hh = u & 7;  // key row, head
+      const int off = (key * (int)p.k_sr + hh * SH_D) * 2;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) kx[j][h2] = __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16 * h2, 0, 0);
+      if constexpr (ROPE) {
+        const int toff = (key * SH_E + hh * SH_D) * 4;
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          kc[j][c4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, toff + 16 * c4, 0, 0));
+          ks[j][c4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, toff + 16 * c4, 0, 0));
         }
       }
-      *(bf16x4*)(lds_k + key * RS_KSTR + d0) = val;
     }
-    for (int u = tid; u < nk * (SH_E / 8); u += NT) {
-      const int key = u >> 4, c8 = (u & 15) * 8;
-      const uint4 val = key < lk ? ldg16(vbase + (int64_t)key * p.v_sr + c8) : make_uint4(0, 0, 0, 0);
-      *(uint4*)(lds_v + key * RS_VSTR + c8) = val;
+#pragma unroll
+    for (int j = 0; j < VU; ++j) {
+      const int u = tid + j * NT, key = u >> 4, c8 = (u & 15) * 8;
+      vx[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (key * (int)p.v_sr + c8) * 2, 0, 0);
     }
-    for (int j = tid; j < nk; j += NT) {
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      const int u = tid + j * NT, key = u >> 3, hh = u & 7;
+      if (u < NK * SH_H) {  // uniform per wave
+        if constexpr (ROPE) {
+          const bf16x8 lo = __builtin_bit_cast(bf16x8, kx[j][0]), hi = __builtin_bit_cast(bf16x8, kx[j][1]);
+          float x[SH_D], y[SH_D];
+#pragma unroll
+          for (int d = 0; d < 8; ++d) {
+            x[d] = (float)lo[d];
+            x[8 + d] = (float)hi[d];
+          }
+#pragma unroll
+          for (int d = 0; d < SH_D; ++d) {
+            // full-width forms only (the launcher sends others to smallhead_fwd_kernel)
+            const float xp = p.rope == 1 ? ((d & 1) ? x[d - 1] : -x[d + 1]) : (d < 8 ? -x[d + 8] : x[d - 8]);
+            y[d] = x[d] * kc[j][d >> 2][d & 3] + xp * ks[j][d >> 2][d & 3];
+          }
+          bf16x8 o0, o1;
+#pragma unroll
+          for (int d = 0; d < 8; ++d) {
+            o0[d] = (bf16)y[d];
+            o1[d] = (bf16)y[8 + d];
+          }
+          *(bf16x8*)(lds_k + key * RS_KSTR + hh * SH_D) = o0;
+          *(bf16x8*)(lds_k + key * RS_KSTR + hh * SH_D + 8) = o1;
+        } else {
+          *(u32x4v*)(lds_k + key * RS_KSTR + hh * SH_D) = kx[j][0];
+          *(u32x4v*)(lds_k + key * RS_KSTR + hh * SH_D + 8) = kx[j][1];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VU; ++j) {
+      const int u = tid + j * NT, key = u >> 4, c8 = (u & 15) * 8;
+      if (u < NK * 16) *(u32x4v*)(lds_v + key * RS_VSTR + c8) = vx[j];
+    }
+    for (int j = tid; j < NK; j += NT) {
       float b2 = TA_NEG_INF;
       if (j < lk) b2 = p.bias ? fmaxf(p.bias[b * p.bias_sb + j] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
       lds_b2[j] = b2;
@@ -730,7 +780,11 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   }
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   const bool fast_rope = rope == 0 || (rope == 1 && rot == 16) || (rope == 2 && half == 8 && rot == 16);
-  if (dtype == 0 && Lk <= RS_LK && fast_rope) {
+  // the resident kernel's buffer loads take 32-bit byte offsets within a batch element (query runs
+  // are at most 64 blocks of 16 rows)
+  const bool offsets_fit = k_sr >= 0 && v_sr >= 0 && q_sr >= 0 && Lk * k_sr * 2 < INT32_MAX &&
+                           Lk * v_sr * 2 < INT32_MAX && 64 * 16 * q_sr * 2 < INT32_MAX;
+  if (dtype == 0 && Lk <= RS_LK && fast_rope && offsets_fit) {
     // all keys resident: one workgroup per (batch element, run of 16-query blocks), one head per wave
     p.nqb = (int)((Lq + 15) / 16);
     // long enough runs to amortise the key fill, while keeping >= ~32 workgroups per CU for the grid
