@@ -391,6 +391,62 @@ def bench_c5(steps: int, warmup: int) -> list:
     return recs
 
 
+def bench_icl_layer(steps: int, warmup: int) -> list:
+    """The fit-time K/V build and the cached attention sub-layer at C4's shape, around the ICL kernel:
+    per block, IclKVCache.append_projected (one GEMM of the 45,000 train rows of each estimator with the
+    K|V thirds of a packed in-projection, heads appended to the cache through strides) and
+    IclKVCache.attention_layer (Q projection of the 5,000 test rows, attention over the cache,
+    out-projection). Random weights of the reference's ICL width (512 = 8 x 64); RoPE / SSMax on q and
+    the block's norm and feed-forward are upstream modules, not part of these lines."""
+    import torch
+
+    import tabicl_mi355_icl as icl
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    W = HEADS * D
+    cache = icl.IclKVCache(EST, BLOCKS, HEADS, TRAIN, D, torch.bfloat16, dev)
+    w_in = [(torch.randn(3 * W, W, generator=g, device=dev) * W ** -0.5).to(torch.bfloat16) for _ in range(BLOCKS)]
+    b_in = [(torch.randn(3 * W, generator=g, device=dev) * 0.1).to(torch.bfloat16) for _ in range(BLOCKS)]
+    w_out = [(torch.randn(W, W, generator=g, device=dev) * W ** -0.5).to(torch.bfloat16) for _ in range(BLOCKS)]
+    b_out = [(torch.randn(W, generator=g, device=dev) * 0.1).to(torch.bfloat16) for _ in range(BLOCKS)]
+    xtr = torch.randn(EST, TRAIN, W, generator=g, device=dev).to(torch.bfloat16)
+    xq = torch.randn(EST, TEST, W, generator=g, device=dev).to(torch.bfloat16)
+
+    def build():
+        for b in range(BLOCKS):
+            cache.append_projected(b, xtr, w_in[b], b_in[b])
+
+    def query():
+        for b in range(BLOCKS):
+            cache.attention_layer(b, xq, w_in[b], b_in[b], w_out[b], b_out[b], valid_kv_len=TRAIN)
+
+    recs = []
+    ms_b = _time(build, max(1, steps // 4), 1)
+    gemm_flops = 2.0 * EST * TRAIN * W * 2 * W * BLOCKS
+    recs.append({"metric": "ms per fit-time ICL K/V cache build (12 blocks, projection + append)",
+                 "value": round(ms_b, 3), "unit": "ms", "n_gpus": 1, "steps": max(1, steps // 4), "warmup": 1,
+                 "higher_is_better": False, "vs_baseline": None, "dtype": "bf16",
+                 "data": "synthetic N(0,1) train rows and random in-projection (seed 5)",
+                 "config": {"workload": "12 blocks x 8 est x 45000 train rows x width 512 -> K|V heads "
+                                        "[est, blk, 8, row, 64]"},
+                 "gemm_tflops": round(gemm_flops / (ms_b * 1e-3) / 1e12, 1),
+                 "cache_gib": round(cache.nbytes() / 2 ** 30, 2)})
+    ms_q = _time(query, steps, warmup)
+    attn_flops = 4.0 * TEST * TRAIN * D * HEADS * EST * BLOCKS
+    proj_flops = 2.0 * EST * TEST * W * W * 2 * BLOCKS
+    recs.append({"metric": "ms per cached-KV ICL attention sub-layer query (12 blocks: Q projection + attention "
+                           "+ out-projection)",
+                 "value": round(ms_q, 3), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup,
+                 "higher_is_better": False, "vs_baseline": None, "dtype": "bf16",
+                 "data": "synthetic N(0,1) rows, random projections (seed 5), cache from the build line",
+                 "config": {"workload": "12 blocks x 8 est x 5000 test rows over 45000 cached keys, width 512, "
+                                        "8 heads x 64"},
+                 "tflops": round((attn_flops + proj_flops) / (ms_q * 1e-3) / 1e12, 1),
+                 "attention_flop_share": round(attn_flops / (attn_flops + proj_flops), 4)})
+    return recs
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -398,9 +454,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf (comma-separated) or "
-                         "all print the other BASELINE configs' lines, the fwd+bwd training lines and the folded "
-                         "first-ISAB lines")
+                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer "
+                         "(comma-separated) or all print the other BASELINE configs' lines, the fwd+bwd training "
+                         "lines, the folded first-ISAB lines and the ICL cache build / attention sub-layer lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -410,7 +466,7 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
@@ -421,6 +477,8 @@ def main() -> int:
             recs += bench_train(args.steps, args.warmup)
         if configs & {"hxf", "all"}:
             recs += bench_hxf(args.steps, args.warmup)
+        if configs & {"icl_layer", "all"}:
+            recs += bench_icl_layer(args.steps, args.warmup)
         for rec in recs:
             print(json.dumps(rec), flush=True)
         return 0

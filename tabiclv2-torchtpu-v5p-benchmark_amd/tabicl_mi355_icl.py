@@ -11,12 +11,18 @@ Replaces the reference's Splash path for the ICL stage:
   * IclKVCache holds the fit-time cache in one [estimator, block, head, row, d] tensor per K and V
     (the reference keeps tuples of per-block [B, H, T, d] tensors, tabicl_tpu_bucketed.py:413-435),
     appended once per block at fit time and read per block at query time (:803-817).
+    append_projected writes a block's K/V straight from the train rows and the packed in-projection;
+    attention_layer runs one block's cached attention sub-layer (Q projection, attention over the
+    cache, out-projection) around the kernel.
 """
 from __future__ import annotations
 
 from typing import Optional, Union
 
+from typing import Callable
+
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 import tabicl_mi355_native as _nat
@@ -162,6 +168,55 @@ class IclKVCache:
         _nat.call("tabicl_icl_cache_append", kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), row0, cap,
                   k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), E, H, T, D,
                   _nat.dtype_code(k.dtype), _nat.stream_of(k))
+
+    def append_projected(self, block: int, x: Tensor, in_proj_weight: Tensor, in_proj_bias: Optional[Tensor] = None,
+                         row0: int = 0) -> None:
+        """Fit-time K/V of one block straight from its train rows x [E, T, width] (the rows the block's
+        attention projects, after its pre-norm): k = x W_k^T + b_k, v = x W_v^T + b_v with W_k, W_v the
+        second and third thirds of the packed in-projection [3 width, width] (the query takes the first,
+        results/tpu_patch.diff:308-310; need_kv returns the K/V projections, diff:1569-1575, 989), split
+        into heads and written to rows [row0, row0 + T) of the block. One GEMM [E T, width] x [width,
+        2 width] (torch / hipBLASLt) produces K|V interleaved per row; the append kernel reads the heads
+        out of it through strides, so no permuted copy is made."""
+        E, NB, H, cap, D = self.keys.shape
+        width = H * D
+        if x.dim() != 3 or x.shape[0] != E or x.shape[2] != width:
+            raise ValueError(f"append_projected expects x [{E}, T, {width}], got {tuple(x.shape)}")
+        if tuple(in_proj_weight.shape) != (3 * width, width):
+            raise ValueError(f"in_proj_weight must be [{3 * width}, {width}], got {tuple(in_proj_weight.shape)}")
+        if in_proj_bias is not None and tuple(in_proj_bias.shape) != (3 * width,):
+            raise ValueError(f"in_proj_bias must be [{3 * width}], got {tuple(in_proj_bias.shape)}")
+        _nat.require_device(x, in_proj_weight)
+        T = x.shape[1]
+        kv = F.linear(x, in_proj_weight[width:], None if in_proj_bias is None else in_proj_bias[width:])
+        if kv.dtype != self.keys.dtype:
+            kv = kv.to(self.keys.dtype)  # the reference stores k_l.to(cache_dtype) (tabicl_tpu_bucketed.py:676, 688)
+        kv = kv.view(E, T, 2, H, D)
+        self.append(block, kv[:, :, 0].permute(0, 2, 1, 3), kv[:, :, 1].permute(0, 2, 1, 3), row0)
+
+    def attention_layer(self, block: int, x: Tensor, in_proj_weight: Tensor, in_proj_bias: Optional[Tensor],
+                        out_proj_weight: Tensor, out_proj_bias: Optional[Tensor],
+                        valid_kv_len: Optional[Union[int, Tensor]] = None,
+                        q_transform: Optional[Callable[[Tensor], Tensor]] = None) -> Tensor:
+        """One block's cached attention sub-layer for test rows x [E, Tq, width] (after the block's
+        pre-norm): q = x W_q^T + b_q split into heads [E, H, Tq, D] (diff:308-312), q_transform applied
+        to it if given (the caller's RoPE on q and SSMax scaling with n = the train length, modules of
+        the upstream model: diff:312-313, 251-254), attention over block `block` of the cache with keys
+        >= valid_kv_len masked and q promoted to the cache dtype (diff:314-317), heads merged and the
+        out-projection applied (diff:383-393). Returns [E, Tq, width] in the promoted dtype; the residual and the
+        feed-forward part of the block stay with the caller."""
+        E, NB, H, cap, D = self.keys.shape
+        width = H * D
+        if x.dim() != 3 or x.shape[0] != E or x.shape[2] != width:
+            raise ValueError(f"attention_layer expects x [{E}, Tq, {width}], got {tuple(x.shape)}")
+        Tq = x.shape[1]
+        q = F.linear(x, in_proj_weight[:width], None if in_proj_bias is None else in_proj_bias[:width])
+        q = q.view(E, Tq, H, D).transpose(1, 2)
+        if q_transform is not None:
+            q = q_transform(q)
+        o = self.query(block, q.contiguous(), valid_kv_len)
+        o = o.transpose(1, 2).reshape(E, Tq, width)
+        return F.linear(o, out_proj_weight.to(o.dtype), None if out_proj_bias is None else out_proj_bias.to(o.dtype))
 
     def block_kv(self, block: int):
         return self.keys[:, block], self.values[:, block]
