@@ -752,6 +752,200 @@ void launch_resident(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStr
     launch_resident_rope<false>(p, ngrp, mode, nblk, stream);
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp32 kernel (every fp32 call: the C1 column ISAB in the reference's fp32 precision). A workgroup of
+// 8 waves takes (batch element, group of 4 heads, run of 16-query blocks); wave = (head of the group,
+// parity of the blocks it takes). Keys go through LDS in tiles of 128 (the group's 64 dims of K
+// row-major and of V transposed: 69 KB, two workgroups per CU). Per block and tile, fp32 MFMA
+// (4 x 16x16x4 per 16x16x16 product):
+//   S^T = K' q'^T (keys x queries), x = S log2e + b2, online softmax (running maximum, rescaled only
+//   when it grows by more than SH_LAZY: exact, o and l share the reference), O^T += V^T P^T.
+// RESIDENT (all keys in one tile): each block in one pass, nothing carried between blocks, any run
+// length; otherwise up to SF_SB blocks per wave carry (o, m, l) across the tiles.
+// ---------------------------------------------------------------------------------------------
+constexpr int SF_HG = 4;
+constexpr int SF_W = SF_HG * SH_D;   // merged dims per workgroup
+constexpr int SF_KT = 128;           // keys per tile
+constexpr int SF_KSTR = SF_W + 4;    // K tile row stride (floats)
+constexpr int SF_VSTR = SF_KT + 4;   // V^T tile row stride (floats)
+constexpr int SF_SB = 4;             // blocks per wave carried across tiles (streaming)
+
+// One tile for one block: online-softmax update of (o, m, l) (l: this lane's partial sum).
+__device__ __forceinline__ void sf_tile(const float* lkt, const float* lvt, const float* lb2, int nkb, f32x4 qop,
+                                        int hd, int l16, int kap, f32x4& o, float& m, float& l) {
+  f32x4 x[SF_KT / 16];
+  float tm = TA_NEG_INF;
+#pragma unroll
+  for (int kt = 0; kt < SF_KT / 16; ++kt) {
+    if (kt < nkb) {
+      const f32x4 a = *(const f32x4*)(lkt + (16 * kt + l16) * SF_KSTR + hd + 4 * kap);
+      x[kt] = mfma16x16x16(a, qop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[kt][r] = fmaf(x[kt][r], TA_LOG2E, b2[r]);
+        tm = fmaxf(tm, x[kt][r]);
+      }
+    }
+  }
+  const float m_new = fmaxf(m, quad_max(tm));  // finite: every tile holds a valid key
+  if (wave_any(m_new - m > SH_LAZY)) {
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    l *= alpha;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] *= alpha;
+    m = m_new;
+  }
+#pragma unroll
+  for (int kt = 0; kt < SF_KT / 16; ++kt) {
+    if (kt < nkb) {
+      f32x4 pv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pv[r] = __builtin_amdgcn_exp2f(x[kt][r] - m);
+        l += pv[r];
+      }
+      const f32x4 a = *(const f32x4*)(lvt + (hd + l16) * SF_VSTR + 16 * kt + 4 * kap);
+      o = mfma16x16x16(a, pv, o);
+    }
+  }
+}
+
+// q' = rope(q) scale (fp32) of query qi, this lane's 4 dims d0..d0+3; zero past Lq.
+__device__ __forceinline__ f32x4 sf_qop(const ShParams& p, int b, int qi, int d0) {
+  if (qi >= p.Lq) return f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* row = (const float*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr;
+  f32x4 y = p.rope ? rope4<float>(row, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E, d0, p.rope, p.half,
+                                  p.rot)
+                   : *(const f32x4*)(row + d0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] *= p.scale;
+  return y;
+}
+
+__device__ __forceinline__ void sf_store(const ShParams& p, int b, int qi, int d0, f32x4 o, float l) {
+  const float lt = quad_sum(l);
+  if (qi >= p.Lq) return;
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  f32x4 out;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[r] = o[r] * inv;
+  *(f32x4*)((float*)p.o + b * p.o_sb + (int64_t)qi * p.o_sr + d0) = out;
+}
+
+// Tile t of keys (rows past lk: zero K / V, b2 = -inf); the group's 64 dims, K with RoPE.
+__device__ __forceinline__ void sf_fill(const ShParams& p, float* lkt, float* lvt, float* lb2, int b, int hg, int t,
+                                        int lk) {
+  const int tid = threadIdx.x, k0 = t * SF_KT;
+  const float* kbase = (const float*)p.k + b * p.k_sb;
+  const float* vbase = (const float*)p.v + b * p.v_sb;
+#pragma unroll 2
+  for (int i = 0; i < SF_KT * (SF_W / 4) / 512; ++i) {
+    const int u = tid + 512 * i, key = u >> 4, c = u & 15, d = hg * SF_W + 4 * c;
+    const int gk = k0 + key, gc = gk < lk ? gk : lk - 1;
+    const float* krow = kbase + (int64_t)gc * p.k_sr;
+    f32x4 kv = p.rope ? rope4<float>(krow, p.ck + (int64_t)gc * SH_E, p.sk + (int64_t)gc * SH_E, d, p.rope, p.half,
+                                     p.rot)
+                      : *(const f32x4*)(krow + d);
+    f32x4 vv = *(const f32x4*)(vbase + (int64_t)gc * p.v_sr + d);
+    if (gk >= lk) kv = vv = f32x4{0.f, 0.f, 0.f, 0.f};
+    *(f32x4*)(lkt + key * SF_KSTR + 4 * c) = kv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lvt[(4 * c + j) * SF_VSTR + key] = vv[j];
+  }
+  for (int j = tid; j < SF_KT; j += 512) {
+    const int gk = k0 + j;
+    float b2 = TA_NEG_INF;
+    if (gk < lk) b2 = p.bias ? fmaxf(p.bias[b * p.bias_sb + gk] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
+    lb2[j] = b2;
+  }
+}
+
+template <bool RESIDENT>
+__global__ __launch_bounds__(512, 4) void sf_kernel(ShParams p) {
+  __shared__ __attribute__((aligned(16))) float lkt[SF_KT * SF_KSTR];
+  __shared__ __attribute__((aligned(16))) float lvt[SF_W * SF_VSTR];
+  __shared__ __attribute__((aligned(16))) float lb2[SF_KT];
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int hg = work % (SH_H / SF_HG), rest = work / (SH_H / SF_HG);
+  const int b = rest / p.nwg_b, qb0 = (rest % p.nwg_b) * p.qbpw;
+  int lk = p.Lk;
+  if (p.valid) {
+    const int vl = p.valid[p.valid_n == 1 ? 0 : b];
+    lk = vl < 0 ? 0 : (vl < lk ? vl : lk);
+  }
+  const int ntiles = (lk + SF_KT - 1) / SF_KT;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, kap = lane >> 4;
+  const int gl = wave & (SF_HG - 1), par = wave / SF_HG;
+  const int hd = gl * SH_D, d0 = hg * SF_W + hd + 4 * kap;
+  const int nb = p.nqb - qb0 < p.qbpw ? p.nqb - qb0 : p.qbpw;
+
+  if constexpr (RESIDENT) {
+    if (ntiles == 1) {
+      sf_fill(p, lkt, lvt, lb2, b, hg, 0, lk);
+      __syncthreads();
+    }
+    const int nkb = (lk + 15) >> 4;
+    for (int bi = par; bi < nb; bi += 2) {
+      const int qi = (qb0 + bi) * 16 + l16;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      float m = TA_NEG_INF, l = 0.f;
+      if (ntiles == 1) sf_tile(lkt, lvt, lb2, nkb, sf_qop(p, b, qi, d0), hd, l16, kap, o, m, l);
+      sf_store(p, b, qi, d0, o, l);
+    }
+  } else {
+    f32x4 qop[SF_SB], o[SF_SB];
+    float m[SF_SB], l[SF_SB];
+#pragma unroll
+    for (int j = 0; j < SF_SB; ++j) {
+      qop[j] = sf_qop(p, b, (qb0 + par + 2 * j) * 16 + l16, d0);
+      o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m[j] = TA_NEG_INF;
+      l[j] = 0.f;
+    }
+    for (int t = 0; t < ntiles; ++t) {
+      __syncthreads();
+      sf_fill(p, lkt, lvt, lb2, b, hg, t, lk);
+      __syncthreads();
+      const int rem = lk - t * SF_KT;
+      const int nkb = rem >= SF_KT ? SF_KT / 16 : (rem + 15) >> 4;
+#pragma unroll
+      for (int j = 0; j < SF_SB; ++j) {
+        if (par + 2 * j < nb)
+          sf_tile(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, o[j], m[j], l[j]);
+        __builtin_amdgcn_sched_barrier(0);  // one block at a time: interleaving them costs registers
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < SF_SB; ++j)
+      if (par + 2 * j < nb) sf_store(p, b, (qb0 + par + 2 * j) * 16 + l16, d0, o[j], l[j]);
+  }
+}
+
+// fp32: runs of query blocks sized for >= ~2048 workgroups (resident) or at most 2 SF_SB blocks
+// (streaming: state carried across tiles), >= ~1024 workgroups when the batch allows.
+void launch_sf(ShParams p, hipStream_t stream) {
+  p.nqb = (p.Lq + 15) / 16;
+  const int64_t groups = (int64_t)p.B * (SH_H / SF_HG);
+  const bool resident = p.Lk <= SF_KT;
+  int64_t run;
+  if (resident) {
+    run = (groups * p.nqb + 2047) / 2048;
+    run = run < 2 ? 2 : (run > 32 ? 32 : run);
+  } else {
+    run = 2 * SF_SB;
+    while (run > 2 && groups * ((p.nqb + run - 1) / run) < 1024) run /= 2;
+  }
+  p.qbpw = (int)(run > p.nqb ? p.nqb : run);
+  p.nwg_b = (p.nqb + p.qbpw - 1) / p.qbpw;
+  const dim3 grid((unsigned)(groups * p.nwg_b)), block(512);
+  if (resident)
+    hipLaunchKernelGGL((sf_kernel<true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((sf_kernel<false>), grid, block, 0, stream, p);
+}
+
 }  // namespace
 
 int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
@@ -813,8 +1007,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     hipLaunchKernelGGL((smallhead_fwd_kernel<bf16, 64>), dim3((unsigned)nblk), dim3(SH_NW * 64), 0,
                        stream, p);
   else
-    hipLaunchKernelGGL((smallhead_fwd_kernel<float, 64>), dim3((unsigned)nblk), dim3(SH_NW * 64), 0,
-                       stream, p);
+    launch_sf(p, stream);
   return (int)hipGetLastError();
 }
 
