@@ -1,14 +1,17 @@
 // Fused small-head attention (8 heads x 16 dims, merged width E = 128) for gfx950.
 //
-// One kernel serves the four small-head ops of the reference (hx, hxq, pk_self, pk_cross;
+// The kernels here serve the four small-head ops of the reference (hx, hxq, pk_self, pk_cross;
 // scripts/tabicl_tpu_pallas_attn.py): q/k/v are read straight from their merged-head rows
 // (separate [B, L, E], packed K|V [B, L, 2E] or packed Q|K|V [B, L, 3E]) and the output is
 // written merged [B, Lq, E]. Per (batch, head):
 //   O = softmax(q' k'^T + bias [+ -inf past valid]) V,
 //   q' = cast(rope(q) * scale), k' = cast(rope(k)) (RoPE and scale in fp32; no RoPE = identity),
-// fp32 scores/softmax, probabilities cast to the value dtype before PV.
+// fp32 scores/softmax, probabilities cast to the value dtype before PV. tabicl_launch_smallhead
+// picks by shape: sh_resident_kernel (bf16, all keys in LDS), sf_kernel (fp32), the streaming
+// kernel of smallhead_stream.hip (bf16, long keys) or smallhead_fwd_kernel below (bf16 with RoPE or
+// a key bias and long keys, partial-rotary RoPE).
 //
-// Work decomposition: a workgroup of 8 waves owns one batch element and a block of 128 queries
+// smallhead_fwd_kernel: a workgroup of 8 waves owns one batch element and a block of 128 queries
 // (wave w: queries 16w..16w+15, all 8 heads; per-head online-softmax state in registers).
 // Keys stream through LDS in tiles of KT keys x all heads (K row-major, V transposed to
 // [E][KT], per-key bias pre-multiplied by log2(e), -inf past the valid length). When all keys
