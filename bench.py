@@ -226,6 +226,16 @@ def bench_train(steps: int, warmup: int) -> list:
             fwd().float().square().mean().backward()
 
         ms = _time(step, steps, warmup)
+        # the attention kernels alone: forward, then backward from a fixed bf16 upstream gradient
+        # (no loss: autograd hands it straight to the backward op)
+        g_out = torch.randn(B, Lq, E, generator=g, device=dev).to(torch.bfloat16)
+
+        def step_kernels():
+            for t in leaves:
+                t.grad = None
+            fwd().backward(g_out)
+
+        ms_k = _time(step_kernels, steps, warmup)
         tf = 3.5 * 4.0 * Lq * Lk * 16 * H * B / (ms * 1e-3) / 1e12
         recs.append({"metric": f"ms per fwd+bwd {name} step", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
                      "steps": steps, "warmup": warmup, "higher_is_better": False,
@@ -233,6 +243,8 @@ def bench_train(steps: int, warmup: int) -> list:
                      "dtype": "bf16", "data": "synthetic N(0,1), q x 0.25", "config": {
                          "workload": f"{B} x {Lq} q over {Lk} keys, 8x16, loss = out.float().square().mean()"},
                      "attn_tflops": round(tf, 2),
+                     "kernels_ms": round(ms_k, 4),
+                     "kernels_note": "forward + backward ops from a given bf16 upstream gradient, no loss",
                      "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                                   "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
     return recs
