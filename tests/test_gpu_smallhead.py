@@ -134,6 +134,37 @@ def test_hxq_ragged_valid_and_empty(dev):
     assert torch.all(out[2] == 0)
 
 
+def test_hxq_ragged_valid_and_empty_fp32(dev):
+    # fp32 kernel: per-batch valid lengths (all keys, one key, none, a partial 128-key tile)
+    pk = _attn()
+    g = _gen(22)
+    B, Lq, Lk = 4, 128, 2048
+    q = torch.randn(B, Lq, E, generator=g) * 0.25
+    kv = torch.randn(B, Lk, 2 * E, generator=g)
+    valid = torch.tensor([2048, 1, 0, 1000], dtype=torch.int32)
+    out = pk.hxq_attention(q.to(dev), kv.to(dev), valid.to(dev), H)
+    ref = O.hxq_ref(q, kv, valid.numpy(), H)
+    assert _err(out, ref) <= 1e-4
+    assert torch.all(out[2] == 0)
+
+
+def test_fp32_stream_long_runs_with_bias(dev):
+    # fp32 kernel over 128-key tiles with runs of 8 query blocks (4 per wave carried across the
+    # tiles), a key bias with masked keys, and keys not a multiple of the tile
+    pk = _attn()
+    g = _gen(21)
+    B, Lq, Lk = 512, 128, 300
+    q = torch.randn(B, Lq, E, generator=g) * 0.25
+    k = torch.randn(B, Lk, E, generator=g)
+    v = torch.randn(B, Lk, E, generator=g)
+    kb = torch.randn(B, Lk, generator=g)
+    kb[:, 290:] = -1e30
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev)).cpu()
+    for b in (0, 255, 511):
+        ref = O.hx_ref(q[b:b + 1], k[b:b + 1], v[b:b + 1], H, kb[b:b + 1])
+        assert _err(out[b:b + 1], ref) <= 1e-4
+
+
 def test_hxq_inference_tile_subset(dev):
     # reference shape col1_infer_tile54 (54 x 128 queries over 53248 keys, 45000 valid); 6 of the
     # 54 batch elements keep the CPU oracle within seconds
