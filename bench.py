@@ -312,10 +312,13 @@ def c5_tables(seed: int = 4):
 
 
 def c5_bucket(n: int) -> int:
-    for b in C5_BUCKETS:
-        if b >= n:
-            return b
-    raise ValueError(n)
+    """Row bucket of the reference's bucketed runner (power-of-two buckets, no step)."""
+    import tabicl_mi355_buckets as bk
+
+    b = bk.pick_row_bucket(n, step=0)
+    if b not in C5_BUCKETS:
+        raise ValueError(n)
+    return b
 
 
 def bench_c5(steps: int, warmup: int) -> list:
