@@ -466,7 +466,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--config", default="c4",
                     help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer "
@@ -545,6 +545,7 @@ def main() -> int:
     ms_per_step = total_ms / args.steps
     launch_ms = [a.elapsed_time(b) for row in ev for (a, b) in row]
     avg_launch_ms = sum(launch_ms) / len(launch_ms)
+    step_ms = [row[0][0].elapsed_time(row[-1][1]) for row in ev]  # first launch start to last launch end
 
     flops_launch = 4.0 * TEST * TRAIN * D * HEADS * EST
     flops_step = flops_launch * BLOCKS
@@ -576,6 +577,8 @@ def main() -> int:
         "attn_tflops": round(tflops, 1),
         "pct_mfma_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "avg_launch_ms": round(avg_launch_ms, 4),
+        "median_launch_ms": round(statistics.median(launch_ms), 4),
+        "median_step_ms": round(statistics.median(step_ms), 3),
         "cache_build_ms": round(t_build * 1000.0, 2),
         "cache_gib": round(cache.nbytes() / 2 ** 30, 2),
         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 1), "peak": PEAK_BF16_TFLOPS,
