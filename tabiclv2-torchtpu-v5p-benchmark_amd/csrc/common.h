@@ -194,6 +194,19 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_addr) {
                : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }
+// The same copy from a wave-uniform base address plus this lane's 32-bit byte offset (the scalar-base
+// form of the instruction: no 64-bit address arithmetic per lane).
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_addr) {
+  // readfirstlane returns int: take each half back as uint32_t so the low half is not sign-extended
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | lo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"((const void*)(uintptr_t)bu), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Byte address of a __shared__ object in the LDS aperture.

@@ -430,20 +430,6 @@ struct IpState {
   float l[2];   // this lane's share of the row sums
 };
 
-// Queue the copy of the tile at key k0 into the buffer at LDS byte address buf: wave w copies K
-// rows 16w..16w+15 and V rows 16w..16w+15, 8 rows (1 KB) per instruction; rows past `valid` are
-// read from row valid-1 (in bounds, and finite whenever the visible rows are).
-__device__ __forceinline__ void ip_issue(const bf16* kbase, const bf16* vbase, int64_t k_st, int64_t v_st,
-                                         uint32_t buf, int k0, int valid, int wave, int lane) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * wave + 8 * (i & 1) + (lane >> 3);
-    const int c = (lane & 7) ^ ip_swz(row);
-    const int64_t key = min(k0 + row, valid - 1);
-    const bf16* src = (i < 2 ? kbase + key * k_st : vbase + key * v_st) + c * 8;
-    lds_dma16(src, buf + (i < 2 ? 0 : ICL_KT * ICL_D * 2) + (16 * wave + 8 * (i & 1)) * ICL_D * 2);
-  }
-}
 
 // K operand of the S product: d-slice sl of rows kr..kr+31 of the K tile.
 __device__ __forceinline__ bf16x8 ip_kop(const bf16* lk, int kr, int sl, int lr, int hh) {
@@ -579,10 +565,35 @@ struct IpCtx {
   const bf16* kbase;
   const bf16* vbase;
   int64_t k_st, v_st;
+  uint32_t koff, voff;  // byte offsets in a tile of this lane's K / V chunk in rows 16w..16w+7
+  uint32_t choff;       // byte offset of that chunk within its row (the same for rows 16w+8..)
+  int lrow;             // this lane's row in rows 16w..16w+7
   uint32_t lds0;
   int t0, nt, valid, wave, lane;
   float sc;
 };
+
+// Queue the copy of the tile at key k0 into the buffer at LDS byte address buf: wave w copies K
+// rows 16w..16w+15 and V rows 16w..16w+15, 8 rows (1 KB) per instruction, from the tile's
+// (wave-uniform) base plus each lane's 32-bit offset. Rows 16w+8.. share the swizzle of rows 16w..
+// (it depends on row & 7). Rows past `valid` are read from row valid-1 (in bounds, and finite
+// whenever the visible rows are); k0 < valid always.
+__device__ __forceinline__ void ip_issue(const IpCtx& c, uint32_t buf, int k0) {
+  const bf16* kt = c.kbase + (int64_t)k0 * c.k_st;
+  const bf16* vt = c.vbase + (int64_t)k0 * c.v_st;
+  const int lim = c.valid - k0;  // rows below lim are visible
+  const int64_t last = lim < ICL_KT ? lim - 1 : 0;  // offsets of the clamped row, used only when lim < 64
+  const uint32_t kcl = (uint32_t)(last * c.k_st * 2) + c.choff;
+  const uint32_t vcl = (uint32_t)(last * c.v_st * 2) + c.choff;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = i & 1;
+    const bool in = c.lrow + 8 * j < lim;
+    const uint32_t off = i < 2 ? (in ? c.koff + (uint32_t)(j * 16 * c.k_st) : kcl)
+                               : (in ? c.voff + (uint32_t)(j * 16 * c.v_st) : vcl);
+    lds_dma16_s(off, i < 2 ? kt : vt, buf + (i < 2 ? 0 : ICL_KT * ICL_D * 2) + (16 * c.wave + 8 * j) * ICL_D * 2);
+  }
+}
 
 // Sweep iteration t (tile t0 + t, buffer t % IP_NBUF, no key past `valid`): phase A = softmax of
 // its first half, S of its second half, PV of the previous tile's second half; join (tile t + 1
@@ -600,8 +611,8 @@ __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&s
   ip_phase<false, true, !FIRST>(st, sA, sB, pA, pB, lk, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
   static_assert(IP_NBUF == 4, "one tile (4 copies per wave) may stay in flight below");
   TA_WAIT_JOIN(4);
-  ip_issue(c.kbase, c.vbase, c.k_st, c.v_st, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
-           min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT, c.valid, c.wave, c.lane);
+  ip_issue(c, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
+           min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
   ip_phase<false, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
 }
 
@@ -642,7 +653,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     valid = valid < 0 ? 0 : (valid > p.Tkv ? p.Tkv : valid);
   }
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 31, hh = lane >> 5;
   const int qw0 = qb * (IP_QW * IP_NW) + wave * IP_QW;
 
@@ -690,10 +701,16 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     c.wave = wave;
     c.lane = lane;
     c.sc = p.sc;
+    {
+      const int row = 16 * wave + (lane >> 3);
+      const int ch = (lane & 7) ^ ip_swz(row);
+      c.lrow = row;
+      c.choff = (uint32_t)(ch * 16);
+      c.koff = (uint32_t)((row * c.k_st + ch * 8) * 2);
+      c.voff = (uint32_t)((row * c.v_st + ch * 8) * 2);
+    }
 #pragma unroll
-    for (int i = 0; i < IP_NBUF - 1; ++i)
-      ip_issue(c.kbase, c.vbase, c.k_st, c.v_st, c.lds0 + i * IP_TILE * 2, min(t0 + i, t1 - 1) * ICL_KT, valid,
-               wave, lane);
+    for (int i = 0; i < IP_NBUF - 1; ++i) ip_issue(c, c.lds0 + i * IP_TILE * 2, min(t0 + i, t1 - 1) * ICL_KT);
     TA_WAIT_JOIN(8);  // tile t0 landed, two more tiles (8 copies) in flight
 
     // reference m: ceiled maximum over the first 32 keys of the range
@@ -839,7 +856,9 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream)
   const int64_t have = ws ? ws_bytes : 0;
   bool fast = false;
   int64_t fb = 0;
-  if (sizeof(T) == 2 && D == ICL_D) {
+  // the pipelined kernel's tile copies take 32-bit byte offsets within a tile (64 rows)
+  const bool strides_fit = p.k_st >= 0 && p.v_st >= 0 && p.k_st < (1 << 24) && p.v_st < (1 << 24);
+  if (sizeof(T) == 2 && D == ICL_D && strides_fit) {
     if (have < flag_bytes(items * p.nsplit) + part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
     fb = flag_bytes(items * p.nsplit);
     fast = have >= fb + part_bytes(p.nsplit, rows, D);
