@@ -531,7 +531,7 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
 #pragma unroll
       for (int r = 0; r < 16; ++r) nxt[qc][r] = 0.f;
   }
-  float ls[2] = {0.f, 0.f};
+  float ls[2] = {st.l[0], st.l[1]};  // the row sums accumulate in place
   bf16x8 op[8];
   if (I0 < I1) op[I0] = read_op(I0);
   if (I0 + 1 < I1) op[I0 + 1] = read_op(I0 + 1);
@@ -557,8 +557,8 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  st.l[0] += ls[0];
-  st.l[1] += ls[1];
+  st.l[0] = ls[0];
+  st.l[1] = ls[1];
 }
 
 struct IpCtx {
@@ -599,19 +599,21 @@ __device__ __forceinline__ void ip_issue(const IpCtx& c, uint32_t buf, int k0) {
 // its first half, S of its second half, PV of the previous tile's second half; join (tile t + 1
 // landed, tile t - 1 retired); queue tile t + IP_NBUF - 1 into tile t - 1's buffer; phase B =
 // softmax of the second half, S of the next tile's first half (unless LAST), PV of this tile's first
-// half.
-template <bool FIRST, bool LAST>
+// half. B = t % IP_NBUF when the caller knows it (unrolled sweep: buffer addresses become
+// immediate offsets), else -1.
+template <bool FIRST, bool LAST, int B = -1>
 __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&sB)[2], bf16x8 (&pA)[2][2],
                                         bf16x8 (&pB)[2][2], bf16 (*lds)[IP_TILE], const IpCtx& c, int t) {
-  const bf16* lk = lds[t % IP_NBUF];
+  const int b = B >= 0 ? B : t % IP_NBUF;
+  const bf16* lk = lds[b];
   const bf16* lv = lk + ICL_KT * ICL_D;
-  const bf16* lvp = lds[(t + IP_NBUF - 1) % IP_NBUF] + ICL_KT * ICL_D;
-  const bf16* lkn = lds[(t + 1) % IP_NBUF];
+  const bf16* lvp = lds[(b + IP_NBUF - 1) % IP_NBUF] + ICL_KT * ICL_D;
+  const bf16* lkn = lds[(b + 1) % IP_NBUF];
   const int k0 = (c.t0 + t) * ICL_KT;
   ip_phase<false, true, !FIRST>(st, sA, sB, pA, pB, lk, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
   static_assert(IP_NBUF == 4, "one tile (4 copies per wave) may stay in flight below");
   TA_WAIT_JOIN(4);
-  ip_issue(c, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
+  ip_issue(c, c.lds0 + ((b + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
            min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
   ip_phase<false, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
 }
@@ -733,7 +735,14 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       ip_iter<true, true>(st, sA, sB, pA, pB, lds, c, 0);
     } else if (nfull > 1) {
       ip_iter<true, false>(st, sA, sB, pA, pB, lds, c, 0);
-      for (int t = 1; t + 1 < nfull; ++t) ip_iter<false, false>(st, sA, sB, pA, pB, lds, c, t);
+      int t = 1;
+      for (; t + IP_NBUF < nfull; t += IP_NBUF) {  // t % IP_NBUF == 1 at the top
+        ip_iter<false, false, 1>(st, sA, sB, pA, pB, lds, c, t);
+        ip_iter<false, false, 2>(st, sA, sB, pA, pB, lds, c, t + 1);
+        ip_iter<false, false, 3>(st, sA, sB, pA, pB, lds, c, t + 2);
+        ip_iter<false, false, 0>(st, sA, sB, pA, pB, lds, c, t + 3);
+      }
+      for (; t + 1 < nfull; ++t) ip_iter<false, false>(st, sA, sB, pA, pB, lds, c, t);
       ip_iter<false, true>(st, sA, sB, pA, pB, lds, c, nfull - 1);
     }
     if (nfull > 0) ip_pv(st, pB, lds[(nfull - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
