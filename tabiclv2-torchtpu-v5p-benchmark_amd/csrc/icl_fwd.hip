@@ -426,9 +426,26 @@ __device__ __forceinline__ int ip_swz(int key) { return ((key & 3) << 1) | ((key
 struct IpState {
   bf16x8 qop[2][4];
   f32x16 o[2][2];
-  float nm[2];  // -m (log2 units) of this lane's query in column block qc
-  float l[2];   // this lane's share of the row sums
+  float nm[2];      // -m (log2 units) of this lane's query in column block qc
+  f32x4 lacc[2];    // row sums of column block qc: element 0 of lanes 0..31 (query lane % 32)
+  bf16x8 rs_ones;   // A operand of the row-sum product
 };
+
+// The row sums come from the matrix core: a 16x16x32 MFMA reads a PV operand pop[qc][m] (lane l:
+// keys 8(l/32)+j of query l%32) as its B operand, i.e. lane group g = l/16 as k rows 8g..8g+7 of
+// column l%16, which hold keys 8(g>>1)+j of query 16(g&1) + l%16. With A row 0 = 1 on the groups
+// g = 0, 2 and A row 4 = 1 on g = 1, 3, D[0][n] is the sum over the 16 keys of query n and D[4][n]
+// that of query 16 + n; lane l < 32 receives D[4(l/16)][l%16], its own query's sum, in element 0,
+// and lanes 32..63 receive zero rows. A lane holds A[l%16][8(l/16)+j].
+__device__ __forceinline__ bf16x8 ip_rs_ones(int lane) {
+  const bool one = ((lane & 15) == 0 && !((lane >> 4) & 1)) || ((lane & 15) == 4 && ((lane >> 4) & 1));
+  const bf16 v = (bf16)(one ? 1.0f : 0.0f);
+  const bf16x8 a = {v, v, v, v, v, v, v, v};
+  return a;
+}
+__device__ __forceinline__ void ip_rowsum(IpState& st, const bf16x8 (&pop)[2][2], int qc, int m) {
+  st.lacc[qc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.rs_ones, pop[qc][m], st.lacc[qc], 0, 0, 0);
+}
 
 
 // K operand of the S product: d-slice sl of rows kr..kr+31 of the K tile.
@@ -473,7 +490,7 @@ __device__ __forceinline__ void ip_s(f32x16 (&s)[2], const IpState& st, const bf
   }
 }
 
-// O^T += V^T P^T for keys kr..kr+31 of the V tile.
+// O^T += V^T P^T for keys kr..kr+31 of the V tile, and the row sums of P.
 __device__ __forceinline__ void ip_pv(IpState& st, const bf16x8 (&pop)[2][2], const bf16* lv, int kr, int lane) {
 #pragma unroll
   for (int db = 0; db < 2; ++db)
@@ -481,7 +498,10 @@ __device__ __forceinline__ void ip_pv(IpState& st, const bf16x8 (&pop)[2][2], co
     for (int m = 0; m < 2; ++m) {
       const bf16x8 a = ip_vop(lv, kr, m, db, lane);
 #pragma unroll
-      for (int qc = 0; qc < 2; ++qc) st.o[qc][db] = mfma32x32x16(a, pop[qc][m], st.o[qc][db]);
+      for (int qc = 0; qc < 2; ++qc) {
+        st.o[qc][db] = mfma32x32x16(a, pop[qc][m], st.o[qc][db]);
+        if (db == 0) ip_rowsum(st, pop, qc, m);
+      }
     }
 }
 
@@ -494,15 +514,14 @@ __device__ __forceinline__ void ip_mask(f32x16 (&s)[2], int k0, int valid, int h
       if (k0 + 8 * (r >> 2) + 4 * hh + (r & 3) >= valid) s[qc][r] = TA_NEG_INF;
 }
 
-// Probabilities 2k, 2k+1 of column block qc: exp2(s sc - m), one packed convert for the PV product,
-// row sum in fp32 (two adds: v_dot2 over the bf16 pair measured slower next to the MFMAs).
+// Probabilities 2k, 2k+1 of column block qc: exp2(s sc - m), one packed convert for the PV product
+// (their row sums are taken with the PV product, on the matrix core).
 __device__ __forceinline__ void ip_exp2(const f32x16 (&s)[2], const IpState& st, float sc, bf16x8 (&pop)[2][2],
-                                        float (&ls)[2], int qc, int k) {
+                                        int qc, int k) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qc][2 * k], sc, st.nm[qc]));
   const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qc][2 * k + 1], sc, st.nm[qc]));
   const bf16x2 pr = {(bf16)p0, (bf16)p1};
-  ls[qc] += p0 + p1;
   pop[qc][k >> 2][(2 * k) & 7] = pr[0];
   pop[qc][k >> 2][(2 * k + 1) & 7] = pr[1];
 }
@@ -530,7 +549,6 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
 #pragma unroll
       for (int r = 0; r < 16; ++r) nxt[qc][r] = 0.f;
   }
-  float ls[2] = {st.l[0], st.l[1]};  // the row sums accumulate in place
   bf16x8 op[8];
   if (I0 < I1) op[I0] = read_op(I0);
   if (I0 + 1 < I1) op[I0 + 1] = read_op(I0 + 1);
@@ -538,8 +556,8 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     if (i < I0 || i >= I1) {
-      ip_exp2(cur, st, sc, pcur, ls, (2 * i) >> 3, (2 * i) & 7);
-      ip_exp2(cur, st, sc, pcur, ls, (2 * i + 1) >> 3, (2 * i + 1) & 7);
+      ip_exp2(cur, st, sc, pcur, (2 * i) >> 3, (2 * i) & 7);
+      ip_exp2(cur, st, sc, pcur, (2 * i + 1) >> 3, (2 * i + 1) & 7);
       continue;
     }
     if (i + 2 < I1) op[i + 2] = read_op(i + 2);
@@ -550,14 +568,13 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
       } else {
         const int j = i - 4;
         st.o[qc][j >> 1] = mfma32x32x16(op[i], pprev[qc][j & 1], st.o[qc][j >> 1]);
+        if (j < 2) ip_rowsum(st, pprev, qc, j);
       }
       const int step = 2 * i + qc;  // 0..15, two probabilities each
-      ip_exp2(cur, st, sc, pcur, ls, step >> 3, step & 7);
+      ip_exp2(cur, st, sc, pcur, step >> 3, step & 7);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  st.l[0] = ls[0];
-  st.l[1] = ls[1];
 }
 
 struct IpCtx {
@@ -628,11 +645,8 @@ __device__ __forceinline__ void ip_tail(IpState& st, const bf16* lk, const bf16*
     bf16x8 pT[2][2];
     ip_s(sT, st, lk, 32 * half, lr, hh);
     ip_mask(sT, k0 + 32 * half, valid, hh);
-    float ls[2] = {0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ip_exp2(sT, st, sc, pT, ls, j >> 3, j & 7);
-    st.l[0] += ls[0];
-    st.l[1] += ls[1];
+    for (int j = 0; j < 16; ++j) ip_exp2(sT, st, sc, pT, j >> 3, j & 7);
     ip_pv(st, pT, lv, 32 * half, lane);
   }
 }
@@ -660,6 +674,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
 
   const bf16* qbase = (const bf16*)p.q + n * p.q_sn + h * p.q_sh;
   IpState st;
+  st.rs_ones = ip_rs_ones(lane);
 #pragma unroll
   for (int qc = 0; qc < 2; ++qc) {
     const int qi = qw0 + qc * 32 + lr;
@@ -669,7 +684,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       st.qop[qc][s] = qi < p.Tq ? *(const bf16x8*)(qbase + (int64_t)qi * p.q_st + 16 * s + 8 * hh) : z;
     }
     st.nm[qc] = 0.f;
-    st.l[qc] = 0.f;
+    st.lacc[qc] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -758,7 +773,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
   bool bad = false;
 #pragma unroll
   for (int qc = 0; qc < 2; ++qc) {
-    lt[qc] = lane_pair_sum(st.l[qc]);
+    lt[qc] = lane_pair_sum(st.lacc[qc][0]);
     bad |= !(lt[qc] <= IP_L_HI);
 #pragma unroll
     for (int db = 0; db < 2; ++db)
