@@ -56,6 +56,7 @@ struct ShParams {
   int nqb, qbpw, nwg_b;
   int exact_scale;  // fold scale and log2e into the K operand: scale is a power of two (bf16(q * scale)
                     // needs no rounding) and the runs are long enough to amortise the K split
+  int half_last;    // the last 32-key group's upper 16 keys are all past Lk (resident kernel, 4 groups)
 };
 
 template <typename T, int KT> struct ShLds {
@@ -309,25 +310,22 @@ __device__ __forceinline__ f32x4 rs_tab(__amdgpu_buffer_rsrc_t rsrc, int off) {
 }
 
 // Lanes l and l ^ 32 (G and G ^ 2) share the 8 dims d8..d8+7 of their operand k-slots; each has
-// computed 4 of them (G < 2: d8..d8+3, G >= 2: d8+4..d8+7) and the two swap (v_permlane32_swap).
+// computed 4 of them (G < 2: d8..d8+3, G >= 2: d8+4..d8+7). One v_permlane32_swap per word trades
+// the upper lanes' vdst with the lower lanes' vsrc; with both operands = the lane's own 4, the
+// swapped vdst holds dims d8..d8+3 and the swapped vsrc dims d8+4..d8+7 in every lane.
 __device__ __forceinline__ bf16x8 rs_pair8(bf16x4 mine, int G) {
-  const bool low = G < 2;  // lanes 0..31
+  (void)G;
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
   const u32x2 sw = __builtin_bit_cast(u32x2, mine);
-  u32x2 rw;
+  u32x4v w;
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const auto r = __builtin_amdgcn_permlane32_swap(sw[w], sw[w], false, false);
-    rw[w] = low ? r[1] : r[0];
+  for (int k = 0; k < 2; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(sw[k], sw[k], false, false);
+    w[k] = r[0];
+    w[2 + k] = r[1];
   }
-  const bf16x4 recv = __builtin_bit_cast(bf16x4, rw);
-  bf16x8 op;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    op[j] = low ? mine[j] : recv[j];
-    op[4 + j] = low ? recv[j] : mine[j];
-  }
-  return op;
+  return __builtin_bit_cast(bf16x8, w);
 }
 
 // K operand with c = scale * log2e folded in: k c as a bf16 high part (G < 2, k-slots 0..15) and
@@ -345,51 +343,46 @@ __device__ __forceinline__ bf16x8 rs_ksplit(bf16x8 k, float c, int G) {
 }
 
 // q' log2e operand from this lane's 4 values of q' = bf16(rope(q) * scale) (the reference's packed
-// kernels, :498-502), held as floats. Each lane splits its 4 into bf16 high parts and bf16
-// remainders and swaps with lane l ^ 32 the half the other needs (v_permlane32_swap), so G < 2 ends
-// with the 8 high parts and G >= 2 with the 8 remainders of the shared dims.
+// kernels, :498-502), held as floats. Each lane splits its 4 into bf16 high parts (vdst) and bf16
+// remainders (vsrc); one v_permlane32_swap per word (upper lanes' vdst <-> lower lanes' vsrc) leaves
+// lanes G < 2 with the 8 high parts and lanes G >= 2 with the 8 remainders of the shared dims, in
+// k-slot order, with no selects.
 __device__ __forceinline__ bf16x8 rs_qsplit(f32x4 qs, int G) {
-  const bool low = G < 2;  // lanes 0..31
-  bf16x4 keep, send;
+  (void)G;
+  f32x4 x, rem;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float x = qs[j] * TA_LOG2E;
-    const bf16 hi = (bf16)x;
-    const bf16 lo = (bf16)(x - (float)hi);
-    keep[j] = low ? hi : lo;
-    send[j] = low ? lo : hi;
-  }
+  for (int j = 0; j < 4; ++j) x[j] = qs[j] * TA_LOG2E;
+  const bf16x4 hi = cvt_bf16x4(x);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) rem[j] = x[j] - (float)hi[j];
+  const bf16x4 lo = cvt_bf16x4(rem);
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 sw = __builtin_bit_cast(u32x2, send);
-  u32x2 rw;
+  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+  const u32x2 hw = __builtin_bit_cast(u32x2, hi), lw = __builtin_bit_cast(u32x2, lo);
+  u32x4v w;
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const auto r = __builtin_amdgcn_permlane32_swap(sw[w], sw[w], false, false);
-    rw[w] = low ? r[1] : r[0];
+  for (int k = 0; k < 2; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(hw[k], lw[k], false, false);
+    w[k] = r[0];
+    w[2 + k] = r[1];
   }
-  const bf16x4 recv = __builtin_bit_cast(bf16x4, rw);
-  bf16x8 op;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    op[j] = low ? keep[j] : recv[j];
-    op[4 + j] = low ? recv[j] : keep[j];
-  }
-  return op;
+  return __builtin_bit_cast(bf16x8, w);
 }
 
 // Scores of the 32-key group kg, x = K (q' log2e) + b2: lane (l16, G) holds keys 32kg + 4G + r (x0)
 // and 32kg + 16 + 4G + r (x1) of query l16 (the k-slot order 8G + j of the 16x16x32 B operand).
 // Groups below MF have b2 = 0 for every key (no bias, all keys valid): a zero accumulator.
+// skip1: keys 32kg+16.. do not exist (x1 is not computed).
 template <int MF>
 __device__ __forceinline__ void rs_scores(bf16x8 ka0, bf16x8 ka1, bf16x8 qop, const float* lds_b2, int kg,
-                                          int G, f32x4& x0, f32x4& x1) {
+                                          int G, f32x4& x0, f32x4& x1, bool skip1 = false) {
   f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
   if (kg >= MF) {
     c0 = *(const f32x4*)(lds_b2 + 32 * kg + 4 * G);
-    c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
+    if (!skip1) c1 = *(const f32x4*)(lds_b2 + 32 * kg + 16 + 4 * G);
   }
   x0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka0, qop, c0, 0, 0, 0);
-  x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
+  if (!skip1) x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka1, qop, c1, 0, 0, 0);
 }
 
 __device__ __forceinline__ float rs_sum(bf16x8 ones, bf16x8 pv) {
@@ -399,20 +392,23 @@ __device__ __forceinline__ float rs_sum(bf16x8 ones, bf16x8 pv) {
 
 // One (16 queries, head) unit over all keys: p = bf16(exp2(x - sub)), l = sum p (ones-operand
 // MFMA), o = V^T p^T, accumulated group by group in key order.
-template <int NG, int MF, bool SUB>
+// HALF: the last group's keys 32(NG-1)+16.. are all past Lk, so its second score product and
+// their probabilities are skipped (zero).
+template <int NG, int MF, bool SUB, bool HALF>
 __device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG], bf16x8 ones,
                                         bf16x8 qop, const float* lds_b2, int G, float sub, f32x4& o, float& l) {
   o = f32x4{0.f, 0.f, 0.f, 0.f};
   l = 0.f;
 #pragma unroll
   for (int kg = 0; kg < NG; ++kg) {
+    const bool half = HALF && kg == NG - 1;
     f32x4 x0, x1;
-    rs_scores<MF>(ka[kg][0], ka[kg][1], qop, lds_b2, kg, G, x0, x1);
+    rs_scores<MF>(ka[kg][0], ka[kg][1], qop, lds_b2, kg, G, x0, x1, half);
     bf16x8 pv;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       pv[r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x0[r] - sub : x0[r]);
-      pv[4 + r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
+      pv[4 + r] = half ? (bf16)0.f : (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
     }
     l += rs_sum(ones, pv);
     o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kg], pv, o, 0, 0, 0);
@@ -422,15 +418,16 @@ __device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 
 }
 
 // Largest x of query l16 over all keys (keys past the valid length hold -inf).
-template <int NG, int MF>
+template <int NG, int MF, bool HALF>
 __device__ __forceinline__ float rs_max(const bf16x8 (&ka)[NG][2], bf16x8 qop, const float* lds_b2, int G) {
   float m = TA_NEG_INF;
 #pragma unroll
   for (int kg = 0; kg < NG; ++kg) {
+    const bool half = HALF && kg == NG - 1;
     f32x4 x0, x1;
-    rs_scores<MF>(ka[kg][0], ka[kg][1], qop, lds_b2, kg, G, x0, x1);
+    rs_scores<MF>(ka[kg][0], ka[kg][1], qop, lds_b2, kg, G, x0, x1, half);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(x0[r], x1[r]));
+    for (int r = 0; r < 4; ++r) m = fmaxf(m, half ? x0[r] : fmaxf(x0[r], x1[r]));
   }
   return quad_max(m);
 }
@@ -475,7 +472,7 @@ __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 c
 // normalised output (this lane's 4 dims, bf16).
 // With RoPE, cs / sn hold this block's cos / sin on entry and the next block's (table byte offset
 // cnext) on return: reloaded as soon as the q' operand is built, a block of work ahead of their use.
-template <int NG, int MF, bool ROPE, bool EXACT>
+template <int NG, int MF, bool ROPE, bool EXACT, bool HALF>
 __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
                                          bf16x8 ones, const float* lds_b2, const bf16* qbase, bf16x8 qr, f32x4& cs,
                                          f32x4& sn, __amdgpu_buffer_rsrc_t crsrc, __amdgpu_buffer_rsrc_t srsrc,
@@ -508,12 +505,12 @@ __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[
   }
   f32x4 o;
   float l;
-  rs_unit<NG, MF, false>(ka, va, ones, qop, lds_b2, G, 0.f, o, l);
+  rs_unit<NG, MF, false, HALF>(ka, va, ones, qop, lds_b2, G, 0.f, o, l);
   if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
     // rare: recompute with the exact maximum subtracted (queries in range keep theirs)
-    const float mx = rs_max<NG, MF>(ka, qop, lds_b2, G);
+    const float mx = rs_max<NG, MF, HALF>(ka, qop, lds_b2, G);
     const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
-    rs_unit<NG, MF, true>(ka, va, ones, qop, lds_b2, G, sub, o, l);
+    rs_unit<NG, MF, true, HALF>(ka, va, ones, qop, lds_b2, G, sub, o, l);
   }
   const float inv = l == 0.f ? 0.f : __builtin_amdgcn_rcpf(l);
   bf16x4 ov;
@@ -531,7 +528,7 @@ __device__ __forceinline__ void rs_store(__amdgpu_buffer_rsrc_t orsrc, u32x2 ov,
 // NG = 32-key groups swept (ceil(Lk / 32)); b2 is read from LDS for groups kg >= MF only; ROPE:
 // q and k take the rotary embedding; EXACT: the scale is a power of two (scale and log2e folded
 // into the K operand, raw q as the B operand).
-template <int NG, int MF, bool ROPE, bool EXACT>
+template <int NG, int MF, bool ROPE, bool EXACT, bool HALF = false>
 __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   constexpr int NT = SH_H * 64;
   __shared__ __attribute__((aligned(16))) bf16 lds_k[RS_LK * RS_KSTR];
@@ -696,18 +693,18 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < nb; i += 2) {
-    u32x2 ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
+    u32x2 ov = rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
                                               coff + (i + 1) * cstep, orow + i * 16 + l16, d4, G);
     qa = rs_qraw(qrsrc, qoff + (i + 2) * qstep);
     rs_store(orsrc, ov, ooff + i * ostep);
-    ov = rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qb, cs, sn, crsrc, srsrc,
+    ov = rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qbase, qb, cs, sn, crsrc, srsrc,
                                        coff + (i + 2) * cstep, orow + (i + 1) * 16 + l16, d4, G);
     qb = rs_qraw(qrsrc, qoff + (i + 3) * qstep);
     rs_store(orsrc, ov, ooff + (i + 1) * ostep);
   }
   if (i < nb)
     rs_store(orsrc,
-             rs_block<NG, MF, ROPE, EXACT>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
+             rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
                                            coff + (i + 1) * cstep, orow + i * 16 + l16, d4, G),
              ooff + i * ostep);
 }
@@ -717,6 +714,17 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
 template <int NG, bool ROPE, bool EXACT>
 void launch_resident_mode(const ShParams& p, int mode, int64_t nblk, hipStream_t stream) {
   const dim3 grid((unsigned)nblk), block(SH_H * 64);
+  if constexpr (NG == 4) {
+    // the row stage's 104 keys: the last group's upper half holds no key
+    if (p.half_last && mode == 0) {
+      hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, EXACT, true>), grid, block, 0, stream, p);
+      return;
+    }
+    if (p.half_last && mode == 1) {
+      hipLaunchKernelGGL((sh_resident_kernel<NG, NG - 1, ROPE, EXACT, true>), grid, block, 0, stream, p);
+      return;
+    }
+  }
   if (mode == 0)
     hipLaunchKernelGGL((sh_resident_kernel<NG, 0, ROPE, EXACT>), grid, block, 0, stream, p);
   else if (mode == 1)
@@ -975,6 +983,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     int e = 0;
     p.exact_scale = scale > 0.f && frexpf(scale, &e) == 0.5f;
   }
+  p.half_last = 0;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   const bool fast_rope = rope == 0 || (rope == 1 && rot == 16) || (rope == 2 && half == 8 && rot == 16);
   // the resident kernel's buffer loads take 32-bit byte offsets within a batch element (query runs
@@ -996,6 +1005,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     if (rope) p.exact_scale = 0;
     const int64_t nblk = B * (int64_t)p.nwg_b;
     const int ngrp = (int)((Lk + 31) / 32);  // 32-key groups every batch element sweeps
+    p.half_last = Lk - 32 * (ngrp - 1) <= 16;
     const int mode = (bias || valid) ? 0 : (Lk == 32 * ngrp ? 2 : 1);
     launch_resident(p, ngrp, mode, nblk, stream);
     return (int)hipGetLastError();
