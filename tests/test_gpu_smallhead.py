@@ -55,6 +55,7 @@ def _rope_np(rope, L):
     ("col2_fp32", 4, 1024, 128, torch.float32, False),
     ("col1_bf16", 4, 128, 576, torch.bfloat16, False),
     ("row_bf16", 16, 104, 104, torch.bfloat16, False),
+    ("row_bf16_bias", 16, 104, 104, torch.bfloat16, True),
     ("row_fp32_bias", 16, 108, 108, torch.float32, True),
     ("cls_bf16", 16, 4, 104, torch.bfloat16, False),
     ("ragged_bf16_bias", 3, 77, 1500, torch.bfloat16, True),
@@ -180,6 +181,7 @@ def test_hxq_inference_tile_subset(dev):
 
 @pytest.mark.parametrize("name,B,L,dtype,interleaved,bias", [
     ("self_bf16_rope_halves", 16, 104, torch.bfloat16, False, False),
+    ("self_bf16_rope_halves_bias", 16, 104, torch.bfloat16, False, True),
     ("self_fp32_rope_halves_bias", 16, 108, torch.float32, False, True),
     ("self_fp32_rope_pairs", 8, 104, torch.float32, True, False),
     ("self_bf16_norope", 4, 300, torch.bfloat16, None, False),
