@@ -328,8 +328,11 @@ def bench_c5(steps: int, warmup: int) -> list:
     attention (8 estimators x 8 heads, test rows padded to the 1k bucket over the train bucket,
     valid = n_train per table) for 12 blocks. Each (bucket, kernel) is timed on its own inputs (so
     only one bucket's tensors are resident); the step time is the sum. TFLOP/s on the real
-    (unpadded) sizes; padding efficiency = real / processed FLOPs (the kernels never visit keys
-    past valid, so only padded query rows cost work)."""
+    (unpadded) sizes. The kernels never visit keys past valid; padded query rows are skipped by the
+    ragged entry points (per-table row counts q_len: ISAB-2 rows n_train + n_test, ICL test rows
+    n_test), which work in 16-row (ISAB-2) and 256-row (ICL) units: padding efficiency = real /
+    processed FLOPs at that granularity. `padded_ms` times the same buckets with every padded row
+    computed, as the reference's bucketed runner does."""
     import torch
 
     import tabicl_mi355_attn as pk
@@ -340,7 +343,8 @@ def bench_c5(steps: int, warmup: int) -> list:
     n_train, n_test = c5_tables()
     g = torch.Generator(device=dev)
     g.manual_seed(4)
-    parts = {"isab1": [0.0, 0.0, 0.0], "isab2": [0.0, 0.0, 0.0], "icl": [0.0, 0.0, 0.0]}  # ms, real, padded FLOPs
+    # ms (ragged), real FLOPs, processed FLOPs, ms with every padded row computed
+    parts = {"isab1": [0.0, 0.0, 0.0, 0.0], "isab2": [0.0, 0.0, 0.0, 0.0], "icl": [0.0, 0.0, 0.0, 0.0]}
     groups = {}
     for i in range(64):
         groups.setdefault(("isab", c5_bucket(int(n_train[i] + n_test[i]))), []).append(i)
@@ -358,13 +362,17 @@ def bench_c5(steps: int, warmup: int) -> list:
             parts["isab1"][0] += ms
             parts["isab1"][1] += real
             parts["isab1"][2] += real  # keys past valid are never visited: no padded work
+            parts["isab1"][3] += ms
             del q, kv
             q2 = torch.randn(B, L, E, generator=g, device=dev, dtype=torch.bfloat16)
             kv2 = torch.randn(B, IND, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
-            ms = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25), steps, warmup)
+            rows = torch.tensor([int(n) + m for n, m in zip(nt, ns)], dtype=torch.int32)
+            qlen = rows.repeat_interleave(EST_ * FEAT).to(dev)
+            parts["isab2"][3] += _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25), steps, warmup)
+            ms = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25, q_len=qlen), steps, warmup)
             parts["isab2"][0] += ms
-            parts["isab2"][1] += sum(4.0 * (int(n) + m) * IND * 16 * H * EST_ * FEAT for n, m in zip(nt, ns))
-            parts["isab2"][2] += 4.0 * L * IND * 16 * H * B
+            parts["isab2"][1] += sum(4.0 * int(r) * IND * 16 * H * EST_ * FEAT for r in rows)
+            parts["isab2"][2] += sum(4.0 * (-(-int(r) // 16) * 16) * IND * 16 * H * EST_ * FEAT for r in rows)
             del q2, kv2
         else:
             N, Tq = len(tabs) * EST_, C5_BUCKETS[0]
@@ -373,32 +381,41 @@ def bench_c5(steps: int, warmup: int) -> list:
             v = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
             q = torch.randn(N, H, Tq, 64, generator=g, device=dev, dtype=torch.bfloat16)
             out = torch.empty_like(q)
+            qlen = torch.tensor(ns, dtype=torch.int32).repeat_interleave(EST_).to(dev)
 
-            def step():
+            def step_padded():
                 for _ in range(BLOCKS):  # one block's cache stands for each of the 12 blocks
                     icl.ICL_FWD_OUT(q, k, v, valid, 64 ** -0.5, out)
 
+            def step():
+                for _ in range(BLOCKS):
+                    icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, out)
+
+            parts["icl"][3] += _time(step_padded, steps, warmup)
             ms = _time(step, steps, warmup)
             parts["icl"][0] += ms
             parts["icl"][1] += BLOCKS * sum(4.0 * m * int(n) * 64 * H * EST_ for n, m in zip(nt, ns))
-            # keys past valid are never visited; the padded query rows are
-            parts["icl"][2] += BLOCKS * sum(4.0 * Tq * int(n) * 64 * H * EST_ for n in nt)
+            # keys past valid are never visited; query rows are processed in 256-row work items
+            parts["icl"][2] += BLOCKS * sum(4.0 * (-(-m // 256) * 256) * int(n) * 64 * H * EST_ for n, m in zip(nt, ns))
             del k, v, q, out
         torch.cuda.empty_cache()
     recs = []
     names = {"isab1": "C5 column ISAB-1 (hxq, ragged valid)", "isab2": "C5 column ISAB-2 (pk_cross)",
              "icl": "C5 cached-KV ICL (12 blocks, per-table valid)"}
-    total = 0.0
-    for key, (ms, real, padded) in parts.items():
+    total = total_padded = 0.0
+    for key, (ms, real, padded, ms_padded) in parts.items():
         total += ms
+        total_padded += ms_padded
         tf = real / (ms * 1e-3) / 1e12
         recs.append({"metric": f"ms per {names[key]} step", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
                      "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": "bf16",
                      "data": "synthetic N(0,1), seed 4", "config": {"workload": "C5: 64 tables, buckets 1k-16k"},
                      "attn_tflops_real": round(tf, 2), "padding_efficiency": round(real / padded, 4),
+                     "padded_ms": round(ms_padded, 4),
                      "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                                   "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
     recs.append({"metric": "ms per C5 ragged mixed-batch step (ISAB pair + ICL)", "value": round(total, 4),
+                 "padded_ms": round(total_padded, 4),
                  "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
                  "dtype": "bf16", "data": "synthetic N(0,1), seed 4",
                  "config": {"workload": "C5: 64 tables, n_train log-uniform [500, 10000], n_test 10%, 8 est, "

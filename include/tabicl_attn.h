@@ -94,6 +94,20 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
                         int32_t dtype, void* stream);
 
 /*
+ * tabicl_pk_cross_fwd over a ragged batch: q_len (device int32 [q_len_n], q_len_n in {1, B}) gives
+ * the query rows each batch element needs. Rows below q_len[b] equal tabicl_pk_cross_fwd's bit for
+ * bit; the contents of rows at or past it are unspecified: the bf16 kernel for Lk <= 128 (the column
+ * ISAB-2 shape) neither computes nor writes them, the other kernels compute them. No counterpart in the reference: its shape-bucketed runner
+ * (scripts/tabicl_tpu_bucketed.py:36-103, 1287-1397) pads each table's rows to the bucket and
+ * computes the padding; callers that know each table's row count pass it here instead.
+ */
+int tabicl_pk_cross_fwd_ragged(const void* q, int64_t q_b, const void* kv, const float* bias,
+                               int64_t bias_b, const float* cq, const float* sq, const float* ck,
+                               const float* sk, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                               int32_t h, int32_t rope, int32_t half, int32_t rot, float scale,
+                               int32_t dtype, const int32_t* q_len, int64_t q_len_n, void* stream);
+
+/*
  * Folded first ISAB attention (inference): U = softmax(qf x^T) x, one head of head dim E = 128 over
  * the raw rows x (K = V = x), qf pre-scaled (no scale applied).
  * Replaces tabicl_pk::hxf_fwd (reference scripts/tabicl_tpu_pallas_attn.py:345-404, 414-419, 429-442).
@@ -174,6 +188,23 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
                    int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn,
                    int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/*
+ * tabicl_icl_fwd over a ragged batch: q_len (device int32 [q_len_n], q_len_n in {1, N}) gives the
+ * query rows of each n that are computed. Rows at or past q_len[n] are neither computed nor written
+ * (out keeps what it held; no key-split partial is stored or merged for them), and work items
+ * (256 query rows x one head) holding none of them exit at once. Rows below q_len[n] equal
+ * tabicl_icl_fwd's bit for bit. No counterpart in the reference: its bucketed runner pads the
+ * test rows of each table to a test bucket (scripts/tabicl_tpu_bucketed.py:36-103, 1329-1378) and
+ * attends with the padding rows too; callers that know each table's test-row count pass it here.
+ */
+int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int32_t* valid,
+                          int64_t valid_n, const int32_t* q_len, int64_t q_len_n, void* out, int64_t N,
+                          int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh,
+                          int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st, int64_t v_sn,
+                          int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                          float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                          void* stream);
 
 /*
  * Workspace size (bytes) that tabicl_icl_fwd uses for these sizes on the current device (0 when

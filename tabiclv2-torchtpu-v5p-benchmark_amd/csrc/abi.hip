@@ -191,11 +191,21 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
                         const float* sk, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
                         int32_t h, int32_t rope, int32_t half, int32_t rot, float scale,
                         int32_t dtype, void* stream) {
+  return tabicl_pk_cross_fwd_ragged(q, q_b, kv, bias, bias_b, cq, sq, ck, sk, out, B, Lq, Lk, E, h, rope, half,
+                                    rot, scale, dtype, nullptr, 0, stream);
+}
+
+int tabicl_pk_cross_fwd_ragged(const void* q, int64_t q_b, const void* kv, const float* bias,
+                               int64_t bias_b, const float* cq, const float* sq, const float* ck,
+                               const float* sk, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                               int32_t h, int32_t rope, int32_t half, int32_t rot, float scale,
+                               int32_t dtype, const int32_t* q_len, int64_t q_len_n, void* stream) {
   int st = smallhead_shape("pk_cross_fwd", B, Lq, Lk, E, h, dtype);
   if (st) return st;
   if ((st = rope_args("pk_cross_fwd", rope, half, rot))) return st;
   if (rope && (!cq || !sq || !ck || !sk)) return fail(1, "pk_cross_fwd: rope tables missing");
   if (q_b != 1 && q_b != B) return fail(1, "pk_cross_fwd: q batch must be 1 or B");
+  if (q_len && q_len_n != 1 && q_len_n != B) return fail(1, "pk_cross_fwd: q_len must hold 1 or B entries");
   if (bias && bias_b != 1 && bias_b != B)
     return fail(1, "pk_cross_fwd: bias batch %lld must be 1 or B", (long long)bias_b);
   if (!aligned16(q) || !aligned16(kv) || !aligned16(out))
@@ -206,7 +216,8 @@ int tabicl_pk_cross_fwd(const void* q, int64_t q_b, const void* kv, const float*
       tabicl_launch_smallhead(q, q_b == 1 && B > 1 ? 0 : Lq * E, E, kvb, Lk * 2 * E, 2 * E,
                               kvb + E * esize(dtype), Lk * 2 * E, 2 * E, out, bias,
                               bias && bias_b == B ? Lk : 0, nullptr, 0, cq, sq, ck, sk, rope, half,
-                              rot, scale, B, Lq, Lk, dtype, nullptr, 0, (hipStream_t)stream),
+                              rot, scale, B, Lq, Lk, dtype, nullptr, 0, (hipStream_t)stream, q_len,
+                              q_len ? q_len_n : 0),
       "pk_cross_fwd");
 }
 
@@ -286,6 +297,18 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
                    int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn,
                    int64_t o_sh, int64_t o_st, float scale, int32_t dtype, void* workspace,
                    int64_t workspace_bytes, void* stream) {
+  return tabicl_icl_fwd_ragged(q, k, v, valid, valid_n, nullptr, 0, out, N, H, Tq, Tkv, D, q_sn, q_sh, q_st, k_sn,
+                               k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype, workspace,
+                               workspace_bytes, stream);
+}
+
+int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int32_t* valid,
+                          int64_t valid_n, const int32_t* q_len, int64_t q_len_n, void* out, int64_t N,
+                          int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh,
+                          int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st, int64_t v_sn,
+                          int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                          float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
   if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
     return fail(1, "icl_fwd: dtype code %d not supported", dtype);
   if (D != 64) return fail(1, "icl_fwd: head dim must be 64, got %lld", (long long)D);
@@ -293,6 +316,8 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
     return fail(1, "icl_fwd: bad sizes");
   if (valid && valid_n != 1 && valid_n != N)
     return fail(1, "icl_fwd: valid must hold 1 or N entries");
+  if (q_len && q_len_n != 1 && q_len_n != N)
+    return fail(1, "icl_fwd: q_len must hold 1 or N entries");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(1, "icl_fwd: pointers must be 16-byte aligned");
   const int64_t strides[12] = {q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st};
@@ -305,7 +330,7 @@ int tabicl_icl_fwd(const void* q, const void* k, const void* v, const int32_t* v
       tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, 64, q_sn, q_sh,
                             q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale,
                             dtype, workspace && aligned16(workspace) ? workspace : nullptr,
-                            workspace_bytes, (hipStream_t)stream),
+                            workspace_bytes, (hipStream_t)stream, q_len, q_len ? q_len_n : 0),
       "icl_fwd");
 }
 

@@ -36,6 +36,10 @@ struct IclParams {
   void* o;
   const int32_t* valid;
   int valid_n;
+  // query rows computed per batch element n (qlen[n], or qlen[0] for all; null: all Tq rows); rows
+  // at or past it are neither computed nor written, work items holding none of them skip the sweep
+  const int32_t* qlen;
+  int qlen_n;
   int N, H, Tq, Tkv, nqb;
   int64_t q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st;
   float sc;  // scale * log2(e)
@@ -46,6 +50,12 @@ struct IclParams {
   // per workgroup: 1 = the fast kernel's result must be recomputed exactly (null: no fast kernel)
   int* flags;
 };
+
+__device__ __forceinline__ int icl_live_rows(const IclParams& p, int n) {
+  if (!p.qlen) return p.Tq;
+  const int r = p.qlen[p.qlen_n == 1 ? 0 : n];
+  return r < 0 ? 0 : (r > p.Tq ? p.Tq : r);
+}
 
 // LDS tiles of the generic kernel for head dim D (64: ICL; 128: the folded ISAB-1 attention).
 template <typename T, int D = ICL_D> struct IclLds {
@@ -267,6 +277,9 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     valid = valid < 0 ? 0 : (valid > p.Tkv ? p.Tkv : valid);
   }
 
+  const int live = icl_live_rows(p, n);
+  if (qb * (QW * NW) >= live) return;  // no live query row: nothing to compute or write
+
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 31, hh = lane >> 5;
   const int qw0 = qb * (QW * NW) + wave * QW;
@@ -323,7 +336,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     for (int qc = 0; qc < QC; ++qc) {
       const float lt = lane_pair_sum(st.l_run[qc]);
       const int qi = qw0 + qc * 32 + lr;
-      if (qi < p.Tq) {
+      if (qi < live) {
         const int64_t row = ((int64_t)split * p.N * p.H + nh) * p.Tq + qi;
         float* orow = p.ws_o + row * D;
 #pragma unroll
@@ -345,7 +358,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     const float lt = lane_pair_sum(st.l_run[qc]);
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const int qi = qw0 + qc * 32 + lr;
-    if (qi < p.Tq) {
+    if (qi < live) {
       T* orow = (T*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st;
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
@@ -369,6 +382,10 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
   if (idx >= rows * (D / 4)) return;
   const int64_t row = idx / (D / 4);
   const int c4 = (int)(idx % (D / 4)) * 4;
+  const int64_t nh = row / p.Tq;
+  const int qi = (int)(row % p.Tq);
+  const int n = (int)(nh / p.H), h = (int)(nh % p.H);
+  if (qi >= icl_live_rows(p, n)) return;  // not computed: no partials to merge, nothing written
   float mstar = TA_NEG_INF;
   for (int s = 0; s < p.nsplit; ++s) {
     const float2 ml = *(const float2*)(p.ws_ml + ((int64_t)s * rows + row) * 2);
@@ -385,9 +402,6 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
     l += w * ml.y;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int64_t nh = row / p.Tq;
-  const int qi = (int)(row % p.Tq);
-  const int n = (int)(nh / p.H), h = (int)(nh % p.H);
   T* dst = (T*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st + c4;
   typename OpVec<T, 4>::type ov;
   ov[0] = from_f32<T>(acc.x * inv); ov[1] = from_f32<T>(acc.y * inv);
@@ -668,6 +682,12 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     valid = valid < 0 ? 0 : (valid > p.Tkv ? p.Tkv : valid);
   }
 
+  const int live = icl_live_rows(p, n);
+  if (qb * (IP_QW * IP_NW) >= live) {  // no live query row: nothing to compute or write
+    if (threadIdx.x == 0) p.flags[work] = 0;
+    return;
+  }
+
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 31, hh = lane >> 5;
   const int qw0 = qb * (IP_QW * IP_NW) + wave * IP_QW;
@@ -768,6 +788,21 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     TA_WAIT_JOIN(0);  // no copy into this workgroup's LDS may outlive it
   }
 
+  if (p.qlen) {
+    // rows at or past the live count are not written: clear their state so that they cannot flag
+    // the work item for the exact recompute
+#pragma unroll
+    for (int qc = 0; qc < 2; ++qc)
+      if (qw0 + qc * 32 + lr >= live) {
+        st.nm[qc] = 0.f;
+        st.lacc[qc] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st.o[qc][db][r] = 0.f;
+      }
+  }
+
   // trust test of the fixed reference; any failing lane flags the work item for exact recompute
   float lt[2];
   bool bad = false;
@@ -788,7 +823,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
 #pragma unroll
     for (int qc = 0; qc < 2; ++qc) {
       const int qi = qw0 + qc * 32 + lr;
-      if (qi < p.Tq) {
+      if (qi < live) {
         const int64_t row = ((int64_t)split * p.N * p.H + nh) * p.Tq + qi;
         float* orow = p.ws_o + row * ICL_D;
 #pragma unroll
@@ -808,7 +843,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
   for (int qc = 0; qc < 2; ++qc) {
     const float inv = lt[qc] > 0.f ? 1.f / lt[qc] : 0.f;
     const int qi = qw0 + qc * 32 + lr;
-    if (qi < p.Tq) {
+    if (qi < live) {
       bf16* orow = (bf16*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
@@ -917,10 +952,12 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
-                          void* ws, int64_t ws_bytes, hipStream_t stream) {
+                          void* ws, int64_t ws_bytes, hipStream_t stream, const int32_t* qlen,
+                          int64_t qlen_n) {
   IclParams p;
   p.q = q; p.k = k; p.v = v; p.o = out;
   p.valid = valid; p.valid_n = (int)valid_n;
+  p.qlen = qlen; p.qlen_n = (int)qlen_n;
   p.N = (int)N; p.H = (int)H; p.Tq = (int)Tq; p.Tkv = (int)Tkv;
   p.nqb = 0;
   p.q_sn = q_sn; p.q_sh = q_sh; p.q_st = q_st;

@@ -5,24 +5,28 @@
 #include <stdint.h>
 
 // Flash attention over [N, H, T, D] views (icl_fwd.hip): D = 64 is the cached-KV ICL attention,
-// D = 128 the folded ISAB-1 attention (one head, K = V = the raw rows).
+// D = 128 the folded ISAB-1 attention (one head, K = V = the raw rows). qlen (device int32,
+// qlen_n in {1, N}): query rows computed per n; rows at or past it are not written (null: all).
 int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
                           int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
                           int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
-                          void* ws, int64_t ws_bytes, hipStream_t stream);
+                          void* ws, int64_t ws_bytes, hipStream_t stream,
+                          const int32_t* qlen = nullptr, int64_t qlen_n = 0);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
 // Small-head (8 x 16) attention (smallhead_fwd.hip): picks the resident, streaming or general
-// kernel for the shape. ws may be null (no key split).
+// kernel for the shape. ws may be null (no key split). qlen (device int32, qlen_n in {1, B}): query
+// rows needed per batch element; the resident kernel neither computes nor writes the rows at or past
+// it, the others compute every row (null: all Lq rows).
 int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
                             int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
                             const float* bias, int64_t bias_sb, const int32_t* valid,
                             int64_t valid_n, const float* cq, const float* sq, const float* ck,
                             const float* sk, int rope, int half, int rot, float scale, int64_t B,
                             int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
-                            hipStream_t stream);
+                            hipStream_t stream, const int32_t* qlen = nullptr, int64_t qlen_n = 0);
 int64_t tabicl_launch_smallhead_ws_bytes(int64_t B, int64_t Lq, int64_t Lk, int dtype, bool bias,
                                          int rope);
 

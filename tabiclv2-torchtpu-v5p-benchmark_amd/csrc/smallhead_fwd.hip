@@ -57,6 +57,10 @@ struct ShParams {
   int exact_scale;  // fold scale and log2e into the K operand: scale is a power of two (bf16(q * scale)
                     // needs no rounding) and the runs are long enough to amortise the K split
   int half_last;    // the last 32-key group's upper 16 keys are all past Lk (resident kernel, 4 groups)
+  // query rows needed per batch element (qlen[b], or qlen[0] for all; null: all Lq rows): the
+  // resident kernel neither computes nor writes the rows at or past it
+  const int32_t* qlen;
+  int qlen_n;
 };
 
 template <typename T, int KT> struct ShLds {
@@ -544,6 +548,17 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
     lk = vl < 0 ? 0 : (vl < lk ? vl : lk);
   }
   const int tid = threadIdx.x;
+  const int lane = tid & 63, g = tid >> 6;
+  const int l16 = lane & 15, G = lane >> 4;
+
+  // live query rows: the rows at or past `live` are neither computed nor written
+  int live = p.Lq;
+  if (p.qlen) {
+    const int r = p.qlen[p.qlen_n == 1 ? 0 : b];
+    live = r < 0 ? 0 : (r < live ? r : live);
+  }
+  const int orow = qb0 * 16;
+  if (live <= orow) return;  // uniform over the workgroup: before the fill and its barrier
 
   // fill: K rows with RoPE (fp32 math, cast), V rows as they are, b2 per key; keys past lk (up to
   // NG 32-key groups) get zero K/V (the buffer loads' range check) and b2 = -inf. Thread units: whole
@@ -632,8 +647,6 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
 
   // wave g owns head g: its K operands (the 16 dims twice, for the high and remainder halves of q)
   // and V^T operands stay in registers for the whole query range
-  const int lane = tid & 63, g = tid >> 6;
-  const int l16 = lane & 15, G = lane >> 4;
   const int kcol = g * SH_D + 8 * (G & 1);
   // transposed-read lane roles: lane 4j + c of group G points at key 4G + j, dims 4c..4c+3
   const int tr_key = 4 * G + (l16 >> 2), tr_col = 4 * (l16 & 3);
@@ -655,12 +668,14 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   }
 
   const bf16* qbase = (const bf16*)p.q + b * p.q_sb;
-  const int nb = p.nqb - qb0 < p.qbpw ? p.nqb - qb0 : p.qbpw;  // 16-query blocks of this workgroup
-  // output rows orow .. orow + nrow - 1 as a buffer resource (byte offsets, range checked)
-  const int orow = qb0 * 16;
-  const int nrow = nb * 16 < p.Lq - orow ? nb * 16 : p.Lq - orow;
+  // 16-query blocks of this workgroup that hold a live row
+  const int nb = (live - orow + 15) / 16 < p.qbpw ? (live - orow + 15) / 16 : p.qbpw;
+  // live output rows orow .. orow + nrow - 1 as a buffer resource (byte offsets, range checked: the
+  // stores of rows past them are dropped by the hardware)
+  const int nrow = nb * 16 < live - orow ? nb * 16 : live - orow;
   const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
       (bf16*)p.o + b * p.o_sb + (int64_t)orow * p.o_sr, 0, nrow * p.o_sr * 2, TA_BUF_WORD3);
+  const int ooff = (l16 * p.o_sr + g * SH_D + 4 * G) * 2, ostep = 16 * p.o_sr * 2;
   const int d4 = kcol + 4 * (G >> 1);  // this lane's 4 dims of q
   // q rows orow .. orow + nrow - 1 likewise; two q buffers, each loaded two blocks ahead of its use
   const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -674,7 +689,6 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   // store): each wait for q then leaves the younger stores and q loads in flight. The two zero
   // stores go to blocks 0 and 1, which their units rewrite later, in order, from this wave (block 1
   // lies outside the resource when the run has one block, and that store is dropped).
-  const int ooff = (l16 * p.o_sr + g * SH_D + 4 * G) * 2, ostep = 16 * p.o_sr * 2;
   // RoPE: cos / sin of the lane's 4 dims at its query's position (tables [Lq][E] fp32; rows past Lq
   // read as zero), one buffer refilled inside each block for the next one
   __amdgpu_buffer_rsrc_t crsrc, srsrc;
@@ -965,7 +979,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
                             int64_t valid_n, const float* cq, const float* sq, const float* ck,
                             const float* sk, int rope, int half, int rot, float scale, int64_t B,
                             int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
-                            hipStream_t stream) {
+                            hipStream_t stream, const int32_t* qlen, int64_t qlen_n) {
   if (dtype == 0 && Lk > RS_LK && bias == nullptr && rope == 0)
     return tabicl_launch_ss(q, q_sb, q_sr, k, k_sb, k_sr, v, v_sb, v_sr, o, valid, valid_n, scale, B,
                             Lq, Lk, ws, ws_bytes, stream);
@@ -984,6 +998,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     p.exact_scale = scale > 0.f && frexpf(scale, &e) == 0.5f;
   }
   p.half_last = 0;
+  p.qlen = qlen; p.qlen_n = (int)qlen_n;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   const bool fast_rope = rope == 0 || (rope == 1 && rot == 16) || (rope == 2 && half == 8 && rot == 16);
   // the resident kernel's buffer loads take 32-bit byte offsets within a batch element (query runs

@@ -249,6 +249,37 @@ def _(q, kv, bias, cq, sq, ck, sk, h, lkp, bq, rope, half, rot, prec, scale):  #
     return q.new_empty(kv.shape[0], q.shape[1], q.shape[2])
 
 
+def _q_len_arg(q_len: Tensor, B: int) -> Tensor:
+    if q_len.dtype != torch.int32 or not q_len.is_contiguous() or q_len.numel() not in (1, B):
+        raise ValueError(f"q_len must be a contiguous int32 tensor of 1 or {B} entries")
+    return q_len
+
+
+@torch.library.custom_op("tabicl_pk::pk_cross_fwd_ragged", mutates_args=())
+def _pk_cross_fwd_ragged(q: Tensor, kv: Tensor, bias: Tensor, cq: Tensor, sq: Tensor, ck: Tensor, sk: Tensor,
+                         q_len: Tensor, h: int, lkp: int, bq: int, rope: int, half: int, rot: int, prec: int,
+                         scale: float) -> Tensor:
+    """pk_cross_fwd over a ragged batch (inference only): rows below q_len[b] equal pk_cross_fwd's;
+    the rows at or past it are padding whose contents are unspecified (the column ISAB-2 kernel skips
+    them). No counterpart in the reference, whose bucketed runner computes its padding rows."""
+    _nat.require_device(q, kv, bias, cq, sq, ck, sk, q_len)
+    _contig(q, kv, bias, cq, sq, ck, sk)
+    Bq, Lq, E = q.shape
+    B, Lk, _ = kv.shape
+    _q_len_arg(q_len, B)
+    out = torch.empty(B, Lq, E, device=q.device, dtype=q.dtype)
+    _nat.call("tabicl_pk_cross_fwd_ragged", q.data_ptr(), Bq, kv.data_ptr(), _bias_ptr(bias), _bias_rows(bias),
+              cq.data_ptr(), sq.data_ptr(), ck.data_ptr(), sk.data_ptr(), out.data_ptr(), B, Lq, Lk, E, h,
+              rope, half, rot, float(scale), _nat.dtype_code(q.dtype), q_len.data_ptr(), q_len.numel(),
+              _nat.stream_of(q))
+    return out
+
+
+@_pk_cross_fwd_ragged.register_fake
+def _(q, kv, bias, cq, sq, ck, sk, q_len, h, lkp, bq, rope, half, rot, prec, scale):  # noqa: ANN001
+    return q.new_empty(kv.shape[0], q.shape[1], q.shape[2])
+
+
 @torch.library.custom_op("tabicl_pk::hxf_fwd", mutates_args=())
 def _hxf_fwd(valid: Tensor, q: Tensor, x: Tensor, bk: int, prec: int) -> Tensor:
     _nat.require_device(valid, q, x)
@@ -410,6 +441,7 @@ HX_FWD = torch.ops.tabicl_pk.hx_fwd
 HXQ_FWD = torch.ops.tabicl_pk.hxq_fwd
 PK_SELF = torch.ops.tabicl_pk.pk_self_fwd
 PK_CROSS = torch.ops.tabicl_pk.pk_cross_fwd
+PK_CROSS_RAGGED = torch.ops.tabicl_pk.pk_cross_fwd_ragged
 HXF_FWD = torch.ops.tabicl_pk.hxf_fwd
 HX_BWD = torch.ops.tabicl_pk.hx_bwd
 PK_SELF_BWD = torch.ops.tabicl_pk.pk_self_bwd
@@ -467,10 +499,13 @@ def pk_self_attention(qkv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,
 
 
 def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,  # noqa: ANN001
-                       scale: float) -> Tensor:
+                       scale: float, q_len: Optional[Tensor] = None) -> Tensor:
     """q [..., Lq, E], kv [..., Lk, 2E] (packed K | V projection); RoPE (optional) with positions
     0..L-1 each (reference :735-752). A q that is one query set broadcast over kv's batch (a single
-    leading element, or an expanded view with batch stride 0) is read once by the kernel, not copied."""
+    leading element, or an expanded view with batch stride 0) is read once by the kernel, not copied.
+    q_len (extension, inference only): int32 tensor with 1 or one entry per flattened batch element
+    giving the rows each one needs (a ragged batch padded to a row bucket); the contents of the rows
+    at or past it are unspecified."""
     lead = q.shape[:-2]
     Lq, E = q.shape[-2], q.shape[-1]
     Lk = kv.shape[-2]
@@ -486,8 +521,14 @@ def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor]
     elif q3.shape[0] != kv3.shape[0]:
         q3 = q3.expand(kv3.shape[0], Lq, E)
     out_lead = lead if q.shape[:-2].numel() == kv3.shape[0] else kv.shape[:-2]
-    out = PK_CROSS(q3.contiguous(), kv3.contiguous(), _bias_arg(key_bias, out_lead, Lk, q.device), cq, sq, ck, sk,
-                   h, lkp, bq, rc, half, rot, prec, float(scale))
+    bias = _bias_arg(key_bias, out_lead, Lk, q.device)
+    if q_len is not None:
+        ql = q_len.to(device=q.device, dtype=torch.int32).reshape(-1).contiguous()
+        out = PK_CROSS_RAGGED(q3.contiguous(), kv3.contiguous(), bias, cq, sq, ck, sk, ql, h, lkp, bq, rc, half, rot,
+                              prec, float(scale))
+    else:
+        out = PK_CROSS(q3.contiguous(), kv3.contiguous(), bias, cq, sq, ck, sk, h, lkp, bq, rc, half, rot, prec,
+                       float(scale))
     return out.reshape(*out_lead, Lq, E)
 
 

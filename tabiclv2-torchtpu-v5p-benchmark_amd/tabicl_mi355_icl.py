@@ -51,8 +51,9 @@ def _workspace(N: int, H: int, Tq: int, Tkv: int, D: int, code: int, device) -> 
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
 
 
-def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float, out: Tensor) -> None:
-    _nat.require_device(q, k, v, valid, out)
+def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float, out: Tensor,
+            q_len: Optional[Tensor] = None) -> None:
+    _nat.require_device(q, k, v, valid, out, q_len)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("icl_cached_attn expects [N, H, T, D] tensors")
     N, H, Tq, D = q.shape
@@ -70,9 +71,16 @@ def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: flo
         vptr, vn = valid.data_ptr(), valid.numel()
     code = _nat.dtype_code(q.dtype)
     ws = _workspace(N, H, Tq, Tkv, D, code, q.device)
-    _nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
-              N, H, Tq, Tkv, D, *_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out), float(scale),
-              code, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _nat.stream_of(q))
+    tail = (*_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out), float(scale), code,
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _nat.stream_of(q))
+    if q_len is None:
+        _nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
+                  N, H, Tq, Tkv, D, *tail)
+        return
+    if q_len.dtype != torch.int32 or not q_len.is_contiguous() or q_len.numel() not in (1, N):
+        raise ValueError(f"q_len must be a contiguous int32 tensor of 1 or {N} entries")
+    _nat.call("tabicl_icl_fwd_ragged", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, q_len.data_ptr(),
+              q_len.numel(), out.data_ptr(), N, H, Tq, Tkv, D, *tail)
 
 
 @torch.library.custom_op("tabicl::icl_cached_attn", mutates_args=())
@@ -100,8 +108,23 @@ def _(q, k, v, valid, scale, out):  # noqa: ANN001
     return None
 
 
+@torch.library.custom_op("tabicl::icl_cached_attn_ragged_out", mutates_args=("out",))
+def _icl_cached_attn_ragged_out(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], q_len: Tensor,
+                                scale: float, out: Tensor) -> None:
+    """icl_cached_attn_out over a ragged batch: rows at or past q_len[n] (1 or N entries) are neither
+    computed nor written (out keeps what it held). No counterpart in the reference, whose bucketed
+    runner attends with the padding rows of each table's test bucket too."""
+    _launch(q, k, v, valid, scale, out, q_len)
+
+
+@_icl_cached_attn_ragged_out.register_fake
+def _(q, k, v, valid, q_len, scale, out):  # noqa: ANN001
+    return None
+
+
 ICL_FWD = torch.ops.tabicl.icl_cached_attn
 ICL_FWD_OUT = torch.ops.tabicl.icl_cached_attn_out
+ICL_FWD_RAGGED_OUT = torch.ops.tabicl.icl_cached_attn_ragged_out
 
 
 def icl_supported(Tq: int, Tkv: int, D: int, dtype: torch.dtype) -> bool:

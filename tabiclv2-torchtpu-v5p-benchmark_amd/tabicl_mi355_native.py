@@ -31,6 +31,8 @@ SIGNATURES = {
                            _f32, _i32, _c_p],
     "tabicl_pk_cross_fwd": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
                             _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_p],
+    "tabicl_pk_cross_fwd_ragged": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
+                                   _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_p, _i64, _c_p],
     "tabicl_hxf_fwd": [_c_p, _i64, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _c_p, _i64, _c_p],
     "tabicl_hxf_workspace_bytes": [_i64, _i64, _i64, _i64, _i32],
     "tabicl_smallhead_bwd_workspace_bytes": [_i64, _i64, _i64, _i32],
@@ -42,6 +44,8 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_fwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i64] + [_i64] * 12
                       + [_f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_fwd_ragged": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i64]
+                             + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i32],
     "tabicl_icl_cache_append": [_c_p, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _i32, _c_p],

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     import tabicl_mi355_native as nat
     lib = nat.load()
     names = _declared()
-    assert len(names) == 17, names
+    assert len(names) == 19, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in nat.SIGNATURES, name
@@ -56,6 +56,14 @@ def test_bad_arguments_rejected_before_launch():
     assert st == 1 and "rope" in nat.last_error()
     st = lib.tabicl_icl_cache_append(None, None, 64, 64, 10, 12, None, None, 64, 64, 64, 1, 1, 5, 64, 0, None)
     assert st == 1 and "capacity" in nat.last_error()
+    # ragged entry points: a q_len array of neither 1 nor N (B) entries is refused before any launch
+    qlen = ctypes.c_int32(3)
+    st = lib.tabicl_icl_fwd_ragged(None, None, None, None, 0, ctypes.byref(qlen), 2, None, 3, 1, 1, 1, 64,
+                                   *([64] * 12), 1.0, 0, None, 0, None)
+    assert st == 1 and "q_len" in nat.last_error()
+    st = lib.tabicl_pk_cross_fwd_ragged(None, 1, None, None, 1, None, None, None, None, None, 4, 8, 8, 128, 8, 0, 0,
+                                        0, 0.25, 0, ctypes.byref(qlen), 2, None)
+    assert st == 1 and "q_len" in nat.last_error()
     with pytest.raises(nat.UnsupportedShapeError):
         nat.check(1, "x")
 

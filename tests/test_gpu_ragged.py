@@ -1,0 +1,104 @@
+"""GPU tests of the ragged-batch entry points (tabicl_icl_fwd_ragged, tabicl_pk_cross_fwd_ragged).
+
+A ragged call takes per-batch query-row counts q_len. Bar (written here): rows below q_len[b] are
+bit-identical to the plain call on the same inputs (same kernels, same key splits), and the plain
+call itself is checked against the fp64 oracle on a subset of rows (2e-2 bf16, 1e-4 fp32), so the
+ragged rows are pinned to the oracle through it. The ICL kernels never write the rows at or past
+q_len (checked with a NaN sentinel); for pk_cross their contents are unspecified (the resident
+kernel skips them, the others compute them). Cases: whole work items past q_len, a work item cut
+inside, q_len = 0, q_len >= Lq, one q_len for the whole batch, key splits, the fp32 kernel, and for
+pk_cross the resident kernel (short runs, long runs, the exact-scale long runs of the column ISAB-2)
+plus the streaming and fp32 kernels.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
+
+
+def _check_rows(out, ref, q_len, row_dim, untouched=False):
+    """out/ref: device tensors with the query-row axis at row_dim and the batch axis 0. untouched:
+    the rows past q_len must still hold the NaN the output was filled with."""
+    B = out.shape[0]
+    for b in range(B):
+        n = max(0, min(int(q_len[b if len(q_len) > 1 else 0]), out.shape[row_dim]))
+        live = out[b].narrow(row_dim - 1, 0, n)
+        assert torch.equal(live, ref[b].narrow(row_dim - 1, 0, n)), f"batch {b}: live rows differ"
+        if untouched:
+            dead = out[b].narrow(row_dim - 1, n, out.shape[row_dim] - n)
+            assert bool(torch.isnan(dead).all()), f"batch {b}: rows past q_len were written"
+
+
+@pytest.mark.parametrize("name,N,H,Tq,Tkv,valid,q_len,dtype", [
+    # key splits (few work items): item 0 cut at 37 rows, items past q_len skipped, q_len = 0
+    ("split_bf16", 3, 8, 520, 3000, [3000, 1500, 700], [37, 0, 300], torch.bfloat16),
+    # one split (Tkv too short to split): q_len past Tq, exactly a work-item edge, one row
+    ("nosplit_bf16", 4, 8, 700, 900, None, [700, 999, 256, 1], torch.bfloat16),
+    ("shared_qlen_bf16", 2, 4, 600, 2000, [2000], [300], torch.bfloat16),
+    ("split_fp32", 3, 2, 300, 2500, [2500, 100, 1], [129, 300, 64], torch.float32),
+])
+def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
+    import tabicl_mi355_icl as icl
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(N, H, Tq, 64, generator=g).to(dtype)
+    k = torch.randn(N, H, Tkv, 64, generator=g).to(dtype)
+    v = torch.randn(N, H, Tkv, 64, generator=g).to(dtype)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    vt = None if valid is None else torch.tensor(valid, dtype=torch.int32, device=dev)
+    ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+    ref = torch.empty_like(qd)
+    icl.ICL_FWD_OUT(qd, kd, vd, vt, 64 ** -0.5, ref)
+    out = torch.full_like(qd, float("nan"))
+    icl.ICL_FWD_RAGGED_OUT(qd, kd, vd, vt, ql, 64 ** -0.5, out)
+    torch.cuda.synchronize()
+    _check_rows(out, ref, q_len, 2, untouched=True)
+    # the plain call on the live rows of batch 0, head 0 against the oracle
+    n0 = min(q_len[0], Tq)
+    if n0 > 0:
+        vl = Tkv if valid is None else valid[0]
+        exp = O.splash_sdpa_ref(q[:1, :1], k[:1, :1], v[:1, :1], [vl])
+        err = float(np.abs(out[0, 0, :n0].double().cpu().numpy() - exp[0, 0, :n0]).max())
+        assert err <= TOL[dtype], f"{name}: max abs err {err}"
+
+
+def _pk_cross_case(dev, B, Lq, Lk, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, Lq, 128, generator=g) * 0.5).to(dtype).to(dev)
+    kv = torch.randn(B, Lk, 256, generator=g).to(dtype).to(dev)
+    return q, kv
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk,dtype,q_len", [
+    # resident kernel, one 16-row block per workgroup: cut blocks, empty rows, full rows
+    ("resident_short", 6, 300, 128, torch.bfloat16, [0, 1, 15, 16, 17, 300]),
+    ("resident_shared", 3, 104, 104, torch.bfloat16, [50]),
+    # resident kernel with runs of 2 blocks (40 x 250 blocks > 8192 workgroups)
+    ("resident_runs", 40, 4000, 128, torch.bfloat16, "random"),
+    # runs of 9 blocks: the exact-scale form (column ISAB-2 at C5's buckets)
+    ("resident_exact", 70, 16000, 128, torch.bfloat16, "random"),
+    # the other kernels compute every row
+    ("stream_bf16", 4, 200, 300, torch.bfloat16, [0, 77, 200, 5000]),
+    ("fp32", 4, 200, 128, torch.float32, [3, 0, 199, 64]),
+])
+def test_pk_cross_ragged(dev, name, B, Lq, Lk, dtype, q_len):
+    import tabicl_mi355_attn as pk
+    q, kv = _pk_cross_case(dev, B, Lq, Lk, dtype, 12)
+    if q_len == "random":
+        rng = np.random.default_rng(5)
+        q_len = [int(x) for x in rng.integers(0, Lq + 1, B)]
+        q_len[0], q_len[1] = Lq, 16 * (Lq // 32)
+    ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+    ref = pk.pk_cross_attention(q, kv, 8, None, None, 0.25)
+    out = pk.pk_cross_attention(q, kv, 8, None, None, 0.25, q_len=ql)
+    torch.cuda.synchronize()
+    _check_rows(out, ref, q_len, 1)
+    # the plain call against the oracle on a few live rows of batch 0
+    n0 = min(q_len[0], Lq, 64)
+    if n0 > 0:
+        exp = O.pk_cross_ref(q[:1, :n0], kv[:1], 8, None, None, None, 0.25)
+        err = float(np.abs(out[:1, :n0].double().cpu().numpy() - exp).max())
+        assert err <= TOL[dtype], f"{name}: max abs err {err}"
