@@ -16,6 +16,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // word 3 of a raw (stride 0) buffer resource on gfx9-family parts: 32-bit data format, no swizzle;
 // accesses at byte offsets >= num_records are dropped (stores) or return 0 (loads)
 #define TA_BUF_WORD3 0x00020000
+// flag on a RoPE form: the cos / sin tables hold one head's 16 columns ([L, 16]) shared by every head
+#define TA_ROPE_SHARED 0x10
 
 // Operand vectors: N consecutive k-values of one row held by one lane.
 template <typename T, int N> struct OpVec;
@@ -125,10 +127,10 @@ __device__ __forceinline__ void rope_partner(int jd, int rope, int half, int rot
 // Four consecutive dims d0..d0+3 (d0 % 4 == 0) of one row after RoPE, in fp32.
 template <typename T>
 __device__ __forceinline__ f32x4 rope4(const T* row, const float* cs, const float* sn, int d0,
-                                       int rope, int half, int rot) {
+                                       int rope, int half, int rot, int tcol) {
   const int hb = d0 & ~15;
-  const float4 c = *(const float4*)(cs + d0);
-  const float4 s = *(const float4*)(sn + d0);
+  const float4 c = *(const float4*)(cs + tcol);  // table columns of dims d0..d0+3
+  const float4 s = *(const float4*)(sn + tcol);
   const float cv[4] = {c.x, c.y, c.z, c.w};
   const float sv[4] = {s.x, s.y, s.z, s.w};
   f32x4 y;
@@ -177,7 +179,7 @@ __device__ __forceinline__ f32x4 rope4_fast(const T* row, const float* cs, const
     }
     return y;
   }
-  return rope4<T>(row, cs, sn, d0, rope, half, rot);
+  return rope4<T>(row, cs, sn, d0, rope, half, rot, d0);
 }
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *(const uint4*)p; }

@@ -90,7 +90,7 @@ __device__ __forceinline__ typename OpVec<T, 4>::type sb_prep4(const T* row, con
   typedef typename OpVec<T, 4>::type Op4;
   Op4 r;
   if (p.rope) {
-    const f32x4 y = rope4<T>(row, cs, sn, d0, p.rope, p.half, p.rot);
+    const f32x4 y = rope4<T>(row, cs, sn, d0, p.rope, p.half, p.rot, d0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = from_f32<T>(y[j] * scale);
   } else {

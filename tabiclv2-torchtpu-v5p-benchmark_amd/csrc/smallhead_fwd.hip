@@ -57,6 +57,9 @@ struct ShParams {
   int exact_scale;  // fold scale and log2e into the K operand: scale is a power of two (bf16(q * scale)
                     // needs no rounding) and the runs are long enough to amortise the K split
   int half_last;    // the last 32-key group's upper 16 keys are all past Lk (resident kernel, 4 groups)
+  // RoPE tables: element (position, dim d) at position * tab_sr + (d & tab_cm); [L, E] tables give
+  // (E, E - 1), tables of one head's columns shared by every head give (16, 15)
+  int tab_sr, tab_cm;
   // query rows needed per batch element (qlen[b], or qlen[0] for all; null: all Lq rows): the
   // resident kernel neither computes nor writes the rows at or past it
   const int32_t* qlen;
@@ -87,8 +90,8 @@ __device__ __forceinline__ void sh_fill(const ShParams& p, T* lds_k, T* lds_vt, 
     if (key < lk) {
       const T* src = kbase + (int64_t)key * p.k_sr;
       if (p.rope) {
-        const f32x4 y = rope4<T>(src, p.ck + (int64_t)key * SH_E, p.sk + (int64_t)key * SH_E, d0,
-                                 p.rope, p.half, p.rot);
+        const f32x4 y = rope4<T>(src, p.ck + (int64_t)key * p.tab_sr, p.sk + (int64_t)key * p.tab_sr, d0,
+                                 p.rope, p.half, p.rot, d0 & p.tab_cm);
 #pragma unroll
         for (int r = 0; r < 4; ++r) val[r] = from_f32<T>(y[r]);
       } else {
@@ -192,8 +195,8 @@ __global__ __launch_bounds__(SH_NW * 64) void smallhead_fwd_kernel(ShParams p) {
       if (p.rope) {
 #pragma unroll
         for (int g = 0; g < SH_H; ++g) {
-          const f32x4 y = rope4<T>(qrow, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E,
-                                   g * SH_D + 4 * kap, p.rope, p.half, p.rot);
+          const f32x4 y = rope4<T>(qrow, p.cq + (int64_t)qi * p.tab_sr, p.sq + (int64_t)qi * p.tab_sr,
+                                   g * SH_D + 4 * kap, p.rope, p.half, p.rot, (g * SH_D + 4 * kap) & p.tab_cm);
 #pragma unroll
           for (int r = 0; r < 4; ++r) qop[g][r] = from_f32<T>(y[r] * p.scale);
         }
@@ -574,8 +577,8 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
         (bf16*)p.v + b * p.v_sb, 0, lk * (int)p.v_sr * 2, TA_BUF_WORD3);
     __amdgpu_buffer_rsrc_t crs, srs;
     if constexpr (ROPE) {
-      crs = __builtin_amdgcn_make_buffer_rsrc((float*)p.ck, 0, lk * SH_E * 4, TA_BUF_WORD3);
-      srs = __builtin_amdgcn_make_buffer_rsrc((float*)p.sk, 0, lk * SH_E * 4, TA_BUF_WORD3);
+      crs = __builtin_amdgcn_make_buffer_rsrc((float*)p.ck, 0, lk * p.tab_sr * 4, TA_BUF_WORD3);
+      srs = __builtin_amdgcn_make_buffer_rsrc((float*)p.sk, 0, lk * p.tab_sr * 4, TA_BUF_WORD3);
     }
     typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
     u32x4v kx[KU][2], vx[VU];
@@ -587,7 +590,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) kx[j][h2] = __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16 * h2, 0, 0);
       if constexpr (ROPE) {
-        const int toff = (key * SH_E + hh * SH_D) * 4;
+        const int toff = (key * p.tab_sr + ((hh * SH_D) & p.tab_cm)) * 4;
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
           kc[j][c4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(crs, toff + 16 * c4, 0, 0));
@@ -692,11 +695,13 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   // RoPE: cos / sin of the lane's 4 dims at its query's position (tables [Lq][E] fp32; rows past Lq
   // read as zero), one buffer refilled inside each block for the next one
   __amdgpu_buffer_rsrc_t crsrc, srsrc;
-  const int coff = (l16 * SH_E + d4) * 4, cstep = 16 * SH_E * 4;
+  const int coff = (l16 * p.tab_sr + (d4 & p.tab_cm)) * 4, cstep = 16 * p.tab_sr * 4;
   f32x4 cs = {0.f, 0.f, 0.f, 0.f}, sn = cs;
   if constexpr (ROPE) {
-    crsrc = __builtin_amdgcn_make_buffer_rsrc((float*)p.cq + (int64_t)orow * SH_E, 0, nrow * SH_E * 4, TA_BUF_WORD3);
-    srsrc = __builtin_amdgcn_make_buffer_rsrc((float*)p.sq + (int64_t)orow * SH_E, 0, nrow * SH_E * 4, TA_BUF_WORD3);
+    crsrc = __builtin_amdgcn_make_buffer_rsrc((float*)p.cq + (int64_t)orow * p.tab_sr, 0, nrow * p.tab_sr * 4,
+                                              TA_BUF_WORD3);
+    srsrc = __builtin_amdgcn_make_buffer_rsrc((float*)p.sq + (int64_t)orow * p.tab_sr, 0, nrow * p.tab_sr * 4,
+                                              TA_BUF_WORD3);
     cs = rs_tab(crsrc, coff);
     sn = rs_tab(srsrc, coff);
   }
@@ -840,8 +845,8 @@ __device__ __forceinline__ void sf_tile(const float* lkt, const float* lvt, cons
 __device__ __forceinline__ f32x4 sf_qop(const ShParams& p, int b, int qi, int d0) {
   if (qi >= p.Lq) return f32x4{0.f, 0.f, 0.f, 0.f};
   const float* row = (const float*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr;
-  f32x4 y = p.rope ? rope4<float>(row, p.cq + (int64_t)qi * SH_E, p.sq + (int64_t)qi * SH_E, d0, p.rope, p.half,
-                                  p.rot)
+  f32x4 y = p.rope ? rope4<float>(row, p.cq + (int64_t)qi * p.tab_sr, p.sq + (int64_t)qi * p.tab_sr, d0, p.rope,
+                                  p.half, p.rot, d0 & p.tab_cm)
                    : *(const f32x4*)(row + d0);
 #pragma unroll
   for (int r = 0; r < 4; ++r) y[r] *= p.scale;
@@ -869,8 +874,8 @@ __device__ __forceinline__ void sf_fill(const ShParams& p, float* lkt, float* lv
     const int u = tid + 512 * i, key = u >> 4, c = u & 15, d = hg * SF_W + 4 * c;
     const int gk = k0 + key, gc = gk < lk ? gk : lk - 1;
     const float* krow = kbase + (int64_t)gc * p.k_sr;
-    f32x4 kv = p.rope ? rope4<float>(krow, p.ck + (int64_t)gc * SH_E, p.sk + (int64_t)gc * SH_E, d, p.rope, p.half,
-                                     p.rot)
+    f32x4 kv = p.rope ? rope4<float>(krow, p.ck + (int64_t)gc * p.tab_sr, p.sk + (int64_t)gc * p.tab_sr, d, p.rope,
+                                     p.half, p.rot, d & p.tab_cm)
                       : *(const f32x4*)(krow + d);
     f32x4 vv = *(const f32x4*)(vbase + (int64_t)gc * p.v_sr + d);
     if (gk >= lk) kv = vv = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -991,6 +996,11 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   p.bias = bias; p.bias_sb = bias_sb;
   p.valid = valid; p.valid_n = (int)valid_n;
   p.cq = cq; p.sq = sq; p.ck = ck; p.sk = sk;
+  // rope: the form (none / pairs / halves) plus TA_ROPE_SHARED when the tables hold one head's 16
+  // columns for every head
+  p.tab_sr = (rope & TA_ROPE_SHARED) ? SH_D : SH_E;
+  p.tab_cm = p.tab_sr - 1;
+  rope &= ~TA_ROPE_SHARED;
   p.rope = rope; p.half = half; p.rot = rot;
   p.scale = scale;
   {

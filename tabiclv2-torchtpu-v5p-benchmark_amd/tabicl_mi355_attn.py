@@ -492,10 +492,26 @@ def pk_self_attention(qkv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,
     E = E3 // 3
     lkp = -(-L // 128) * 128
     cos, sin, rc, half, rot = rope_tables(rope_mod, L, E, h, qkv.device)
+    if rc and not _needs_grad(qkv, key_bias):
+        cos, sin, rc = _shared_tables(cos, sin, rc, E // h)
     prec = _fp32_prec_code() if qkv.dtype == torch.float32 else 0
     out = PK_SELF(qkv.reshape(-1, L, E3).contiguous(), _bias_arg(key_bias, lead, L, qkv.device), cos, sin, h, lkp, rc,
                   half, rot, prec, float(scale))
     return out.reshape(*lead, L, E)
+
+
+ROPE_SHARED_TABLES = 0x10  # TABICL_ROPE_SHARED_TABLES of include/tabicl_attn.h
+
+
+def _needs_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
+def _shared_tables(cos: Tensor, sin: Tensor, rc: int, d: int):
+    """Forward-only form of rope_tables' output: its columns repeat every head (d columns), so one
+    head's [L, d] slice serves all heads and the kernels read h times fewer table bytes. The backward
+    kernels take the [L, E] tables, so this is used only when no gradient is needed."""
+    return cos[:, :d].contiguous(), sin[:, :d].contiguous(), rc | ROPE_SHARED_TABLES
 
 
 def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,  # noqa: ANN001
@@ -513,6 +529,9 @@ def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor]
     bq = _pick_bq(Lq, lkp)
     cq, sq, rc, half, rot = rope_tables(rope_mod, Lq, E, h, q.device)
     ck, sk, _, _, _ = rope_tables(rope_mod, Lk, E, h, q.device)
+    if rc and (q_len is not None or not _needs_grad(q, kv, key_bias)):
+        cq, sq, _ = _shared_tables(cq, sq, rc, E // h)
+        ck, sk, rc = _shared_tables(ck, sk, rc, E // h)
     prec = _fp32_prec_code() if q.dtype == torch.float32 else 0
     q3 = q.reshape(-1, Lq, E)
     kv3 = kv.reshape(-1, Lk, 2 * E)

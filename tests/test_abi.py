@@ -56,6 +56,10 @@ def test_bad_arguments_rejected_before_launch():
     assert st == 1 and "rope" in nat.last_error()
     st = lib.tabicl_icl_cache_append(None, None, 64, 64, 10, 12, None, None, 64, 64, 64, 1, 1, 5, 64, 0, None)
     assert st == 1 and "capacity" in nat.last_error()
+    # shared-table RoPE flag: forward entry points only
+    a = 0x1000  # 16-byte aligned placeholder address: the rope code is refused before any use
+    st = lib.tabicl_pk_self_bwd(a, None, 1, a, a, a, a, a, 1, 8, 128, 8, 2 | 0x10, 8, 16, 0.25, 0, a, 1 << 20, None)
+    assert st == 1 and "rope code" in nat.last_error()
     # ragged entry points: a q_len array of neither 1 nor N (B) entries is refused before any launch
     qlen = ctypes.c_int32(3)
     st = lib.tabicl_icl_fwd_ragged(None, None, None, None, 0, ctypes.byref(qlen), 2, None, 3, 1, 1, 1, 64,
