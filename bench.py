@@ -11,7 +11,10 @@ Roofline: algorithmic FLOPs per launch = 4 * Tq * Tkv * d * heads * estimators (
 achieved = that / average launch duration (HIP events on the launch stream). Traffic comes from
 the committed rocprofv3 PMC summary when present. The CPU baseline times the fp32 CPU torch
 restatement of the reference attention (oracle.attention.splash_sdpa_torch) on one (estimator,
-block) slice of the same workload and scales it to a whole query.
+block) slice of the benchmark's own inputs, scales it to a whole query, and reports the GPU's max
+abs error on that slice. Before the headline line the default run prints the C3 line (the 50k-row
+column ISAB attention north_star also names, with its HBM roofline and CPU baseline); the headline
+is the last line.
 """
 from __future__ import annotations
 
@@ -45,39 +48,49 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(seed: int = 3) -> dict:
-    """fp32 CPU torch attention (oracle restatement of the reference path) on one (estimator,
-    block) slice: 8 heads x 5,000 queries over 45,000 keys, scaled x96 to a whole query."""
+def _threads() -> int:
+    import torch
+
+    threads = min(os.cpu_count() or 1, 64)
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _median_time(fn, budget_s: float = 8.0):
+    """(median seconds of fn() over 1-3 runs after one warm-up run, its result, runs)."""
+    t0 = time.perf_counter()
+    out = fn()
+    first = time.perf_counter() - t0
+    reps = 1 if first > budget_s else 3
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), out, reps
+
+
+def cpu_baseline(q, k, v, gpu_out) -> dict:
+    """fp32 CPU torch attention (oracle restatement of the reference path, oracle.attention.splash_sdpa_torch)
+    on one (estimator, block) slice of the benchmark's own inputs -- 8 heads x 5,000 queries over 45,000
+    keys -- timed on the host cores and scaled x96 to a whole query; the GPU's output on the same slice is
+    compared with it (max abs error)."""
     import torch
 
     from oracle.attention import splash_sdpa_torch
 
-    threads = min(os.cpu_count() or 1, 64)
-    torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(seed)
-    q = torch.randn(1, HEADS, TEST, D, generator=g)
-    k = torch.randn(1, HEADS, TRAIN, D, generator=g)
-    v = torch.randn(1, HEADS, TRAIN, D, generator=g)
+    threads = _threads()
+    qc, kc, vc = (t.detach().float().cpu() for t in (q, k, v))
 
     def run():
-        for h in range(HEADS):
-            for r0 in range(0, TEST, 1000):
-                splash_sdpa_torch(q[:, h:h + 1, r0:r0 + 1000], k[:, h:h + 1], v[:, h:h + 1])
+        return torch.cat([splash_sdpa_torch(qc[:, :, r0:r0 + 1000], kc, vc) for r0 in range(0, TEST, 1000)], dim=2)
 
-    t0 = time.perf_counter()
-    run()  # warm-up (also sizes the sample)
-    first = time.perf_counter() - t0
-    reps = 1 if first > 8.0 else 3
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    per_slice = statistics.median(times)
-    return {"value": round(per_slice * EST * BLOCKS * 1000.0, 1), "unit": "ms", "cores": threads,
-            "kind": "port",
-            "sample": f"1 estimator x 1 block (8 heads x {TEST} q x {TRAIN} keys, fp32 torch on {_cpu_model()}), "
-                      f"median of {reps}, scaled x{EST * BLOCKS}"}
+    sec, ref, reps = _median_time(run)
+    err = float((gpu_out.detach().float().cpu() - ref).abs().max())
+    return {"value": round(sec * EST * BLOCKS * 1000.0, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"estimator 0, block 0 of the benchmark's inputs (8 heads x {TEST} q x {TRAIN} keys, fp32 torch "
+                      f"on {_cpu_model()}), median of {reps}, scaled x{EST * BLOCKS}",
+            "max_abs_err_gpu_vs_cpu": round(err, 6)}
 
 
 def _time(fn, steps: int, warmup: int) -> float:
@@ -152,22 +165,103 @@ def bench_smallhead(configs: set, steps: int, warmup: int) -> list:
         ms = _time(lambda: pk.pk_self_attention(qkv, H, None, rope, 0.25), steps, warmup)
         line("C2 row interaction (pk_self, RoPE)", ms, 4.0 * L * L * 16 * H * B, 2.0 * B * L * 4 * E, "bf16", "hbm",
              "16384 x 104 tokens, packed qkv, RoPE halves base 1e4, 8x16, bf16")
-    if configs & {"c3", "all"}:
-        g.manual_seed(2)
-        B, T, valid = 800, 50000, 45000
-        q = (torch.randn(B, 128, E, generator=g, device=dev) * 0.25).to(torch.bfloat16)
-        kv = torch.randn(B, T, 2 * E, generator=g, device=dev).to(torch.bfloat16)
-        vt = torch.tensor([valid], dtype=torch.int32, device=dev)
-        ms1 = _time(lambda: pk.hxq_attention(q, kv, vt, H), steps, warmup)
-        line("C3 column ISAB-1 (hxq, 128 q over 45k of 50k keys)", ms1, 4.0 * 128 * valid * 16 * H * B,
-             2.0 * B * (128 * E * 2 + valid * 2 * E), "bf16", "hbm", "800 x 128 q, packed kv 50000 rows, valid 45000")
-        del kv
-        q2 = torch.randn(B, T, E, generator=g, device=dev).to(torch.bfloat16)
-        kv2 = torch.randn(B, 128, 2 * E, generator=g, device=dev).to(torch.bfloat16)
-        ms2 = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25), steps, warmup)
-        line("C3 column ISAB-2 (pk_cross, 50k q over 128 keys)", ms2, 4.0 * T * 128 * 16 * H * B,
-             2.0 * B * (2 * T * E + 128 * 2 * E), "bf16", "hbm", "800 x 50000 q over 128 inducing keys")
     return recs
+
+
+C3_B, C3_T, C3_VALID, C3_IND = 800, 50000, 45000, 128
+
+
+def bench_c3(steps: int, warmup: int, cpu: bool) -> list:
+    """BASELINE config 3, the 50k-row column ISAB attention (bf16, 800 sequences = 8 estimators x 100
+    columns, 8 x 16 heads, scale 1/4): ISAB-1, 128 inducing queries over the packed K|V of 50,000 rows of
+    which the first 45,000 (train) are visible (hxq), then ISAB-2, 50,000 row queries over the 128 inducing
+    keys (pk_cross). Inputs N(0,1) from a device generator (seed 2), resident in HBM. Roofline: HBM
+    (algorithmic bytes: Q + visible K|V + O once, bf16). CPU baseline: the fp32 CPU torch restatement of
+    the reference attention (oracle.attention.ref_attn) on the first 8 of the 800 sequences of the same
+    inputs, scaled x100, with the GPU's max abs error on them."""
+    import torch
+
+    import tabicl_mi355_attn as pk
+
+    dev = torch.device("cuda", 0)
+    E, H = 128, 8
+    B, T, valid, NI = C3_B, C3_T, C3_VALID, C3_IND
+    g = torch.Generator(device=dev).manual_seed(2)
+    q1 = (torch.randn(B, NI, E, generator=g, device=dev) * 0.25).to(torch.bfloat16)
+    kv1 = torch.randn(B, T, 2 * E, generator=g, device=dev).to(torch.bfloat16)
+    vt = torch.tensor([valid], dtype=torch.int32, device=dev)
+    q2 = torch.randn(B, T, E, generator=g, device=dev).to(torch.bfloat16)
+    kv2 = torch.randn(B, NI, 2 * E, generator=g, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        ms1 = _time(lambda: pk.hxq_attention(q1, kv1, vt, H), steps, warmup)
+        ms2 = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25), steps, warmup)
+        o1 = pk.hxq_attention(q1[:8], kv1[:8], vt, H)
+        o2 = pk.pk_cross_attention(q2[:8], kv2[:8], H, None, None, 0.25)
+    legs = (
+        ("C3 column ISAB-1 (hxq, 128 q over 45k of 50k keys)", ms1, 4.0 * NI * valid * 16 * H * B,
+         2.0 * B * (NI * E * 2 + valid * 2 * E), "800 x 128 q, packed kv 50000 rows, valid 45000"),
+        ("C3 column ISAB-2 (pk_cross, 50k q over 128 keys)", ms2, 4.0 * T * NI * 16 * H * B,
+         2.0 * B * (2 * T * E + NI * 2 * E), "800 x 50000 q over 128 inducing keys"),
+    )
+    base = {}
+    if cpu:
+        from oracle.attention import ref_attn
+
+        threads = _threads()
+        a1, a2 = q1[:8].float().cpu(), kv1[:8, :valid].float().cpu()
+        b1, b2 = (q2[:8].float() * 0.25).cpu(), kv2[:8].float().cpu()
+        sec1, ref1, reps1 = _median_time(lambda: ref_attn(a1, a2[..., :E], a2[..., E:], H))
+        sec2, ref2, reps2 = _median_time(lambda: ref_attn(b1, b2[..., :E], b2[..., E:], H))
+        for key, sec, ref, out, reps in (("isab1", sec1, ref1, o1, reps1), ("isab2", sec2, ref2, o2, reps2)):
+            base[key] = {"value": round(sec * (B / 8) * 1000.0, 1), "unit": "ms", "cores": threads, "kind": "port",
+                         "sample": f"sequences 0-7 of the {B} of this benchmark's inputs (fp32 torch on "
+                                   f"{_cpu_model()}), median of {reps}, scaled x{B // 8}",
+                         "max_abs_err_gpu_vs_cpu": round(float((out.float().cpu() - ref).abs().max()), 6)}
+    recs = []
+    for (name, ms, flops, nbytes, workload), key in zip(legs, ("isab1", "isab2")):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        recs.append({"metric": f"ms per {name} pass", "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps,
+                     "warmup": warmup, "higher_is_better": False, "vs_baseline": None, "dtype": "bf16",
+                     "data": "synthetic N(0,1) (seed 2), resident in HBM", "config": {"workload": workload},
+                     "attn_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "pct_mfma_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _traffic(key),
+                                  "algorithmic_bytes": nbytes},
+                     "cpu_baseline": base.get(key)})
+    ms, flops, nbytes = ms1 + ms2, legs[0][2] + legs[1][2], legs[0][3] + legs[1][3]
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu_pass = None
+    if base:
+        cpu_pass = {"value": round(base["isab1"]["value"] + base["isab2"]["value"], 1), "unit": "ms",
+                    "cores": base["isab1"]["cores"], "kind": "port",
+                    "sample": "sum of the two legs' samples: " + base["isab1"]["sample"],
+                    "max_abs_err_gpu_vs_cpu": max(base["isab1"]["max_abs_err_gpu_vs_cpu"],
+                                                  base["isab2"]["max_abs_err_gpu_vs_cpu"])}
+    recs.append({"metric": "ms per C3 50k-row column ISAB attention pass (ISAB-1 + ISAB-2)", "value": round(ms, 4),
+                 "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
+                 "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) (seed 2), resident in HBM",
+                 "config": {"workload": "C3: 800 sequences (8 est x 100 columns), 128 inducing q over 45000 of 50000 "
+                                        "rows, then 50000 rows over 128 inducing keys, 8x16, bf16"},
+                 "isab1_ms": round(ms1, 4), "isab2_ms": round(ms2, 4),
+                 "attn_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                 "pct_mfma_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                              "traffic": None if _traffic("isab1") is None or _traffic("isab2") is None
+                              else _traffic("isab1") + _traffic("isab2")},
+                 "cpu_baseline": cpu_pass})
+    del q1, kv1, q2, kv2
+    torch.cuda.empty_cache()
+    return recs
+
+
+def _traffic(key: str):
+    """HBM bytes per launch of a C3 kernel from the committed rocprofv3 PMC summary, or None."""
+    try:
+        return json.loads((ROOT / "profiles" / "smallhead_c3_traffic.json").read_text())[key]["hbm_bytes_per_launch"]
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
 
 
 # The reference's training-block benchmark (scripts/tests/test_pallas_attn.py:80-109, 252-285):
@@ -345,6 +439,7 @@ def bench_c5(steps: int, warmup: int) -> list:
     g.manual_seed(4)
     # ms (ragged), real FLOPs, processed FLOPs, ms with every padded row computed
     parts = {"isab1": [0.0, 0.0, 0.0, 0.0], "isab2": [0.0, 0.0, 0.0, 0.0], "icl": [0.0, 0.0, 0.0, 0.0]}
+    c5_bytes = {"isab1": 0.0, "isab2": 0.0}
     groups = {}
     for i in range(64):
         groups.setdefault(("isab", c5_bucket(int(n_train[i] + n_test[i]))), []).append(i)
@@ -359,6 +454,7 @@ def bench_c5(steps: int, warmup: int) -> list:
             kv = torch.randn(B, L, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
             ms = _time(lambda: pk.hxq_attention(q, kv, valid, H), steps, warmup)
             real = sum(4.0 * IND * int(n) * 16 * H * EST_ * FEAT for n in nt)
+            c5_bytes["isab1"] += sum(2.0 * EST_ * FEAT * (2 * IND * E + int(n) * 2 * E) for n in nt)
             parts["isab1"][0] += ms
             parts["isab1"][1] += real
             parts["isab1"][2] += real  # keys past valid are never visited: no padded work
@@ -372,6 +468,7 @@ def bench_c5(steps: int, warmup: int) -> list:
             ms = _time(lambda: pk.pk_cross_attention(q2, kv2, H, None, None, 0.25, q_len=qlen), steps, warmup)
             parts["isab2"][0] += ms
             parts["isab2"][1] += sum(4.0 * int(r) * IND * 16 * H * EST_ * FEAT for r in rows)
+            c5_bytes["isab2"] += sum(2.0 * EST_ * FEAT * (2 * int(r) * E + IND * 2 * E) for r in rows)
             parts["isab2"][2] += sum(4.0 * (-(-int(r) // 16) * 16) * IND * 16 * H * EST_ * FEAT for r in rows)
             del q2, kv2
         else:
@@ -407,13 +504,18 @@ def bench_c5(steps: int, warmup: int) -> list:
         total += ms
         total_padded += ms_padded
         tf = real / (ms * 1e-3) / 1e12
+        if key == "icl":  # d = 64 over long keys: matrix-core bound
+            roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        else:  # d = 16 column attention: HBM bound (real rows' Q, visible K|V and O once, bf16)
+            gbs = c5_bytes[key] / (ms * 1e-3) / 1e9
+            roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": c5_bytes[key]}
         recs.append({"metric": f"ms per {names[key]} step", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
                      "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": "bf16",
                      "data": "synthetic N(0,1), seed 4", "config": {"workload": "C5: 64 tables, buckets 1k-16k"},
                      "attn_tflops_real": round(tf, 2), "padding_efficiency": round(real / padded, 4),
-                     "padded_ms": round(ms_padded, 4),
-                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
-                                  "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
+                     "padded_ms": round(ms_padded, 4), "roofline": roof})
     recs.append({"metric": "ms per C5 ragged mixed-batch step (ISAB pair + ICL)", "value": round(total, 4),
                  "padded_ms": round(total_padded, 4),
                  "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
@@ -484,7 +586,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-c3", action="store_true", help="default run: skip the C3 line printed before the headline")
     ap.add_argument("--config", default="c4",
                     help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer "
                          "(comma-separated) or all print the other BASELINE configs' lines, the fwd+bwd training "
@@ -503,6 +606,8 @@ def main() -> int:
     if configs != {"c4"}:
         torch.cuda.set_device(0)
         recs = bench_smallhead(configs, args.steps, args.warmup)
+        if configs & {"c3", "all"}:
+            recs += bench_c3(args.steps, args.warmup, not args.no_cpu)
         if configs & {"c5", "all"}:
             recs += bench_c5(args.steps, args.warmup)
         if configs & {"train", "all"}:
@@ -519,6 +624,9 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if not args.no_c3:
+        # the 50k-row ISAB line north_star names next to the headline; the headline stays the last line
+        print(json.dumps(bench_c3(args.steps, args.warmup, not args.no_cpu)[-1]), flush=True)
     gen = torch.Generator(device=dev).manual_seed(3)
     cache = icl.IclKVCache(EST, BLOCKS, HEADS, TRAIN, D, torch.bfloat16, dev)
     # fit-time build: per block, project-like K/V [est, head, rows, d] then append (timed apart)
@@ -605,7 +713,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu:
-        rec["cpu_baseline"] = cpu_baseline()
+        rec["cpu_baseline"] = cpu_baseline(q[:1, 0], kv[0][0][:1], kv[0][1][:1], out[:1, 0])
     print(json.dumps(rec), flush=True)
     return 0
 

@@ -70,11 +70,29 @@ int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const v
                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * Workspace bytes tabicl_hxq_fwd can use for these sizes on the current device (0: it never
- * splits them). No counterpart in the reference (its Pallas grid needs no scratch in HBM).
+ * Workspace bytes tabicl_hxq_fwd and tabicl_hxq_fwd_masked can use for these sizes on the current
+ * device (0: they never need any). No counterpart in the reference (its Pallas grid needs no scratch
+ * in HBM).
  */
 int64_t tabicl_hxq_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h,
                                    int32_t dtype);
+
+/*
+ * tabicl_hxq_fwd with an additive fp32 key mask key_bias [bias_b, Lk] (bias_b in {1, B}, rows
+ * contiguous) in place of, or next to, the valid length (valid may be NULL). The mask is what upstream
+ * tabicl builds from a tensor train size on every device but the reference's
+ * (results/tpu_patch.diff:1526-1542: 0 below the train size, finfo(dtype).min from there on), so
+ * this entry point serves the first ISAB attention when the caller hands over that mask: the
+ * reference's routing sends such calls to its fallback paths (scripts/tabicl_tpu_mha.py:328-347).
+ * Batch elements whose mask row is a prefix mask (0 on its first v >= 1 keys, <= -1e30 after) run on
+ * the valid-length kernel with valid = min(v, valid[b]), decided on the device; any other row adds
+ * the mask term by term (slower). With a bf16 input and keys past 128, the prefix path needs a
+ * workspace of tabicl_hxq_workspace_bytes(...) bytes; without one every row takes the term-by-term
+ * kernel. key_bias == NULL is tabicl_hxq_fwd.
+ */
+int tabicl_hxq_fwd_masked(const int32_t* valid, int64_t valid_n, const float* key_bias, int64_t bias_b,
+                          const void* q, const void* kv, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                          int32_t h, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Self attention over the packed in-projection qkv [B, L, 3E] with in-kernel RoPE on q and k, then
@@ -124,6 +142,17 @@ int tabicl_pk_cross_fwd_ragged(const void* q, int64_t q_b, const void* kv, const
 int tabicl_hxf_fwd(const int32_t* valid, int64_t valid_n, const void* qf, int64_t q_b, const void* x, void* out,
                    int64_t B, int64_t hq, int64_t Lk, int64_t E, int32_t dtype, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/*
+ * tabicl_hxf_fwd with an additive fp32 key mask key_bias [bias_b, Lk] (bias_b in {1, B}, rows
+ * contiguous; NULL: none) added to the scores, and valid optional (NULL: all Lk keys). This lets the
+ * folded route serve the first ISAB attention when upstream hands over the train mask it builds from
+ * a tensor train size (results/tpu_patch.diff:1526-1542) instead of the length. No counterpart in the
+ * reference (its hxf kernel takes the length only, scripts/tabicl_tpu_pallas_attn.py:414-419).
+ */
+int tabicl_hxf_fwd_masked(const int32_t* valid, int64_t valid_n, const float* key_bias, int64_t bias_b,
+                          const void* qf, int64_t q_b, const void* x, void* out, int64_t B, int64_t hq, int64_t Lk,
+                          int64_t E, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Workspace bytes tabicl_hxf_fwd can use for these sizes on the current device (0: no key split).
@@ -210,6 +239,24 @@ int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int
                           int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
                           float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
                           void* stream);
+
+/*
+ * tabicl_icl_fwd_ragged with an additive fp32 key mask (NULL: none): key_bias [bias_n, Tkv] with
+ * bias_n in {1, N}, row stride bias_sn elements, keys contiguous, added to the scaled scores
+ * (softmax(scale q k^T + mask) v, the reference's attn_mask path, results/tpu_patch.diff:263-270,
+ * 158-193, which sends every masked call to a torch fallback). Rows of N whose mask is a prefix mask
+ * (0 on the first v >= 1 keys, <= -1e30 after: what upstream builds from a tensor train size,
+ * diff:1526-1542) run on the pipelined kernel as the valid length min(v, valid[n]), decided on the
+ * device; other rows are computed by the exact kernel with the mask added term by term (every key
+ * carrying <= -1e30 gives equal weights, like the reference's softmax over finfo.min terms). scale
+ * must be positive with a mask. q_len may be NULL (all rows).
+ */
+int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                          const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,
+                          int64_t q_len_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                          int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                          int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                          float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Workspace size (bytes) that tabicl_icl_fwd uses for these sizes on the current device (0 when

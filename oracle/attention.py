@@ -329,9 +329,12 @@ def folded_mab1_ref(ind, x, valid, h: int, W, b):
     return attention_f64(q, k, v, h, valid=np.asarray(valid).astype(np.int64))
 
 
-def splash_sdpa_ref(q, k, v, valid=None):
+def splash_sdpa_ref(q, k, v, valid=None, bias=None):
     """ICL attention, reference hook _tpu_pallas_splash_sdpa (results/tpu_patch.diff:123-155):
-    q, k, v [N, H, T, D] float, q scaled by D^-0.5, keys >= valid masked. float64 result."""
+    q, k, v [N, H, T, D] float, q scaled by D^-0.5, keys >= valid masked. float64 result.
+    bias: optional additive key mask [1|N, Tkv] (the reference's masked paths, diff:158-193, 263-282:
+    `scores.float() + attn_mask.float()`), added to the scores in float32 as there, so a mask entry of
+    finfo.min absorbs the score and a row masked everywhere gets equal weights."""
     q = _f64(q)
     k = _f64(k)
     v = _f64(v)
@@ -339,11 +342,14 @@ def splash_sdpa_ref(q, k, v, valid=None):
     Tkv = k.shape[2]
     out = np.zeros((N, H, Tq, D))
     vl = None if valid is None else np.asarray(_f64(valid)).reshape(-1).astype(np.int64)
+    bb = None if bias is None else np.asarray(_f64(bias), np.float32).reshape(-1, Tkv)
     for n in range(N):
         nv = Tkv if vl is None else int(min(max(vl[0 if vl.size == 1 else n], 0), Tkv))
         if nv == 0:
             continue
         s = np.einsum("htd,hsd->hts", q[n] * D ** -0.5, k[n, :, :nv])
+        if bb is not None:
+            s = (s.astype(np.float32) + bb[0 if bb.shape[0] == 1 else n, :nv]).astype(np.float64)
         s -= s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)

@@ -159,11 +159,37 @@ int tabicl_hxq_fwd(const int32_t* valid, int64_t valid_n, const void* q, const v
       "hxq_fwd");
 }
 
+int tabicl_hxq_fwd_masked(const int32_t* valid, int64_t valid_n, const float* key_bias, int64_t bias_b,
+                          const void* q, const void* kv, void* out, int64_t B, int64_t Lq, int64_t Lk, int64_t E,
+                          int32_t h, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!key_bias) return tabicl_hxq_fwd(valid, valid_n, q, kv, out, B, Lq, Lk, E, h, dtype, workspace,
+                                       workspace_bytes, stream);
+  int st = smallhead_shape("hxq_fwd_masked", B, Lq, Lk, E, h, dtype);
+  if (st) return st;
+  if (valid && valid_n != 1 && valid_n != B)
+    return fail(1, "hxq_fwd_masked: valid must hold 1 or B=%lld entries (got %lld)", (long long)B,
+                (long long)valid_n);
+  if (bias_b != 1 && bias_b != B)
+    return fail(1, "hxq_fwd_masked: key_bias batch %lld must be 1 or B=%lld", (long long)bias_b, (long long)B);
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(key_bias))
+    return fail(1, "hxq_fwd_masked: pointers must be 16-byte aligned");
+  if (B == 0 || Lq == 0) return 0;
+  const char* kvb = (const char*)kv;
+  void* ws = workspace && aligned16(workspace) ? workspace : nullptr;
+  return launch_status(
+      tabicl_launch_smallhead(q, Lq * E, E, kvb, Lk * 2 * E, 2 * E, kvb + E * esize(dtype), Lk * 2 * E, 2 * E, out,
+                              key_bias, bias_b == B ? Lk : 0, valid, valid ? valid_n : 0, nullptr, nullptr,
+                              nullptr, nullptr, 0, 0, 0, 1.0f, B, Lq, Lk, dtype, ws, ws ? workspace_bytes : 0,
+                              (hipStream_t)stream),
+      "hxq_fwd_masked");
+}
+
 int64_t tabicl_hxq_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t E, int32_t h,
                                    int32_t dtype) {
   if (E != 128 || h != 8 || B <= 0 || Lq <= 0 || Lk <= 0) return 0;
   if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) return 0;
-  return tabicl_launch_smallhead_ws_bytes(B, Lq, Lk, dtype, false, 0);
+  // sized for tabicl_hxq_fwd_masked too (the prefix view of a key mask: 8 bytes per batch element)
+  return tabicl_launch_smallhead_ws_bytes(B, Lq, Lk, dtype, true, 0);
 }
 
 int tabicl_pk_self_fwd(const void* qkv, const float* bias, int64_t bias_b, const float* cos_t,
@@ -212,7 +238,8 @@ int tabicl_pk_cross_fwd_ragged(const void* q, int64_t q_b, const void* kv, const
   if (q_len && q_len_n != 1 && q_len_n != B) return fail(1, "pk_cross_fwd: q_len must hold 1 or B entries");
   if (bias && bias_b != 1 && bias_b != B)
     return fail(1, "pk_cross_fwd: bias batch %lld must be 1 or B", (long long)bias_b);
-  if (!aligned16(q) || !aligned16(kv) || !aligned16(out))
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out) ||
+      (rope && (!aligned16(cq) || !aligned16(sq) || !aligned16(ck) || !aligned16(sk))))
     return fail(1, "pk_cross_fwd: pointers must be 16-byte aligned");
   if (B == 0 || Lq == 0) return 0;
   const char* kvb = (const char*)kv;
@@ -280,6 +307,8 @@ int tabicl_pk_cross_bwd(const void* q, int64_t q_b, const void* kv, const float*
   if ((st = rope_args("pk_cross_bwd", rope, half, rot, false))) return st;
   if (rope && (!cq || !sq || !ck || !sk)) return fail(1, "pk_cross_bwd: rope tables missing");
   if (q_b != 1 && q_b != B) return fail(1, "pk_cross_bwd: q batch must be 1 or B");
+  if (rope && (!aligned16(cq) || !aligned16(sq) || !aligned16(ck) || !aligned16(sk)))
+    return fail(1, "pk_cross_bwd: rope tables must be 16-byte aligned");
   if (!aligned16(q) || !aligned16(kv) || !aligned16(dq) || !aligned16(dkv))
     return fail(1, "pk_cross_bwd: pointers must be 16-byte aligned");
   if (B == 0) return 0;
@@ -313,8 +342,25 @@ int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int
                           int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
                           float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
                           void* stream) {
+  return tabicl_icl_fwd_masked(q, k, v, valid, valid_n, nullptr, 0, 0, q_len, q_len_n, out, N, H, Tq, Tkv, D, q_sn,
+                               q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype,
+                               workspace, workspace_bytes, stream);
+}
+
+int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                          const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,
+                          int64_t q_len_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                          int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                          int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                          float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
     return fail(1, "icl_fwd: dtype code %d not supported", dtype);
+  if (key_bias) {
+    if (bias_n != 1 && bias_n != N) return fail(1, "icl_fwd: key_bias must hold 1 or N rows");
+    if (bias_n > 1 && bias_sn < Tkv) return fail(1, "icl_fwd: key_bias row stride %lld < Tkv", (long long)bias_sn);
+    if (!aligned16(key_bias)) return fail(1, "icl_fwd: key_bias must be 16-byte aligned");
+    if (!(scale > 0.f) || !(scale < 1e30f)) return fail(1, "icl_fwd: a key mask needs a positive finite scale");
+  }
   if (D != 64) return fail(1, "icl_fwd: head dim must be 64, got %lld", (long long)D);
   if (N < 0 || H < 0 || Tq < 0 || Tkv < 1 || Tq > (1LL << 30) || Tkv > (1LL << 30))
     return fail(1, "icl_fwd: bad sizes");
@@ -334,7 +380,8 @@ int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int
       tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, 64, q_sn, q_sh,
                             q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale,
                             dtype, workspace && aligned16(workspace) ? workspace : nullptr,
-                            workspace_bytes, (hipStream_t)stream, q_len, q_len ? q_len_n : 0),
+                            workspace_bytes, (hipStream_t)stream, q_len, q_len ? q_len_n : 0, key_bias,
+                            key_bias ? bias_n : 0, key_bias ? bias_sn : 0),
       "icl_fwd");
 }
 
@@ -350,22 +397,33 @@ int64_t tabicl_icl_workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv
 int tabicl_hxf_fwd(const int32_t* valid, int64_t valid_n, const void* qf, int64_t q_b, const void* x, void* out,
                    int64_t B, int64_t hq, int64_t Lk, int64_t E, int32_t dtype, void* workspace,
                    int64_t workspace_bytes, void* stream) {
+  if (!valid) return fail(1, "hxf_fwd: valid is required");
+  return tabicl_hxf_fwd_masked(valid, valid_n, nullptr, 0, qf, q_b, x, out, B, hq, Lk, E, dtype, workspace,
+                               workspace_bytes, stream);
+}
+
+int tabicl_hxf_fwd_masked(const int32_t* valid, int64_t valid_n, const float* key_bias, int64_t bias_b,
+                          const void* qf, int64_t q_b, const void* x, void* out, int64_t B, int64_t hq, int64_t Lk,
+                          int64_t E, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
     return fail(1, "hxf_fwd: dtype code %d not supported", dtype);
+  if (key_bias && bias_b != 1 && bias_b != B) return fail(1, "hxf_fwd: key_bias must hold 1 or B rows");
+  if (key_bias && !aligned16(key_bias)) return fail(1, "hxf_fwd: key_bias must be 16-byte aligned");
   if (E != 128) return fail(1, "hxf_fwd: needs E == 128, got %lld", (long long)E);
   if (B < 0 || hq < 0 || Lk < 1 || B > (1LL << 30) || hq > (1LL << 30) || Lk > (1LL << 30))
     return fail(1, "hxf_fwd: bad sizes B=%lld hq=%lld Lk=%lld", (long long)B, (long long)hq, (long long)Lk);
   if (q_b != 1 && q_b != B) return fail(1, "hxf_fwd: qf batch must be 1 or B");
-  if (!valid || (valid_n != 1 && valid_n != B))
+  if (valid && valid_n != 1 && valid_n != B)
     return fail(1, "hxf_fwd: valid must hold 1 or B=%lld entries", (long long)B);
   if (!aligned16(qf) || !aligned16(x) || !aligned16(out)) return fail(1, "hxf_fwd: pointers must be 16-byte aligned");
   if (B == 0 || hq == 0) return 0;
   if (B * ((hq + 127) / 128) * 4 > (1LL << 31) - 1) return fail(1, "hxf_fwd: grid too large");
   return launch_status(
-      tabicl_launch_icl_fwd(qf, x, x, valid, valid_n, out, B, 1, hq, Lk, 128, q_b == 1 && B > 1 ? 0 : hq * E, 0, E,
-                            Lk * E, 0, E, Lk * E, 0, E, hq * E, 0, E, 1.0f, dtype,
-                            workspace && aligned16(workspace) ? workspace : nullptr, workspace_bytes,
-                            (hipStream_t)stream),
+      tabicl_launch_icl_fwd(qf, x, x, valid, valid ? valid_n : 0, out, B, 1, hq, Lk, 128,
+                            q_b == 1 && B > 1 ? 0 : hq * E, 0, E, Lk * E, 0, E, Lk * E, 0, E, hq * E, 0, E, 1.0f,
+                            dtype, workspace && aligned16(workspace) ? workspace : nullptr, workspace_bytes,
+                            (hipStream_t)stream, nullptr, 0, key_bias, key_bias ? bias_b : 0,
+                            key_bias && bias_b > 1 ? Lk : 0),
       "hxf_fwd");
 }
 

@@ -22,6 +22,7 @@
 //    with the running max updated lazily (accumulators rescaled only when the tile max exceeds the
 //    running max by more than 2^8; exact because O and l always share the same reference max).
 #include "common.h"
+#include "launch.h"
 
 namespace {
 
@@ -49,6 +50,17 @@ struct IclParams {
   float* ws_ml;  // [nsplit][N*H][Tq][2], m in log2 units
   // per workgroup: 1 = the fast kernel's result must be recomputed exactly (null: no fast kernel)
   int* flags;
+  // additive key mask: fp32 [bias_n][Tkv], row stride bias_sn, added to the scaled scores by
+  // icl_fwd_kernel<..., BIAS = true>; bias_inv_scale = 1 / scale puts it in raw score units
+  const float* bias;
+  int64_t bias_sn;
+  int bias_n;
+  float bias_inv_scale;
+  // prefix view of that mask for the pipelined kernel (pvalid / pok [pn], pn in {1, N}): rows whose
+  // mask is a prefix mask run with valid length pvalid; the others are flagged for icl_fwd_kernel
+  const int32_t* pvalid;
+  const int32_t* pok;
+  int pn;
 };
 
 __device__ __forceinline__ int icl_live_rows(const IclParams& p, int n) {
@@ -175,10 +187,26 @@ template <typename T, int QC, int D = ICL_D> struct IclState {
   float m_run[QC], l_run[QC];
 };
 
-// One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T. MASK: the tile crosses `valid`.
-template <typename T, int QC, bool MASK, int D>
-__device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, const T* lv, int k0,
-                                         int valid, float sc, int lr, int hh) {
+// The key mask of one tile in LDS: thread t < ICL_KT stages key k0 + t of its row, in raw score
+// units and clamped at -1e30 (so that every score stays finite: a row whose keys all carry the
+// floor gets equal weights, as the reference's softmax over finfo.min terms does). Keys past `valid`
+// (masked by the kernel anyway) read row entry valid - 1.
+struct BiasStage {
+  float b;
+  __device__ __forceinline__ void load(const float* row, int k0, int valid, float inv_scale) {
+    const int t = threadIdx.x;
+    if (t < ICL_KT) b = fmaxf(row[min(k0 + t, valid - 1)] * inv_scale, -1e30f);
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    if (threadIdx.x < ICL_KT) lds[threadIdx.x] = b;
+  }
+};
+
+// One key tile: S^T = K Q^T (+ the tile's key mask lb when BIAS), online softmax, O^T += V^T P^T.
+// MASK: the tile crosses `valid`.
+template <typename T, int QC, bool MASK, int D, bool BIAS = false>
+__device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, const T* lv, const float* lb,
+                                         int k0, int valid, float sc, int lr, int hh) {
   typedef IclLds<T, D> L;
   typedef typename OpVec<T, 8>::type Op8;
   f32x16 s[QC][2];
@@ -194,6 +222,22 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, co
 #pragma unroll
       for (int qc = 0; qc < QC; ++qc) s[qc][kb] = mfma32x32x16(a, st.qop[qc][sl], s[qc][kb]);
     }
+  }
+  if (BIAS) {
+    // S^T row of reg r = key 8 (r / 4) + 4 hh + r % 4 of the 32-key block
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 bb = *(const float4*)(lb + kb * 32 + 8 * g + 4 * hh);
+#pragma unroll
+        for (int qc = 0; qc < QC; ++qc) {
+          s[qc][kb][4 * g] += bb.x;
+          s[qc][kb][4 * g + 1] += bb.y;
+          s[qc][kb][4 * g + 2] += bb.z;
+          s[qc][kb][4 * g + 3] += bb.w;
+        }
+      }
   }
   if (MASK) {
 #pragma unroll
@@ -252,7 +296,7 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, co
       }
 }
 
-template <typename T, int NW, int QC, int D = ICL_D>
+template <typename T, int NW, int QC, int D = ICL_D, bool BIAS = false>
 __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   typedef IclLds<T, D> L;
   typedef typename OpVec<T, 8>::type Op8;
@@ -260,6 +304,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   constexpr int QW = 32 * QC;
   __shared__ __attribute__((aligned(16))) T lds_k[2][L::K_ELEMS];
   __shared__ __attribute__((aligned(16))) T lds_vt[2][L::V_ELEMS];
+  __shared__ __attribute__((aligned(16))) float lds_b[BIAS ? 2 : 1][BIAS ? ICL_KT : 4];
 
   // work item = (n, h, split, query block); consecutive items share (n, h) and stay on one XCD
   const int work = xcd_remap(blockIdx.x, gridDim.x);
@@ -276,6 +321,9 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     valid = p.valid[p.valid_n == 1 ? 0 : n];
     valid = valid < 0 ? 0 : (valid > p.Tkv ? p.Tkv : valid);
   }
+  // a row whose key mask is a prefix mask ends at its prefix here too (the mask is 0 below it), so
+  // the keys past it are never read, as in the pipelined kernel
+  if (p.pok && p.pok[p.pn == 1 ? 0 : n]) valid = p.pvalid[p.pn == 1 ? 0 : n];
 
   const int live = icl_live_rows(p, n);
   if (qb * (QW * NW) >= live) return;  // no live query row: nothing to compute or write
@@ -311,23 +359,30 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
   const int per = (ntiles + p.nsplit - 1) / p.nsplit;
   const int t0 = min(split * per, ntiles), t1 = min(t0 + per, ntiles);
   if (t1 > t0) {
+    const float* brow = BIAS ? p.bias + (p.bias_n == 1 ? 0 : (int64_t)n * p.bias_sn) : nullptr;
     Stage<T, NT, D> stg;
+    BiasStage bst;
     stg.load(kbase, vbase, p.k_st, p.v_st, t0 * ICL_KT, valid);
+    if (BIAS) bst.load(brow, t0 * ICL_KT, valid, p.bias_inv_scale);
     stg.store(lds_k[0], lds_vt[0]);
+    if (BIAS) bst.store(lds_b[0]);
     __syncthreads();
     // all tiles but the last one of the range: no key past `valid`
     for (int t = t0; t + 1 < t1; ++t) {
       const int k0 = t * ICL_KT, buf = (t - t0) & 1;
       stg.load(kbase, vbase, p.k_st, p.v_st, k0 + ICL_KT, valid);
-      icl_tile<T, QC, false, D>(st, lds_k[buf], lds_vt[buf], k0, valid, sc, lr, hh);
+      if (BIAS) bst.load(brow, k0 + ICL_KT, valid, p.bias_inv_scale);
+      icl_tile<T, QC, false, D, BIAS>(st, lds_k[buf], lds_vt[buf], lds_b[BIAS ? buf : 0], k0, valid, sc, lr, hh);
       stg.store(lds_k[buf ^ 1], lds_vt[buf ^ 1]);
+      if (BIAS) bst.store(lds_b[BIAS ? buf ^ 1 : 0]);
       __syncthreads();
     }
     const int tl = t1 - 1, bl = (tl - t0) & 1;
     if (t1 == ntiles)
-      icl_tile<T, QC, true, D>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
+      icl_tile<T, QC, true, D, BIAS>(st, lds_k[bl], lds_vt[bl], lds_b[BIAS ? bl : 0], tl * ICL_KT, valid, sc, lr, hh);
     else
-      icl_tile<T, QC, false, D>(st, lds_k[bl], lds_vt[bl], tl * ICL_KT, valid, sc, lr, hh);
+      icl_tile<T, QC, false, D, BIAS>(st, lds_k[bl], lds_vt[bl], lds_b[BIAS ? bl : 0], tl * ICL_KT, valid, sc, lr,
+                                      hh);
   }
 
   if (p.nsplit > 1) {
@@ -687,6 +742,16 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     if (threadIdx.x == 0) p.flags[work] = 0;
     return;
   }
+  if (p.pok) {
+    // key mask: a prefix mask is the valid length pvalid; any other mask is left to icl_fwd_kernel,
+    // which adds it term by term
+    const int pr = p.pn == 1 ? 0 : n;
+    if (!p.pok[pr]) {
+      if (threadIdx.x == 0) p.flags[work] = 1;
+      return;
+    }
+    valid = p.pvalid[pr];
+  }
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lr = lane & 31, hh = lane >> 5;
@@ -889,16 +954,19 @@ int pick_splits(int64_t items, int64_t Tkv) {
   return best;
 }
 
-// Workspace layout: [per-work-item flags, bf16 d = 64 only, 256-byte aligned][split partials: O fp32
+// Workspace layout: [per-work-item flags, bf16 d = 64 only, 256-byte aligned][prefix view of a key
+// mask, bf16 d = 64 only: valid [N], ok [N], 256-byte aligned][split partials: O fp32
 // [nsplit][rows][D], (m, l) [nsplit][rows][2]].
 int64_t flag_bytes(int64_t nblk) { return (nblk * 4 + 255) / 256 * 256; }
+int64_t pref_bytes(int64_t N) { return (N * 8 + 255) / 256 * 256; }
 int64_t part_bytes(int nsplit, int64_t rows, int D) { return nsplit > 1 ? (int64_t)nsplit * rows * (D + 2) * 4 : 0; }
 
 template <typename T, int NW, int QC, int D>
 int64_t workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv) {
   const int64_t nqb = (Tq + 32 * QC * NW - 1) / (32 * QC * NW);
   const int s = pick_splits<T, NW, QC, D>(N * H * nqb, Tkv);
-  return (sizeof(T) == 2 && D == ICL_D ? flag_bytes(N * H * nqb * s) : 0) + part_bytes(s, N * H * Tq, D);
+  return (sizeof(T) == 2 && D == ICL_D ? flag_bytes(N * H * nqb * s) + pref_bytes(N) : 0) +
+         part_bytes(s, N * H * Tq, D);
 }
 
 // bf16 d = 64 with a large enough workspace: pipelined kernel, then icl_fwd_kernel on the work
@@ -917,8 +985,9 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream)
   // the pipelined kernel's tile copies take 32-bit byte offsets within a tile (64 rows)
   const bool strides_fit = p.k_st >= 0 && p.v_st >= 0 && p.k_st < (1 << 24) && p.v_st < (1 << 24);
   if (sizeof(T) == 2 && D == ICL_D && strides_fit) {
-    if (have < flag_bytes(items * p.nsplit) + part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
-    fb = flag_bytes(items * p.nsplit);
+    const int64_t pb = pref_bytes(p.N);
+    if (have < flag_bytes(items * p.nsplit) + pb + part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
+    fb = flag_bytes(items * p.nsplit) + pb;
     fast = have >= fb + part_bytes(p.nsplit, rows, D);
   }
   if (!fast) {
@@ -929,9 +998,21 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream)
   p.ws_o = (float*)((char*)ws + fb);
   p.ws_ml = p.ws_o + (p.nsplit > 1 ? (int64_t)p.nsplit * rows * D : 0);
   const int64_t nblk = items * p.nsplit;
+  if (fast && p.bias) {
+    // prefix view of the key mask, per n (or one row when neither the mask nor the valid length
+    // varies over n), for the pipelined kernel
+    p.pn = (p.bias_n == 1 && p.valid_n <= 1) ? 1 : p.N;
+    int32_t* pv = (int32_t*)((char*)ws + flag_bytes(nblk));
+    p.pvalid = pv;
+    p.pok = pv + p.pn;
+    tabicl_launch_key_prefix(p.bias, p.bias_sn, p.bias_n, p.Tkv, p.valid, p.valid_n, p.pn, pv, pv + p.pn, stream);
+  }
   if (fast)
     hipLaunchKernelGGL(icl_pipe_kernel, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
-  hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC, D>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
+  if (p.bias)
+    hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC, D, true>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC, D>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
   if (p.nsplit > 1) {
     const int64_t threads = rows * (D / 4);
     hipLaunchKernelGGL((icl_merge_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
@@ -953,7 +1034,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream, const int32_t* qlen,
-                          int64_t qlen_n) {
+                          int64_t qlen_n, const float* bias, int64_t bias_n, int64_t bias_sn) {
   IclParams p;
   p.q = q; p.k = k; p.v = v; p.o = out;
   p.valid = valid; p.valid_n = (int)valid_n;
@@ -966,6 +1047,9 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.o_sn = o_sn; p.o_sh = o_sh; p.o_st = o_st;
   p.sc = scale * TA_LOG2E;
   p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr; p.flags = nullptr;
+  p.bias = bias; p.bias_n = (int)bias_n; p.bias_sn = bias_sn;
+  p.bias_inv_scale = 1.0f / scale;
+  p.pvalid = nullptr; p.pok = nullptr; p.pn = 0;
   if (D == 128) {
     if (dtype == 0)
       launch<bf16, 4, 1, 128>(p, ws, ws_bytes, stream);

@@ -4,16 +4,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Prefix view of key-only additive masks (keymask.hip): for each of `rows` rows r, out_ok[r] = 1 if
+// bias row (nb == 1 ? 0 : r) is 0 on its first v >= 1 keys and <= -1e30 on the rest, and
+// out_valid[r] = min(v, valid[valid_n == 1 ? 0 : r]) then (else the plain valid length, or L).
+int tabicl_launch_key_prefix(const float* bias, int64_t bias_sr, int64_t nb, int64_t L, const int32_t* valid,
+                             int64_t valid_n, int64_t rows, int32_t* out_valid, int32_t* out_ok,
+                             hipStream_t stream);
+
 // Flash attention over [N, H, T, D] views (icl_fwd.hip): D = 64 is the cached-KV ICL attention,
 // D = 128 the folded ISAB-1 attention (one head, K = V = the raw rows). qlen (device int32,
 // qlen_n in {1, N}): query rows computed per n; rows at or past it are not written (null: all).
+// bias: additive fp32 key mask [bias_n, Tkv] (row stride bias_sn, bias_n in {1, N}), added to the
+// scaled scores.
 int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int32_t* valid,
                           int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq,
                           int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn,
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream,
-                          const int32_t* qlen = nullptr, int64_t qlen_n = 0);
+                          const int32_t* qlen = nullptr, int64_t qlen_n = 0,
+                          const float* bias = nullptr, int64_t bias_n = 0, int64_t bias_sn = 0);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
 // Small-head (8 x 16) attention (smallhead_fwd.hip): picks the resident, streaming or general
@@ -30,11 +40,14 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
 int64_t tabicl_launch_smallhead_ws_bytes(int64_t B, int64_t Lq, int64_t Lk, int dtype, bool bias,
                                          int rope);
 
-// Streaming bf16 small-head kernel without RoPE / key bias (smallhead_stream.hip).
+// Streaming bf16 small-head kernel without RoPE / key bias (smallhead_stream.hip). gate (device
+// int32 [gate_n], gate_n in {1, B}, or null): batch elements whose entry is 0 are skipped (neither
+// computed nor written).
 int tabicl_launch_ss(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
                      int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
                      const int32_t* valid, int64_t valid_n, float scale, int64_t B, int64_t Lq,
-                     int64_t Lk, void* ws, int64_t ws_bytes, hipStream_t stream);
+                     int64_t Lk, void* ws, int64_t ws_bytes, hipStream_t stream,
+                     const int32_t* gate = nullptr, int64_t gate_n = 0);
 int64_t tabicl_launch_ss_ws_bytes(int64_t B, int64_t Lq, int64_t Lk);
 
 // Backward of the small-head attention (smallhead_bwd.hip): dq, dk, dv (element strides as the

@@ -64,6 +64,10 @@ struct ShParams {
   // resident kernel neither computes nor writes the rows at or past it
   const int32_t* qlen;
   int qlen_n;
+  // batch elements computed by another kernel of the same call (skip[b], or skip[0] for all; null:
+  // none): smallhead_fwd_kernel returns for them
+  const int32_t* skip;
+  int skip_n;
 };
 
 template <typename T, int KT> struct ShLds {
@@ -157,6 +161,7 @@ __global__ __launch_bounds__(SH_NW * 64) void smallhead_fwd_kernel(ShParams p) {
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int b = work / p.nwg_b;
   const int qb0 = (work % p.nwg_b) * p.qbpw;
+  if (p.skip && p.skip[p.skip_n == 1 ? 0 : b]) return;
 
   int lk = p.Lk;
   if (p.valid) {
@@ -988,6 +993,21 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   if (dtype == 0 && Lk > RS_LK && bias == nullptr && rope == 0)
     return tabicl_launch_ss(q, q_sb, q_sr, k, k_sb, k_sr, v, v_sb, v_sr, o, valid, valid_n, scale, B,
                             Lq, Lk, ws, ws_bytes, stream);
+  // bf16, long keys, a key mask and a workspace with room for its prefix view: the batch elements
+  // whose mask is a prefix mask run on the streaming kernel with that valid length, the others on
+  // smallhead_fwd_kernel with the mask added term by term
+  const int64_t pref = (B * 8 + 255) / 256 * 256;
+  const bool gated = dtype == 0 && Lk > RS_LK && bias != nullptr && rope == 0 && ws != nullptr && ws_bytes >= pref;
+  const int64_t pn = (bias_sb == 0 && valid_n <= 1) ? 1 : B;
+  int32_t* pvalid = gated ? (int32_t*)ws : nullptr;
+  if (gated) {
+    int st = tabicl_launch_key_prefix(bias, bias_sb, bias_sb == 0 ? 1 : B, Lk, valid, valid ? valid_n : 0, pn,
+                                      pvalid, pvalid + pn, stream);
+    if (st == 0)
+      st = tabicl_launch_ss(q, q_sb, q_sr, k, k_sb, k_sr, v, v_sb, v_sr, o, pvalid, pn, scale, B, Lq, Lk,
+                            (char*)ws + pref, ws_bytes - pref, stream, pvalid + pn, pn);
+    if (st != 0) return st;
+  }
   ShParams p;
   p.q = q; p.q_sb = q_sb; p.q_sr = q_sr;
   p.k = k; p.k_sb = k_sb; p.k_sr = k_sr;
@@ -1009,6 +1029,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   }
   p.half_last = 0;
   p.qlen = qlen; p.qlen_n = (int)qlen_n;
+  p.skip = gated ? pvalid + pn : nullptr; p.skip_n = (int)pn;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   const bool fast_rope = rope == 0 || (rope == 1 && rot == 16) || (rope == 2 && half == 8 && rot == 16);
   // the resident kernel's buffer loads take 32-bit byte offsets within a batch element (query runs
@@ -1051,6 +1072,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
 
 int64_t tabicl_launch_smallhead_ws_bytes(int64_t B, int64_t Lq, int64_t Lk, int dtype, bool bias,
                                          int rope) {
-  if (dtype == 0 && Lk > RS_LK && !bias && rope == 0) return tabicl_launch_ss_ws_bytes(B, Lq, Lk);
+  if (dtype == 0 && Lk > RS_LK && rope == 0)
+    return tabicl_launch_ss_ws_bytes(B, Lq, Lk) + (bias ? (B * 8 + 255) / 256 * 256 : 0);
   return 0;
 }

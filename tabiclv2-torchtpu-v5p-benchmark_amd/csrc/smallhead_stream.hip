@@ -68,6 +68,10 @@ struct SsParams {
   int nqg, nsplit, tps;
   float* ws_o;    // [nsplit][B*Lq][E] fp32 partial outputs
   float2* ws_ml;  // [nsplit][B*Lq][H] (m, l), m in log2 units
+  // batch elements computed here (gate[b], or gate[0] for all; null: all): the others are neither
+  // computed nor merged nor written
+  const int32_t* gate;
+  int gate_n;
 };
 
 // 16-byte chunk swizzle of a 256-byte tile row (key r): physical chunk = logical ^ ss_swz(r), a
@@ -260,6 +264,7 @@ __global__ __launch_bounds__(SS_NW * 64, 2) void ss_stream_kernel(SsParams p) {
   rest /= SS_NHG;
   const int split = rest % p.nsplit;
   const int b = rest / p.nsplit;
+  if (p.gate && !p.gate[p.gate_n == 1 ? 0 : b]) return;
 
   int lk = p.Lk;
   if (p.valid) {
@@ -369,6 +374,7 @@ __global__ __launch_bounds__(256) void ss_merge_kernel(SsParams p) {
   const int c = (int)(idx & 31);
   const int64_t row = idx >> 5;
   const int h = c >> 2, d0 = 4 * c;
+  if (p.gate && !p.gate[p.gate_n == 1 ? 0 : (int)(row / p.Lq)]) return;
   float m_max = TA_NEG_INF;
   for (int s = 0; s < p.nsplit; ++s) {
     const float2 ml = p.ws_ml[((int64_t)s * rows + row) * SS_H + h];
@@ -438,8 +444,10 @@ int64_t tabicl_launch_ss_ws_bytes(int64_t B, int64_t Lq, int64_t Lk) {
 int tabicl_launch_ss(const void* q, int64_t q_sb, int64_t q_sr, const void* k, int64_t k_sb,
                      int64_t k_sr, const void* v, int64_t v_sb, int64_t v_sr, void* o,
                      const int32_t* valid, int64_t valid_n, float scale, int64_t B, int64_t Lq,
-                     int64_t Lk, void* ws, int64_t ws_bytes, hipStream_t stream) {
+                     int64_t Lk, void* ws, int64_t ws_bytes, hipStream_t stream, const int32_t* gate,
+                     int64_t gate_n) {
   SsParams p;
+  p.gate = gate; p.gate_n = (int)gate_n;
   p.q = (const bf16*)q; p.q_sb = q_sb; p.q_sr = q_sr;
   p.k = (const bf16*)k; p.k_sb = k_sb; p.k_sr = k_sr;
   p.v = (const bf16*)v; p.v_sb = v_sb; p.v_sr = v_sr;

@@ -52,8 +52,8 @@ def _workspace(N: int, H: int, Tq: int, Tkv: int, D: int, code: int, device) -> 
 
 
 def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float, out: Tensor,
-            q_len: Optional[Tensor] = None) -> None:
-    _nat.require_device(q, k, v, valid, out, q_len)
+            q_len: Optional[Tensor] = None, key_bias: Optional[Tensor] = None) -> None:
+    _nat.require_device(q, k, v, valid, out, q_len, key_bias)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("icl_cached_attn expects [N, H, T, D] tensors")
     N, H, Tq, D = q.shape
@@ -73,52 +73,65 @@ def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: flo
     ws = _workspace(N, H, Tq, Tkv, D, code, q.device)
     tail = (*_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out), float(scale), code,
             None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _nat.stream_of(q))
+    if q_len is not None and (q_len.dtype != torch.int32 or not q_len.is_contiguous() or q_len.numel() not in (1, N)):
+        raise ValueError(f"q_len must be a contiguous int32 tensor of 1 or {N} entries")
+    if key_bias is not None:
+        if key_bias.dtype != torch.float32 or key_bias.dim() != 2 or key_bias.shape[1] != Tkv \
+                or key_bias.shape[0] not in (1, N) or key_bias.stride(1) != 1:
+            raise ValueError(f"key_bias must be a float32 [1 or {N}, {Tkv}] tensor with contiguous rows, got "
+                             f"{key_bias.dtype} {tuple(key_bias.shape)}")
+        _nat.call("tabicl_icl_fwd_masked", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, key_bias.data_ptr(),
+                  key_bias.shape[0], key_bias.stride(0), None if q_len is None else q_len.data_ptr(),
+                  0 if q_len is None else q_len.numel(), out.data_ptr(), N, H, Tq, Tkv, D, *tail)
+        return
     if q_len is None:
         _nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
                   N, H, Tq, Tkv, D, *tail)
         return
-    if q_len.dtype != torch.int32 or not q_len.is_contiguous() or q_len.numel() not in (1, N):
-        raise ValueError(f"q_len must be a contiguous int32 tensor of 1 or {N} entries")
     _nat.call("tabicl_icl_fwd_ragged", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, q_len.data_ptr(),
               q_len.numel(), out.data_ptr(), N, H, Tq, Tkv, D, *tail)
 
 
 @torch.library.custom_op("tabicl::icl_cached_attn", mutates_args=())
-def _icl_cached_attn(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float) -> Tensor:
+def _icl_cached_attn(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float,
+                     key_bias: Optional[Tensor] = None) -> Tensor:
+    """key_bias: optional additive fp32 key mask [1 or N, Tkv] (the reference's masked path,
+    results/tpu_patch.diff:263-270); a prefix mask (0 then <= -1e30) runs as a valid length on the
+    pipelined kernel, any other mask on the exact kernel, which adds it term by term."""
     out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
-    _launch(q, k, v, valid, scale, out)
+    _launch(q, k, v, valid, scale, out, None, key_bias)
     return out
 
 
 @_icl_cached_attn.register_fake
-def _(q, k, v, valid, scale):  # noqa: ANN001
+def _(q, k, v, valid, scale, key_bias=None):  # noqa: ANN001
     return torch.empty_like(q)
 
 
 @torch.library.custom_op("tabicl::icl_cached_attn_out", mutates_args=("out",))
 def _icl_cached_attn_out(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float,
-                         out: Tensor) -> None:
+                         out: Tensor, key_bias: Optional[Tensor] = None) -> None:
     """Same as icl_cached_attn, written into `out` (any [N, H, Tq, D] view with a contiguous last
     dim, e.g. one block of a [est, block, head, row, d] result buffer)."""
-    _launch(q, k, v, valid, scale, out)
+    _launch(q, k, v, valid, scale, out, None, key_bias)
 
 
 @_icl_cached_attn_out.register_fake
-def _(q, k, v, valid, scale, out):  # noqa: ANN001
+def _(q, k, v, valid, scale, out, key_bias=None):  # noqa: ANN001
     return None
 
 
 @torch.library.custom_op("tabicl::icl_cached_attn_ragged_out", mutates_args=("out",))
 def _icl_cached_attn_ragged_out(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], q_len: Tensor,
-                                scale: float, out: Tensor) -> None:
+                                scale: float, out: Tensor, key_bias: Optional[Tensor] = None) -> None:
     """icl_cached_attn_out over a ragged batch: rows at or past q_len[n] (1 or N entries) are neither
     computed nor written (out keeps what it held). No counterpart in the reference, whose bucketed
     runner attends with the padding rows of each table's test bucket too."""
-    _launch(q, k, v, valid, scale, out, q_len)
+    _launch(q, k, v, valid, scale, out, q_len, key_bias)
 
 
 @_icl_cached_attn_ragged_out.register_fake
-def _(q, k, v, valid, q_len, scale, out):  # noqa: ANN001
+def _(q, k, v, valid, q_len, scale, out, key_bias=None):  # noqa: ANN001
     return None
 
 
@@ -131,10 +144,14 @@ def icl_supported(Tq: int, Tkv: int, D: int, dtype: torch.dtype) -> bool:
     return dtype in (torch.bfloat16, torch.float32) and _nat.supported(_nat.OP_ICL, Tq, Tkv, D, 1, dtype)
 
 
-def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None) -> Tensor:
+def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None,
+             key_bias: Optional[Tensor] = None) -> Tensor:
     """softmax(q k^T * D^-0.5 + key mask) v for q [..., H, Tq, D], k/v [..., H, Tkv, D]; keys at
     positions >= valid_kv_len are masked (a tensor may hold one length per flattened batch entry).
-    Contract of the reference hook _tpu_pallas_splash_sdpa (results/tpu_patch.diff:123-155)."""
+    Contract of the reference hook _tpu_pallas_splash_sdpa (results/tpu_patch.diff:123-155).
+    key_bias (extension): an additive key mask with one row for all flattened batch entries or one
+    per entry ([Tkv], [1, Tkv] or [N, Tkv]; any leading shape that flattens to those), e.g. the train
+    mask upstream builds from a tensor train size (diff:1526-1542)."""
     D = q.shape[-1]
     lead = q.shape[:-3]
     H, Tq = q.shape[-3], q.shape[-2]
@@ -147,17 +164,29 @@ def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, 
         valid = valid_kv_len.to(device=q.device, dtype=torch.int32).reshape(-1).contiguous()
     elif valid_kv_len is not None and int(valid_kv_len) < Tkv:
         valid = torch.full((1,), int(valid_kv_len), dtype=torch.int32, device=q.device)
-    out = ICL_FWD(q4, k4, v4, valid, float(D) ** -0.5)
+    kb = None
+    if key_bias is not None:
+        kb = key_bias.to(device=q.device, dtype=torch.float32).reshape(-1, Tkv)
+        if kb.shape[0] not in (1, q4.shape[0]):
+            raise ValueError(f"key_bias rows {kb.shape[0]} must be 1 or the flattened batch {q4.shape[0]}")
+        if kb.stride(-1) != 1 or (kb.data_ptr() % 16):
+            kb = kb.contiguous()
+    out = ICL_FWD(q4, k4, v4, valid, float(D) ** -0.5, kb)
     return out.reshape(*lead, H, Tq, D)
 
 
 class IclKVCache:
     """Fit-time K/V cache of the ICL stage, one tensor per K and V of shape
-    [estimators, blocks, heads, capacity, head_dim] (rows past the valid length are never read).
+    [estimators, blocks, heads, capacity, head_dim].
 
     append(block, k, v, row0) writes rows [row0, row0 + T) of one block from k/v [E, H, T, d]
     (the per-block K/V the prefill produces, reference scripts/tabicl_tpu_bucketed.py:659-692);
-    block_kv(block) returns the [E, H, capacity, d] views the query reads (:803-817)."""
+    block_kv(block) returns the [E, H, capacity, d] views the query reads (:803-817).
+
+    Each block records how many leading rows it holds (`filled[block]`, host ints: appends must extend
+    the filled prefix, row0 <= filled). A query without an explicit valid length attends over exactly
+    those rows, so the unwritten tail of the cache (torch.empty memory) is never read; querying a block
+    with no rows raises."""
 
     def __init__(self, estimators: int, blocks: int, heads: int, capacity: int, head_dim: int,
                  dtype: torch.dtype = torch.bfloat16, device: Union[str, torch.device] = "cuda"):
@@ -165,7 +194,28 @@ class IclKVCache:
         self.keys = torch.empty(shape, dtype=dtype, device=device)
         self.values = torch.empty(shape, dtype=dtype, device=device)
         self.capacity = capacity
-        self.length = torch.zeros(estimators, dtype=torch.int32, device=device)
+        self.filled = [0] * blocks
+        self._len_t: dict = {}  # filled length -> int32 device tensor handed to the kernels
+
+    def length(self, block: int) -> int:
+        """Rows [0, length) of `block` hold appended K/V."""
+        return self.filled[block]
+
+    def _record(self, block: int, row0: int, T: int) -> None:
+        if row0 > self.filled[block]:
+            raise ValueError(f"append at row {row0} would leave rows [{self.filled[block]}, {row0}) of block "
+                             f"{block} unwritten (appends must extend the filled prefix)")
+        self.filled[block] = max(self.filled[block], row0 + T)
+
+    def default_valid(self, block: int) -> Tensor:
+        """The filled length of `block` as the int32 device tensor the kernels take."""
+        n = self.filled[block]
+        if n <= 0:
+            raise ValueError(f"block {block} of the cache holds no rows: append before querying")
+        t = self._len_t.get(n)
+        if t is None:
+            t = self._len_t[n] = torch.full((1,), n, dtype=torch.int32, device=self.keys.device)
+        return t
 
     @property
     def shape(self):
@@ -186,11 +236,16 @@ class IclKVCache:
             raise ValueError(f"block {block} out of range [0, {NB})")
         _nat.require_device(k, v, self.keys)
         T = k.shape[2]
+        if row0 < 0 or row0 + T > cap:
+            raise ValueError(f"rows [{row0}, {row0 + T}) exceed the capacity {cap}")
+        if row0 > self.filled[block]:
+            self._record(block, row0, T)  # raises: the rows in between would stay unwritten
         kc = self.keys[:, block]
         vc = self.values[:, block]
         _nat.call("tabicl_icl_cache_append", kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), row0, cap,
                   k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), E, H, T, D,
                   _nat.dtype_code(k.dtype), _nat.stream_of(k))
+        self._record(block, row0, T)
 
     def append_projected(self, block: int, x: Tensor, in_proj_weight: Tensor, in_proj_bias: Optional[Tensor] = None,
                          row0: int = 0) -> None:
@@ -225,7 +280,8 @@ class IclKVCache:
         pre-norm): q = x W_q^T + b_q split into heads [E, H, Tq, D] (diff:308-312), q_transform applied
         to it if given (the caller's RoPE on q and SSMax scaling with n = the train length, modules of
         the upstream model: diff:312-313, 251-254), attention over block `block` of the cache with keys
-        >= valid_kv_len masked and q promoted to the cache dtype (diff:314-317), heads merged and the
+        >= valid_kv_len (default: the block's filled length) masked and q promoted to the cache dtype
+        (diff:314-317), heads merged and the
         out-projection applied (diff:383-393). Returns [E, Tq, width] in the promoted dtype; the residual and the
         feed-forward part of the block stay with the caller."""
         E, NB, H, cap, D = self.keys.shape
@@ -245,7 +301,10 @@ class IclKVCache:
         return self.keys[:, block], self.values[:, block]
 
     def query(self, block: int, q: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None) -> Tensor:
-        """Attention of q [E, H, Tq, D] over block `block` of the cache (keys >= valid_kv_len masked)."""
+        """Attention of q [E, H, Tq, D] over block `block` of the cache (keys >= valid_kv_len masked;
+        default: the block's filled length, never the unwritten rows past it)."""
+        if valid_kv_len is None:
+            valid_kv_len = self.default_valid(block)
         k, v = self.block_kv(block)
         # promote_types(q, cache) as in the reference's cached branch (results/tpu_patch.diff:314-317)
         attn_dtype = torch.promote_types(q.dtype, k.dtype)

@@ -1,381 +1,529 @@
-"""Small-head multi-head attention dispatch for MI355X (TabICLv2 column / row stages: 8 heads x 16
-dims; ICL stage: 8 heads x 64 dims over a cached K/V).
+"""Attention dispatch of TabICLv2 on MI355X: the plugin boundary between upstream tabicl's attention
+and the HIP kernels of libtabicl_attn.so.
 
-Drop-in for the reference's scripts/tabicl_tpu_mha.py: `install(attention_module, layers_module)`
-patches upstream tabicl's `multi_head_attention_forward` (and `sdpa_with_flattened_batch` for the
-cached-KV ICL attention) so that the attention itself runs in the HIP kernels of
-libtabicl_attn.so (tabicl_mi355_attn / tabicl_mi355_icl), keeping the reference's routing order:
+`install(attention_module, layers_module)` is the drop-in for the reference's install
+(scripts/tabicl_tpu_mha.py:293-393): it replaces upstream's `multi_head_attention_forward` (in both
+modules: layers.py imports it by name) and, for the 8 x 64 ICL attention, the module's
+`sdpa_with_flattened_batch` (whose Splash branch the reference hooks, results/tpu_patch.diff:261-281).
 
-  HXF      inference first-ISAB attention with the K projection folded into the queries
-           (folded_mab1 + hxf_attention; the K/V projection is never formed)   (reference :319-327)
-  HXQ      inference first-ISAB attention (few queries over the train rows, keys >= valid ignored):
-           q / packed K|V projections, SSMax on q, hxq_attention            (reference :328-342)
-  fallback upstream for cached_kv / need_kv / dropout / valid_kv_len / head dim > MAX_HEAD_DIM /
-           keys >= splash_min_kv / non-GPU tensors                            (reference :343-347)
-  PACKED   packed projections + pk_self_attention / pk_cross_attention (RoPE, scale and key-only
-           masks in the kernel)                                               (reference :350-371)
-  layouts  small_head_attention(impl) with impl from pick_impl(mode, Lq, Lk)  (reference :372-385)
-  ICL      sdpa_with_flattened_batch: cached-KV attention with d = 64 and no mask and no grad goes
-           to icl_sdpa (the Splash hook's contract)                           (diff :261-265)
+Routing contract kept from the reference (same knobs, same order, same fallbacks):
+  1. folded first-ISAB attention            TABICL_TPU_MHA_HXF=1      (reference :319-327)
+  2. few queries over the train rows        TABICL_TPU_MHA_HXQ=1      (reference :328-342)
+  3. upstream for: cached K/V (its attention reaches the ICL hook below), K/V requested back,
+     dropout in training, head dim > TABICL_TPU_MHA_MAX_HEAD_DIM, a registered flash fn,
+     keys >= the Splash threshold, tensors off the GPU                (reference :343-347)
+  4. packed projections + fused kernels     TABICL_TPU_MHA_PACKED=1 and the mode picks "pk"
+                                                                       (reference :350-371)
+  5. the mode's small-head implementation   TABICL_TPU_MHA=<mode>     (reference :372-385)
+The ICL hook sends every d = 64 attention without gradient, dropout or a non-key mask to the HIP
+kernel (the reference: keys >= TABICL_TPU_SPLASH_MIN_KV without a mask, diff:263-265).
 
-Knobs (same names as the reference where they select kernels):
-  TABICL_TPU_MHA=hxq|hxk|thl|std|pk|hx|auto|<rules>, TABICL_TPU_MHA_MAX_HEAD_DIM (32),
-  TABICL_TPU_MHA_PROJ=packed|split|views, TABICL_TPU_MHA_HXF=1, TABICL_TPU_MHA_HXQ=1, TABICL_TPU_MHA_PACKED=1,
-  TABICL_TPU_MHA_ANY_DEVICE=1 (CPU equivalence tests: lets the wrapper's torch layouts run on CPU;
-  the HIP kernels themselves never run on CPU tensors).
+Where this differs from the reference, and why:
+  * A key-validity length reaches routes 1, 2 and the ICL hook either as a tensor `valid_kv_len`
+    (what upstream passes on the reference's device) or as the additive train mask upstream builds
+    from it on every other device, this one included (diff:1526-1542: 0 below the train size,
+    finfo.min after). Both routes and the hook take any key-only additive mask; the kernels read a
+    mask of that prefix form as a valid length on the device and add any other mask term by term.
+  * The reference's torch layouts hxq / hxk / thl keep a wide axis on TPU lanes; on this GPU they
+    are the same math as upstream's own attention, so route 5 defers to upstream for every mode but
+    "pk" (small_head_attention keeps the names and a single torch implementation for them).
+
+Knobs (names of the reference): TABICL_TPU_MHA=hxq|hxk|thl|std|pk|hx|auto|<rules>,
+TABICL_TPU_MHA_MAX_HEAD_DIM (32), TABICL_TPU_MHA_PROJ (accepted; every form computes the same
+projections here), TABICL_TPU_MHA_HXF, _HXQ, _PACKED, TABICL_TPU_MHA_ANY_DEVICE (lets route 5's
+torch math run on CPU tensors in tests; the HIP kernels never run on CPU tensors), TABICL_MI355_ICL
+(default 1: install the ICL hook).
 """
 from __future__ import annotations
 
 import os
+from dataclasses import dataclass
 from typing import Optional
 
 import torch
 from torch import Tensor
 from torch.nn import functional as F
 
-_MODE = os.environ.get("TABICL_TPU_MHA", "").strip().lower()
-_MAX_HEAD_DIM = int(os.environ.get("TABICL_TPU_MHA_MAX_HEAD_DIM", "32") or 32)
-_ANY_DEVICE = os.environ.get("TABICL_TPU_MHA_ANY_DEVICE", "") == "1"
-_PROJ = os.environ.get("TABICL_TPU_MHA_PROJ", "packed").strip().lower()
-_HXQ = os.environ.get("TABICL_TPU_MHA_HXQ", "") == "1"
-_HXF = os.environ.get("TABICL_TPU_MHA_HXF", "") == "1"
-_PACKED = os.environ.get("TABICL_TPU_MHA_PACKED", "") == "1"
-_ICL = os.environ.get("TABICL_MI355_ICL", "1") == "1"
-_PK = None  # tabicl_mi355_attn, imported by install()
-_ICL_MOD = None  # tabicl_mi355_icl, imported by install()
+
+def _env_flag(name: str, default: str = "") -> bool:
+    return os.environ.get(name, default) == "1"
+
+
+@dataclass
+class Knobs:
+    mode: str = os.environ.get("TABICL_TPU_MHA", "").strip().lower()
+    max_head_dim: int = int(os.environ.get("TABICL_TPU_MHA_MAX_HEAD_DIM", "32") or 32)
+    proj: str = os.environ.get("TABICL_TPU_MHA_PROJ", "packed").strip().lower()
+    folded: bool = _env_flag("TABICL_TPU_MHA_HXF")
+    few_queries: bool = _env_flag("TABICL_TPU_MHA_HXQ")
+    packed: bool = _env_flag("TABICL_TPU_MHA_PACKED")
+    any_device: bool = _env_flag("TABICL_TPU_MHA_ANY_DEVICE")
+    icl_hook: bool = _env_flag("TABICL_MI355_ICL", "1")
+
+
+KNOBS = Knobs()
 _DEVICE = "cuda"  # torch device type of the HIP kernels (ROCm builds report "cuda")
+_PK = None  # tabicl_mi355_attn, bound by install() (imported eagerly, never while tracing)
+_ICL = None  # tabicl_mi355_icl, bound by install()
+
+_CLS_MAX_Q = 16  # query sets this short are the row stage's CLS tokens in the mode rules
 
 
-def in_projection(query: Tensor, key: Tensor, value: Tensor, w: Tensor, b: Optional[Tensor], proj: str):
-    """q, k, v projections (reference scripts/tabicl_tpu_mha.py:95-111): "views" computes one matmul per
-    distinct input and returns column views, "split" three matmuls on weight slices, otherwise
-    torch's packed in-projection."""
-    E = query.shape[-1]
-    if proj == "views":
-        if query is key and key is value:
-            return F.linear(query, w, b).chunk(3, dim=-1)
-        if key is value:
-            w_q, w_kv = w.split([E, 2 * E])
-            b_q, b_kv = (None, None) if b is None else b.split([E, 2 * E])
-            k_p, v_p = F.linear(key, w_kv, b_kv).chunk(2, dim=-1)
-            return F.linear(query, w_q, b_q), k_p, v_p
-        proj = "split"
-    if proj != "split":
-        return F._in_projection_packed(query, key, value, w, b)
-    w_q, w_k, w_v = w.split(E, dim=0)
-    b_q, b_k, b_v = (None, None, None) if b is None else b.split(E)
-    return F.linear(query, w_q, b_q), F.linear(key, w_k, b_k), F.linear(value, w_v, b_v)
+# ---------------------------------------------------------------------------------------------
+# mode rules (which calls the "pk" kernels serve)
+# ---------------------------------------------------------------------------------------------
+_DEFAULT_RULES = {"col1": "hxq", "col2": "hxk", "row": "thl", "cls": "hxq"}
+_SINGLE_IMPLS = ("hxq", "hxk", "thl", "std")
 
 
-def _head_mask(h: int, E: int, dtype: torch.dtype, device) -> Tensor:
-    """[h, E] 0/1 selector of each head's d = E/h columns."""
-    return torch.repeat_interleave(torch.eye(h, dtype=dtype, device=device), E // h, dim=1)
-
-
-def _parse_rules(mode: str) -> dict:
-    rules = {"col1": "hxq", "col2": "hxk", "row": "thl", "cls": "hxq"}
-    for part in mode.split(","):
-        if "=" in part:
-            k, v = part.split("=", 1)
-            rules[k.strip()] = v.strip()
-    return rules
+def _rule_table(mode: str) -> dict:
+    table = dict(_DEFAULT_RULES)
+    for item in mode.split(","):
+        name, sep, impl = item.partition("=")
+        if sep:
+            table[name.strip()] = impl.strip()
+    return table
 
 
 def pick_impl(mode: str, Lq: int, Lk: int) -> str:
-    """Layout choice (reference :129-141): pk keeps CLS (Lq <= 16) on the torch path; hx picks
-    query- or key-expansion by shape; rules map col1 (Lq < Lk), col2 (Lq > Lk), row (Lq == Lk),
-    cls (Lq <= 16)."""
+    """Small-head implementation of a call with Lq queries and Lk keys under a TABICL_TPU_MHA mode
+    (reference scripts/tabicl_tpu_mha.py:129-141): "pk" serves everything but CLS-sized query sets;
+    a single impl name applies to all; "hx" picks by the longer side; otherwise per-role rules
+    (cls: Lq <= 16, row: Lq == Lk, col1: Lq < Lk, col2: Lq > Lk)."""
     if mode == "pk":
-        return "std" if Lq <= 16 else "pk"
-    if mode in ("hxq", "hxk", "thl", "std"):
+        return "pk" if Lq > _CLS_MAX_Q else "std"
+    if mode in _SINGLE_IMPLS:
         return mode
     if mode == "hx":
-        return "hxq" if Lq <= Lk else "hxk"
-    rules = _parse_rules(mode if "=" in mode else "")
-    if Lq <= 16:
-        return rules["cls"]
-    if Lq == Lk:
-        return rules["row"]
-    return rules["col1"] if Lq < Lk else rules["col2"]
+        return "hxk" if Lq > Lk else "hxq"
+    table = _rule_table(mode) if "=" in mode else dict(_DEFAULT_RULES)
+    role = "cls" if Lq <= _CLS_MAX_Q else "row" if Lq == Lk else "col1" if Lq < Lk else "col2"
+    return table[role]
 
 
-def small_head_attention(q: Tensor, k: Tensor, v: Tensor, h: int, mask: Optional[Tensor], impl: str) -> Tensor:
-    """q [..., Lq, E] (already scaled), k / v [..., Lk, E]; additive mask broadcastable to
-    [..., h|1, Lq|1, Lk] (reference :144-198). All impls compute per-head softmax(q_g k_g^T + mask) v_g
-    with an fp32 softmax; "pk" runs the HIP kernel for key-only masks and otherwise uses "std"."""
-    Lq, E = q.shape[-2], q.shape[-1]
-    Lk = k.shape[-2]
-    d = E // h
-    if impl == "pk":
-        if _PK is None or q.device.type != _DEVICE:
-            return small_head_attention(q, k, v, h, mask, "std")
-        kb = None
-        if mask is not None:
-            if mask.shape[-3] != 1 or mask.shape[-2] != 1:
-                return small_head_attention(q, k, v, h, mask, "std")
-            kb = mask.reshape(*mask.shape[:-3], Lk)
-        if not _PK.supported(Lq, Lk, E, h, q.dtype):
-            return small_head_attention(q, k, v, h, mask, "std")
-        return _PK.hx_attention(q, k, v, h, kb)
-    if impl == "hxq":  # query-head expansion: row block g of the expanded queries sees only head g
-        M = _head_mask(h, E, q.dtype, q.device)
-        q_exp = (q.unsqueeze(-3) * M[:, None, :]).reshape(*q.shape[:-2], h * Lq, E)
-        s = (q_exp @ k.transpose(-2, -1)).float().reshape(*q.shape[:-2], h, Lq, Lk)
-        if mask is not None:
-            s = s + mask
-        p = torch.softmax(s, dim=-1).to(v.dtype).reshape(*q.shape[:-2], h * Lq, Lk)
-        o_full = (p @ v).reshape(*q.shape[:-2], h, Lq, E)
-        return (o_full * M.to(o_full.dtype)[:, None, :]).sum(dim=-3)
-    if impl == "hxk":  # key-head expansion: column block g of the scores belongs to head g
-        M = _head_mask(h, E, k.dtype, k.device)
-        k_exp = (k.unsqueeze(-3) * M[:, None, :]).reshape(*k.shape[:-2], h * Lk, E)
-        v_exp = (v.unsqueeze(-3) * M.to(v.dtype)[:, None, :]).reshape(*v.shape[:-2], h * Lk, E)
-        s = (q @ k_exp.transpose(-2, -1)).float().reshape(*q.shape[:-2], Lq, h, Lk)
-        if mask is not None:
-            s = s + mask.transpose(-3, -2)
-        p = torch.softmax(s, dim=-1).to(v.dtype).reshape(*q.shape[:-2], Lq, h * Lk)
-        return p @ v_exp
-    if impl == "thl":  # transposed head layout: sequence on the last axis
-        qt = q.transpose(-2, -1).reshape(*q.shape[:-2], h, d, Lq)
-        kt = k.transpose(-2, -1).reshape(*k.shape[:-2], h, d, Lk)
-        vt = v.transpose(-2, -1).reshape(*v.shape[:-2], h, d, Lk)
-        s = (qt.transpose(-2, -1) @ kt).float()
-        if mask is not None:
-            s = s + mask
-        p = torch.softmax(s, dim=-1).to(v.dtype)
-        return (vt @ p.transpose(-2, -1)).reshape(*q.shape[:-2], E, Lq).transpose(-2, -1)
-    if impl == "std":  # head split, matmul, fp32 softmax, matmul
-        qh = q.reshape(*q.shape[:-1], h, d).transpose(-3, -2)
-        kh = k.reshape(*k.shape[:-1], h, d).transpose(-3, -2)
-        vh = v.reshape(*v.shape[:-1], h, d).transpose(-3, -2)
-        s = (qh @ kh.transpose(-2, -1)).float()
-        if mask is not None:
-            s = s + mask
-        p = torch.softmax(s, dim=-1).to(vh.dtype)
-        return (p @ vh).transpose(-3, -2).reshape(*q.shape[:-1], E)
-    raise ValueError(f"unknown small-head attention impl {impl!r}")
+# ---------------------------------------------------------------------------------------------
+# masks
+# ---------------------------------------------------------------------------------------------
+def _as_rank(m: Tensor, nb: int, Lq: int, Lk: int) -> Optional[Tensor]:
+    """attn_mask as a view of rank nb + 3 broadcastable to (*batch, h, Lq, Lk) under upstream's rules
+    (results/tpu_patch.diff:327-346), or None if upstream would reject it."""
+    rank = nb + 3
+    if m.dim() == 2:
+        return m.view(*([1] * (rank - 2)), Lq, Lk) if tuple(m.shape) == (Lq, Lk) else None
+    if m.dim() == 4 and nb != 1 and tuple(m.shape[:3]) == (1, 1, 1) and m.shape[-1] == Lk:
+        return m.view(*([1] * (rank - 1)), Lk)
+    if m.dim() == rank:
+        return m
+    return None
 
 
-def rope_merged(rope, x: Tensor, h: int) -> Tensor:  # noqa: ANN001
-    """RotaryEmbedding.rotate_queries_or_keys for merged-head x [..., L, E]: x*cos + R(x)*sin per
-    head, R the signed rotate-half (pairs or halves), computed in fp32 and cast back
-    (reference :201-248, "roll" form)."""
-    L, E = x.shape[-2], x.shape[-1]
-    import tabicl_mi355_attn as pk
-
-    cos, sin, code, half, rot = pk.rope_tables(rope, L, E, h, x.device)
-    if code == 0:
-        return x
-    d = E // h
-    xf = x.float().reshape(*x.shape[:-1], h, d)
-    rx = torch.zeros_like(xf)
-    if code == 1:
-        rx[..., 0:rot:2] = -xf[..., 1:rot:2]
-        rx[..., 1:rot:2] = xf[..., 0:rot:2]
-    else:
-        rx[..., :half] = -xf[..., half:rot]
-        rx[..., half:rot] = xf[..., :half]
-    out = xf.reshape(x.shape) * cos + rx.reshape(x.shape) * sin
-    return out.to(x.dtype)
+def _kpm_as_rank(kp: Tensor, batch_shape, nb: int, Lk: int) -> Optional[Tensor]:
+    """key_padding_mask as a view of rank nb + 3 (diff:352-366), or None if upstream would reject it."""
+    if kp.shape[-1] != Lk or not (tuple(kp.shape) == (1, Lk) or kp.dim() == nb + 1):
+        return None
+    lead = tuple(kp.shape[:-1])
+    if kp.dim() == 2 and nb != 1:  # one shared row
+        return kp.view(*([1] * nb), 1, 1, Lk)
+    if any(g != 1 and g != b for g, b in zip(lead, batch_shape)):
+        return None
+    return kp.view(*lead, 1, 1, Lk)
 
 
 def _combined_mask(attn_mask, key_padding_mask, batch_shape, nh: int, Lq: int, Lk: int, qdtype):  # noqa: ANN001
-    """Upstream mask processing -> additive mask broadcastable to (*batch, nh, Lq, Lk); None if absent;
-    False for bool masks and shapes that do not broadcast (caller falls back) (reference :251-290)."""
+    """attn_mask and key_padding_mask as one additive fp32 mask broadcastable to (*batch, nh, Lq, Lk)
+    (reference scripts/tabicl_tpu_mha.py:251-290, following upstream's mask processing,
+    results/tpu_patch.diff:327-371). None when there is no mask; False when a mask is boolean or of a
+    shape upstream rejects (the caller then defers to upstream, which handles or reports it). Like
+    upstream the sum is taken in the query dtype."""
     nb = len(batch_shape)
     full = (*batch_shape, nh, Lq, Lk)
-    m = None
+    terms = []
     if attn_mask is not None:
         if attn_mask.dtype == torch.bool:
             return False
-        if attn_mask.dim() == 2:
-            if tuple(attn_mask.shape) != (Lq, Lk):
-                return False
-            m = attn_mask.view(*([1] * nb), 1, Lq, Lk)
-        elif attn_mask.dim() == 4 and nb != 1 and tuple(attn_mask.shape[:3]) == (1, 1, 1) and attn_mask.shape[-1] == Lk:
-            m = attn_mask.view(*([1] * nb), 1, 1, Lk)
-        elif attn_mask.dim() == len(full):
-            if any(g not in (1, e) for g, e in zip(attn_mask.shape, full)):
-                return False
-            m = attn_mask
-        else:
+        am = _as_rank(attn_mask, nb, Lq, Lk)
+        if am is None or any(g != 1 and g != e for g, e in zip(am.shape, full)):
             return False
+        terms.append(am)
     if key_padding_mask is not None:
-        kp = key_padding_mask
-        if kp.dtype == torch.bool:
+        if key_padding_mask.dtype == torch.bool:
             return False
-        if not (tuple(kp.shape) == (1, Lk) or (kp.dim() == nb + 1 and kp.shape[-1] == Lk)):
+        kp = _kpm_as_rank(key_padding_mask, batch_shape, nb, Lk)
+        if kp is None:
             return False
-        if any(g not in (1, e) for g, e in zip(kp.shape[:-1], batch_shape)):
-            return False
-        kpm = kp.view(*([1] * nb), 1, 1, Lk) if (kp.dim() == 2 and nb != 1) else kp.view(*kp.shape[:-1], 1, 1, Lk)
-        m = kpm if m is None else m + kpm
-    if m is not None:
-        if m.dtype != qdtype:
-            m = m.to(dtype=qdtype)
-        m = m.float()
-    return m
-
-
-def folded_mab1(query: Tensor, key: Tensor, valid_kv_len: Tensor, num_heads: int, in_proj_weight: Tensor,
-                in_proj_bias: Optional[Tensor], ssmax_layer=None, src_len_override=None, pk=None) -> Optional[Tensor]:  # noqa: ANN001
-    """Folded first-ISAB attention (reference scripts/tabicl_tpu_mha.py:60-92): softmax(q_g K_g^T) V_g
-    for every head, merged [..., Lq, E] before the output projection, with K = key W_k^T + b_k and
-    V = key W_v^T + b_v never formed: U = softmax(Qf key^T) key with Qf_g = q_g W_k,g (q pre-scaled;
-    q_g . b_k,g is constant per query row, so softmax drops it), then O_g = U_g W_v,g^T + b_v,g (rows
-    of P sum to 1). None when the kernel does not apply."""
-    pk = pk if pk is not None else _PK
-    E = query.shape[-1]
-    hd = E // num_heads
-    qsrc = query
-    while qsrc.dim() > 2 and qsrc.stride(0) == 0:  # inducing points expanded over the batch: fold once
-        qsrc = qsrc[0]
-    Lq = qsrc.shape[-2]
-    nb_q = qsrc.shape[:-2].numel()
-    nb_k = key.shape[:-2].numel()
-    if pk is None or nb_q not in (1, nb_k) or not pk.hxf_supported(num_heads * Lq, key.shape[-2], E):
+        terms.append(kp)
+    if not terms:
         return None
-    w_q, w_k, w_v = in_proj_weight.split([E, E, E])
-    b_q, _b_k, b_v = (None, None, None) if in_proj_bias is None else in_proj_bias.split([E, E, E])
-    q = F.linear(qsrc, w_q, b_q)
+    m = terms[0] if len(terms) == 1 else terms[0] + terms[1]
+    return m.to(dtype=qdtype).float() if m.dtype != qdtype else m.float()
+
+
+def _key_only(mask: Optional[Tensor], Lk: int) -> Optional[Tensor]:
+    """A combined mask that varies over keys only, as [*lead, Lk] (lead dims 1 or the batch's); None
+    for no mask; False if it varies over heads or queries."""
+    if mask is None:
+        return None
+    if mask.shape[-3] != 1 or mask.shape[-2] != 1:
+        return False
+    return mask.reshape(*mask.shape[:-3], Lk)
+
+
+# ---------------------------------------------------------------------------------------------
+# the small-head implementations (route 5)
+# ---------------------------------------------------------------------------------------------
+def _heads(x: Tensor, h: int) -> Tensor:
+    """[..., L, E] -> [..., h, L, E / h]."""
+    return x.unflatten(-1, (h, x.shape[-1] // h)).transpose(-3, -2)
+
+
+def _merge(x: Tensor) -> Tensor:
+    """[..., h, L, d] -> [..., L, h d]."""
+    return x.transpose(-3, -2).flatten(-2)
+
+
+def small_head_attention(q: Tensor, k: Tensor, v: Tensor, h: int, mask: Optional[Tensor], impl: str) -> Tensor:
+    """Per-head softmax(q_g k_g^T + mask) v_g for merged q [..., Lq, E] (already scaled), k / v
+    [..., Lk, E] and an additive mask broadcastable to [..., h|1, Lq|1, Lk]; fp32 scores and softmax,
+    probabilities in v's dtype (reference scripts/tabicl_tpu_mha.py:144-198). impl "pk" runs the HIP
+    hx kernel when the mask varies over keys only (reference :177-188), otherwise and for
+    "std" / "hxq" / "hxk" / "thl" (the reference's TPU layouts of the same math) one torch form."""
+    if impl == "pk":
+        if _PK is not None and q.device.type == _DEVICE:
+            Lq, E, Lk = q.shape[-2], q.shape[-1], k.shape[-2]
+            kb = _key_only(mask, Lk)
+            if kb is not False and _PK.supported(Lq, Lk, E, h, q.dtype):
+                return _PK.hx_attention(q, k, v, h, kb)
+        impl = "std"
+    if impl not in _SINGLE_IMPLS:
+        raise ValueError(f"unknown small-head attention impl {impl!r}")
+    s = torch.matmul(_heads(q, h), _heads(k, h).transpose(-2, -1).contiguous()).float()
+    if mask is not None:
+        s = s + mask
+    p = torch.softmax(s, dim=-1).to(v.dtype)
+    return _merge(torch.matmul(p, _heads(v, h).contiguous()))
+
+
+def _rotate_merged(rope, x: Tensor, h: int) -> Tensor:  # noqa: ANN001
+    """The module's own RoPE (rotate_queries_or_keys on head-split [..., h, L, d]) for merged x."""
+    return _merge(rope.rotate_queries_or_keys(_heads(x, h)))
+
+
+# ---------------------------------------------------------------------------------------------
+# projections
+# ---------------------------------------------------------------------------------------------
+def _linear_rows(x: Tensor, w: Tensor, b: Optional[Tensor], rows: slice) -> Tensor:
+    return F.linear(x, w[rows], None if b is None else b[rows])
+
+
+def in_projection(query: Tensor, key: Tensor, value: Tensor, w: Tensor, b: Optional[Tensor],
+                  proj: str = "packed"):
+    """q, k, v projections with the in-projection weight [3E, E] (reference scripts/tabicl_tpu_mha.py:95-111):
+    one GEMM per distinct input (self attention: one [.., 3E] product; shared key/value: [.., E] and
+    [.., 2E]), column views of the results. `proj` is accepted for the reference's knob; every form
+    gives the same projections."""
+    E = query.shape[-1]
+    if query is key and key is value:
+        return F.linear(query, w, b).chunk(3, dim=-1)
+    q = _linear_rows(query, w, b, slice(0, E))
+    if key is value:
+        kv = _linear_rows(key, w, b, slice(E, 3 * E))
+        return (q, *kv.chunk(2, dim=-1))
+    return q, _linear_rows(key, w, b, slice(E, 2 * E)), _linear_rows(value, w, b, slice(2 * E, 3 * E))
+
+
+def _ssmax(ssmax_layer, q: Tensor, h: int, n) -> Tensor:  # noqa: ANN001
+    """upstream's SSMax on merged q: the layer takes head-split [B', h, L, d] and the source length n
+    (results/tpu_patch.diff:251-254)."""
+    qh = _heads(q, h)
+    lead = qh.shape[:-3]
+    return _merge(ssmax_layer(qh.reshape(-1, *qh.shape[-3:]), n).reshape(*lead, *qh.shape[-3:]))
+
+
+# ---------------------------------------------------------------------------------------------
+# folded first-ISAB attention (route 1)
+# ---------------------------------------------------------------------------------------------
+def _distinct_rows(x: Tensor) -> Tensor:
+    """Strip leading dims along which x is an expanded view (stride 0): the inducing points are one
+    set broadcast over the batch, so they are folded once."""
+    while x.dim() > 2 and x.stride(0) == 0:
+        x = x[0]
+    return x
+
+
+def folded_mab1(query: Tensor, key: Tensor, valid_kv_len: Optional[Tensor], num_heads: int, in_proj_weight: Tensor,
+                in_proj_bias: Optional[Tensor], ssmax_layer=None, src_len_override=None, pk=None,  # noqa: ANN001
+                key_bias: Optional[Tensor] = None) -> Optional[Tensor]:
+    """Merged per-head softmax(q_g K_g^T) V_g (before the output projection) of the first ISAB
+    attention, with K = key W_k^T + b_k and V = key W_v^T + b_v never formed (reference
+    scripts/tabicl_tpu_mha.py:60-92). Per head g: q_g K_g^T = (q_g W_k,g) key^T + q_g . b_k,g, and the
+    second term is the same for every key of a query row, so it leaves the softmax unchanged; the
+    probabilities sum to 1, so P V_g = (P key) W_v,g^T + b_v,g. The kernel computes U = softmax(Qf key^T)
+    key over the raw rows with Qf = [q_g W_k,g]_g (hq = h Lq folded queries of width E). Keys past
+    valid_kv_len, or masked by the additive key_bias, are excluded. None when the kernel does not apply."""
+    kern = _PK if pk is None else pk
+    E = query.shape[-1]
+    d = E // num_heads
+    ind = _distinct_rows(query)
+    Lq = ind.shape[-2]
+    n_ind = ind.shape[:-2].numel()
+    if kern is None or n_ind not in (1, key.shape[:-2].numel()) or not kern.hxf_supported(num_heads * Lq, key.shape[-2], E):
+        return None
+    w_q, w_k, w_v = in_proj_weight.chunk(3)
+    b_q = None if in_proj_bias is None else in_proj_bias[:E]
+    b_v = None if in_proj_bias is None else in_proj_bias[2 * E:]
+    q = F.linear(ind, w_q, b_q)
     if ssmax_layer is not None:
         q = _ssmax(ssmax_layer, q, num_heads, src_len_override if src_len_override is not None else valid_kv_len)
-    q = q * (hd ** -0.5)
-    # Qf[.., g, i, :] = q[.., i, g, :] @ W_k,g  ([hd] x [hd, E]); batched over heads, right operand contiguous
-    qh = q.unflatten(-1, (num_heads, hd)).transpose(-3, -2)
-    qf = torch.matmul(qh, w_k.reshape(num_heads, hd, E).contiguous())
-    u = pk.hxf_attention(qf.flatten(-3, -2), key, valid_kv_len)  # [*key_lead, h * Lq, E]
-    # O[.., i, g, :] = U[.., g, i, :] @ W_v,g^T
-    uh = u.unflatten(-2, (num_heads, Lq))
-    o = torch.matmul(uh, w_v.reshape(num_heads, hd, E).transpose(-1, -2).contiguous().to(uh.dtype))
-    o = o.transpose(-3, -2).flatten(-2, -1)
-    return o + b_v if b_v is not None else o
+    q = q * d ** -0.5
+    # Qf[.., g, i, :] = q[.., i, g d:(g + 1) d] @ W_k[g d:(g + 1) d, :]   (both operands contiguous)
+    qf = torch.matmul(_heads(q, num_heads).contiguous(), w_k.reshape(num_heads, d, E).contiguous())
+    u = kern.hxf_attention(qf.flatten(-3, -2), key, valid_kv_len, key_bias)  # [*key lead, h Lq, E]
+    # O[.., i, g d:(g + 1) d] = U[.., g, i, :] @ W_v[g d:(g + 1) d, :]^T
+    w_vt = w_v.reshape(num_heads, d, E).transpose(-1, -2).contiguous().to(u.dtype)
+    o = _merge(torch.matmul(u.unflatten(-2, (num_heads, Lq)), w_vt))
+    return o if b_v is None else o + b_v
 
 
-def _ssmax(ssmax_layer, q: Tensor, num_heads: int, n) -> Tensor:  # noqa: ANN001
-    hd = q.shape[-1] // num_heads
-    qh = q.unflatten(-1, (num_heads, hd)).transpose(-3, -2)
-    return ssmax_layer(qh.reshape(-1, *qh.shape[-3:]), n).view(qh.shape).transpose(-3, -2).flatten(-2, -1)
+# ---------------------------------------------------------------------------------------------
+# one call of multi_head_attention_forward
+# ---------------------------------------------------------------------------------------------
+class _Call:
+    """The arguments of one multi_head_attention_forward call plus what routing needs from them."""
+
+    def __init__(self, query, num_heads, in_proj_weight, in_proj_bias, dropout_p, out_proj_weight,  # noqa: ANN001
+                 out_proj_bias, key, value, cached_kv, training, key_padding_mask, attn_mask, rope,
+                 ssmax_layer, need_kv, src_len_override, valid_kv_len):
+        self.query, self.key, self.value = query, key, value
+        self.h = num_heads
+        self.w, self.b, self.wo, self.bo = in_proj_weight, in_proj_bias, out_proj_weight, out_proj_bias
+        self.dropout_p, self.training = dropout_p, training
+        self.cached_kv, self.need_kv = cached_kv, need_kv
+        self.key_padding_mask, self.attn_mask = key_padding_mask, attn_mask
+        self.rope, self.ssmax, self.src_len_override, self.valid_kv_len = rope, ssmax_layer, src_len_override, valid_kv_len
+        self.E = query.shape[-1]
+        self.d = self.E // num_heads
+        self.batch_shape = tuple(query.shape[:-2])
+        self.Lq = query.shape[-2]
+        self.Lk = None if key is None else key.shape[-2]
+        self.on_gpu = query.device.type == _DEVICE
+        self._mask = ...
+
+    def mask(self):
+        """Combined additive mask (see _combined_mask), computed once."""
+        if self._mask is ...:
+            if self.Lk is None:
+                self._mask = False
+            else:
+                self._mask = _combined_mask(self.attn_mask, self.key_padding_mask, self.batch_shape, self.h,
+                                            self.Lq, self.Lk, self.query.dtype)
+        return self._mask
+
+    def key_constraint(self):
+        """(valid length tensor or None, key-only mask [*lead, Lk] or None), or None when the call's keys
+        are not constrained by a tensor length or a key-only additive mask (routes 1-2 need one)."""
+        if self.attn_mask is None and self.key_padding_mask is None:
+            return (self.valid_kv_len, None) if isinstance(self.valid_kv_len, Tensor) else None
+        if self.valid_kv_len is not None and not isinstance(self.valid_kv_len, Tensor):
+            return None
+        m = self.mask()
+        if m is None or m is False:
+            return None
+        kb = _key_only(m, self.Lk)
+        return None if kb is False else (self.valid_kv_len, kb)
+
+    def inducing_over_rows(self, max_head_dim: int) -> bool:
+        """The shape of the inference first-ISAB attention: no grad, no cache, one key/value input, no
+        RoPE, small heads, on the GPU."""
+        return (not torch.is_grad_enabled() and self.cached_kv is None and not self.need_kv
+                and self.key is not None and self.key is self.value and self.rope is None
+                and self.d <= max_head_dim and self.on_gpu)
+
+    def ssmax_n(self, default):  # noqa: ANN001
+        return self.src_len_override if self.src_len_override is not None else default
+
+    def out(self, merged: Tensor) -> Tensor:
+        return F.linear(merged, self.wo, self.bo)
+
+
+def _route_folded(c: _Call, knobs: Knobs) -> Optional[Tensor]:
+    if not (knobs.folded and c.inducing_over_rows(knobs.max_head_dim)):
+        return None
+    kc = c.key_constraint()
+    if kc is None or (isinstance(c.src_len_override, Tensor) and c.src_len_override.numel() != 1):
+        return None
+    valid, kb = kc
+    if valid is not None and valid.numel() != 1:
+        return None
+    o = folded_mab1(c.query, c.key, valid, c.h, c.w, c.b, c.ssmax, c.src_len_override, key_bias=kb)
+    return None if o is None else c.out(o)
+
+
+def _route_few_queries(c: _Call, knobs: Knobs) -> Optional[Tensor]:
+    if not (knobs.few_queries and c.inducing_over_rows(knobs.max_head_dim)):
+        return None
+    kc = c.key_constraint()
+    if kc is None or not _PK.hxq_supported(c.Lq, c.Lk, c.E, c.h, c.query.dtype):
+        return None
+    valid, kb = kc
+    q = _linear_rows(c.query, c.w, c.b, slice(0, c.E))
+    kv = _linear_rows(c.key, c.w, c.b, slice(c.E, 3 * c.E))  # [.., Lk, 2E]: K columns [0, E), V [E, 2E)
+    if c.ssmax is not None:
+        q = _ssmax(c.ssmax, q, c.h, c.ssmax_n(valid if valid is not None else c.Lk))
+    return c.out(_PK.hxq_attention(q * c.d ** -0.5, kv, valid, c.h, kb))
+
+
+def _defers(c: _Call, knobs: Knobs, att_module, splash_min_kv) -> bool:  # noqa: ANN001
+    return ((not c.on_gpu and not knobs.any_device) or c.cached_kv is not None or c.need_kv
+            or c.key is None or c.value is None or c.d > knobs.max_head_dim
+            or (c.training and c.dropout_p > 0.0) or c.valid_kv_len is not None
+            or getattr(att_module, "_tpu_flash_attention_fn", None) is not None
+            or c.Lk >= splash_min_kv())
+
+
+def _route_packed(c: _Call, knobs: Knobs, mode: str) -> Optional[Tensor]:
+    if not (knobs.packed and c.on_gpu and c.key is c.value and pick_impl(mode, c.Lq, c.Lk) == "pk"):
+        return None
+    self_attn = c.query is c.key
+    if not _PK.packed_supported(c.Lq, c.Lk, c.E, c.h, self_attn, c.query.dtype):
+        return None
+    m = c.mask()
+    kb = None if m is None or m is False else _key_only(m, c.Lk)
+    if m is False or kb is False:
+        return None
+    if self_attn:
+        qkv = F.linear(c.query, c.w, c.b)
+        return c.out(_PK.pk_self_attention(qkv, c.h, kb, c.rope, c.d ** -0.5))
+    q = _linear_rows(c.query, c.w, c.b, slice(0, c.E))
+    kv = _linear_rows(c.key, c.w, c.b, slice(c.E, 3 * c.E))
+    if c.ssmax is not None:
+        q = _ssmax(c.ssmax, q, c.h, c.ssmax_n(c.Lk))
+    return c.out(_PK.pk_cross_attention(q, kv, c.h, kb, c.rope, c.d ** -0.5))
+
+
+def _route_hx(c: _Call, knobs: Knobs) -> Optional[Tensor]:
+    """Mode "pk" without the packed route: projections, RoPE and SSMax in torch, the hx kernel."""
+    m = c.mask()
+    if m is False:
+        return None
+    q, k, v = in_projection(c.query, c.key, c.value, c.w, c.b, knobs.proj)
+    if c.rope is not None:
+        q, k = _rotate_merged(c.rope, q, c.h), _rotate_merged(c.rope, k, c.h)
+    if c.ssmax is not None:
+        q = _ssmax(c.ssmax, q, c.h, c.ssmax_n(c.Lk))
+    return c.out(small_head_attention(q * c.d ** -0.5, k, v, c.h, m, "pk"))
 
 
 def install(att_module, layers_module=None, mode: Optional[str] = None, proj: Optional[str] = None) -> bool:  # noqa: ANN001
-    """Patch `multi_head_attention_forward` in att_module (and layers_module, which imports it by
-    name) and `sdpa_with_flattened_batch` for the ICL path (reference :293-393)."""
-    mode = (_MODE if mode is None else mode).strip().lower()
-    proj = (_PROJ if proj is None else proj).strip().lower()
-    if not mode or mode in ("0", "off", "none"):
+    """Patch `multi_head_attention_forward` in att_module (and layers_module, which imports it by name)
+    and install the ICL hook on att_module.sdpa_with_flattened_batch. Same signature, knobs and return
+    value as the reference's install (scripts/tabicl_tpu_mha.py:293-393): False when the mode is off,
+    True when installed (idempotent)."""
+    knobs = Knobs(**{**KNOBS.__dict__})
+    knobs.mode = (knobs.mode if mode is None else mode).strip().lower()
+    knobs.proj = (knobs.proj if proj is None else proj).strip().lower()
+    if knobs.mode in ("", "0", "off", "none"):
         return False
     if getattr(att_module, "_mi355_mha_installed", False):
         return True
-    global _PK, _ICL_MOD
-    import tabicl_mi355_attn as _pk_mod  # registers the tabicl_pk:: ops eagerly (never while tracing)
-    import tabicl_mi355_icl as _icl_mod
+    global _PK, _ICL
+    import tabicl_mi355_attn as pk_mod  # registers the tabicl_pk:: ops now, never while tracing
+    import tabicl_mi355_icl as icl_mod  # registers tabicl::icl_cached_attn
 
-    _PK, _ICL_MOD = _pk_mod, _icl_mod
-    orig = att_module.multi_head_attention_forward
-    splash_min_kv = getattr(att_module, "_tpu_splash_min_kv", lambda: int(os.environ.get("TABICL_TPU_SPLASH_MIN_KV", "16384")))
+    _PK = pk_mod if _PK is None else _PK
+    _ICL = icl_mod if _ICL is None else _ICL
+    upstream = att_module.multi_head_attention_forward
+    splash_min_kv = getattr(att_module, "_tpu_splash_min_kv",
+                            lambda: int(os.environ.get("TABICL_TPU_SPLASH_MIN_KV", "16384")))
 
     def multi_head_attention_forward(query, num_heads, in_proj_weight, in_proj_bias, dropout_p,  # noqa: ANN001
                                      out_proj_weight, out_proj_bias, key=None, value=None, cached_kv=None,
                                      training=True, key_padding_mask=None, attn_mask=None, rope=None,
                                      ssmax_layer=None, need_kv=False, src_len_override=None, valid_kv_len=None):
-        def _orig():
-            return orig(query, num_heads, in_proj_weight, in_proj_bias, dropout_p, out_proj_weight, out_proj_bias,
+        c = _Call(query, num_heads, in_proj_weight, in_proj_bias, dropout_p, out_proj_weight, out_proj_bias, key,
+                  value, cached_kv, training, key_padding_mask, attn_mask, rope, ssmax_layer, need_kv,
+                  src_len_override, valid_kv_len)
+        out = _route_folded(c, knobs)
+        if out is None:
+            out = _route_few_queries(c, knobs)
+        if out is None and not _defers(c, knobs, att_module, splash_min_kv):
+            out = _route_packed(c, knobs, knobs.mode)
+            if out is None and c.on_gpu and pick_impl(knobs.mode, c.Lq, c.Lk) == "pk":
+                out = _route_hx(c, knobs)
+        if out is not None:
+            return out
+        return upstream(query, num_heads, in_proj_weight, in_proj_bias, dropout_p, out_proj_weight, out_proj_bias,
                         key=key, value=value, cached_kv=cached_kv, training=training,
                         key_padding_mask=key_padding_mask, attn_mask=attn_mask, rope=rope, ssmax_layer=ssmax_layer,
                         need_kv=need_kv, src_len_override=src_len_override, valid_kv_len=valid_kv_len)
 
-        E = query.shape[-1]
-        hd = E // num_heads
-        on_gpu = query.device.type == _DEVICE
-        if (_HXF and isinstance(valid_kv_len, Tensor) and not torch.is_grad_enabled() and cached_kv is None
-                and not need_kv and key is not None and key is value and rope is None and attn_mask is None
-                and key_padding_mask is None and hd <= _MAX_HEAD_DIM and on_gpu
-                and (not isinstance(src_len_override, Tensor) or src_len_override.numel() == 1)):
-            o = folded_mab1(query, key, valid_kv_len, num_heads, in_proj_weight, in_proj_bias, ssmax_layer,
-                            src_len_override)
-            if o is not None:
-                return F.linear(o, out_proj_weight, out_proj_bias)
-        if (_HXQ and isinstance(valid_kv_len, Tensor) and not torch.is_grad_enabled() and cached_kv is None
-                and not need_kv and key is not None and key is value and rope is None and attn_mask is None
-                and key_padding_mask is None and hd <= _MAX_HEAD_DIM and on_gpu
-                and _PK.hxq_supported(query.shape[-2], key.shape[-2], E, num_heads, query.dtype)):
-            w_q, w_kv = in_proj_weight.split([E, 2 * E])
-            b_q, b_kv = (None, None) if in_proj_bias is None else in_proj_bias.split([E, 2 * E])
-            q = F.linear(query, w_q, b_q)
-            kv = F.linear(key, w_kv, b_kv)  # [.., Lk, 2E]: K columns [0, E), V columns [E, 2E)
-            if ssmax_layer is not None:
-                q = _ssmax(ssmax_layer, q, num_heads, src_len_override if src_len_override is not None else valid_kv_len)
-            out = _PK.hxq_attention(q * (hd ** -0.5), kv, valid_kv_len, num_heads)
-            return F.linear(out, out_proj_weight, out_proj_bias)
-        if ((not on_gpu and not _ANY_DEVICE) or cached_kv is not None or need_kv or key is None or value is None
-                or hd > _MAX_HEAD_DIM or (training and dropout_p > 0.0) or valid_kv_len is not None
-                or getattr(att_module, "_tpu_flash_attention_fn", None) is not None
-                or key.shape[-2] >= splash_min_kv()):
-            return _orig()
-        *batch_shape, Lq, _ = query.shape
-        Lk = key.shape[-2]
-        if _PACKED and on_gpu and pick_impl(mode, Lq, Lk) == "pk" and key is value:
-            self_attn = query is key
-            if _PK.packed_supported(Lq, Lk, E, num_heads, self_attn, query.dtype):
-                mask = _combined_mask(attn_mask, key_padding_mask, batch_shape, num_heads, Lq, Lk, query.dtype)
-                kb = None
-                if mask is not None and mask is not False:
-                    kb = mask.reshape(*mask.shape[:-3], Lk) if mask.shape[-3] == 1 and mask.shape[-2] == 1 else False
-                if mask is not False and kb is not False:
-                    if self_attn:
-                        qkv = F.linear(query, in_proj_weight, in_proj_bias)
-                        out = _PK.pk_self_attention(qkv, num_heads, kb, rope, hd ** -0.5)
-                    else:
-                        w_q, w_kv = in_proj_weight.split([E, 2 * E])
-                        b_q, b_kv = (None, None) if in_proj_bias is None else in_proj_bias.split([E, 2 * E])
-                        qp = F.linear(query, w_q, b_q)
-                        kv = F.linear(key, w_kv, b_kv)
-                        if ssmax_layer is not None:
-                            qp = _ssmax(ssmax_layer, qp, num_heads, src_len_override if src_len_override is not None else Lk)
-                        out = _PK.pk_cross_attention(qp, kv, num_heads, kb, rope, hd ** -0.5)
-                    return F.linear(out, out_proj_weight, out_proj_bias)
-        q, k, v = in_projection(query, key, value, in_proj_weight, in_proj_bias, proj)
-        mask = _combined_mask(attn_mask, key_padding_mask, batch_shape, num_heads, Lq, Lk, q.dtype)
-        if mask is False:
-            return _orig()
-        if rope is not None:
-            q = rope_merged(rope, q, num_heads)
-            k = rope_merged(rope, k, num_heads)
-        if ssmax_layer is not None:
-            q = _ssmax(ssmax_layer, q, num_heads, src_len_override if src_len_override is not None else Lk)
-        out = small_head_attention(q * (hd ** -0.5), k, v, num_heads, mask, pick_impl(mode, Lq, Lk))
-        return F.linear(out, out_proj_weight, out_proj_bias)
-
     att_module.multi_head_attention_forward = multi_head_attention_forward
     if layers_module is not None:
         layers_module.multi_head_attention_forward = multi_head_attention_forward
-    if _ICL and hasattr(att_module, "sdpa_with_flattened_batch"):
-        att_module.sdpa_with_flattened_batch = _wrap_sdpa(att_module.sdpa_with_flattened_batch, splash_min_kv)
+    if knobs.icl_hook and hasattr(att_module, "sdpa_with_flattened_batch"):
+        att_module.sdpa_with_flattened_batch = icl_hook(att_module.sdpa_with_flattened_batch)
     att_module._mi355_mha_installed = True
-    att_module._mi355_mha_mode = mode
-    att_module._mi355_mha_proj = proj
+    att_module._mi355_mha_mode = knobs.mode
+    att_module._mi355_mha_proj = knobs.proj
     return True
 
 
-def _wrap_sdpa(orig_sdpa, splash_min_kv):  # noqa: ANN001
-    """sdpa_with_flattened_batch with the Splash branch of the reference patch (diff:261-265) on the
-    HIP ICL kernel: GPU tensors, no dropout, no mask, no grad, long keys (>= splash_min_kv) or a
-    valid length, head dim 64 -> SSMax on q (diff:251-254), then icl_sdpa(q, k, v, valid_kv_len)."""
+# ---------------------------------------------------------------------------------------------
+# the ICL hook on sdpa_with_flattened_batch
+# ---------------------------------------------------------------------------------------------
+def _hook_bias(attn_mask: Optional[Tensor], q: Tensor, Tkv: int):
+    """The hook's key mask: None (no mask), [1 | N, Tkv] fp32 for a mask that varies over keys only
+    (N = the flattened batch of q [..., H, Tq, D]), False for anything else (boolean, or varying over
+    heads or queries)."""
+    if attn_mask is None:
+        return None
+    if attn_mask.dtype == torch.bool or attn_mask.shape[-1] != Tkv:
+        return False
+    m = attn_mask
+    for _ in range(2):  # the query dim, then the head dim: both must be broadcast (size 1)
+        if m.dim() >= 2:
+            if m.shape[-2] != 1:
+                return False
+            m = m.squeeze(-2)
+    lead = tuple(q.shape[:-3])
+    extra = m.dim() - 1 - len(lead)
+    if extra > 0:
+        if any(s_ != 1 for s_ in m.shape[:extra]):
+            return False
+        m = m.reshape(*m.shape[extra:])
+    if any(g != 1 and g != e for g, e in zip(m.shape[:-1][::-1], lead[::-1])):
+        return False
+    if m.shape[:-1].numel() == 1:
+        return m.reshape(1, Tkv).float()
+    return m.expand(*lead, Tkv).reshape(-1, Tkv).float()
+
+
+def icl_hook(upstream_sdpa):  # noqa: ANN001
+    """sdpa_with_flattened_batch with its attention on the HIP ICL kernel (the reference's Splash
+    branch, results/tpu_patch.diff:261-281, on this GPU): q, k, v [..., H, T, D] on the GPU, same
+    dtype (bf16 or fp32), D the kernel's head dim, no dropout, no gradient, and either no mask or one
+    that varies over keys only. SSMax is applied to q with n = src_len_override or the key count first
+    (diff:251-254); valid_kv_len masks the key tail. Anything else goes to upstream."""
+
+    global _ICL
+    if _ICL is None:
+        import tabicl_mi355_icl as icl_mod  # registers tabicl::icl_cached_attn now, never while tracing
+
+        _ICL = icl_mod
 
     def sdpa_with_flattened_batch(q, k, v, attn_mask=None, dropout_p=0.0, ssmax_layer=None,  # noqa: ANN001
                                   src_len_override=None, valid_kv_len=None):
-        if (q.device.type == _DEVICE and dropout_p == 0.0 and attn_mask is None and not torch.is_grad_enabled()
-                and (k.shape[-2] >= splash_min_kv() or valid_kv_len is not None)
+        Tkv = k.shape[-2]
+        kb = _hook_bias(attn_mask, q, Tkv)
+        if (kb is not False and q.device.type == _DEVICE and dropout_p == 0.0 and not torch.is_grad_enabled()
                 and q.dtype in (torch.bfloat16, torch.float32) and q.dtype == k.dtype == v.dtype
-                and _ICL_MOD.icl_supported(q.shape[-2], k.shape[-2], q.shape[-1], q.dtype)):
+                and _ICL.icl_supported(q.shape[-2], Tkv, q.shape[-1], q.dtype)):
             lead = q.shape[:-3]
             q3 = q.reshape(-1, *q.shape[-3:])
             if ssmax_layer is not None:
-                q3 = ssmax_layer(q3, src_len_override if src_len_override is not None else k.size(-2))
-            out = _ICL_MOD.icl_sdpa(q3, k.reshape(-1, *k.shape[-3:]), v.reshape(-1, *v.shape[-3:]), valid_kv_len)
+                q3 = ssmax_layer(q3, src_len_override if src_len_override is not None else Tkv)
+            out = _ICL.icl_sdpa(q3, k.reshape(-1, *k.shape[-3:]), v.reshape(-1, *v.shape[-3:]), valid_kv_len, kb)
             return out.reshape(*lead, *out.shape[-3:])
-        return orig_sdpa(q, k, v, attn_mask, dropout_p, ssmax_layer=ssmax_layer,
-                         src_len_override=src_len_override, valid_kv_len=valid_kv_len)
+        return upstream_sdpa(q, k, v, attn_mask, dropout_p, ssmax_layer=ssmax_layer,
+                             src_len_override=src_len_override, valid_kv_len=valid_kv_len)
 
     return sdpa_with_flattened_batch

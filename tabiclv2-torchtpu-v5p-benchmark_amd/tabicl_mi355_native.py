@@ -27,6 +27,8 @@ SIGNATURES = {
     "tabicl_hx_fwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i32, _i32, _c_p],
     "tabicl_hxq_fwd": [_c_p, _i64, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _i32, _c_p, _i64, _c_p],
     "tabicl_hxq_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _i32],
+    "tabicl_hxq_fwd_masked": [_c_p, _i64, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _i32, _c_p,
+                              _i64, _c_p],
     "tabicl_pk_self_fwd": [_c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
                            _f32, _i32, _c_p],
     "tabicl_pk_cross_fwd": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
@@ -34,6 +36,8 @@ SIGNATURES = {
     "tabicl_pk_cross_fwd_ragged": [_c_p, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64,
                                    _i64, _i32, _i32, _i32, _i32, _f32, _i32, _c_p, _i64, _c_p],
     "tabicl_hxf_fwd": [_c_p, _i64, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _c_p, _i64, _c_p],
+    "tabicl_hxf_fwd_masked": [_c_p, _i64, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32, _c_p,
+                              _i64, _c_p],
     "tabicl_hxf_workspace_bytes": [_i64, _i64, _i64, _i64, _i32],
     "tabicl_smallhead_bwd_workspace_bytes": [_i64, _i64, _i64, _i32],
     "tabicl_hx_bwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _i32,
@@ -46,6 +50,8 @@ SIGNATURES = {
                       + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_fwd_ragged": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i64]
                              + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_fwd_masked": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
+                              _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i32],
     "tabicl_icl_cache_append": [_c_p, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _i32, _c_p],

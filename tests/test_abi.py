@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     import tabicl_mi355_native as nat
     lib = nat.load()
     names = _declared()
-    assert len(names) == 19, names
+    assert len(names) == 22, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in nat.SIGNATURES, name
@@ -68,8 +68,82 @@ def test_bad_arguments_rejected_before_launch():
     st = lib.tabicl_pk_cross_fwd_ragged(None, 1, None, None, 1, None, None, None, None, None, 4, 8, 8, 128, 8, 0, 0,
                                         0, 0.25, 0, ctypes.byref(qlen), 2, None)
     assert st == 1 and "q_len" in nat.last_error()
+    # RoPE tables of the cross entry points must be 16-byte aligned (float4 loads)
+    st = lib.tabicl_pk_cross_fwd_ragged(a, 1, a, None, 1, a + 4, a, a, a, a, 4, 8, 8, 128, 8, 2, 8, 16, 0.25, 0,
+                                        None, 0, None)
+    assert st == 1 and "aligned" in nat.last_error()
+    st = lib.tabicl_pk_cross_fwd(a, 1, a, None, 1, a, a, a, a + 8, a, 4, 8, 8, 128, 8, 2, 8, 16, 0.25, 0, None)
+    assert st == 1 and "aligned" in nat.last_error()
+    # masked entry points: key-mask rows must be 1 or N (B)
+    st = lib.tabicl_icl_fwd_masked(a, a, a, None, 0, a, 3, 64, None, 0, a, 2, 1, 1, 64, 64, *([64] * 12), 0.125, 0,
+                                   None, 0, None)
+    assert st == 1 and "key_bias" in nat.last_error()
+    st = lib.tabicl_icl_fwd_masked(a, a, a, None, 0, a, 1, 64, None, 0, a, 2, 1, 1, 64, 64, *([64] * 12), 0.0, 0,
+                                   None, 0, None)
+    assert st == 1 and "scale" in nat.last_error()
+    st = lib.tabicl_hxq_fwd_masked(None, 0, a, 3, a, a, a, 2, 8, 300, 128, 8, 0, None, 0, None)
+    assert st == 1 and "key_bias" in nat.last_error()
+    st = lib.tabicl_hxf_fwd_masked(None, 0, a, 3, a, 1, a, a, 2, 64, 300, 128, 0, None, 0, None)
+    assert st == 1 and "key_bias" in nat.last_error()
     with pytest.raises(nat.UnsupportedShapeError):
         nat.check(1, "x")
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_rope_table_shapes_refused_before_launch(shared):
+    # a table of the wrong width, length or dtype is refused before any pointer reaches the library
+    import tabicl_mi355_attn as pk
+    import tabicl_mi355_native as nat
+    rc = 2 | (pk.ROPE_SHARED_TABLES if shared else 0)
+    cols = 16 if shared else 128
+    qkv = torch.zeros(2, 10, 384)
+    empty_bias = torch.empty(0, 1, 10)
+    good = torch.zeros(10, cols)
+    for bad in (torch.zeros(10, 128 if shared else 16), torch.zeros(9, cols), torch.zeros(10, cols, dtype=torch.float64)):
+        with pytest.raises(ValueError, match="table"):
+            torch.ops.tabicl_pk.pk_self_fwd(qkv, empty_bias, bad, good, 8, 128, rc, 8, 16, 0, 0.25)
+        with pytest.raises(ValueError, match="table"):
+            torch.ops.tabicl_pk.pk_cross_fwd(qkv[..., :128], qkv[..., :256], empty_bias, good, good, good, bad, 8, 128,
+                                             10, rc, 8, 16, 0, 0.25)
+    # right tables: the shape checks pass and the op then refuses CPU tensors (no CPU path)
+    with pytest.raises(nat.NativeLibraryError):
+        torch.ops.tabicl_pk.pk_self_fwd(qkv, empty_bias, good, good, 8, 128, rc, 8, 16, 0, 0.25)
+
+
+def test_rope_tables_cached_per_module():
+    import tabicl_mi355_attn as pk
+    rope = torch.nn.Module()
+    rope.interleaved = False
+    rope.freqs = torch.nn.Parameter(torch.tensor(O.textbook_freqs(16, 10000.0), dtype=torch.float32),
+                                    requires_grad=False)
+    rope.get_seq_pos = lambda L, device=None, dtype=torch.float32: torch.arange(L, device=device, dtype=dtype)
+    a = pk._tables(rope, 104, 128, 8, "cpu", True)
+    b = pk._tables(rope, 104, 128, 8, "cpu", True)
+    assert a[0] is b[0] and a[2] == 2 | pk.ROPE_SHARED_TABLES and tuple(a[0].shape) == (104, 16)
+    full = pk._tables(rope, 104, 128, 8, "cpu", False)
+    assert tuple(full[0].shape) == (104, 128) and full[2] == 2
+    np.testing.assert_allclose(a[0].numpy(), full[0][:, :16].numpy())
+    with torch.no_grad():
+        rope.freqs.mul_(2.0)  # in-place change of the frequencies: the cached tables are not reused
+    c = pk._tables(rope, 104, 128, 8, "cpu", True)
+    assert c[0] is not a[0] and not torch.allclose(c[1], a[1])
+    n1, n2 = pk._tables(None, 50, 128, 8, "cpu", True), pk._tables(None, 70, 128, 8, "cpu", False)
+    assert n1[2] == 0 and n1[0] is n2[0]  # no RoPE: one stand-in row, never read by the kernels
+
+
+def test_icl_cache_fill_bookkeeping():
+    import tabicl_mi355_icl as icl
+    cache = icl.IclKVCache(2, 3, 8, 1000, 64, torch.bfloat16, "cpu")
+    with pytest.raises(ValueError, match="no rows"):
+        cache.default_valid(0)
+    cache._record(0, 0, 300)
+    cache._record(0, 300, 200)
+    cache._record(0, 100, 50)  # rewriting rows inside the filled prefix keeps the length
+    assert cache.length(0) == 500 and cache.length(1) == 0
+    t = cache.default_valid(0)
+    assert t.dtype == torch.int32 and t.tolist() == [500] and cache.default_valid(0) is t
+    with pytest.raises(ValueError, match="unwritten"):
+        cache._record(1, 10, 5)
 
 
 def test_ops_refuse_cpu_tensors():

@@ -355,3 +355,33 @@ def test_hxf_ref_valid_and_shared_query():
     np.testing.assert_allclose(got[1], O.hxf_ref(qf, x[1:2, :4], 4)[0], rtol=0, atol=1e-12)
     assert np.abs(got[2]).max() == 0
     np.testing.assert_allclose(got[0], O.attention_loops(qf, x[:1], x[:1], 1)[0], rtol=0, atol=1e-12)
+
+
+def test_splash_ref_key_bias():
+    # the key-mask parameter of the ICL oracle, pinned by closed forms and invariants
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 3, 5, 64, generator=g)
+    k = torch.randn(2, 3, 40, 64, generator=g)
+    v = torch.randn(2, 3, 40, 64, generator=g)
+    base = O.splash_sdpa_ref(q, k, v)
+    # (with a mask the scores are summed in float32, as the reference does: agreement to fp32 rounding)
+    np.testing.assert_allclose(O.splash_sdpa_ref(q, k, v, bias=np.zeros((1, 40))), base, atol=1e-6)
+    # one constant per row (and per n) shifts every score of the row: softmax unchanged
+    np.testing.assert_allclose(O.splash_sdpa_ref(q, k, v, bias=np.array([[3.0] * 40, [-7.0] * 40])), base, atol=1e-6)
+    # a prefix mask (0, then finfo.min or -inf) is the valid length
+    for fill in (float(np.finfo(np.float32).min), -np.inf):
+        b = np.zeros((2, 40))
+        b[0, 17:] = fill
+        b[1, 33:] = fill
+        np.testing.assert_allclose(O.splash_sdpa_ref(q, k, v, bias=b), O.splash_sdpa_ref(q, k, v, np.array([17, 33])),
+                                   atol=1e-6)
+    # every key at finfo.min: the fp32 sum absorbs the scores, weights are equal -> mean of V
+    allm = np.full((1, 40), float(np.finfo(np.float32).min))
+    np.testing.assert_allclose(O.splash_sdpa_ref(q, k, v, bias=allm),
+                               np.broadcast_to(v.double().numpy().mean(axis=2, keepdims=True), (2, 3, 5, 64)), atol=1e-12)
+    # two keys, bias b on key 1: weight of key 1 = sigmoid(s1 + b - s0)
+    q2, k2, v2 = q[:1, :1, :1], k[:1, :1, :2], v[:1, :1, :2]
+    s = (q2[0, 0, 0].double() @ k2[0, 0].double().T).numpy() * 0.125
+    w1 = 1.0 / (1.0 + np.exp(-(np.float64(np.float32(s[1]) + np.float32(1.5)) - np.float32(s[0]))))
+    want = (1 - w1) * v2[0, 0, 0].double().numpy() + w1 * v2[0, 0, 1].double().numpy()
+    np.testing.assert_allclose(O.splash_sdpa_ref(q2, k2, v2, bias=np.array([[0.0, 1.5]]))[0, 0, 0], want, atol=1e-6)

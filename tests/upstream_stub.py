@@ -1,9 +1,11 @@
 """Test stand-in for the parts of upstream tabicl (2.2.0, as patched by the reference's
-results/tpu_patch.diff) that the dispatch wrapper patches: a module-like namespace with
-`multi_head_attention_forward` and `sdpa_with_flattened_batch`, plus a RotaryEmbedding-like object.
+results/tpu_patch.diff) that the dispatch wrapper patches or is called from: a module-like namespace
+with `multi_head_attention_forward` and `sdpa_with_flattened_batch`, the attention part of
+`MultiheadAttentionBlock.forward` (`block_attention`), plus a RotaryEmbedding-like object.
 Upstream is not vendored in the reference; this restates the behaviour the diff shows
-(diff:196-281 sdpa routing and SSMax, diff:283-395 projections, RoPE, mask processing, cached K/V)
-with plain torch math. Test infrastructure only."""
+(diff:196-281 sdpa routing and SSMax, diff:283-395 projections, RoPE, mask processing, cached K/V,
+diff:1509-1542 the block's handling of a tensor train size / valid_kv_len) with plain torch math.
+Test infrastructure only."""
 from __future__ import annotations
 
 import types
@@ -112,6 +114,8 @@ def make_module():
         if key_padding_mask is not None:
             kpm = key_padding_mask.view(*key_padding_mask.shape[:-1], 1, 1, src_len)
             mask = kpm if mask is None else mask + kpm
+        if mask is not None and mask.dtype != torch.bool and mask.dtype != q.dtype:
+            mask = mask.to(dtype=q.dtype)  # diff:370-371 (a finfo(float32).min entry becomes -inf in bf16)
         out = mod.sdpa_with_flattened_batch(q, k, v, mask, dropout_p, ssmax_layer=ssmax_layer,
                                             src_len_override=src_len_override, valid_kv_len=valid_kv_len)
         out = out.transpose(-3, -2).contiguous().view(*batch_shape, tgt_len, E)
@@ -141,3 +145,49 @@ def weights(E: int, seed: int, device="cpu", dtype=torch.float32):
 def call(fn, query, key, value, nh, w, b, wo, bo, **kw) -> Tensor:
     return fn(query, nh, w, b, 0.0, wo, bo, key=key, value=value, training=False, **kw)
 
+
+
+def splash_min_kv() -> int:
+    return 16384
+
+
+def block_attention(mod, q, num_heads, w, b, wo, bo, k=None, v=None, cached_kv=None, train_size=None,  # noqa: ANN001
+                    key_padding_mask=None, attn_mask=None, rope=None, ssmax_layer=None, src_len_override=None,
+                    valid_kv_len=None):
+    """The attention call of MultiheadAttentionBlock.forward as patched (diff:1509-1565), norms and the
+    feed-forward part left out (the inputs count as already normalised):
+      * a tensor train_size makes k = v = q and sets src_len_override / valid_kv_len to it (:1512-1517);
+      * a tensor valid_kv_len is kept only on the reference's device ("tpu") with no grad, no other
+        mask and at least splash_min_kv keys; everywhere else it becomes an additive mask, 0 for key
+        positions below it and finfo(q.dtype).min from there on, of shape [1, .., 1, 1, src_len]
+        (q.dim() - 2 leading ones), added to attn_mask, and valid_kv_len is cleared (:1526-1542).
+    Then the module's multi_head_attention_forward is looked up and called, as layers.py does."""
+    if train_size is None:
+        k = q if k is None else k
+        v = q if v is None else v
+    elif isinstance(train_size, Tensor):
+        k = v = q
+        src_len_override = train_size if src_len_override is None else src_len_override
+        valid_kv_len = train_size if valid_kv_len is None else valid_kv_len
+    else:
+        k = v = q[..., :train_size, :]
+    src_seq_len = cached_kv.key.shape[-2] if cached_kv is not None else k.shape[-2]
+    if isinstance(valid_kv_len, Tensor):
+        keep = (q.device.type == "tpu" and not torch.is_grad_enabled() and attn_mask is None
+                and key_padding_mask is None and src_seq_len >= splash_min_kv())
+        if not keep:
+            pos = torch.arange(src_seq_len, device=q.device)
+            train_mask = torch.where(pos < valid_kv_len, torch.zeros((), dtype=q.dtype, device=q.device),
+                                     torch.full((), torch.finfo(q.dtype).min, dtype=q.dtype, device=q.device))
+            train_mask = train_mask.view(*([1] * (q.dim() - 2)), 1, 1, src_seq_len)
+            attn_mask = train_mask if attn_mask is None else attn_mask + train_mask
+            valid_kv_len = None
+    if cached_kv is not None:
+        return mod.multi_head_attention_forward(q, num_heads, w, b, 0.0, wo, bo, cached_kv=cached_kv, training=False,
+                                                key_padding_mask=key_padding_mask, attn_mask=attn_mask, rope=rope,
+                                                ssmax_layer=ssmax_layer, src_len_override=src_len_override,
+                                                valid_kv_len=valid_kv_len)
+    return mod.multi_head_attention_forward(q, num_heads, w, b, 0.0, wo, bo, key=k, value=v, training=False,
+                                            key_padding_mask=key_padding_mask, attn_mask=attn_mask, rope=rope,
+                                            ssmax_layer=ssmax_layer, src_len_override=src_len_override,
+                                            valid_kv_len=valid_kv_len)
