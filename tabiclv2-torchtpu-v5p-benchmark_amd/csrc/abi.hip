@@ -95,6 +95,31 @@ int bwd_common(const char* op, int64_t B, int64_t Lq, int64_t Lk, int64_t E, int
   return 0;
 }
 
+// Argument checks shared by the ICL entry points (status 0 or 1 with the message set).
+int icl_args(const char* op, const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+             const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len, int64_t q_len_n,
+             const void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, const int64_t* strides,
+             float scale, int32_t dtype) {
+  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) return fail(1, "%s: dtype code %d not supported", op, dtype);
+  if (key_bias) {
+    if (bias_n != 1 && bias_n != N) return fail(1, "%s: key_bias must hold 1 or N rows", op);
+    if (bias_n > 1 && bias_sn < Tkv) return fail(1, "%s: key_bias row stride %lld < Tkv", op, (long long)bias_sn);
+    if (!aligned16(key_bias)) return fail(1, "%s: key_bias must be 16-byte aligned", op);
+    if (!(scale > 0.f) || !(scale < 1e30f)) return fail(1, "%s: a key mask needs a positive finite scale", op);
+  }
+  if (D != 64) return fail(1, "%s: head dim must be 64, got %lld", op, (long long)D);
+  if (N < 0 || H < 0 || Tq < 0 || Tkv < 1 || Tq > (1LL << 30) || Tkv > (1LL << 30)) return fail(1, "%s: bad sizes", op);
+  if (valid && valid_n != 1 && valid_n != N) return fail(1, "%s: valid must hold 1 or N entries", op);
+  if (q_len && q_len_n != 1 && q_len_n != N) return fail(1, "%s: q_len must hold 1 or N entries", op);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(1, "%s: pointers must be 16-byte aligned", op);
+  for (int i = 0; i < 12; ++i)
+    if (strides[i] < 0 || !stride_ok(strides[i], dtype))
+      return fail(1, "%s: strides must be non-negative multiples of 16 bytes", op);
+  if (N * H * ((Tq + 127) / 128) > (1LL << 31) - 1) return fail(1, "%s: grid too large", op);
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -353,29 +378,10 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
                           int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
                           int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
                           float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32)
-    return fail(1, "icl_fwd: dtype code %d not supported", dtype);
-  if (key_bias) {
-    if (bias_n != 1 && bias_n != N) return fail(1, "icl_fwd: key_bias must hold 1 or N rows");
-    if (bias_n > 1 && bias_sn < Tkv) return fail(1, "icl_fwd: key_bias row stride %lld < Tkv", (long long)bias_sn);
-    if (!aligned16(key_bias)) return fail(1, "icl_fwd: key_bias must be 16-byte aligned");
-    if (!(scale > 0.f) || !(scale < 1e30f)) return fail(1, "icl_fwd: a key mask needs a positive finite scale");
-  }
-  if (D != 64) return fail(1, "icl_fwd: head dim must be 64, got %lld", (long long)D);
-  if (N < 0 || H < 0 || Tq < 0 || Tkv < 1 || Tq > (1LL << 30) || Tkv > (1LL << 30))
-    return fail(1, "icl_fwd: bad sizes");
-  if (valid && valid_n != 1 && valid_n != N)
-    return fail(1, "icl_fwd: valid must hold 1 or N entries");
-  if (q_len && q_len_n != 1 && q_len_n != N)
-    return fail(1, "icl_fwd: q_len must hold 1 or N entries");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
-    return fail(1, "icl_fwd: pointers must be 16-byte aligned");
   const int64_t strides[12] = {q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st};
-  for (int i = 0; i < 12; ++i)
-    if (strides[i] < 0 || !stride_ok(strides[i], dtype))
-      return fail(1, "icl_fwd: strides must be non-negative multiples of 16 bytes");
-  if (N == 0 || H == 0 || Tq == 0) return 0;
-  if (N * H * ((Tq + 127) / 128) > (1LL << 31) - 1) return fail(1, "icl_fwd: grid too large");
+  int st = icl_args("icl_fwd", q, k, v, valid, valid_n, key_bias, bias_n, bias_sn, q_len, q_len_n, out, N, H, Tq,
+                    Tkv, D, strides, scale, dtype);
+  if (st || N == 0 || H == 0 || Tq == 0) return st;
   return launch_status(
       tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, 64, q_sn, q_sh,
                             q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale,

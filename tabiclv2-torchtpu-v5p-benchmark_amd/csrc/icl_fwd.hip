@@ -271,14 +271,19 @@ __device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, co
       st.m_run[qc] = m_new;
     }
     const float nm = -st.m_run[qc] * sc;
+    const float mr = st.m_run[qc];
     float lsum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          pop[qc][kb][m][j] = from_f32<T>(__builtin_amdgcn_exp2f(fmaf(s[qc][kb][8 * m + j], sc, nm)));
+        for (int j = 0; j < 8; ++j) {
+          // with a key mask the scores can be huge (down to the -1e30 floor); there fma(s, sc, -m sc)
+          // would turn the rounding of m sc into the exponent, so the difference is taken first
+          const float x = BIAS ? (s[qc][kb][8 * m + j] - mr) * sc : fmaf(s[qc][kb][8 * m + j], sc, nm);
+          pop[qc][kb][m][j] = from_f32<T>(__builtin_amdgcn_exp2f(x));
+        }
         lsum = psum8(pop[qc][kb][m], lsum);
       }
     st.l_run[qc] += lsum;
@@ -1062,3 +1067,4 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   }
   return (int)hipGetLastError();
 }
+

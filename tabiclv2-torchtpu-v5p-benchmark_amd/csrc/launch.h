@@ -26,6 +26,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           const float* bias = nullptr, int64_t bias_n = 0, int64_t bias_sn = 0);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
+
 // Small-head (8 x 16) attention (smallhead_fwd.hip): picks the resident, streaming or general
 // kernel for the shape. ws may be null (no key split). qlen (device int32, qlen_n in {1, B}): query
 // rows needed per batch element; the resident kernel neither computes nor writes the rows at or past

@@ -183,10 +183,10 @@ class IclKVCache:
     (the per-block K/V the prefill produces, reference scripts/tabicl_tpu_bucketed.py:659-692);
     block_kv(block) returns the [E, H, capacity, d] views the query reads (:803-817).
 
-    Each block records how many leading rows it holds (`filled[block]`, host ints: appends must extend
-    the filled prefix, row0 <= filled). A query without an explicit valid length attends over exactly
-    those rows, so the unwritten tail of the cache (torch.empty memory) is never read; querying a block
-    with no rows raises."""
+    Each block records which rows appends have written (merged row intervals); `length(block)` is the
+    contiguous run from row 0. A query without an explicit valid length attends over exactly that run,
+    so the unwritten rows of the cache (torch.empty memory) are never read; querying a block whose row 0
+    was never written raises."""
 
     def __init__(self, estimators: int, blocks: int, heads: int, capacity: int, head_dim: int,
                  dtype: torch.dtype = torch.bfloat16, device: Union[str, torch.device] = "cuda"):
@@ -194,24 +194,32 @@ class IclKVCache:
         self.keys = torch.empty(shape, dtype=dtype, device=device)
         self.values = torch.empty(shape, dtype=dtype, device=device)
         self.capacity = capacity
-        self.filled = [0] * blocks
-        self._len_t: dict = {}  # filled length -> int32 device tensor handed to the kernels
+        self.written = [[] for _ in range(blocks)]  # per block: sorted, disjoint [start, end) row intervals
+        self._len_t: dict = {}  # length -> int32 device tensor handed to the kernels
 
     def length(self, block: int) -> int:
         """Rows [0, length) of `block` hold appended K/V."""
-        return self.filled[block]
+        iv = self.written[block]
+        return iv[0][1] if iv and iv[0][0] == 0 else 0
 
     def _record(self, block: int, row0: int, T: int) -> None:
-        if row0 > self.filled[block]:
-            raise ValueError(f"append at row {row0} would leave rows [{self.filled[block]}, {row0}) of block "
-                             f"{block} unwritten (appends must extend the filled prefix)")
-        self.filled[block] = max(self.filled[block], row0 + T)
+        if T <= 0:
+            return
+        merged = []
+        lo, hi = row0, row0 + T
+        for a, b in self.written[block]:
+            if b < lo or a > hi:
+                merged.append((a, b))
+            else:
+                lo, hi = min(lo, a), max(hi, b)
+        merged.append((lo, hi))
+        self.written[block] = sorted(merged)
 
     def default_valid(self, block: int) -> Tensor:
-        """The filled length of `block` as the int32 device tensor the kernels take."""
-        n = self.filled[block]
+        """The block's filled length from row 0 as the int32 device tensor the kernels take."""
+        n = self.length(block)
         if n <= 0:
-            raise ValueError(f"block {block} of the cache holds no rows: append before querying")
+            raise ValueError(f"block {block} of the cache has no rows from row 0: append before querying")
         t = self._len_t.get(n)
         if t is None:
             t = self._len_t[n] = torch.full((1,), n, dtype=torch.int32, device=self.keys.device)
@@ -238,8 +246,6 @@ class IclKVCache:
         T = k.shape[2]
         if row0 < 0 or row0 + T > cap:
             raise ValueError(f"rows [{row0}, {row0 + T}) exceed the capacity {cap}")
-        if row0 > self.filled[block]:
-            self._record(block, row0, T)  # raises: the rows in between would stay unwritten
         kc = self.keys[:, block]
         vc = self.values[:, block]
         _nat.call("tabicl_icl_cache_append", kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), row0, cap,

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     import tabicl_mi355_native as nat
     lib = nat.load()
     names = _declared()
-    assert len(names) == 22, names
+    assert set(names) == set(nat.SIGNATURES), sorted(set(names) ^ set(nat.SIGNATURES))
     for name in names:
         assert hasattr(lib, name), name
         assert name in nat.SIGNATURES, name
@@ -136,14 +136,19 @@ def test_icl_cache_fill_bookkeeping():
     cache = icl.IclKVCache(2, 3, 8, 1000, 64, torch.bfloat16, "cpu")
     with pytest.raises(ValueError, match="no rows"):
         cache.default_valid(0)
-    cache._record(0, 0, 300)
-    cache._record(0, 300, 200)
-    cache._record(0, 100, 50)  # rewriting rows inside the filled prefix keeps the length
+    cache._record(0, 300, 200)  # rows [300, 500) first: row 0 not written yet, no default length
+    assert cache.length(0) == 0
+    with pytest.raises(ValueError, match="no rows"):
+        cache.default_valid(0)
+    cache._record(0, 0, 300)  # now [0, 500) is contiguous
+    cache._record(0, 100, 50)  # rewriting rows inside it keeps the length
+    cache._record(0, 700, 10)  # a later island does not extend it
     assert cache.length(0) == 500 and cache.length(1) == 0
+    assert cache.written[0] == [(0, 500), (700, 710)]
     t = cache.default_valid(0)
     assert t.dtype == torch.int32 and t.tolist() == [500] and cache.default_valid(0) is t
-    with pytest.raises(ValueError, match="unwritten"):
-        cache._record(1, 10, 5)
+    cache._record(0, 500, 200)  # closes the gap: [0, 710)
+    assert cache.length(0) == 710
 
 
 def test_ops_refuse_cpu_tensors():
