@@ -259,6 +259,28 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
                           float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * tabicl_icl_fwd_masked without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
+ * in the reference. The key-split partials, work-item flags and the prefix view of a key mask live in
+ * a file-scope device array of the library, one per GPU, of tabicl_icl_noalloc_scratch_bytes() bytes
+ * (32 MiB), held until the process ends; the entry point itself calls no allocating routine. Calls
+ * whose split partials do not fit run with the keys unsplit (the results then differ from
+ * tabicl_icl_fwd's split result by rounding only); a call that needs more than the array even unsplit
+ * (more than ~8M work items of 256 query rows x one head) returns 1 with a message. Every call on a GPU
+ * shares that GPU's array and keeps no state in it between calls (each kernel writes every entry it
+ * later reads): calls that overlap on one GPU (other streams, other host threads) race.
+ */
+int tabicl_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                           const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,
+                           int64_t q_len_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                           int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                           int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                           float scale, int32_t dtype, void* stream);
+
+/* Bytes of the per-GPU scratch array tabicl_icl_fwd_noalloc uses (no counterpart in the reference). */
+int64_t tabicl_icl_noalloc_scratch_bytes(void);
+
+/*
  * Workspace size (bytes) that tabicl_icl_fwd uses for these sizes on the current device (0 when
  * the call would not split). Queries the device's CU count and occupancy; no device memory is
  * touched. Returns <0 on bad arguments.

@@ -391,6 +391,30 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
       "icl_fwd");
 }
 
+int tabicl_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                           const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,
+                           int64_t q_len_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                           int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                           int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                           float scale, int32_t dtype, void* stream) {
+  const int64_t strides[12] = {q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st};
+  int st = icl_args("icl_fwd_noalloc", q, k, v, valid, valid_n, key_bias, bias_n, bias_sn, q_len, q_len_n, out, N, H,
+                    Tq, Tkv, D, strides, scale, dtype);
+  if (st || N == 0 || H == 0 || Tq == 0) return st;
+  const int64_t need = tabicl_launch_icl_noalloc_min_bytes(N, H, Tq, D, dtype);
+  if (need > TABICL_ICL_SCRATCH_BYTES)
+    return fail(1, "icl_fwd_noalloc: the call needs %lld bytes of scratch, more than the library's %lld (use "
+                "tabicl_icl_fwd with a workspace)", (long long)need, (long long)TABICL_ICL_SCRATCH_BYTES);
+  return launch_status(
+      tabicl_launch_icl_fwd_noalloc(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, q_sn, q_sh, q_st, k_sn,
+                                    k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype, (hipStream_t)stream,
+                                    q_len, q_len ? q_len_n : 0, key_bias, key_bias ? bias_n : 0,
+                                    key_bias ? bias_sn : 0),
+      "icl_fwd_noalloc");
+}
+
+int64_t tabicl_icl_noalloc_scratch_bytes(void) { return TABICL_ICL_SCRATCH_BYTES; }
+
 int64_t tabicl_icl_workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
                                    int32_t dtype) {
   if ((dtype != TABICL_DTYPE_BF16 && dtype != TABICL_DTYPE_F32) || D != 64 || N < 0 || H < 0 ||

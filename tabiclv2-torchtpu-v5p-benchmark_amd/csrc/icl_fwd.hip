@@ -21,6 +21,8 @@
 //                                        layout converted to bf16 in place (no shuffles)
 //    with the running max updated lazily (accumulators rescaled only when the tile max exceeds the
 //    running max by more than 2^8; exact because O and l always share the same reference max).
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
@@ -1068,3 +1070,58 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   return (int)hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// Allocation-free launch: the work-item flags, the prefix view of a key mask and the key-split
+// partials live in `scratch`, a file-scope device array (one per GPU, held until the process ends),
+// instead of a workspace from the caller. Host code never passes the array's name to a kernel: its
+// device address is taken once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+// Every call on a GPU shares that GPU's array (no call clears it: each kernel writes every entry it
+// later reads), so calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[TABICL_ICL_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int ICL_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[ICL_MAX_DEVICES] = {};
+
+// Device address of the current device's scratch array (looked up on the first call per device).
+hipError_t scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= ICL_MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+int64_t tabicl_launch_icl_noalloc_min_bytes(int64_t N, int64_t H, int64_t Tq, int64_t D, int dtype) {
+  // unsplit: flags per work item and the prefix view (bf16, d = 64, the pipelined kernel); nothing else
+  if (dtype != 0 || D != ICL_D) return 0;
+  const int64_t nqb = (Tq + IP_QW * IP_NW - 1) / (IP_QW * IP_NW);
+  return flag_bytes(N * H * nqb) + pref_bytes(N);
+}
+
+int tabicl_launch_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid,
+                                  int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                                  int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                                  int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                                  float scale, int dtype, hipStream_t stream, const int32_t* qlen, int64_t qlen_n,
+                                  const float* bias, int64_t bias_n, int64_t bias_sn) {
+  void* ws = nullptr;
+  const hipError_t e = scratch_ptr(&ws);
+  if (e != hipSuccess) return (int)e;
+  return tabicl_launch_icl_fwd(q, k, v, valid, valid_n, out, N, H, Tq, Tkv, ICL_D, q_sn, q_sh, q_st, k_sn, k_sh, k_st,
+                               v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype, ws, TABICL_ICL_SCRATCH_BYTES, stream,
+                               qlen, qlen_n, bias, bias_n, bias_sn);
+}

@@ -26,6 +26,17 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           const float* bias = nullptr, int64_t bias_n = 0, int64_t bias_sn = 0);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
+// The same launch (D = 64) with the library's per-GPU scratch array of TABICL_ICL_SCRATCH_BYTES in
+// place of a workspace: no allocation. Key splits whose partials do not fit run unsplit; a call whose
+// unsplit need (tabicl_launch_icl_noalloc_min_bytes) exceeds the array must be refused by the caller.
+#define TABICL_ICL_SCRATCH_BYTES (32ll << 20)
+int64_t tabicl_launch_icl_noalloc_min_bytes(int64_t N, int64_t H, int64_t Tq, int64_t D, int dtype);
+int tabicl_launch_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid,
+                                  int64_t valid_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                                  int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                                  int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                                  float scale, int dtype, hipStream_t stream, const int32_t* qlen, int64_t qlen_n,
+                                  const float* bias, int64_t bias_n, int64_t bias_sn);
 
 // Small-head (8 x 16) attention (smallhead_fwd.hip): picks the resident, streaming or general
 // kernel for the shape. ws may be null (no key split). qlen (device int32, qlen_n in {1, B}): query

@@ -52,6 +52,9 @@ SIGNATURES = {
                              + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_fwd_masked": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
                               _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_fwd_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
+                               _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p],
+    "tabicl_icl_noalloc_scratch_bytes": [],
     "tabicl_icl_workspace_bytes": [_i64, _i64, _i64, _i64, _i64, _i32],
     "tabicl_icl_cache_append": [_c_p, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _i32, _c_p],
@@ -61,7 +64,8 @@ SIGNATURES = {
 }
 _RESTYPES = {"tabicl_attn_last_error": ctypes.c_char_p, "tabicl_attn_version": ctypes.c_char_p,
              "tabicl_icl_workspace_bytes": ctypes.c_int64, "tabicl_hxq_workspace_bytes": ctypes.c_int64,
-             "tabicl_smallhead_bwd_workspace_bytes": ctypes.c_int64, "tabicl_hxf_workspace_bytes": ctypes.c_int64}
+             "tabicl_smallhead_bwd_workspace_bytes": ctypes.c_int64, "tabicl_hxf_workspace_bytes": ctypes.c_int64,
+             "tabicl_icl_noalloc_scratch_bytes": ctypes.c_int64}
 
 
 class NativeLibraryError(RuntimeError):
