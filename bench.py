@@ -581,6 +581,79 @@ def bench_icl_layer(steps: int, warmup: int) -> list:
     return recs
 
 
+def bench_icl_stage(steps: int, warmup: int) -> list:
+    """The cached ICL query step at C4's shape: the reference's per-block loop (scripts/tabicl_tpu_bucketed.py
+    :803-817) over 12 pre-norm blocks (IclKVCache.query_blocks: LayerNorm in fp32, Q projection, an SSMax
+    stand-in on q, the cached attention kernel, out-projection, residual, feed-forward 512 -> 1024 -> 512 with
+    GELU, residual), then the final LayerNorm and a decoder MLP (512 -> 1024 -> 10), on 8 estimators x 5,000
+    test rows over 45,000 cached train rows per block. bf16 GEMMs (the reference's bf16 autocast of the ICL
+    stage), fp32 residual stream. Random weights and rows (seed 6); the cache is built by append_projected.
+    The reference publishes no cached ICL-stage time: its ICL stage of the no-cache forward (train rows
+    included) took 2.41 s on a TPU v5p (APPENDIX.md:93) and its whole cached query 938.49 ms
+    (results/inference/best_model_forward_and_e2e.jsonl:2); both are context, not this workload."""
+    import torch
+    import torch.nn.functional as F
+
+    import tabicl_mi355_icl as icl
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(6)
+    W, FF, NCLS = HEADS * D, 2 * HEADS * D, 10
+
+    def lin(o, i):
+        return ((torch.randn(o, i, generator=g, device=dev) * i ** -0.5).to(torch.bfloat16),
+                (torch.randn(o, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+
+    def norm():
+        return (1 + 0.05 * torch.randn(W, generator=g, device=dev), 0.05 * torch.randn(W, generator=g, device=dev))
+
+    blocks = []
+    for _ in range(BLOCKS):
+        (l1w, l1b), (inw, inb), (ow, ob), (l2w, l2b), (f1w, f1b), (f2w, f2b) = \
+            norm(), lin(3 * W, W), lin(W, W), norm(), lin(FF, W), lin(W, FF)
+        blocks.append(icl.IclBlockWeights(l1w, l1b, inw, inb, ow, ob, l2w, l2b, f1w, f1b, f2w, f2b))
+    lnf_w, lnf_b = norm()
+    (d1w, d1b), (d2w, d2b) = lin(FF, W), lin(NCLS, FF)
+    cache = icl.IclKVCache(EST, BLOCKS, HEADS, TRAIN, D, torch.bfloat16, dev)
+    xtr = torch.randn(EST, TRAIN, W, generator=g, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        for b, w in enumerate(blocks):
+            cache.append_projected(b, xtr, w.in_w, w.in_b)
+    del xtr
+    x0 = torch.randn(EST, TEST, W, generator=g, device=dev)
+    a = 0.05 * torch.randn(HEADS, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    logn = float(torch.log(torch.tensor(float(TRAIN))))
+    ssmax = (lambda q: q * (1.0 + a * logn))  # stand-in for upstream's elementwise SSMax on q (n = train rows)
+    valid = torch.tensor([TRAIN], dtype=torch.int32, device=dev)
+
+    def stage():
+        x = cache.query_blocks(x0, blocks, valid, ssmax)
+        h = F.layer_norm(x, (W,), lnf_w, lnf_b).to(torch.bfloat16)
+        return F.linear(F.gelu(F.linear(h, d1w, d1b)), d2w, d2b).float()
+
+    qs = [torch.randn(EST, HEADS, TEST, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
+
+    def attention_only():
+        for b in range(BLOCKS):
+            cache.query(b, qs[b % 2], valid)
+
+    with torch.no_grad():
+        ms = _time(stage, steps, warmup)
+        ms_att = _time(attention_only, steps, warmup)
+    attn_flops = 4.0 * TEST * TRAIN * D * HEADS * EST * BLOCKS
+    gemm_flops = 2.0 * EST * TEST * (W * W * 2 + 2 * W * FF) * BLOCKS + 2.0 * EST * TEST * (W * FF + FF * NCLS)
+    return [{"metric": "ms per cached ICL query stage (12 blocks: norm, Q projection, SSMax, attention, out-projection, "
+                       "feed-forward; final norm and decoder)", "value": round(ms, 3), "unit": "ms", "n_gpus": 1,
+             "steps": steps, "warmup": warmup, "higher_is_better": False, "vs_baseline": None, "dtype": "bf16",
+             "data": "synthetic rows and random weights (seed 6), cache from append_projected",
+             "config": {"workload": "C4 shape: 8 est x 5000 test rows, 12 blocks over 45000 cached train rows, width 512, "
+                                    "8 heads x 64, ff 1024, 10 classes"},
+             "attention_ms": round(ms_att, 3), "attention_share": round(ms_att / ms, 4),
+             "tflops": round((attn_flops + gemm_flops) / (ms * 1e-3) / 1e12, 1),
+             "context": "reference (TPU v5p): ICL stage of the no-cache forward 2.41 s (APPENDIX.md:93), whole "
+                        "cached-KV query 938.49 ms (best_model_forward_and_e2e.jsonl:2); not the same workload"}]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -589,9 +662,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-c3", action="store_true", help="default run: skip the C3 line printed before the headline")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer "
+                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer, icl_stage "
                          "(comma-separated) or all print the other BASELINE configs' lines, the fwd+bwd training "
-                         "lines, the folded first-ISAB lines and the ICL cache build / attention sub-layer lines")
+                         "lines, the folded first-ISAB lines, the ICL cache build / attention sub-layer lines and the "
+                         "cached ICL query stage (12 blocks with norms and feed-forward)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -601,7 +675,7 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
@@ -616,6 +690,8 @@ def main() -> int:
             recs += bench_hxf(args.steps, args.warmup)
         if configs & {"icl_layer", "all"}:
             recs += bench_icl_layer(args.steps, args.warmup)
+        if configs & {"icl_stage", "all"}:
+            recs += bench_icl_stage(args.steps, args.warmup)
         for rec in recs:
             print(json.dumps(rec), flush=True)
         return 0

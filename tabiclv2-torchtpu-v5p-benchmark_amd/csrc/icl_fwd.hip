@@ -21,6 +21,7 @@
 //                                        layout converted to bf16 in place (no shuffles)
 //    with the running max updated lazily (accumulators rescaled only when the tile max exceeds the
 //    running max by more than 2^8; exact because O and l always share the same reference max).
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -930,26 +931,36 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
   }
 }
 
-// Resident workgroups per CU of the kernel that carries the work (the pipelined one for bf16, d = 64).
+constexpr int ICL_DEV_CACHE = 64;
+
+// Resident workgroups per CU of the kernel that carries the work (the pipelined one for bf16, d = 64),
+// times the CU count of the current device: queried once per device and kernel, then cached.
 template <typename T, int NW, int QC, int D>
-int blocks_per_cu() {
-  int n = 0;
+int64_t resident_slots() {
+  static std::atomic<int64_t> cache[ICL_DEV_CACHE];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < ICL_DEV_CACHE) {
+    const int64_t hit = cache[dev].load(std::memory_order_relaxed);
+    if (hit > 0) return hit;
+  }
+  int cus = 0, n = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
   const hipError_t e =
       sizeof(T) == 2 && D == ICL_D
           ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel, IP_NW * 64, 0)
           : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC, D>, NW * 64, 0);
-  return e == hipSuccess && n > 0 ? n : 1;
+  const int64_t slots = (int64_t)cus * (e == hipSuccess && n > 0 ? n : 1);
+  if (dev >= 0 && dev < ICL_DEV_CACHE) cache[dev].store(slots, std::memory_order_relaxed);
+  return slots;
 }
 
 // Number of key splits that best fills whole rounds of resident workgroups:
 // minimises ceil(items * S / slots) / S over S = 1..4, each split keeping >= 8 key tiles.
 template <typename T, int NW, int QC, int D>
 int pick_splits(int64_t items, int64_t Tkv) {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 1;
-  const int64_t slots = (int64_t)cus * blocks_per_cu<T, NW, QC, D>();
+  const int64_t slots = resident_slots<T, NW, QC, D>();
+  if (slots <= 0) return 1;
   const int64_t tiles = (Tkv + ICL_KT - 1) / ICL_KT;
   int best = 1;
   double best_cost = (double)((items + slots - 1) / slots);

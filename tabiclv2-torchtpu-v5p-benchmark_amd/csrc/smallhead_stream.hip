@@ -32,6 +32,8 @@
 // exact powers of two. No test or branch runs per tile in the fast sweep.
 //
 // Key splits write fp32 partial (O, m, l) into a caller workspace; a merge kernel combines them.
+#include <atomic>
+
 #include "common.h"
 
 namespace {
@@ -399,24 +401,29 @@ __global__ __launch_bounds__(256) void ss_merge_kernel(SsParams p) {
   *(bf16x4*)(p.o + b * p.o_sb + (int64_t)qi * p.o_sr + d0) = ov;
 }
 
-int ss_blocks_per_cu() {
-  static int cached = 0;
-  if (cached > 0) return cached;
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, ss_stream_kernel, SS_NW * 64, 0) != hipSuccess || n < 1)
-    n = 1;
-  cached = n;
-  return n;
+// Resident streaming workgroups on the current device (CUs x workgroups per CU), queried once per
+// device and cached.
+int64_t ss_slots() {
+  static std::atomic<int64_t> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int64_t hit = cache[dev].load(std::memory_order_relaxed);
+    if (hit > 0) return hit;
+  }
+  int cus = 0, n = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, ss_stream_kernel, SS_NW * 64, 0) != hipSuccess || n < 1) n = 1;
+  const int64_t slots = (int64_t)cus * n;
+  if (dev >= 0 && dev < 64) cache[dev].store(slots, std::memory_order_relaxed);
+  return slots;
 }
 
 // Key splits: the fewest that bring the grid within a few percent of whole waves of workgroups
 // on the device, each split keeping at least SS_MIN_TILES tiles.
 int ss_pick_splits(int64_t items, int64_t Lk) {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 1;
-  const int64_t slots = (int64_t)cus * ss_blocks_per_cu();
+  const int64_t slots = ss_slots();
+  if (slots <= 0) return 1;
   const int64_t tiles = (Lk + SS_KT - 1) / SS_KT;
   int best = 1;
   double best_cost = (double)((items + slots - 1) / slots);

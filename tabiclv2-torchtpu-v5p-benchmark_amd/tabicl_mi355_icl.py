@@ -17,9 +17,8 @@ Replaces the reference's Splash path for the ICL stage:
 """
 from __future__ import annotations
 
-from typing import Optional, Union
-
-from typing import Callable
+from dataclasses import dataclass
+from typing import Callable, Optional, Union
 
 import torch
 import torch.nn.functional as F
@@ -296,23 +295,88 @@ class IclKVCache:
             raise ValueError(f"attention_layer expects x [{E}, Tq, {width}], got {tuple(x.shape)}")
         Tq = x.shape[1]
         q = F.linear(x, in_proj_weight[:width], None if in_proj_bias is None else in_proj_bias[:width])
-        q = q.view(E, Tq, H, D).transpose(1, 2)
+        q = q.view(E, Tq, H, D).transpose(1, 2)  # heads as a strided view: the kernel takes row strides
         if q_transform is not None:
             q = q_transform(q)
-        o = self.query(block, q.contiguous(), valid_kv_len)
-        o = o.transpose(1, 2).reshape(E, Tq, width)
+        attn_dtype = torch.promote_types(q.dtype, self.keys.dtype)
+        merged = torch.empty(E, Tq, H, D, dtype=attn_dtype, device=x.device)
+        self.query(block, q, valid_kv_len, out=merged.transpose(1, 2))  # written in merged-head order
+        o = merged.view(E, Tq, width)
         return F.linear(o, out_proj_weight.to(o.dtype), None if out_proj_bias is None else out_proj_bias.to(o.dtype))
+
+    def query_blocks(self, x: Tensor, blocks, valid_kv_len: Optional[Union[int, Tensor]] = None,  # noqa: ANN001
+                     q_transform: Optional[Callable[[Tensor], Tensor]] = None,
+                     activation: Callable[[Tensor], Tensor] = F.gelu) -> Tensor:
+        """The cached ICL query loop of the reference (scripts/tabicl_tpu_bucketed.py:803-817): test-row
+        representations x [E, Tq, width] through every block of the cache, each a pre-norm transformer
+        block (results/tpu_patch.diff:1454-1462, norm_first; SafeLayerNorm :1385-1397 normalises in its
+        weights' dtype and returns the input dtype) whose attention reads the block's cached K/V:
+            x = x + attention_layer(LN1(x)),   x = x + W2 act(W1 LN2(x) + b1) + b2.
+        blocks: one IclBlockWeights per cache block, in order. The GEMMs run in the weights' dtype (bf16
+        weights: the reference's bf16 autocast of the ICL stage) and the residual stream keeps x's dtype.
+        q_transform (RoPE / SSMax on q: upstream modules) is applied to every block's head-split q."""
+        if len(blocks) > self.keys.shape[1]:
+            raise ValueError(f"{len(blocks)} blocks of weights for a cache of {self.keys.shape[1]} blocks")
+        for b, w in enumerate(blocks):
+            h = _safe_layer_norm(x, w.ln1_w, w.ln1_b, w.eps, w.in_w.dtype)
+            x = x + self.attention_layer(b, h, w.in_w, w.in_b, w.out_w, w.out_b, valid_kv_len, q_transform).to(x.dtype)
+            h = _safe_layer_norm(x, w.ln2_w, w.ln2_b, w.eps, w.ff1_w.dtype)
+            x = x + F.linear(activation(F.linear(h, w.ff1_w, w.ff1_b)), w.ff2_w, w.ff2_b).to(x.dtype)
+        return x
 
     def block_kv(self, block: int):
         return self.keys[:, block], self.values[:, block]
 
-    def query(self, block: int, q: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None) -> Tensor:
-        """Attention of q [E, H, Tq, D] over block `block` of the cache (keys >= valid_kv_len masked;
-        default: the block's filled length, never the unwritten rows past it)."""
+    def query(self, block: int, q: Tensor, valid_kv_len: Optional[Union[int, Tensor]] = None,
+              out: Optional[Tensor] = None) -> Tensor:
+        """Attention of q [E, H, Tq, D] (any row / head / estimator strides, contiguous head dim) over
+        block `block` of the cache (keys >= valid_kv_len masked; default: the block's filled length, never
+        the unwritten rows past it); into `out` (any [E, H, Tq, D] view with a contiguous head dim) if given."""
         if valid_kv_len is None:
             valid_kv_len = self.default_valid(block)
         k, v = self.block_kv(block)
         # promote_types(q, cache) as in the reference's cached branch (results/tpu_patch.diff:314-317)
         attn_dtype = torch.promote_types(q.dtype, k.dtype)
         q, k, v = q.to(attn_dtype), k.to(attn_dtype), v.to(attn_dtype)
-        return icl_sdpa(q, k, v, valid_kv_len)
+        if out is None:
+            return icl_sdpa(q, k, v, valid_kv_len)
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        ICL_FWD_OUT(q, k, v, _valid_arg(valid_kv_len, k.shape[-2], q.device), float(q.shape[-1]) ** -0.5, out)
+        return out
+
+
+@dataclass
+class IclBlockWeights:
+    """Parameters of one ICL block (a pre-norm transformer encoder layer, results/tpu_patch.diff:1454-1462):
+    norm1 / norm2 LayerNorm weight and bias [width] (fp32 in the reference, SafeLayerNorm :1385-1397), the
+    packed in-projection [3 width, width] and bias, the out-projection [width, width] and bias, and the
+    feed-forward linear1 [ff, width] / linear2 [width, ff] with biases (ff = ff_factor x width; the
+    reference trains with ff_factor 2, scripts/train_stage1_optimized.py:205). Biases may be None."""
+    ln1_w: Tensor
+    ln1_b: Optional[Tensor]
+    in_w: Tensor
+    in_b: Optional[Tensor]
+    out_w: Tensor
+    out_b: Optional[Tensor]
+    ln2_w: Tensor
+    ln2_b: Optional[Tensor]
+    ff1_w: Tensor
+    ff1_b: Optional[Tensor]
+    ff2_w: Tensor
+    ff2_b: Optional[Tensor]
+    eps: float = 1e-5
+
+
+def _safe_layer_norm(x: Tensor, w: Tensor, b: Optional[Tensor], eps: float, out_dtype: torch.dtype) -> Tensor:
+    """LayerNorm over the last dim computed in the weights' dtype (results/tpu_patch.diff:1385-1397), the
+    result cast to the next GEMM's dtype."""
+    return F.layer_norm(x.to(w.dtype), (x.shape[-1],), w, b, eps).to(out_dtype)
+
+
+def _valid_arg(valid_kv_len, Tkv: int, device) -> Optional[Tensor]:  # noqa: ANN001
+    if isinstance(valid_kv_len, Tensor):
+        return valid_kv_len.to(device=device, dtype=torch.int32).reshape(-1).contiguous()
+    if valid_kv_len is not None and int(valid_kv_len) < Tkv:
+        return torch.full((1,), int(valid_kv_len), dtype=torch.int32, device=device)
+    return None
