@@ -219,3 +219,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Wait until at most N of this wave's vector-memory operations are outstanding (LDS operations:
 // none), then join the workgroup.
 #define TA_WAIT_JOIN(N) asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
+// Join the workgroup after this wave's LDS operations have completed, leaving its vector-memory
+// operations (copies into LDS, loads, stores) in flight: a barrier whose fence does not wait for them.
+#define TA_JOIN_LDS() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")

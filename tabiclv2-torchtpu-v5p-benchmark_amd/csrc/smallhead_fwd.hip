@@ -20,6 +20,9 @@
 //   S^T (16 keys x 16 queries) = K Q^T,  O^T (16 dims x 16 queries) += V^T P^T
 // so that the S^T accumulator is already the B operand of the PV product and every softmax
 // statistic of a query lives in the four lanes l%16 + 16j.
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
@@ -68,6 +71,9 @@ struct ShParams {
   // none): smallhead_fwd_kernel returns for them
   const int32_t* skip;
   int skip_n;
+  // persistent resident kernel: the q RoPE tables are staged in LDS rows of their own (cross
+  // attention with q tables other than the key tables) instead of reading the key rows' tables
+  int rp_qsep;
 };
 
 template <typename T, int KT> struct ShLds {
@@ -309,6 +315,10 @@ constexpr int RS_VSTR = SH_E + 16;  // V rows of 288 B: the transposed reads of 
 constexpr float RS_L_HI = 0x1p64f;
 constexpr float RS_L_LO = 0x1p-64f;
 
+// One rotated K element, x cos + x' sin with x' the signed partner dim, in one fixed rounding order
+// (both resident kernels use it, so they give the same bits).
+__device__ __forceinline__ float rs_rot(float x, float xp, float c, float s) { return __builtin_fmaf(xp, s, x * c); }
+
 // This lane's 8 dims of q (those of its B-operand k-slots) at byte offset off of the workgroup's q
 // rows. A buffer load: rows past Lq lie outside the resource and read as zero, and the compiler
 // keeps a load issued ahead of its use where it is (it does not merge these into the loop's phi).
@@ -479,6 +489,44 @@ __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 c
   return y;
 }
 
+// q' log2e operand for scales that are not folded into K (or short runs): q' = bf16(rope(q) scale)
+// rounded here from the raw q (with RoPE: this block's cos / sin of the lane's 4 dims), split over
+// the two k-halves.
+template <bool ROPE>
+__device__ __forceinline__ bf16x8 rs_qop_split(const ShParams& p, bf16x8 qr, f32x4 cs, f32x4 sn, int G) {
+  f32x4 qs;
+  if constexpr (!ROPE) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)((float)qr[(G >> 1) * 4 + j] * p.scale);
+  } else {
+    const f32x4 y = rs_rope_q(p, qr, cs, sn, G);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
+  }
+  return rs_qsplit(qs, G);
+}
+
+// The sweep of one 16-query block over all keys from its q' operand, the exact-maximum recompute
+// when l is out of range, and the normalised output (this lane's 4 dims, bf16).
+template <int NG, int MF, bool HALF>
+__device__ __forceinline__ u32x2 rs_finish(const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG], bf16x8 ones,
+                                          const float* lds_b2, bf16x8 qop, int G) {
+  f32x4 o;
+  float l;
+  rs_unit<NG, MF, false, HALF>(ka, va, ones, qop, lds_b2, G, 0.f, o, l);
+  if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
+    // rare: recompute with the exact maximum subtracted (queries in range keep theirs)
+    const float mx = rs_max<NG, MF, HALF>(ka, qop, lds_b2, G);
+    const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
+    rs_unit<NG, MF, true, HALF>(ka, va, ones, qop, lds_b2, G, sub, o, l);
+  }
+  const float inv = l == 0.f ? 0.f : __builtin_amdgcn_rcpf(l);
+  bf16x4 ov;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
+  return __builtin_bit_cast(u32x2, ov);
+}
+
 // One 16-query block of head g: q' operand from the raw q (and, with RoPE, its prefetched cos / sin),
 // one sweep over all keys, the exact-maximum recompute when l is out of range; returns the
 // normalised output (this lane's 4 dims, bf16).
@@ -499,36 +547,13 @@ __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[
     for (int j = 0; j < 4; ++j) y4[j] = (bf16)y[j];  // bf16(rope(q) scale) = bf16(rope(q)) scale
     qop = rs_pair8(y4, G);
   } else {
-    // other scales or short runs: q' = bf16(q scale) rounded here, log2e split over the two k-halves
-    f32x4 qs;
-    if (!ROPE) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)((float)qr[(G >> 1) * 4 + j] * p.scale);
-    } else {
-      const f32x4 y = rs_rope_q(p, qr, cs, sn, G);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
-    }
-    qop = rs_qsplit(qs, G);
+    qop = rs_qop_split<ROPE>(p, qr, cs, sn, G);
   }
   if constexpr (ROPE) {
     cs = rs_tab(crsrc, cnext);
     sn = rs_tab(srsrc, cnext);
   }
-  f32x4 o;
-  float l;
-  rs_unit<NG, MF, false, HALF>(ka, va, ones, qop, lds_b2, G, 0.f, o, l);
-  if (wave_any(!(l >= RS_L_LO && l <= RS_L_HI))) {
-    // rare: recompute with the exact maximum subtracted (queries in range keep theirs)
-    const float mx = rs_max<NG, MF, HALF>(ka, qop, lds_b2, G);
-    const float sub = (l >= RS_L_LO && l <= RS_L_HI) || !(mx > TA_NEG_INF) ? 0.f : mx;
-    rs_unit<NG, MF, true, HALF>(ka, va, ones, qop, lds_b2, G, sub, o, l);
-  }
-  const float inv = l == 0.f ? 0.f : __builtin_amdgcn_rcpf(l);
-  bf16x4 ov;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) ov[r] = (bf16)(o[r] * inv);
-  return __builtin_bit_cast(u32x2, ov);
+  return rs_finish<NG, MF, HALF>(ka, va, ones, lds_b2, qop, G);
 }
 
 // Every lane stores (the buffer range check drops rows past Lq): an unconditional store keeps the
@@ -624,7 +649,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
           for (int d = 0; d < SH_D; ++d) {
             // full-width forms only (the launcher sends others to smallhead_fwd_kernel)
             const float xp = p.rope == 1 ? ((d & 1) ? x[d - 1] : -x[d + 1]) : (d < 8 ? -x[d + 8] : x[d - 8]);
-            y[d] = x[d] * kc[j][d >> 2][d & 3] + xp * ks[j][d >> 2][d & 3];
+            y[d] = rs_rot(x[d], xp, kc[j][d >> 2][d & 3], ks[j][d >> 2][d & 3]);
           }
           bf16x8 o0, o1;
 #pragma unroll
@@ -733,6 +758,254 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
              ooff + i * ostep);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Persistent resident-keys kernel (bf16, Lk <= 128, at most 8 query blocks per batch element, no
+// per-batch row counts; RoPE only from the shared one-head tables): the row stage's 104-token self
+// attention and the CLS cross attention over many batch elements. The one-element-per-workgroup
+// kernel above waits for every element's K / V fill before it computes; here each workgroup stays
+// resident (two per CU) and walks the batch elements blockIdx.x, + gridDim.x, ...: the load unit
+// copies the next element's K and V rows global -> LDS (global_load_lds_dwordx4, no registers)
+// while the current element is computed from the register operands, which were read from LDS
+// before the copies were issued. Per element:
+//   wait for its copies, b2 into one of two LDS rows, barrier; with RoPE, rotate its K rows in LDS
+//   (tables staged once per workgroup), barrier; read head g's K and V^T operands; barrier; issue
+//   the next element's copies; then the same per-block sweep as the kernel above.
+// LDS (dynamic): K and V rows of 256 bytes with 16-byte chunks XOR-swizzled per row (K: by r & 7,
+// for the b128 operand reads of 8 rows; V: by 2 (r & 3), for the transposed reads of 4 rows x 2
+// chunks), b2 [2][NK], then the tables (16 cos + 16 sin floats per key row, and per query row when
+// the q tables are other tensors). Rows past the valid length are copied from the last valid row (so
+// they hold finite values) and masked by b2 = -inf; an element without valid keys writes zeros.
+// q comes by buffer loads two blocks ahead along the workgroup's stream of (element, block)
+// pairs, so the first two blocks of an element are loaded during the previous one.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ int rp_kchunk(int r, int c) { return r * 16 + (c ^ (r & 7)); }
+__device__ __forceinline__ int rp_vchunk(int r, int c) { return r * 16 + (c ^ ((r & 3) << 1)); }
+
+// LDS bytes of the persistent kernel for NK key rows (the tables only with RoPE).
+__host__ __device__ inline int rp_lds_bytes(int NK, bool rope, int Lk, int Lq, bool qsep) {
+  return 2 * NK * 256 + 2 * NK * 4 + (rope ? 128 * (Lk + (qsep ? Lq : 0)) : 0);
+}
+
+template <int NG, int MF, bool ROPE, bool HALF, int NB>
+__global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
+  constexpr int NT = SH_H * 64;
+  constexpr int NK = NG * 32;
+  extern __shared__ __attribute__((aligned(16))) unsigned char rp_lds[];
+  bf16* const lds_k = (bf16*)rp_lds;
+  bf16* const lds_v = (bf16*)(rp_lds + NK * 256);
+  float* const lds_b2 = (float*)(rp_lds + 2 * NK * 256);
+  float* const lds_tk = lds_b2 + 2 * NK;
+  float* const lds_tq = p.rp_qsep ? lds_tk + 32 * p.Lk : lds_tk;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = tid >> 6;
+  const int l16 = lane & 15, G = lane >> 4;
+  const int stride = gridDim.x;
+  const int nitems = (p.B - (int)blockIdx.x + stride - 1) / stride;  // >= 1 (grid <= B)
+  constexpr int nb = NB;  // query blocks per element (p.nqb)
+
+  // valid keys of element bb: a scalar load (the lengths do not change while the kernel runs), so
+  // that no wait for it also waits for the copies in flight
+  auto klen = [&](int bb) {
+    int lk = p.Lk;
+    if (p.valid) {
+      const int vl = ((const __attribute__((address_space(4))) int32_t*)p.valid)[p.valid_n == 1 ? 0 : bb];
+      lk = vl < 0 ? 0 : (vl < lk ? vl : lk);
+    }
+    return lk;
+  };
+  // the copies of element bb's NK K and V rows (rows >= lk from row lk - 1; lk >= 1): wave g copies
+  // the 4-row slabs g, g + 8, ...; lane: row 4 slab + lane / 16, LDS chunk lane % 16
+  auto issue = [&](int bb, int lk) {
+    const bf16* kb = (const bf16*)p.k + (int64_t)bb * p.k_sb;
+    const bf16* vb = (const bf16*)p.v + (int64_t)bb * p.v_sb;
+#pragma unroll
+    for (int s4 = 0; s4 < NG; ++s4) {
+      const int slab = g + 8 * s4, r = 4 * slab + (lane >> 4), pos = lane & 15;
+      const int rs = r < lk ? r : lk - 1;
+      lds_dma16_s((uint32_t)((rs * (int)p.k_sr + 8 * (pos ^ (r & 7))) * 2), kb, lds_addr(lds_k) + slab * 1024);
+      lds_dma16_s((uint32_t)((rs * (int)p.v_sr + 8 * (pos ^ ((r & 3) << 1))) * 2), vb,
+                  lds_addr(lds_v) + slab * 1024);
+    }
+  };
+  // this thread's key bias of element bb (threads < NK; keys past Lk read as zero through the
+  // buffer range check), loaded ahead of the element
+  auto bias_raw = [&](int bb) -> float {
+    if (!p.bias) return 0.f;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (float*)p.bias + (int64_t)bb * p.bias_sb, 0, p.Lk * 4, TA_BUF_WORD3);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (tid & (NK - 1)) * 4, 0, 0));
+  };
+  const int kcol = g * SH_D + 8 * (G & 1);
+  const int d4 = kcol + 4 * (G >> 1);
+  const int qoff = (l16 * (int)p.q_sr + kcol) * 2, qstep = 16 * (int)p.q_sr * 2;
+  const int ooff = (l16 * (int)p.o_sr + g * SH_D + 4 * G) * 2, ostep = 16 * (int)p.o_sr * 2;
+  // q of stream block t (element t / nb of this workgroup, block t % nb); past the last element the
+  // resource is empty and the load reads zeros
+  auto qload = [&](int t) {
+    const int it = t / nb, m = t - it * nb;
+    const int bb = (int)blockIdx.x + it * stride;
+    const int rows = it < nitems ? p.Lq : 0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (bf16*)p.q + (int64_t)(it < nitems ? bb : 0) * p.q_sb, 0, rows * (int)p.q_sr * 2, TA_BUF_WORD3);
+    int so = m * qstep;
+    asm volatile("" : "+s"(so));  // formed at the load, not hoisted into a register per block
+    return rs_qraw(rs, qoff + so);
+  };
+
+  int b = blockIdx.x;
+  int lk = klen(b);
+  if (lk > 0) issue(b, lk);
+  if constexpr (ROPE) {
+    // tables of the key rows (and of the query rows when they are other tensors), once per workgroup
+    for (int u = tid; u < 8 * p.Lk; u += NT) {
+      const int r = u >> 3, c = u & 7;
+      const float* src = (c < 4 ? p.ck : p.sk) + (int64_t)r * p.tab_sr + 4 * (c & 3);
+      *(f32x4*)(lds_tk + 32 * r + 4 * c) = *(const f32x4*)src;
+    }
+    if (p.rp_qsep) {
+      for (int u = tid; u < 8 * p.Lq; u += NT) {
+        const int r = u >> 3, c = u & 7;
+        const float* src = (c < 4 ? p.cq : p.sq) + (int64_t)r * p.tab_sr + 4 * (c & 3);
+        *(f32x4*)(lds_tq + 32 * r + 4 * c) = *(const f32x4*)src;
+      }
+    }
+  }
+  float braw = bias_raw(b);
+  bf16x8 qa = qload(0), qb = qload(1);
+  __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc((bf16*)p.o + (int64_t)b * p.o_sb, 0,
+                                                                 p.Lq * (int)p.o_sr * 2, TA_BUF_WORD3);
+  // a zero store to the first element's block 0 (which this wave rewrites later, in order): the
+  // element loop is then entered with the pending memory operations of its back edge (q, q, store)
+  rs_store(ors, u32x2{0u, 0u}, ooff);
+  bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  asm volatile("" : "+v"(ones));
+  const int tr_key = 4 * G + (l16 >> 2);
+  const int tr_c = 2 * g + ((l16 & 3) >> 1), tr_e = 4 * (l16 & 1);
+  bf16x8 ka[NG][2], va[NG];
+  int b2off = 0;  // the element's b2 row: lds_b2 + b2off
+
+  // Element set-up: its copies have landed (first element: everything; later ones: the copies are
+  // older than the previous element's last q load and output store, so all but the two youngest
+  // memory operations), b2, RoPE on K, operands, then the next element's copies.
+  auto setup = [&](int it, bf16x8& q0, bf16x8& q1) {
+    if (it == 0)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    float* b2 = lds_b2 + (it & 1) * NK;
+    if (tid < NK)
+      b2[tid] = tid < lk ? (p.bias ? fmaxf(braw * TA_LOG2E, SH_BIAS_FLOOR) : 0.f) : TA_NEG_INF;
+    b2off = (it & 1) * NK;
+    TA_JOIN_LDS();
+    if constexpr (ROPE) {
+      for (int u = tid; u < lk * SH_H; u += NT) {
+        const int r = u >> 3, hh = u & 7;
+        bf16x8* c0 = (bf16x8*)lds_k + rp_kchunk(r, 2 * hh);
+        bf16x8* c1 = (bf16x8*)lds_k + rp_kchunk(r, 2 * hh + 1);
+        const bf16x8 lo = *c0, hi = *c1;
+        const float* tc = lds_tk + 32 * r;
+        float x[SH_D], y[SH_D];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          x[d] = (float)lo[d];
+          x[8 + d] = (float)hi[d];
+        }
+#pragma unroll
+        for (int d = 0; d < SH_D; ++d) {
+          const float xp = p.rope == 1 ? ((d & 1) ? x[d - 1] : -x[d + 1]) : (d < 8 ? -x[d + 8] : x[d - 8]);
+          y[d] = rs_rot(x[d], xp, tc[d], tc[16 + d]);
+        }
+        bf16x8 o0, o1;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          o0[d] = (bf16)y[d];
+          o1[d] = (bf16)y[8 + d];
+        }
+        *c0 = o0;
+        *c1 = o1;
+      }
+      TA_JOIN_LDS();
+    }
+#pragma unroll
+    for (int kg = 0; kg < NG; ++kg) {
+      ka[kg][0] = *((const bf16x8*)lds_k + rp_kchunk(32 * kg + l16, 2 * g + (G & 1)));
+      ka[kg][1] = *((const bf16x8*)lds_k + rp_kchunk(32 * kg + 16 + l16, 2 * g + (G & 1)));
+      const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(lds_v + 8 * rp_vchunk(32 * kg + tr_key, tr_c) + tr_e));
+      const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(lds_v + 8 * rp_vchunk(32 * kg + 16 + tr_key, tr_c) + tr_e));
+      const bf16x4 a0 = __builtin_bit_cast(bf16x4, t0), a1 = __builtin_bit_cast(bf16x4, t1);
+      va[kg] = bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    }
+    ors = __builtin_amdgcn_make_buffer_rsrc((bf16*)p.o + (int64_t)b * p.o_sb, 0, p.Lq * (int)p.o_sr * 2,
+                                            TA_BUF_WORD3);
+    // the element's first two q blocks (one with a single block per element) were loaded during the
+    // previous ones: waited for here, before the next copies are issued (a wait after them would also
+    // wait for the copies)
+    if constexpr (NB >= 2)
+      asm volatile("" : "+v"(q0), "+v"(q1));
+    else
+      asm volatile("" : "+v"(q0));
+    TA_JOIN_LDS();  // every wave holds its operands: the K / V rows may be overwritten
+    const int bn = b + stride;
+    if (bn < p.B) {
+      const int lkn = klen(bn);
+      if (lkn > 0) issue(bn, lkn);
+      braw = bias_raw(bn);
+    }
+  };
+
+  // one block of the stream: q' operand (RoPE tables from LDS), sweep, store
+  auto block = [&](bf16x8 qr, int m) -> u32x2 {
+    if (lk == 0) return u32x2{0u, 0u};
+    f32x4 cs = {0.f, 0.f, 0.f, 0.f}, sn = cs;
+    if constexpr (ROPE) {
+      const int row = 16 * m + l16 < p.Lq ? 16 * m + l16 : p.Lq - 1;
+      cs = *(const f32x4*)(lds_tq + 32 * row + (d4 & 15));
+      sn = *(const f32x4*)(lds_tq + 32 * row + 16 + (d4 & 15));
+    }
+    const bf16x8 qop = rs_qop_split<ROPE>(p, qr, cs, sn, G);
+    // b2 is read inside each block, not hoisted over the element's blocks (registers)
+    int bo = b2off;
+    asm volatile("" : "+s"(bo));
+    return rs_finish<NG, MF, HALF>(ka, va, ones, lds_b2 + bo, qop, G);
+  };
+
+  // One element: set-up, then its blocks, each computing with q0 / q1 alternately and loading the
+  // block two ahead into the same register. After an odd block count the next element's block 0 is in
+  // q1 and block 1 in q0, so elements alternate the roles of qa and qb (no register moves).
+  auto element = [&](int it, bf16x8& q0, bf16x8& q1) {
+    setup(it, q0, q1);
+    const int t0 = it * NB;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+      bf16x8& qr = (m & 1) ? q1 : q0;
+      const u32x2 ov = block(qr, m);
+      qr = qload(t0 + m + 2);
+      int so = m * ostep;
+      asm volatile("" : "+s"(so));
+      rs_store(ors, ov, ooff + so);
+    }
+  };
+  auto next = [&]() {
+    b += stride;
+    lk = klen(b);
+  };
+#pragma unroll 1
+  for (int it = 0;; it += 2) {
+    element(it, qa, qb);
+    if (it + 1 == nitems) break;
+    next();
+    if constexpr (NB & 1)
+      element(it + 1, qb, qa);
+    else
+      element(it + 1, qa, qb);
+    if (it + 2 == nitems) break;
+    next();
+  }
+}
+
 // mode 0: b2 read for every group (key bias or per-batch valid lengths); 1: last group only (Lk not
 // a multiple of 32); 2: none.
 template <int NG, bool ROPE, bool EXACT>
@@ -778,6 +1051,68 @@ void launch_resident_rope(const ShParams& p, int ngrp, int mode, int64_t nblk, h
     case 3: launch_resident_ng<3, ROPE>(p, mode, nblk, stream); break;
     default: launch_resident_ng<4, ROPE>(p, mode, nblk, stream); break;
   }
+}
+
+// Compute units of the current device (cached per device; 0 if the query fails).
+constexpr int RP_DEV_CACHE = 64;
+int rp_cus() {
+  static std::atomic<int> cache[RP_DEV_CACHE];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < RP_DEV_CACHE) {
+    const int hit = cache[dev].load(std::memory_order_relaxed);
+    if (hit > 0) return hit;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+  if (dev >= 0 && dev < RP_DEV_CACHE) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// LDS bytes that still let two persistent workgroups share a CU (160 KB of LDS per CU).
+constexpr int RP_LDS_MAX = 80 * 1024;
+
+template <int MF, bool ROPE, int NB>
+int launch_persist_inst(const ShParams& p, int nwg, int lds, hipStream_t stream) {
+  const void* fn = (const void*)sh_persist_kernel<4, MF, ROPE, true, NB>;
+  static std::once_flag once;
+  std::call_once(once, [fn] {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, RP_LDS_MAX);
+  });
+  hipLaunchKernelGGL((sh_persist_kernel<4, MF, ROPE, true, NB>), dim3((unsigned)nwg), dim3(SH_H * 64),
+                     (unsigned)lds, stream, p);
+  return (int)hipGetLastError();
+}
+
+template <bool ROPE, int NB>
+int launch_persist_nb(const ShParams& p, int mode, int nwg, int lds, hipStream_t stream) {
+  return mode == 0 ? launch_persist_inst<0, ROPE, NB>(p, nwg, lds, stream)
+                   : launch_persist_inst<3, ROPE, NB>(p, nwg, lds, stream);
+}
+
+// The persistent kernel for a resident-keys call, or -1 when the call does not suit it (then the
+// one-element-per-workgroup kernel runs): 97..112 keys (the row stage's 104 tokens), 1 or 7 query
+// blocks per element (CLS queries, the row stage's self attention), no per-batch row counts, the
+// shared one-head RoPE tables (q tables equal to the key tables, or staged separately), 16-byte
+// aligned K / V rows, LDS for two workgroups per CU and at least two elements per workgroup.
+int launch_persist(ShParams& p, int ngrp, int mode, hipStream_t stream) {
+  if (ngrp != 4 || !p.half_last || mode == 2 || (p.nqb != 1 && p.nqb != 7) || p.qlen != nullptr ||
+      p.exact_scale)
+    return -1;
+  if (p.rope && p.tab_sr != SH_D) return -1;
+  if ((p.k_sr & 7) || (p.v_sr & 7) || ((uintptr_t)p.k & 15) || ((uintptr_t)p.v & 15)) return -1;
+  p.rp_qsep = p.rope && !(p.cq == p.ck && p.sq == p.sk && p.Lq <= p.Lk);
+  const int lds = rp_lds_bytes(128, p.rope != 0, p.Lk, p.Lq, p.rp_qsep != 0);
+  if (lds > RP_LDS_MAX) return -1;
+  const int cus = rp_cus();
+  if (cus <= 0) return -1;
+  const int nwg = 2 * cus;
+  if (p.B < 2 * nwg) return -1;
+  if (p.nqb == 1)
+    return p.rope ? launch_persist_nb<true, 1>(p, mode, nwg, lds, stream)
+                  : launch_persist_nb<false, 1>(p, mode, nwg, lds, stream);
+  return p.rope ? launch_persist_nb<true, 7>(p, mode, nwg, lds, stream)
+                : launch_persist_nb<false, 7>(p, mode, nwg, lds, stream);
 }
 
 void launch_resident(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStream_t stream) {
@@ -1030,6 +1365,7 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   p.half_last = 0;
   p.qlen = qlen; p.qlen_n = (int)qlen_n;
   p.skip = gated ? pvalid + pn : nullptr; p.skip_n = (int)pn;
+  p.rp_qsep = 0;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   const bool fast_rope = rope == 0 || (rope == 1 && rot == 16) || (rope == 2 && half == 8 && rot == 16);
   // the resident kernel's buffer loads take 32-bit byte offsets within a batch element (query runs
@@ -1053,6 +1389,9 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
     const int ngrp = (int)((Lk + 31) / 32);  // 32-key groups every batch element sweeps
     p.half_last = Lk - 32 * (ngrp - 1) <= 16;
     const int mode = (bias || valid) ? 0 : (Lk == 32 * ngrp ? 2 : 1);
+    p.rp_qsep = 0;
+    const int st = launch_persist(p, ngrp, mode, stream);
+    if (st >= 0) return st;
     launch_resident(p, ngrp, mode, nblk, stream);
     return (int)hipGetLastError();
   }

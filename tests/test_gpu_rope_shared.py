@@ -65,3 +65,59 @@ def test_pk_cross_shared_tables_cls(dev):
     shared = pk.PK_CROSS(q, kv, none, cqs, sqs, cks, sks, 8, 128, 4, rcs, half, r, 0, 0.25)
     torch.cuda.synchronize()
     assert torch.equal(full, shared)
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk,dtype", [
+    ("general_bf16", 4, 200, 300, torch.bfloat16),  # keys past the resident limit
+    ("fp32", 4, 100, 200, torch.float32),
+])
+def test_pk_cross_shared_tables_general(dev, name, B, Lq, Lk, dtype):
+    import tabicl_mi355_attn as pk
+    g = torch.Generator().manual_seed(23)
+    q = (torch.randn(B, Lq, 128, generator=g) * 0.5).to(dtype).to(dev)
+    kv = torch.randn(B, Lk, 256, generator=g).to(dtype).to(dev)
+    rope = _Rope(False)
+    cq, sq, rc, half, r = pk.rope_tables(rope, Lq, 128, 8, dev)
+    ck, sk, _, _, _ = pk.rope_tables(rope, Lk, 128, 8, dev)
+    none = torch.empty(0, device=dev)
+    lkp = -(-Lk // 128) * 128
+    bq = pk._pick_bq(Lq, lkp)
+    prec = pk._fp32_prec_code() if dtype == torch.float32 else 0
+    full = pk.PK_CROSS(q, kv, none, cq, sq, ck, sk, 8, lkp, bq, rc, half, r, prec, 0.25)
+    cqs, sqs, _ = pk._shared_tables(cq, sq, rc, 16)
+    cks, sks, rcs = pk._shared_tables(ck, sk, rc, 16)
+    shared = pk.PK_CROSS(q, kv, none, cqs, sqs, cks, sks, 8, lkp, bq, rcs, half, r, prec, 0.25)
+    torch.cuda.synchronize()
+    assert torch.equal(full, shared), name
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk,dtype,q_len", [
+    ("resident_cls", 6, 40, 104, torch.bfloat16, [0, 1, 17, 40, 100, 16]),
+    ("general_bf16", 3, 200, 300, torch.bfloat16, [200, 77, 0]),
+    ("fp32", 3, 100, 128, torch.float32, [3, 100, 64]),
+])
+def test_pk_cross_ragged_with_rope(dev, name, B, Lq, Lk, dtype, q_len):
+    # a ragged call with a RoPE module: the live rows are bit-identical to the plain call (both read the
+    # shared tables), and the plain call matches the oracle on batch 0 (2e-2 bf16, 1e-4 fp32)
+    import numpy as np
+
+    import tabicl_mi355_attn as pk
+    from oracle import attention as O
+    g = torch.Generator().manual_seed(24)
+    q = (torch.randn(B, Lq, 128, generator=g) * 0.5).to(dtype).to(dev)
+    kv = torch.randn(B, Lk, 256, generator=g).to(dtype).to(dev)
+    rope = _Rope(False)
+    with torch.no_grad():
+        ref = pk.pk_cross_attention(q, kv, 8, None, rope, 0.25)
+        out = pk.pk_cross_attention(q, kv, 8, None, rope, 0.25, q_len=torch.tensor(q_len, dtype=torch.int32,
+                                                                                    device=dev))
+    torch.cuda.synchronize()
+    for b in range(B):
+        n = min(q_len[b], Lq)
+        assert torch.equal(out[b, :n], ref[b, :n]), (name, b)
+    freqs = rope.freqs.double().numpy()
+    rq = O.rope_tables_ref(freqs, Lq, 128, 8, False)
+    rk = O.rope_tables_ref(freqs, Lk, 128, 8, False)
+    exp = O.pk_cross_ref(q[:1].cpu(), kv[:1].cpu(), 8, None, rq, rk, 0.25)
+    err = float(np.abs(ref[:1].double().cpu().numpy() - exp).max())
+    assert err <= (2e-2 if dtype == torch.bfloat16 else 1e-4), (name, err)
