@@ -955,18 +955,23 @@ int64_t resident_slots() {
   return slots;
 }
 
-// Number of key splits that best fills whole rounds of resident workgroups:
-// minimises ceil(items * S / slots) / S over S = 1..4, each split keeping >= 8 key tiles.
+// Number of key splits that best fills whole rounds of resident workgroups: minimises
+// ceil(items * S / slots) * (tiles / S + F) over S = 1..4, each split keeping >= 8 key tiles. F is
+// a work item's fixed cost in key tiles (q loads, the first tiles in flight, the softmax reference,
+// the epilogue); measured on the box, a split of a short key range does not pay for it: with F = 12
+// C5's 2k- and 8k-key buckets run unsplit (0.41 -> 0.29 ms and 1.35 -> 1.19 ms per launch) while C4
+// (703 tiles, 1280 items) keeps two splits.
 template <typename T, int NW, int QC, int D>
 int pick_splits(int64_t items, int64_t Tkv) {
   const int64_t slots = resident_slots<T, NW, QC, D>();
   if (slots <= 0) return 1;
   const int64_t tiles = (Tkv + ICL_KT - 1) / ICL_KT;
+  constexpr double fixed = 12.0;
   int best = 1;
-  double best_cost = (double)((items + slots - 1) / slots);
+  double best_cost = (double)((items + slots - 1) / slots) * ((double)tiles + fixed);
   for (int s = 2; s <= 4; ++s) {
     if (tiles / s < 8) break;
-    const double cost = (double)((items * s + slots - 1) / slots) / s;
+    const double cost = (double)((items * s + slots - 1) / slots) * ((double)tiles / s + fixed);
     if (cost < best_cost - 1e-9) { best = s; best_cost = cost; }
   }
   return best;

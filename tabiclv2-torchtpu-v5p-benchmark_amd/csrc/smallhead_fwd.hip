@@ -21,7 +21,6 @@
 // so that the S^T accumulator is already the B operand of the PV product and every softmax
 // statistic of a query lives in the four lanes l%16 + 16j.
 #include <atomic>
-#include <mutex>
 
 #include "common.h"
 #include "launch.h"
@@ -1053,12 +1052,10 @@ void launch_resident_rope(const ShParams& p, int ngrp, int mode, int64_t nblk, h
   }
 }
 
-// Compute units of the current device (cached per device; 0 if the query fails).
+// Compute units of device dev (cached per device; 0 if the query fails).
 constexpr int RP_DEV_CACHE = 64;
-int rp_cus() {
+int rp_cus(int dev) {
   static std::atomic<int> cache[RP_DEV_CACHE];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (dev >= 0 && dev < RP_DEV_CACHE) {
     const int hit = cache[dev].load(std::memory_order_relaxed);
     if (hit > 0) return hit;
@@ -1073,21 +1070,23 @@ int rp_cus() {
 constexpr int RP_LDS_MAX = 80 * 1024;
 
 template <int MF, bool ROPE, int NB>
-int launch_persist_inst(const ShParams& p, int nwg, int lds, hipStream_t stream) {
-  const void* fn = (const void*)sh_persist_kernel<4, MF, ROPE, true, NB>;
-  static std::once_flag once;
-  std::call_once(once, [fn] {
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, RP_LDS_MAX);
-  });
+int launch_persist_inst(const ShParams& p, int dev, int nwg, int lds, hipStream_t stream) {
+  // the dynamic-LDS limit of this instance, raised once per device
+  static std::atomic<bool> raised[RP_DEV_CACHE];
+  if (dev >= 0 && dev < RP_DEV_CACHE && !raised[dev].load(std::memory_order_relaxed)) {
+    (void)hipFuncSetAttribute((const void*)sh_persist_kernel<4, MF, ROPE, true, NB>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, RP_LDS_MAX);
+    raised[dev].store(true, std::memory_order_relaxed);
+  }
   hipLaunchKernelGGL((sh_persist_kernel<4, MF, ROPE, true, NB>), dim3((unsigned)nwg), dim3(SH_H * 64),
                      (unsigned)lds, stream, p);
   return (int)hipGetLastError();
 }
 
 template <bool ROPE, int NB>
-int launch_persist_nb(const ShParams& p, int mode, int nwg, int lds, hipStream_t stream) {
-  return mode == 0 ? launch_persist_inst<0, ROPE, NB>(p, nwg, lds, stream)
-                   : launch_persist_inst<3, ROPE, NB>(p, nwg, lds, stream);
+int launch_persist_nb(const ShParams& p, int dev, int mode, int nwg, int lds, hipStream_t stream) {
+  return mode == 0 ? launch_persist_inst<0, ROPE, NB>(p, dev, nwg, lds, stream)
+                   : launch_persist_inst<3, ROPE, NB>(p, dev, nwg, lds, stream);
 }
 
 // The persistent kernel for a resident-keys call, or -1 when the call does not suit it (then the
@@ -1104,15 +1103,17 @@ int launch_persist(ShParams& p, int ngrp, int mode, hipStream_t stream) {
   p.rp_qsep = p.rope && !(p.cq == p.ck && p.sq == p.sk && p.Lq <= p.Lk);
   const int lds = rp_lds_bytes(128, p.rope != 0, p.Lk, p.Lq, p.rp_qsep != 0);
   if (lds > RP_LDS_MAX) return -1;
-  const int cus = rp_cus();
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  const int cus = rp_cus(dev);
   if (cus <= 0) return -1;
   const int nwg = 2 * cus;
   if (p.B < 2 * nwg) return -1;
   if (p.nqb == 1)
-    return p.rope ? launch_persist_nb<true, 1>(p, mode, nwg, lds, stream)
-                  : launch_persist_nb<false, 1>(p, mode, nwg, lds, stream);
-  return p.rope ? launch_persist_nb<true, 7>(p, mode, nwg, lds, stream)
-                : launch_persist_nb<false, 7>(p, mode, nwg, lds, stream);
+    return p.rope ? launch_persist_nb<true, 1>(p, dev, mode, nwg, lds, stream)
+                  : launch_persist_nb<false, 1>(p, dev, mode, nwg, lds, stream);
+  return p.rope ? launch_persist_nb<true, 7>(p, dev, mode, nwg, lds, stream)
+                : launch_persist_nb<false, 7>(p, dev, mode, nwg, lds, stream);
 }
 
 void launch_resident(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStream_t stream) {
