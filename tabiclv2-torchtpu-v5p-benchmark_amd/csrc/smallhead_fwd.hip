@@ -758,9 +758,10 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Persistent resident-keys kernel (bf16, Lk <= 128, at most 8 query blocks per batch element, no
-// per-batch row counts; RoPE only from the shared one-head tables): the row stage's 104-token self
-// attention and the CLS cross attention over many batch elements. The one-element-per-workgroup
+// Persistent resident-keys kernel (bf16, 97..112 keys: four 32-key groups, the last one half; NB = 1
+// or 7 query blocks per batch element; no per-batch row counts; RoPE only from the shared one-head
+// tables): the row stage's 104-token self attention and the CLS cross attention over many batch
+// elements. The one-element-per-workgroup
 // kernel above waits for every element's K / V fill before it computes; here each workgroup stays
 // resident (two per CU) and walks the batch elements blockIdx.x, + gridDim.x, ...: the load unit
 // copies the next element's K and V rows global -> LDS (global_load_lds_dwordx4, no registers)
