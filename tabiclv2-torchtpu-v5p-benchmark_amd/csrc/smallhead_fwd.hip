@@ -533,9 +533,8 @@ __device__ __forceinline__ u32x2 rs_finish(const bf16x8 (&ka)[NG][2], const bf16
 // cnext) on return: reloaded as soon as the q' operand is built, a block of work ahead of their use.
 template <int NG, int MF, bool ROPE, bool EXACT, bool HALF>
 __device__ __forceinline__ u32x2 rs_block(const ShParams& p, const bf16x8 (&ka)[NG][2], const bf16x8 (&va)[NG],
-                                         bf16x8 ones, const float* lds_b2, const bf16* qbase, bf16x8 qr, f32x4& cs,
-                                         f32x4& sn, __amdgpu_buffer_rsrc_t crsrc, __amdgpu_buffer_rsrc_t srsrc,
-                                         int cnext, int qi, int d4, int G) {
+                                         bf16x8 ones, const float* lds_b2, bf16x8 qr, f32x4& cs, f32x4& sn,
+                                         __amdgpu_buffer_rsrc_t crsrc, __amdgpu_buffer_rsrc_t srsrc, int cnext, int G) {
   bf16x8 qop;
   if (EXACT && !ROPE) {
     qop = qr;  // q' = q scale exactly: scale and log2e ride on the K operand
@@ -741,19 +740,19 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   int i = 0;
 #pragma unroll 1
   for (; i + 1 < nb; i += 2) {
-    u32x2 ov = rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
-                                              coff + (i + 1) * cstep, orow + i * 16 + l16, d4, G);
+    u32x2 ov = rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qa, cs, sn, crsrc, srsrc,
+                                              coff + (i + 1) * cstep, G);
     qa = rs_qraw(qrsrc, qoff + (i + 2) * qstep);
     rs_store(orsrc, ov, ooff + i * ostep);
-    ov = rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qbase, qb, cs, sn, crsrc, srsrc,
-                                       coff + (i + 2) * cstep, orow + (i + 1) * 16 + l16, d4, G);
+    ov = rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qb, cs, sn, crsrc, srsrc,
+                                       coff + (i + 2) * cstep, G);
     qb = rs_qraw(qrsrc, qoff + (i + 3) * qstep);
     rs_store(orsrc, ov, ooff + (i + 1) * ostep);
   }
   if (i < nb)
     rs_store(orsrc,
-             rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qbase, qa, cs, sn, crsrc, srsrc,
-                                           coff + (i + 1) * cstep, orow + i * 16 + l16, d4, G),
+             rs_block<NG, MF, ROPE, EXACT, HALF>(p, ka, va, ones, lds_b2, qa, cs, sn, crsrc, srsrc,
+                                           coff + (i + 1) * cstep, G),
              ooff + i * ostep);
 }
 
