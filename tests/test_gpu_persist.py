@@ -159,3 +159,58 @@ def test_repeat_calls_identical(dev):
         b = pk.pk_self_attention(x, H, None, rope, 0.25)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_pk_cross_cls_rope_with_feature_mask(dev):
+    # the CLS queries as the row stage runs them: a per-sequence key mask over the padded feature slots
+    # (finfo.min, results/tpu_patch.diff:1253-1271) on top of RoPE
+    import tabicl_mi355_attn as pk
+    g = torch.Generator().manual_seed(95)
+    B, Lq, Lk = 4100, 4, 104
+    q = (torch.randn(B, Lq, E, generator=g) * 0.5).to(torch.bfloat16)
+    kv = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
+    kb = torch.zeros(B, Lk)
+    real = torch.randint(1, Lk + 1, (B,), generator=g)
+    for b in range(B):
+        kb[b, int(real[b]):] = float(torch.finfo(torch.float32).min)
+    rope = _Rope(False)
+    qd, kvd, kbd = q.to(dev), kv.to(dev), kb.to(dev)
+    print("[persist] pk_cross cls masked", flush=True)
+    with torch.no_grad():
+        out = pk.pk_cross_attention(qd, kvd, H, kbd, rope, 0.25)
+        cq, sq, rc, half, r = pk.rope_tables(rope, Lq, E, H, dev)
+        ck, sk, _, _, _ = pk.rope_tables(rope, Lk, E, H, dev)
+        tiled = pk.PK_CROSS(qd, kvd, pk._bias_arg(kbd, (B,), Lk, dev), cq, sq, ck, sk, H, 128, 4, rc, half, r, 0,
+                            0.25)
+    torch.cuda.synchronize()
+    assert torch.equal(out, tiled)
+    for b in _sample(B):
+        ref = O.pk_cross_ref(q[b:b + 1], kv[b:b + 1], H, kb[b:b + 1], _rope_np(rope, Lq), _rope_np(rope, Lk), 0.25)
+        assert _err(out[b:b + 1], ref) <= TOL, b
+
+
+def test_hxq_short_keys_valid_and_key_mask(dev):
+    # both a per-element valid length and a per-element key mask (random terms and finfo.min entries)
+    import tabicl_mi355_attn as pk
+    g = torch.Generator().manual_seed(96)
+    B, Lq, Lk = 4100, 16, 104
+    q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16)
+    kv = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
+    valid = torch.randint(1, Lk + 1, (B,), generator=g).to(torch.int32)
+    kb = torch.randn(B, Lk, generator=g)
+    kb[torch.rand(B, Lk, generator=g) < 0.1] = float(torch.finfo(torch.float32).min)
+    kb[:, 0] = 0.0  # one finite key per row (a fully masked row has no defined softmax in fp64)
+    for b in range(B):
+        kv[b, int(valid[b]):] = float("nan")
+    qd, kvd, vd, kbd = q.to(dev), kv.to(dev), valid.to(dev), kb.to(dev)
+    print("[persist] hxq valid + mask", flush=True)
+    out = pk.hxq_attention(qd, kvd, vd, H, kbd)
+    part = pk.hxq_attention(qd[:300], kvd[:300], vd[:300], H, kbd[:300])
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out[:300], part)
+    for b in _sample(B):
+        vb = int(valid[b])
+        ref = O.attention_f64(q[b:b + 1].double().numpy(), kv[b:b + 1, :vb, :E].double().numpy(),
+                              kv[b:b + 1, :vb, E:].double().numpy(), H, kb[b:b + 1, :vb].double().numpy())
+        assert _err(out[b:b + 1], ref) <= TOL, b
