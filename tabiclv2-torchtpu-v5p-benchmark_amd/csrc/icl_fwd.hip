@@ -933,45 +933,63 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
 
 constexpr int ICL_DEV_CACHE = 64;
 
-// Resident workgroups per CU of the kernel that carries the work (the pipelined one for bf16, d = 64),
-// times the CU count of the current device: queried once per device and kernel, then cached.
+// CUs of the current device and resident workgroups per CU of the kernel that carries the work (the
+// pipelined one for bf16, d = 64): queried once per device and kernel, then cached (cus * 256 + per_cu).
+struct Residency {
+  int64_t cus, per_cu;
+};
 template <typename T, int NW, int QC, int D>
-int64_t resident_slots() {
+Residency residency() {
   static std::atomic<int64_t> cache[ICL_DEV_CACHE];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipGetDevice(&dev) != hipSuccess) return {0, 0};
   if (dev >= 0 && dev < ICL_DEV_CACHE) {
     const int64_t hit = cache[dev].load(std::memory_order_relaxed);
-    if (hit > 0) return hit;
+    if (hit > 0) return {hit >> 8, hit & 255};
   }
   int cus = 0, n = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return {0, 0};
   const hipError_t e =
       sizeof(T) == 2 && D == ICL_D
           ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel, IP_NW * 64, 0)
           : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC, D>, NW * 64, 0);
-  const int64_t slots = (int64_t)cus * (e == hipSuccess && n > 0 ? n : 1);
-  if (dev >= 0 && dev < ICL_DEV_CACHE) cache[dev].store(slots, std::memory_order_relaxed);
-  return slots;
+  const int64_t per_cu = e == hipSuccess && n > 0 ? (n < 255 ? n : 255) : 1;
+  if (dev >= 0 && dev < ICL_DEV_CACHE) cache[dev].store((int64_t)cus * 256 + per_cu, std::memory_order_relaxed);
+  return {cus, per_cu};
 }
 
-// Number of key splits that best fills whole rounds of resident workgroups: minimises
-// ceil(items * S / slots) * (tiles / S + F) over S = 1..4, each split keeping >= 8 key tiles. F is
-// a work item's fixed cost in key tiles (q loads, the first tiles in flight, the softmax reference,
-// the epilogue); measured on the box, a split of a short key range does not pay for it: with F = 12
-// C5's 2k- and 8k-key buckets run unsplit (0.41 -> 0.29 ms and 1.35 -> 1.19 ms per launch) while C4
-// (703 tiles, 1280 items) keeps two splits.
+// Number of key splits S = 1..4 (each keeping >= 8 key tiles) with the least modelled time, in
+// units of one key tile of one work item at full occupancy:
+//  - W = items S work items of u = tiles / S + F tiles; F = 12 is a work item's fixed cost (q loads,
+//    the first tiles in flight, the softmax reference, the epilogue);
+//  - each full round of R C items (C CUs, R resident per CU) takes R u; a last partial round takes
+//    R u when some CU holds R of its items, else k u / 0.9 with k = its most items on one CU: fewer
+//    workgroups on a CU each run faster, at 0.9 of the CU's full-occupancy throughput for one
+//    (icl_pipe_kernel at C4: 42.09 ms per query at one workgroup per CU, 38.33 ms at two);
+//  - each split beyond the first adds 3.5% for its partial results and the merge.
+// Measured on one box, splits pay only when the grid would leave CUs idle: C4 (703 tiles, 1280
+// items) runs 38.33 ms unsplit and 38.90 / 39.13 ms at 2 / 4 splits, and every bucket of C5's ICL
+// leg runs fastest unsplit (43.07 ms per step against 51.1 - 60.2 ms at 2 - 4 splits).
+double split_time(int64_t W, double u, int64_t C, int64_t R) {
+  const int64_t per_round = C * R, full = W / per_round, rem = W % per_round;
+  double t = (double)full * R * u;
+  if (rem > 0) {
+    const int64_t k = (rem + C - 1) / C;
+    t += k >= R ? R * u : k * u / 0.9;
+  }
+  return t;
+}
 template <typename T, int NW, int QC, int D>
 int pick_splits(int64_t items, int64_t Tkv) {
-  const int64_t slots = resident_slots<T, NW, QC, D>();
-  if (slots <= 0) return 1;
+  const Residency r = residency<T, NW, QC, D>();
+  if (r.cus <= 0) return 1;
   const int64_t tiles = (Tkv + ICL_KT - 1) / ICL_KT;
   constexpr double fixed = 12.0;
   int best = 1;
-  double best_cost = (double)((items + slots - 1) / slots) * ((double)tiles + fixed);
+  double best_cost = split_time(items, (double)tiles + fixed, r.cus, r.per_cu);
   for (int s = 2; s <= 4; ++s) {
     if (tiles / s < 8) break;
-    const double cost = (double)((items * s + slots - 1) / slots) * ((double)tiles / s + fixed);
+    const double cost = split_time(items * s, (double)tiles / s + fixed, r.cus, r.per_cu) * (1.0 + 0.035 * (s - 1));
     if (cost < best_cost - 1e-9) { best = s; best_cost = cost; }
   }
   return best;

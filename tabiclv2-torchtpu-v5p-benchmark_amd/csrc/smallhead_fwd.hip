@@ -431,7 +431,8 @@ __device__ __forceinline__ void rs_unit(const bf16x8 (&ka)[NG][2], const bf16x8 
       pv[r] = (bf16)__builtin_amdgcn_exp2f(SUB ? x0[r] - sub : x0[r]);
       pv[4 + r] = half ? (bf16)0.f : (bf16)__builtin_amdgcn_exp2f(SUB ? x1[r] - sub : x1[r]);
     }
-    l += rs_sum(ones, pv);
+    const float sk = rs_sum(ones, pv);
+    l = kg == 0 ? sk : l + sk;  // sums are >= +0: the first needs no add
     o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kg], pv, o, 0, 0, 0);
     // keep the groups apart: hoisting every group's scores first costs registers
     __builtin_amdgcn_sched_barrier(0);
