@@ -104,6 +104,19 @@ def test_icl_cache_append_and_query(dev):
         cache.append(0, ks[0].to(dev), vs[0].to(dev), row0=400)  # past capacity
 
 
+def test_icl_split_choice(dev):
+    # the launcher splits keys only when the grid would leave CUs idle (workspace = flags + prefix view,
+    # plus fp32 partials [S][N*H*Tq][66] when S > 1): a C4 block launch (8 x 8 heads x 20 query blocks =
+    # 1280 work items on 256 CUs) runs unsplit; one estimator's 160 work items over 45k keys split
+    import tabicl_mi355_native as nat
+    lib = nat.load()
+    c4 = lib.tabicl_icl_workspace_bytes(8, 8, 5000, 45000, 64, 0)
+    assert c4 == (1280 * 4 + 255) // 256 * 256 + 256  # flags + prefix view, no partials
+    one = lib.tabicl_icl_workspace_bytes(1, 8, 5000, 45000, 64, 0)
+    split = {s: (160 * s * 4 + 255) // 256 * 256 + 256 + s * 8 * 5000 * 66 * 4 for s in (2, 3, 4)}
+    assert one in split.values(), (one, split)
+
+
 def test_icl_split_matches_unsplit(dev):
     # the key-split path (workspace given) and the single-pass path (no workspace) agree; ragged
     # valid lengths leave some splits empty
