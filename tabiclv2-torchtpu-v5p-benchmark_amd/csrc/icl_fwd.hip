@@ -64,6 +64,9 @@ struct IclParams {
   const int32_t* pvalid;
   const int32_t* pok;
   int pn;
+  // ragged calls of the pipelined kernel: [count, work items...] of the work items that hold a live
+  // query row, in work-item order (written by icl_live_list_kernel; null: every work item is run)
+  const int32_t* live;
 };
 
 __device__ __forceinline__ int icl_live_rows(const IclParams& p, int n) {
@@ -732,7 +735,21 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
   __shared__ __attribute__((aligned(1024))) bf16 lds[IP_NBUF][IP_TILE];
   __shared__ int wg_bad;
 
-  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  int work;
+  if (p.live) {
+    // ragged call: the listed (live) work items, each XCD a contiguous, equal share of the list (the
+    // work items of one (n, h) stay together, for L2), workgroups past the share exit at once. The
+    // padded grid's order would interleave live and empty work items, and the dispatcher's
+    // placement then leaves part of the CUs with the live ones (C5's small buckets ran 2.4x slower
+    // than a call of the live rows alone).
+    const int cnt = p.live[0];
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int q8 = cnt >> 3, r8 = cnt & 7;
+    if (j >= q8 + (xcd < r8 ? 1 : 0)) return;  // no flag written: icl_fwd_kernel checks the rows first
+    work = p.live[1 + xcd * q8 + (xcd < r8 ? xcd : r8) + j];
+  } else {
+    work = xcd_remap(blockIdx.x, gridDim.x);
+  }
   const int qb = work % p.nqb;
   const int rest = work / p.nqb;
   const int split = rest % p.nsplit;
@@ -995,10 +1012,64 @@ int pick_splits(int64_t items, int64_t Tkv) {
   return best;
 }
 
+constexpr int ICL_LIST_MAXN = 8192;  // batch elements the live list takes (per-element counts in LDS)
+
+// Live work items of a ragged call of the pipelined kernel (one workgroup of 1024 threads): per batch
+// element n its H * nsplit * ceil(live rows / 256) work items, listed in work-item order
+// ((n * H + h) * nsplit + split) * nqb + qb after the count. Per-element counts are scanned in LDS
+// (each thread a run of up to 8 elements, then a scan of the 1024 run totals); every list entry
+// finds its element by binary search over the scanned counts.
+__global__ __launch_bounds__(1024) void icl_live_list_kernel(IclParams p, int32_t* list) {
+  __shared__ int pre[ICL_LIST_MAXN + 1];
+  __shared__ int tot[1024];
+  const int tid = threadIdx.x;
+  const int per = p.H * p.nsplit, qbr = IP_QW * IP_NW;
+  constexpr int RUN = ICL_LIST_MAXN / 1024;
+  int acc = 0;
+  int c[RUN];
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) {
+    const int n = tid * RUN + i;
+    c[i] = n < p.N ? per * ((icl_live_rows(p, n) + qbr - 1) / qbr) : 0;
+    acc += c[i];
+  }
+  tot[tid] = acc;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan of the run totals
+    const int x = tid >= d ? tot[tid - d] : 0;
+    __syncthreads();
+    tot[tid] += x;
+    __syncthreads();
+  }
+  int run0 = tid == 0 ? 0 : tot[tid - 1];
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) {
+    const int n = tid * RUN + i;
+    if (n <= p.N) pre[n] = run0;
+    run0 += c[i];
+  }
+  __syncthreads();
+  const int total = pre[p.N];
+  for (int t = tid; t < total; t += 1024) {
+    int lo = 0, hi = p.N;  // pre[lo] <= t < pre[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pre[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int n = lo, j = t - pre[n];
+    const int lq = (pre[n + 1] - pre[n]) / per;  // live query blocks of n (>= 1 here)
+    const int h = j / (p.nsplit * lq), rem = j % (p.nsplit * lq);
+    list[1 + t] = ((n * p.H + h) * p.nsplit + rem / lq) * p.nqb + rem % lq;
+  }
+  if (tid == 0) list[0] = total;
+}
+
 // Workspace layout: [per-work-item flags, bf16 d = 64 only, 256-byte aligned][prefix view of a key
-// mask, bf16 d = 64 only: valid [N], ok [N], 256-byte aligned][split partials: O fp32
-// [nsplit][rows][D], (m, l) [nsplit][rows][2]].
+// mask, bf16 d = 64 only: valid [N], ok [N], 256-byte aligned][live work-item list of ragged calls,
+// bf16 d = 64 only: count, items, 256-byte aligned][split partials: O fp32 [nsplit][rows][D], (m, l)
+// [nsplit][rows][2]].
 int64_t flag_bytes(int64_t nblk) { return (nblk * 4 + 255) / 256 * 256; }
+int64_t list_bytes(int64_t nblk) { return ((nblk + 1) * 4 + 255) / 256 * 256; }
 int64_t pref_bytes(int64_t N) { return (N * 8 + 255) / 256 * 256; }
 int64_t part_bytes(int nsplit, int64_t rows, int D) { return nsplit > 1 ? (int64_t)nsplit * rows * (D + 2) * 4 : 0; }
 
@@ -1006,7 +1077,7 @@ template <typename T, int NW, int QC, int D>
 int64_t workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv) {
   const int64_t nqb = (Tq + 32 * QC * NW - 1) / (32 * QC * NW);
   const int s = pick_splits<T, NW, QC, D>(N * H * nqb, Tkv);
-  return (sizeof(T) == 2 && D == ICL_D ? flag_bytes(N * H * nqb * s) + pref_bytes(N) : 0) +
+  return (sizeof(T) == 2 && D == ICL_D ? flag_bytes(N * H * nqb * s) + pref_bytes(N) + list_bytes(N * H * nqb * s) : 0) +
          part_bytes(s, N * H * Tq, D);
 }
 
@@ -1027,8 +1098,9 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream)
   const bool strides_fit = p.k_st >= 0 && p.v_st >= 0 && p.k_st < (1 << 24) && p.v_st < (1 << 24);
   if (sizeof(T) == 2 && D == ICL_D && strides_fit) {
     const int64_t pb = pref_bytes(p.N);
-    if (have < flag_bytes(items * p.nsplit) + pb + part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
-    fb = flag_bytes(items * p.nsplit) + pb;
+    auto head = [&](int s) { return flag_bytes(items * s) + pb + list_bytes(items * s); };
+    if (have < head(p.nsplit) + part_bytes(p.nsplit, rows, D)) p.nsplit = 1;
+    fb = head(p.nsplit);
     fast = have >= fb + part_bytes(p.nsplit, rows, D);
   }
   if (!fast) {
@@ -1047,6 +1119,11 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream)
     p.pvalid = pv;
     p.pok = pv + p.pn;
     tabicl_launch_key_prefix(p.bias, p.bias_sn, p.bias_n, p.Tkv, p.valid, p.valid_n, p.pn, pv, pv + p.pn, stream);
+  }
+  if (fast && p.qlen && p.N < ICL_LIST_MAXN) {
+    int32_t* list = (int32_t*)((char*)ws + flag_bytes(nblk) + pref_bytes(p.N));
+    hipLaunchKernelGGL(icl_live_list_kernel, dim3(1), dim3(1024), 0, stream, p, list);
+    p.live = list;
   }
   if (fast)
     hipLaunchKernelGGL(icl_pipe_kernel, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
@@ -1090,7 +1167,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr; p.flags = nullptr;
   p.bias = bias; p.bias_n = (int)bias_n; p.bias_sn = bias_sn;
   p.bias_inv_scale = 1.0f / scale;
-  p.pvalid = nullptr; p.pok = nullptr; p.pn = 0;
+  p.pvalid = nullptr; p.pok = nullptr; p.pn = 0; p.live = nullptr;
   if (D == 128) {
     if (dtype == 0)
       launch<bf16, 4, 1, 128>(p, ws, ws_bytes, stream);
@@ -1105,8 +1182,8 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
 }
 
 // ---------------------------------------------------------------------------------------------
-// Allocation-free launch: the work-item flags, the prefix view of a key mask and the key-split
-// partials live in `scratch`, a file-scope device array (one per GPU, held until the process ends),
+// Allocation-free launch: the work-item flags, the prefix view of a key mask, the live work-item list
+// of ragged calls and the key-split partials live in `scratch`, a file-scope device array (one per GPU, held until the process ends),
 // instead of a workspace from the caller. Host code never passes the array's name to a kernel: its
 // device address is taken once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
 // Every call on a GPU shares that GPU's array (no call clears it: each kernel writes every entry it
@@ -1140,10 +1217,11 @@ hipError_t scratch_ptr(void** out) {
 }  // namespace
 
 int64_t tabicl_launch_icl_noalloc_min_bytes(int64_t N, int64_t H, int64_t Tq, int64_t D, int dtype) {
-  // unsplit: flags per work item and the prefix view (bf16, d = 64, the pipelined kernel); nothing else
+  // unsplit: flags per work item, the prefix view and the live list (bf16, d = 64, the pipelined
+  // kernel); nothing else
   if (dtype != 0 || D != ICL_D) return 0;
   const int64_t nqb = (Tq + IP_QW * IP_NW - 1) / (IP_QW * IP_NW);
-  return flag_bytes(N * H * nqb) + pref_bytes(N);
+  return flag_bytes(N * H * nqb) + pref_bytes(N) + list_bytes(N * H * nqb);
 }
 
 int tabicl_launch_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid,

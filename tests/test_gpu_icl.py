@@ -105,15 +105,20 @@ def test_icl_cache_append_and_query(dev):
 
 
 def test_icl_split_choice(dev):
-    # the launcher splits keys only when the grid would leave CUs idle (workspace = flags + prefix view,
-    # plus fp32 partials [S][N*H*Tq][66] when S > 1): a C4 block launch (8 x 8 heads x 20 query blocks =
-    # 1280 work items on 256 CUs) runs unsplit; one estimator's 160 work items over 45k keys split
+    # the launcher splits keys only when the grid would leave CUs idle (workspace = flags + prefix view +
+    # live work-item list, plus fp32 partials [S][N*H*Tq][66] when S > 1): a C4 block launch (8 x 8
+    # heads x 20 query blocks = 1280 work items on 256 CUs) runs unsplit; one estimator's 160 work
+    # items over 45k keys split
     import tabicl_mi355_native as nat
     lib = nat.load()
+
+    def head(items):  # flags, prefix view, list (count + items), each 256-byte aligned
+        return (items * 4 + 255) // 256 * 256 + 256 + ((items + 1) * 4 + 255) // 256 * 256
+
     c4 = lib.tabicl_icl_workspace_bytes(8, 8, 5000, 45000, 64, 0)
-    assert c4 == (1280 * 4 + 255) // 256 * 256 + 256  # flags + prefix view, no partials
+    assert c4 == head(1280)  # no partials
     one = lib.tabicl_icl_workspace_bytes(1, 8, 5000, 45000, 64, 0)
-    split = {s: (160 * s * 4 + 255) // 256 * 256 + 256 + s * 8 * 5000 * 66 * 4 for s in (2, 3, 4)}
+    split = {s: head(160 * s) + s * 8 * 5000 * 66 * 4 for s in (2, 3, 4)}
     assert one in split.values(), (one, split)
 
 

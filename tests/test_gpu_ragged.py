@@ -6,7 +6,8 @@ call itself is checked against the fp64 oracle on a subset of rows (2e-2 bf16, 1
 ragged rows are pinned to the oracle through it. The ICL kernels never write the rows at or past
 q_len (checked with a NaN sentinel); for pk_cross their contents are unspecified (the resident
 kernel skips them, the others compute them). Cases: whole work items past q_len, a work item cut
-inside, q_len = 0, q_len >= Lq, one q_len for the whole batch, key splits, the fp32 kernel, and for
+inside, q_len = 0, q_len >= Lq, one q_len for the whole batch, key splits, the fp32 kernel, many
+work items (the pipelined kernel's list of live work items), and for
 pk_cross the resident kernel (short runs, long runs, the exact-scale long runs of the column ISAB-2)
 plus the streaming and fp32 kernels.
 """
@@ -40,6 +41,9 @@ def _check_rows(out, ref, q_len, row_dim, untouched=False):
     ("nosplit_bf16", 4, 8, 700, 900, None, [700, 999, 256, 1], torch.bfloat16),
     ("shared_qlen_bf16", 2, 4, 600, 2000, [2000], [300], torch.bfloat16),
     ("split_fp32", 3, 2, 300, 2500, [2500, 100, 1], [129, 300, 64], torch.float32),
+    # many work items (the live work-item list of the pipelined kernel, a count that is not a multiple
+    # of the 8 XCDs): per-element valid lengths and row counts across work-item edges, 0 and past Tq
+    ("list_bf16", 37, 8, 1024, 2500, "random", "random", torch.bfloat16),
 ])
 def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
     import tabicl_mi355_icl as icl
@@ -48,6 +52,11 @@ def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
     k = torch.randn(N, H, Tkv, 64, generator=g).to(dtype)
     v = torch.randn(N, H, Tkv, 64, generator=g).to(dtype)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    if valid == "random":
+        valid = [int(x) for x in np.random.default_rng(5).integers(1, Tkv + 1, N)]
+    if q_len == "random":
+        q_len = [int(x) for x in np.random.default_rng(6).choice([0, 1, 100, 255, 256, 257, 700, 1024, 2000], N)]
+        q_len[0] = 300
     vt = None if valid is None else torch.tensor(valid, dtype=torch.int32, device=dev)
     ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
     ref = torch.empty_like(qd)
