@@ -737,16 +737,21 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
 
   int work;
   if (p.live) {
-    // ragged call: the listed (live) work items, each XCD a contiguous, equal share of the list (the
-    // work items of one (n, h) stay together, for L2), workgroups past the share exit at once. The
+    // ragged call: the listed (live) work items, each XCD its section or an equal contiguous share of
+    // the list (the work items of one (n, h) stay together, for L2); workgroups past it exit. The
     // padded grid's order would interleave live and empty work items, and the dispatcher's
     // placement then leaves part of the CUs with the live ones (C5's small buckets ran 2.4x slower
     // than a call of the live rows alone).
     const int cnt = p.live[0];
     const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
-    const int q8 = cnt >> 3, r8 = cnt & 7;
-    if (j >= q8 + (xcd < r8 ? 1 : 0)) return;  // no flag written: icl_fwd_kernel checks the rows first
-    work = p.live[1 + xcd * q8 + (xcd < r8 ? xcd : r8) + j];
+    if (p.H % 8 == 0) {  // one section per XCD (its heads h = xcd mod 8), cnt entries each
+      if (j >= cnt) return;  // no flag written: icl_fwd_kernel checks the rows first
+      work = p.live[1 + xcd * cnt + j];
+    } else {  // one section: each XCD an equal contiguous share
+      const int q8 = cnt >> 3, r8 = cnt & 7;
+      if (j >= q8 + (xcd < r8 ? 1 : 0)) return;
+      work = p.live[1 + xcd * q8 + (xcd < r8 ? xcd : r8) + j];
+    }
   } else {
     work = xcd_remap(blockIdx.x, gridDim.x);
   }
@@ -1014,23 +1019,26 @@ int pick_splits(int64_t items, int64_t Tkv) {
 
 constexpr int ICL_LIST_MAXN = 8192;  // batch elements the live list takes (per-element counts in LDS)
 
-// Live work items of a ragged call of the pipelined kernel (one workgroup of 1024 threads): per batch
-// element n its H * nsplit * ceil(live rows / 256) work items, listed in work-item order
-// ((n * H + h) * nsplit + split) * nqb + qb after the count. Per-element counts are scanned in LDS
-// (each thread a run of up to 8 elements, then a scan of the 1024 run totals); every list entry
-// finds its element by binary search over the scanned counts.
+// Live work items of a ragged call of the pipelined kernel (one workgroup of 1024 threads). Batch
+// element n has lq(n) = ceil(live rows / 256) live query blocks, so nsplit * lq(n) live work items per
+// head. With H a multiple of 8 the list is 8 sections of equal length C, one per XCD: section x holds
+// the heads h = x (mod 8) of every element, in work-item order, so every XCD gets the same work and
+// each (n, h)'s work items stay together (its K / V shared in that XCD's L2); list[0] = C. Otherwise
+// one section in work-item order; list[0] = its length. Entries are work-item indices
+// ((n * H + h) * nsplit + split) * nqb + qb. lq is scanned in LDS (each thread a run of up to 8
+// elements, then a scan of the 1024 run totals); every entry finds its element by binary search.
 __global__ __launch_bounds__(1024) void icl_live_list_kernel(IclParams p, int32_t* list) {
   __shared__ int pre[ICL_LIST_MAXN + 1];
   __shared__ int tot[1024];
   const int tid = threadIdx.x;
-  const int per = p.H * p.nsplit, qbr = IP_QW * IP_NW;
+  const int qbr = IP_QW * IP_NW;
   constexpr int RUN = ICL_LIST_MAXN / 1024;
   int acc = 0;
   int c[RUN];
 #pragma unroll
   for (int i = 0; i < RUN; ++i) {
     const int n = tid * RUN + i;
-    c[i] = n < p.N ? per * ((icl_live_rows(p, n) + qbr - 1) / qbr) : 0;
+    c[i] = n < p.N ? (icl_live_rows(p, n) + qbr - 1) / qbr : 0;
     acc += c[i];
   }
   tot[tid] = acc;
@@ -1049,19 +1057,26 @@ __global__ __launch_bounds__(1024) void icl_live_list_kernel(IclParams p, int32_
     run0 += c[i];
   }
   __syncthreads();
-  const int total = pre[p.N];
-  for (int t = tid; t < total; t += 1024) {
-    int lo = 0, hi = p.N;  // pre[lo] <= t < pre[hi]
+  const bool by_xcd = p.H % 8 == 0;
+  const int hx = by_xcd ? p.H / 8 : p.H;     // heads per section
+  const int per = hx * p.nsplit;              // section entries per live query block
+  const int C = per * pre[p.N];               // section length
+  const int nsec = by_xcd ? 8 : 1;
+  for (int t = tid; t < nsec * C; t += 1024) {
+    const int x = t / C, r = t % C;
+    const int key = r / per;  // the element n holds pre[n] <= key < pre[n + 1]
+    int lo = 0, hi = p.N;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (pre[mid] <= t) lo = mid; else hi = mid;
+      if (pre[mid] <= key) lo = mid; else hi = mid;
     }
-    const int n = lo, j = t - pre[n];
-    const int lq = (pre[n + 1] - pre[n]) / per;  // live query blocks of n (>= 1 here)
-    const int h = j / (p.nsplit * lq), rem = j % (p.nsplit * lq);
+    const int n = lo, lq = pre[n + 1] - pre[n];
+    const int rr = r - per * pre[n];
+    const int hh = rr / (p.nsplit * lq), rem = rr % (p.nsplit * lq);
+    const int h = by_xcd ? hh * 8 + x : hh;
     list[1 + t] = ((n * p.H + h) * p.nsplit + rem / lq) * p.nqb + rem % lq;
   }
-  if (tid == 0) list[0] = total;
+  if (tid == 0) list[0] = C;
 }
 
 // Workspace layout: [per-work-item flags, bf16 d = 64 only, 256-byte aligned][prefix view of a key
