@@ -714,6 +714,14 @@ __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&s
   ip_phase<false, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
 }
 
+// Sweep iteration t of a wave whose query rows are all past the live count (ragged calls): the same
+// join and tile copy as ip_iter, in the same order, without the products and the softmax.
+__device__ __forceinline__ void ip_iter_idle(const IpCtx& c, int t) {
+  TA_WAIT_JOIN(4);
+  ip_issue(c, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
+           min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
+}
+
 // The tile that crosses `valid` (buffer b, keys k0..): S, mask, probabilities and PV per half,
 // without the MFMA/VALU interleave (once per work item at most).
 __device__ __forceinline__ void ip_tail(IpState& st, const bf16* lk, const bf16* lv, int k0, int valid, float sc,
@@ -843,6 +851,14 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
 #pragma unroll
     for (int i = 0; i < IP_NBUF - 1; ++i) ip_issue(c, c.lds0 + i * IP_TILE * 2, min(t0 + i, t1 - 1) * ICL_KT);
     TA_WAIT_JOIN(8);  // tile t0 landed, two more tiles (8 copies) in flight
+    // tiles entirely below `valid` through the pipelined sweep, the crossing one (if any) after it
+    const int nfull = (t1 == ntiles && valid % ICL_KT != 0) ? nt - 1 : nt;
+    if (qw0 >= live) {
+      // a ragged call's wave with no live row: only its share of the tile copies and the joins
+      for (int t = 0; t < nfull; ++t) ip_iter_idle(c, t);
+      TA_WAIT_JOIN(0);
+      goto swept;
+    }
 
     // reference m: ceiled maximum over the first 32 keys of the range
     f32x16 sA[2], sB[2];
@@ -858,8 +874,6 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       st.nm[qc] = mx > -1e4f ? -fminf(ceilf(mx), 1e4f) : 0.f;
     }
 
-    // tiles entirely below `valid` through the pipelined sweep, the crossing one (if any) after it
-    const int nfull = (t1 == ntiles && valid % ICL_KT != 0) ? nt - 1 : nt;
     if (nfull == 1) {
       ip_iter<true, true>(st, sA, sB, pA, pB, lds, c, 0);
     } else if (nfull > 1) {
@@ -882,6 +896,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     }
     TA_WAIT_JOIN(0);  // no copy into this workgroup's LDS may outlive it
   }
+swept:
 
   if (p.qlen) {
     // rows at or past the live count are not written: clear their state so that they cannot flag
