@@ -281,9 +281,11 @@ int tabicl_icl_fwd_noalloc(const void* q, const void* k, const void* v, const in
 int64_t tabicl_icl_noalloc_scratch_bytes(void);
 
 /*
- * Workspace size (bytes) that tabicl_icl_fwd uses for these sizes on the current device (0 when
- * the call would not split). Queries the device's CU count and occupancy; no device memory is
- * touched. Returns <0 on bad arguments.
+ * Workspace size (bytes) that tabicl_icl_fwd uses for these sizes on the current device: for bf16
+ * with D = 64, the per-work-item trust flags, the prefix view of a key mask and the list of live
+ * work items of ragged calls; plus the fp32 key-split partials when the launch splits the keys (0
+ * for an fp32 call that does not split). Queries the device's CU count and occupancy; no device
+ * memory is touched. Returns <0 on bad arguments.
  */
 int64_t tabicl_icl_workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
                                    int32_t dtype);

@@ -6,7 +6,8 @@ Each case captures one call on static input tensors, then replays the graph thre
 each replay the inputs are rewritten in place by eager work, and after it the graph's output must
 equal (bit for bit) an eager call of the same op on the same inputs, with a synchronisation in
 between. Cases: the cached ICL attention with a valid length (pipelined kernel, trust-flag gate, key
-split merge), the same with a prefix key mask (device-side prefix reduction), the persistent
+split merge), the same with a prefix key mask (device-side prefix reduction), the ragged ICL entry
+point (device-built list of live work items, row counts rewritten between replays), the persistent
 row-stage kernel (pk_self, RoPE) and the few-query streaming hxq with a key mask.
 """
 import pytest
@@ -73,6 +74,31 @@ def test_graph_icl_prefix_key_mask(dev):
     refresh(0)
     print("[graph] icl key mask", flush=True)
     _replays(dev, lambda: icl.icl_sdpa(q, k, v, None, bias), (q, k, v, bias), refresh)
+
+
+def test_graph_icl_ragged(dev):
+    # the ragged entry point: the live work-item list is rebuilt on the device at every replay from the
+    # row counts the eager work rewrote (rows past them are not written: the output starts at zero)
+    import tabicl_mi355_icl as icl
+    g = torch.Generator(device=dev).manual_seed(74)
+    N = 24
+    q = torch.randn(N, 8, 1024, 64, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(N, 8, 3000, 64, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(N, 8, 3000, 64, generator=g, device=dev).to(torch.bfloat16)
+    valid = torch.randint(1, 3001, (N,), generator=g, device=dev).to(torch.int32)
+    qlen = torch.randint(0, 1100, (N,), generator=g, device=dev).to(torch.int32)
+
+    def fn():
+        out = torch.zeros_like(q)  # a fill kernel, not a memset node
+        icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, out)
+        return out
+
+    def refresh(step):
+        qlen.copy_(torch.randint(0, 1100, (N,), generator=g, device=dev).to(torch.int32))
+        valid.copy_(torch.randint(1, 3001, (N,), generator=g, device=dev).to(torch.int32))
+
+    print("[graph] icl ragged", flush=True)
+    _replays(dev, fn, (q, k, v, valid, qlen), refresh)
 
 
 def test_graph_row_stage_persistent(dev):

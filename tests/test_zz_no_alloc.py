@@ -19,12 +19,13 @@ def _strides(t):
     return t.stride(0), t.stride(1), t.stride(2)
 
 
-def _call_noalloc(nat, lib, q, k, v, out, valid=None, bias=None):
+def _call_noalloc(nat, lib, q, k, v, out, valid=None, bias=None, qlen=None):
     N, H, Tq, D = q.shape
     st = lib.tabicl_icl_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), None if valid is None else valid.data_ptr(),
         0 if valid is None else valid.numel(), None if bias is None else bias.data_ptr(),
-        0 if bias is None else bias.shape[0], 0 if bias is None else bias.stride(0), None, 0, out.data_ptr(),
+        0 if bias is None else bias.shape[0], 0 if bias is None else bias.stride(0),
+        None if qlen is None else qlen.data_ptr(), 0 if qlen is None else qlen.numel(), out.data_ptr(),
         N, H, Tq, k.shape[2], D, *_strides(q), *_strides(k), *_strides(v), *_strides(out), D ** -0.5,
         nat.dtype_code(q.dtype), nat.stream_of(q))
     nat.check(st, "tabicl_icl_fwd_noalloc")
@@ -55,6 +56,20 @@ def test_noalloc_matches_workspace_entry(dev, dtype):
         torch.cuda.synchronize()
         assert torch.isfinite(out.float()).all()
         assert float((out.float() - want.float()).abs().max()) <= tol
+    # a ragged call (per-element row counts: the live work-item list goes to the scratch array too)
+    N, H, Tq, Tkv = 9, 8, 1024, 2000
+    q = torch.randn(N, H, Tq, 64, generator=g).to(dtype).to(dev)
+    k = torch.randn(N, H, Tkv, 64, generator=g).to(dtype).to(dev)
+    v = torch.randn(N, H, Tkv, 64, generator=g).to(dtype).to(dev)
+    vt = torch.randint(1, Tkv + 1, (N,), generator=g).to(torch.int32).to(dev)
+    ql = torch.tensor([0, 1, 100, 256, 257, 700, 1024, 5000, 33], dtype=torch.int32, device=dev)
+    out = torch.zeros_like(q)
+    _call_noalloc(nat, lib, q, k, v, out, vt, qlen=ql)
+    import tabicl_mi355_icl as icl
+    want = torch.zeros_like(q)
+    icl.ICL_FWD_RAGGED_OUT(q, k, v, vt, ql, 64 ** -0.5, want)
+    torch.cuda.synchronize()
+    assert float((out.float() - want.float()).abs().max()) <= tol
     # a key-masked call (prefix rows and a row with scattered masked keys)
     N, H, Tq, Tkv = 3, 4, 300, 3000
     q = torch.randn(N, H, Tq, 64, generator=g).to(dtype).to(dev)
