@@ -1134,10 +1134,16 @@ void launch_resident(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStr
 // fp32 kernel (every fp32 call: the C1 column ISAB in the reference's fp32 precision). A workgroup of
 // 8 waves takes (batch element, group of 4 heads, run of 16-query blocks); wave = (head of the group,
 // parity of the blocks it takes). Keys go through LDS in tiles of 128 (the group's 64 dims of K
-// row-major and of V transposed: 69 KB, two workgroups per CU). Per block and tile, fp32 MFMA
-// (4 x 16x16x4 per 16x16x16 product):
-//   S^T = K' q'^T (keys x queries), x = S log2e + b2, online softmax (running maximum, rescaled only
-//   when it grows by more than SH_LAZY: exact, o and l share the reference), O^T += V^T P^T.
+// row-major and of V transposed: 69 KB, two workgroups per CU). Per block and 16-key group, fp32
+// MFMA (4 x 16x16x4 per 16x16x16 product):
+//   x = K (q' log2e) - m     S^T with the accumulator initialised to -m (m: the softmax reference,
+//                            fixed by the block's first 16 keys), plus b2 on masked tiles
+//   p = exp2(x), l += p, O^T += V^T P^T
+// so the VALU work per score is one v_exp_f32 and one add. A row sum outside [2^-64, 2^96] or a
+// non-finite O (a score far above the reference, all keys masked, NaN / inf inputs) sends the block
+// (RESIDENT: the wave's blocks, keys still in LDS) or the workgroup (streaming: its keys streamed
+// again) through the exact online softmax: x = S log2e + b2 per tile, running maximum rescaled only
+// when it grows by more than SH_LAZY.
 // RESIDENT (all keys in one tile): each block in one pass, nothing carried between blocks, any run
 // length; otherwise up to SF_SB blocks per wave carry (o, m, l) across the tiles.
 // ---------------------------------------------------------------------------------------------
@@ -1146,7 +1152,7 @@ constexpr int SF_W = SF_HG * SH_D;   // merged dims per workgroup
 constexpr int SF_KT = 128;           // keys per tile
 constexpr int SF_KSTR = SF_W + 4;    // K tile row stride (floats)
 constexpr int SF_VSTR = SF_KT + 4;   // V^T tile row stride (floats)
-constexpr int SF_SB = 4;             // blocks per wave carried across tiles (streaming)
+constexpr int SF_SB = 2;             // blocks per wave carried across tiles (streaming)
 
 // One tile for one block: online-softmax update of (o, m, l) (l: this lane's partial sum).
 __device__ __forceinline__ void sf_tile(const float* lkt, const float* lvt, const float* lb2, int nkb, f32x4 qop,
@@ -1187,6 +1193,59 @@ __device__ __forceinline__ void sf_tile(const float* lkt, const float* lvt, cons
       o = mfma16x16x16(a, pv, o);
     }
   }
+}
+
+// One tile against a fixed softmax reference m (log2 units; the fast pass): x = K q'' - m comes
+// straight from the MFMA (q'' = q' log2e, the accumulator initialised to -m), plus b2 on tiles with
+// masked keys (addb), p = exp2(x), l += p, O^T += V^T P^T, one 16-key group at a time (no score
+// array). FIRST: the first tile of the sweep, whose first 16 keys set m (their ceiled maximum,
+// clamped to [-1e4, 1e4]; -inf and NaN give 0). p may exceed 1; the caller's trust test (l <= 2^96,
+// O finite) decides whether the exact pass must redo the block.
+template <bool FIRST>
+__device__ __forceinline__ void sf_tile_fix(const float* lkt, const float* lvt, const float* lb2, int nkb,
+                                            f32x4 qop, int hd, int l16, int kap, bool addb, f32x4& o, float& m,
+                                            float& l) {
+#pragma unroll
+  for (int kt = 0; kt < SF_KT / 16; ++kt) {
+    if (kt < nkb) {
+      const bool first = FIRST && kt == 0;
+      const f32x4 a = *(const f32x4*)(lkt + (16 * kt + l16) * SF_KSTR + hd + 4 * kap);
+      const f32x4 init = first ? f32x4{0.f, 0.f, 0.f, 0.f} : f32x4{-m, -m, -m, -m};
+      f32x4 x = mfma16x16x16(a, qop, init);
+      if (addb) {
+        const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] += b2[r];
+      }
+      if (first) {
+        const float tm = quad_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+        m = tm > -1e4f ? fminf(ceilf(tm), 1e4f) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] -= m;
+      }
+      f32x4 pv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pv[r] = __builtin_amdgcn_exp2f(x[r]);
+        l += pv[r];
+      }
+      const f32x4 va = *(const f32x4*)(lvt + (hd + l16) * SF_VSTR + 16 * kt + 4 * kap);
+      o = mfma16x16x16(va, pv, o);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one 16-key group at a time: hoisted operand reads cost registers
+  }
+}
+
+// True when a fast-pass result may not be trusted: the row sum outside [2^-64, 2^96] or not finite,
+// or O not finite. Above: a score ~66 nats above the first 16 keys' maximum, or NaN / inf in the
+// inputs. Below: the first 16 keys' maximum was clamped (every score far below any finite reference,
+// e.g. all keys under a -1e30 bias, whose softmax is uniform) or no key is visible; a trusted row
+// has l >= 1/2 from its first 16 keys on.
+__device__ __forceinline__ bool sf_suspect(f32x4 o, float l) {
+  bool bad = !(l >= 0x1p-64f && l <= 0x1p96f);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(o[r]) <= 0x1p127f);
+  return bad;
 }
 
 // q' = rope(q) scale (fp32) of query qi, this lane's 4 dims d0..d0+3; zero past Lq.
@@ -1244,6 +1303,7 @@ __global__ __launch_bounds__(512, 4) void sf_kernel(ShParams p) {
   __shared__ __attribute__((aligned(16))) float lkt[SF_KT * SF_KSTR];
   __shared__ __attribute__((aligned(16))) float lvt[SF_W * SF_VSTR];
   __shared__ __attribute__((aligned(16))) float lb2[SF_KT];
+  __shared__ int sf_bad;
   const int work = xcd_remap(blockIdx.x, gridDim.x);
   const int hg = work % (SH_H / SF_HG), rest = work / (SH_H / SF_HG);
   const int b = rest / p.nwg_b, qb0 = (rest % p.nwg_b) * p.qbpw;
@@ -1265,34 +1325,85 @@ __global__ __launch_bounds__(512, 4) void sf_kernel(ShParams p) {
       __syncthreads();
     }
     const int nkb = (lk + 15) >> 4;
+    const bool addb = p.bias != nullptr || (lk & 15) != 0;
     for (int bi = par; bi < nb; bi += 2) {
       const int qi = (qb0 + bi) * 16 + l16;
       f32x4 o = {0.f, 0.f, 0.f, 0.f};
-      float m = TA_NEG_INF, l = 0.f;
-      if (ntiles == 1) sf_tile(lkt, lvt, lb2, nkb, sf_qop(p, b, qi, d0), hd, l16, kap, o, m, l);
+      float m = 0.f, l = 0.f;
+      if (ntiles == 1) {
+        const f32x4 q = sf_qop(p, b, qi, d0);
+        f32x4 q2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q2[r] = q[r] * TA_LOG2E;
+        sf_tile_fix<true>(lkt, lvt, lb2, nkb, q2, hd, l16, kap, addb, o, m, l);
+        if (wave_any(sf_suspect(o, l))) {
+          // rare: the exact online softmax over the same keys (still in LDS)
+          o = f32x4{0.f, 0.f, 0.f, 0.f};
+          m = TA_NEG_INF;
+          l = 0.f;
+          sf_tile(lkt, lvt, lb2, nkb, q, hd, l16, kap, o, m, l);
+        }
+      }
       sf_store(p, b, qi, d0, o, l);
     }
   } else {
     f32x4 qop[SF_SB], o[SF_SB];
     float m[SF_SB], l[SF_SB];
+    // fast pass: a softmax reference fixed by each block's first 16 keys
 #pragma unroll
     for (int j = 0; j < SF_SB; ++j) {
-      qop[j] = sf_qop(p, b, (qb0 + par + 2 * j) * 16 + l16, d0);
+      const f32x4 q = sf_qop(p, b, (qb0 + par + 2 * j) * 16 + l16, d0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qop[j][r] = q[r] * TA_LOG2E;
       o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m[j] = TA_NEG_INF;
+      m[j] = 0.f;
       l[j] = 0.f;
     }
+    if (threadIdx.x == 0) sf_bad = 0;
     for (int t = 0; t < ntiles; ++t) {
       __syncthreads();
       sf_fill(p, lkt, lvt, lb2, b, hg, t, lk);
       __syncthreads();
       const int rem = lk - t * SF_KT;
       const int nkb = rem >= SF_KT ? SF_KT / 16 : (rem + 15) >> 4;
+      const bool addb = p.bias != nullptr || (rem < SF_KT && (rem & 15) != 0);
 #pragma unroll
       for (int j = 0; j < SF_SB; ++j) {
-        if (par + 2 * j < nb)
-          sf_tile(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, o[j], m[j], l[j]);
+        if (par + 2 * j < nb) {
+          if (t == 0)
+            sf_tile_fix<true>(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, addb, o[j], m[j], l[j]);
+          else
+            sf_tile_fix<false>(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, addb, o[j], m[j], l[j]);
+        }
         __builtin_amdgcn_sched_barrier(0);  // one block at a time: interleaving them costs registers
+      }
+    }
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < SF_SB; ++j)
+      if (par + 2 * j < nb) bad |= sf_suspect(o[j], l[j]);
+    if (wave_any(bad) && lane == 0) sf_bad = 1;
+    __syncthreads();
+    if (sf_bad) {
+      // rare: the whole workgroup sweeps its keys again with the exact online softmax
+#pragma unroll
+      for (int j = 0; j < SF_SB; ++j) {
+        qop[j] = sf_qop(p, b, (qb0 + par + 2 * j) * 16 + l16, d0);
+        o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m[j] = TA_NEG_INF;
+        l[j] = 0.f;
+      }
+      for (int t = 0; t < ntiles; ++t) {
+        __syncthreads();
+        sf_fill(p, lkt, lvt, lb2, b, hg, t, lk);
+        __syncthreads();
+        const int rem = lk - t * SF_KT;
+        const int nkb = rem >= SF_KT ? SF_KT / 16 : (rem + 15) >> 4;
+#pragma unroll
+        for (int j = 0; j < SF_SB; ++j) {
+          if (par + 2 * j < nb) sf_tile(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, o[j], m[j], l[j]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
 #pragma unroll

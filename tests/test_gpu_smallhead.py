@@ -268,6 +268,23 @@ def test_all_keys_masked_by_bias_is_uniform(dev):
     assert torch.isfinite(out).all()
 
 
+@pytest.mark.parametrize("Lk", [100, 700])
+def test_fp32_sharp_key_far_above_first_keys(dev, Lk):
+    # fp32 kernel, resident (Lk <= 128) and streaming: one key per head whose score lies up to ~150 nats above
+    # the first 16 keys' maximum (the fast pass's fixed reference) overflows its row-sum bound; those
+    # blocks must come out of the exact pass equal to the oracle
+    pk = _attn()
+    g = _gen(12)
+    q = torch.randn(3, 40, E, generator=g) * 0.25
+    k = torch.randn(3, Lk, E, generator=g)
+    v = torch.randn(3, Lk, E, generator=g)
+    k[:, Lk - 5] = q[:, 7] * 80.0  # key Lk-5 aligns with query 7: score ~ 80 |q_7|^2 (30-150 nats) per head
+    out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H)
+    ref = O.hx_ref(q, k, v, H)
+    assert torch.isfinite(out).all()
+    assert _err(out, ref) <= 1e-4
+
+
 def test_no_nan_with_garbage_past_valid(dev):
     # NaN/inf in key/value rows past valid must not leak into the output
     pk = _attn()
