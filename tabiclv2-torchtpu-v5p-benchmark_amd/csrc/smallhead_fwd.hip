@@ -1200,11 +1200,14 @@ __device__ __forceinline__ void sf_tile(const float* lkt, const float* lvt, cons
 // masked keys (addb), p = exp2(x), l += p, O^T += V^T P^T, one 16-key group at a time (no score
 // array). FIRST: the first tile of the sweep, whose first 16 keys set m (their ceiled maximum,
 // clamped to [-1e4, 1e4]; -inf and NaN give 0). p may exceed 1; the caller's trust test (l <= 2^96,
-// O finite) decides whether the exact pass must redo the block.
+// O finite) decides whether the exact pass must redo the block. Even and odd 16-key groups
+// accumulate O into separate registers (summed at the end): the PV products of consecutive groups
+// do not wait on each other.
 template <bool FIRST>
 __device__ __forceinline__ void sf_tile_fix(const float* lkt, const float* lvt, const float* lb2, int nkb,
                                             f32x4 qop, int hd, int l16, int kap, bool addb, f32x4& o, float& m,
                                             float& l) {
+  f32x4 o1 = {0.f, 0.f, 0.f, 0.f};  // odd groups: two independent PV accumulation chains
 #pragma unroll
   for (int kt = 0; kt < SF_KT / 16; ++kt) {
     if (kt < nkb) {
@@ -1230,10 +1233,15 @@ __device__ __forceinline__ void sf_tile_fix(const float* lkt, const float* lvt, 
         l += pv[r];
       }
       const f32x4 va = *(const f32x4*)(lvt + (hd + l16) * SF_VSTR + 16 * kt + 4 * kap);
-      o = mfma16x16x16(va, pv, o);
+      if (kt & 1)
+        o1 = mfma16x16x16(va, pv, o1);
+      else
+        o = mfma16x16x16(va, pv, o);
     }
     __builtin_amdgcn_sched_barrier(0);  // one 16-key group at a time: hoisted operand reads cost registers
   }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o[r] += o1[r];
 }
 
 // True when a fast-pass result may not be trusted: the row sum outside [2^-64, 2^96] or not finite,
