@@ -324,6 +324,35 @@ class IclKVCache:
             x = x + F.linear(activation(F.linear(h, w.ff1_w, w.ff1_b)), w.ff2_w, w.ff2_b).to(x.dtype)
         return x
 
+    def estimators(self, start: int, stop: int) -> "IclKVCache":
+        """Estimators [start, stop) of this cache as a cache of their own: views of the same storage and
+        the same per-block row record (appends through either are seen by both). The per-chunk caches
+        of a query whose batch is cut into ICL calls (query_chunked)."""
+        E = self.keys.shape[0]
+        if not 0 <= start < stop <= E:
+            raise ValueError(f"estimators [{start}, {stop}) out of range [0, {E})")
+        view = object.__new__(IclKVCache)
+        view.keys = self.keys[start:stop]
+        view.values = self.values[start:stop]
+        view.capacity = self.capacity
+        view.written = self.written
+        view._len_t = self._len_t
+        return view
+
+    def query_chunked(self, x: Tensor, blocks, chunks, valid_kv_len: Optional[Union[int, Tensor]] = None,  # noqa: ANN001
+                      q_transform: Optional[Callable[[Tensor], Tensor]] = None,
+                      activation: Callable[[Tensor], Tensor] = F.gelu) -> Tensor:
+        """query_blocks run once per batch chunk [start, stop) of x [E, Tq, width] (each against those
+        estimators of the cache) and concatenated: the reference runner's ICL call pattern for a batch
+        cut by its memory rule (scripts/tabicl_tpu_bucketed.py:1329-1375; chunks from
+        BucketPlan.chunks()). Every row's result is that of one query_blocks call over the whole batch."""
+        if not chunks or chunks[0][0] != 0 or chunks[-1][1] != x.shape[0] or any(
+                a[1] != b[0] for a, b in zip(chunks, chunks[1:])):
+            raise ValueError(f"chunks {chunks} do not cover the batch [0, {x.shape[0]}) in order")
+        parts = [self.estimators(a, b).query_blocks(x[a:b], blocks, valid_kv_len, q_transform, activation)
+                 for a, b in chunks]
+        return parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)
+
     def block_kv(self, block: int):
         return self.keys[:, block], self.values[:, block]
 

@@ -151,6 +151,24 @@ def test_icl_cache_fill_bookkeeping():
     assert cache.length(0) == 710
 
 
+def test_icl_cache_estimator_views():
+    import tabicl_mi355_icl as icl
+    cache = icl.IclKVCache(4, 2, 8, 100, 64, torch.bfloat16, "cpu")
+    v = cache.estimators(1, 3)
+    assert v.shape == (2, 2, 8, 100, 64) and v.keys.data_ptr() == cache.keys[1].data_ptr()
+    v.keys.fill_(1.0)
+    assert float(cache.keys[1:3].float().sum()) == 2 * 2 * 8 * 100 * 64  # same storage
+    v._record(0, 0, 40)  # the row record is shared with the whole cache
+    assert cache.length(0) == 40 and v.length(0) == 40
+    for bad in ((0, 0), (3, 5), (-1, 2)):
+        with pytest.raises(ValueError, match="out of range"):
+            cache.estimators(*bad)
+    x = torch.zeros(4, 5, 512)
+    for chunks in ([], [(0, 2)], [(0, 2), (3, 4)], [(1, 4)]):
+        with pytest.raises(ValueError, match="do not cover"):
+            cache.query_chunked(x, [], chunks)
+
+
 def test_ops_refuse_cpu_tensors():
     import tabicl_mi355_attn as pk
     import tabicl_mi355_native as nat

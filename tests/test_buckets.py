@@ -56,3 +56,72 @@ def test_feature_bucket_step(monkeypatch):
 ])
 def test_other_buckets(fn, val, want):
     assert fn(val) == want
+
+
+# ---- dispatch plan (reference scripts/tabicl_tpu_bucketed.py:83, 1160-1162, 1184, 1222, 1298-1336) ----
+
+def test_plan_prefill_fused_and_tiled(monkeypatch):
+    monkeypatch.delenv("TABICL_TPU_ROW_BUCKET_STEP", raising=False)
+    # small: 4 x 1024 x (16 + 4) = 81,920 elements, fused: the ICL stage takes the whole batch
+    p = bk.plan_prefill(3, 700, 10)
+    assert (p.batch_bkt, p.rows_bkt, p.features_bkt, p.tiled, p.icl_step) == (4, 1024, 16, False, 4)
+    assert p.chunks() == [(0, 4)]
+    # C4's fit: 8 x 65536 x 132 elements, tiled, 65536 padded rows: one estimator per ICL call
+    p = bk.plan_prefill(8, 45000, 100)
+    assert (p.batch_bkt, p.rows_bkt, p.features_bkt, p.tiled, p.icl_step) == (8, 65536, 128, True, 1)
+    assert p.chunks() == [(i, i + 1) for i in range(8)]
+    # tiled with 32768 <= rows < 65536: two per call
+    p = bk.plan_prefill(8, 20000, 100)
+    assert (p.rows_bkt, p.tiled, p.icl_step) == (32768, True, 2)
+    assert p.chunks() == [(0, 2), (2, 4), (4, 6), (6, 8)]
+    # tiled below 32768 rows: the whole batch
+    p = bk.plan_prefill(32, 10000, 100)
+    assert (p.rows_bkt, p.tiled, p.icl_step) == (16384, True, 32)
+    # with a row step the one-per-call threshold is 40960 padded rows: 45,000 -> 45,056 (step 4096)
+    p = bk.plan_prefill(8, 45000, 100, row_step=4096, feature_step=4)
+    assert (p.rows_bkt, p.features_bkt, p.icl_step) == (45056, 100, 1)
+    p = bk.plan_prefill(8, 40000, 100, row_step=4096)
+    assert (p.rows_bkt, p.icl_step) == (40960, 1)
+    p = bk.plan_prefill(8, 36000, 100, row_step=4096)
+    assert (p.rows_bkt, p.icl_step) == (36864, 2)
+    assert bk.icl_step_min_rows(0) == 65536 and bk.icl_step_min_rows(4096) == 40960
+
+
+def test_plan_query_steps():
+    pre = bk.plan_prefill(3, 700, 10)
+    q = bk.plan_query(pre, 300)
+    # test rows to 512; the batch (4) and feature (16) buckets come from the prefill
+    assert (q.batch, q.batch_bkt, q.rows, q.rows_bkt, q.features_bkt, q.train_bkt) == (3, 4, 300, 512, 16, 1024)
+    assert q.icl_step == 4  # 4 x 512 x 20 = 40,960 elements
+    # the element count rule: B T_test (H + 4) above max_fused_elements -> one per call
+    assert bk.plan_query(pre, 300, max_fused_elements=40959).icl_step == 1
+    assert bk.plan_query(pre, 300, max_fused_elements=40960).icl_step == 4
+    # a cache spanning 65536 padded train rows: one per call whatever the test rows
+    big = bk.plan_prefill(8, 45000, 100)
+    assert bk.plan_query(big, 256, max_fused_elements=10 ** 12, row_step=0).icl_step == 1
+
+
+def test_pad_batch_and_unpad_output():
+    import torch
+    pre = bk.plan_prefill(3, 5, 6)
+    x = torch.arange(3 * 5 * 6, dtype=torch.float64).view(3, 5, 6) + 1
+    xp = bk.pad_batch(x, pre)
+    assert xp.shape == (4, 1024, 16) and xp.dtype == torch.float32
+    assert torch.equal(xp[:3, :5, :6], x.float())
+    assert float(xp[:3, 5:].abs().sum()) == 0 and float(xp[:3, :, 6:].abs().sum()) == 0
+    assert torch.equal(xp[3], xp[0])  # the padded element repeats element 0
+    y = torch.ones(3, 5)
+    assert bk.pad_batch(y, pre).shape == (4, 1024)
+    reps = torch.randn(3, 5, 7)
+    assert bk.pad_batch(reps, pre, pad_features=False).shape == (4, 1024, 7)
+    with pytest.raises(ValueError):
+        bk.pad_batch(torch.zeros(2, 5, 6), pre)
+    q = bk.plan_query(pre, 5)
+    raw = torch.randn(4, 256, 10)
+    out = bk.unpad_output(raw, q)
+    assert torch.equal(out, raw[:3, :5])
+    out = bk.unpad_output(raw, q, num_classes=4)
+    assert torch.equal(out, raw[:3, :5, :4])
+    prob = bk.unpad_output(raw, q, num_classes=4, return_logits=False, softmax_temperature=0.5)
+    e = torch.exp(raw[:3, :5, :4] * 2.0)
+    assert torch.allclose(prob, e / e.sum(-1, keepdim=True), atol=1e-6)

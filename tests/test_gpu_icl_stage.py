@@ -111,3 +111,49 @@ def test_attention_layer_strided_q_and_merged_output(dev):
         o = icl.icl_sdpa(q, cache.keys[:, 0], cache.values[:, 0], 650).transpose(1, 2).reshape(2, 130, W)
         want = F.linear(o, w_out)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("max_fused", [40959, 10 ** 9])
+def test_bucketed_dispatch_matches_unpadded_call(dev, max_fused):
+    # The reference runner's call pattern around the ICL stage (scripts/tabicl_tpu_bucketed.py:1298-1382):
+    # batch and test rows padded to their buckets (padded batch elements repeat element 0), the batch cut
+    # into ICL calls by the plan (one estimator per call for max_fused 40959, all four in one for 1e9),
+    # the real part sliced out. Here the same real rows come from one unpadded call over the real batch;
+    # both match the CPU restatement (same bar as above), and the padded element matches element 0.
+    import tabicl_mi355_buckets as bk
+    import tabicl_mi355_icl as icl
+    g = torch.Generator().manual_seed(82)
+    pre = bk.plan_prefill(3, 700, 10)
+    plan = bk.plan_query(pre, 300, max_fused_elements=max_fused)
+    assert (pre.batch_bkt, pre.train_bkt, plan.rows_bkt) == (4, 1024, 512)
+    assert plan.icl_step == (1 if max_fused < 40960 else 4)
+    NB, ff = 2, 2 * W
+    cache = icl.IclKVCache(pre.batch_bkt, NB, H, pre.train_bkt, D, torch.bfloat16, dev)
+    kc = torch.randn(3, NB, H, 700, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(3, NB, H, 700, D, generator=g).to(torch.bfloat16)
+    kp, vp = torch.cat([kc, kc[:1]]), torch.cat([vc, vc[:1]])  # the padded estimator's K/V repeat element 0's
+    for b in range(NB):
+        cache.append(b, kp[:, b].to(dev), vp[:, b].to(dev))
+    blocks = [_to(w, dev) for w in _weights(NB, ff, g)]
+    x = torch.randn(3, 300, W, generator=g)
+    xp = bk.pad_batch(x, plan, pad_features=False)
+    print(f"[icl_stage] bucketed dispatch, chunks {plan.chunks()}", flush=True)
+    with torch.no_grad():
+        raw = cache.query_chunked(xp.to(dev), blocks, plan.chunks())
+        padded = bk.unpad_output(raw, plan)
+        direct = cache.estimators(0, 3).query_blocks(x.to(dev), blocks)
+    torch.cuda.synchronize()
+    assert raw.shape == (4, 512, W) and padded.shape == direct.shape == (3, 300, W)
+    ref = _reference(x, [_cpu(w) for w in blocks], kc, vc, 700, torch.zeros(H, 1, D))
+    bar = 2e-2 * max(1.0, float(ref.abs().max()))
+    for got in (padded, direct):
+        assert torch.isfinite(got).all()
+        assert float((got.cpu() - ref).abs().max()) <= bar
+    assert float((padded - direct).abs().max()) <= bar
+    assert float((raw[3] - raw[0]).abs().max()) <= bar
+
+
+def _cpu(w):
+    import dataclasses
+    return dataclasses.replace(w, **{f.name: getattr(w, f.name).cpu() for f in dataclasses.fields(w)
+                                     if isinstance(getattr(w, f.name), torch.Tensor)})
