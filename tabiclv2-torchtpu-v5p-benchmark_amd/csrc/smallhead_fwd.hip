@@ -571,15 +571,24 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_resident_kernel(ShParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lds_v[RS_LK * RS_VSTR];
   __shared__ __attribute__((aligned(16))) float lds_b2[RS_LK];
 
-  // Run-major work order (all batch elements' first runs, then their second runs, ...) in the
-  // hardware's dispatch order: the runs of one element differ in work (the last one is shorter, and
-  // with per-element row counts any run past an element's rows is empty), and interleaving them
-  // element by element (or by XCD-contiguous ranges of elements) left part of the CUs with the heavy
-  // runs: measured on the 2k-row ISAB-2 shape with every element's rows cut to its first run, 3.41 ms
-  // element-major against 2.04 ms run-major (4.11 ms uncut); C5's ragged ISAB-2 leg 44.3 -> 36.3 ms.
-  // The runs of one element share only its 32 KB of K / V, which a second read takes from L2 / MALL.
-  const int b = blockIdx.x % p.B;
-  const int qb0 = (blockIdx.x / p.B) * p.qbpw;
+  // Work order. Ragged calls (per-element row counts): run-major (all batch elements' first runs,
+  // then their second runs, ...) in the hardware's dispatch order. Their runs differ in work (any
+  // run past an element's rows is empty), and interleaving them element by element (or by
+  // XCD-contiguous ranges of elements) left part of the CUs with the heavy runs: measured on the
+  // 2k-row ISAB-2 shape with every element's rows cut to its first run, 3.41 ms element-major
+  // against 2.04 ms run-major (4.11 ms uncut); C5's ragged ISAB-2 leg 44.3 -> 36.3 ms.
+  // Dense calls: element-major in XCD-contiguous ranges, so an element's runs share its K / V
+  // through one XCD's L2 (run-major spread them over the XCDs: C3 ISAB-2 read its 64 KB of K / V
+  // once per run from HBM, 2.5 GB more traffic, 1.13x the algorithmic bytes).
+  int b, qb0;
+  if (p.qlen) {
+    b = blockIdx.x % p.B;
+    qb0 = (blockIdx.x / p.B) * p.qbpw;
+  } else {
+    const int work = xcd_remap(blockIdx.x, gridDim.x);
+    b = work / p.nwg_b;
+    qb0 = (work % p.nwg_b) * p.qbpw;
+  }
   int lk = p.Lk;
   if (p.valid) {
     const int vl = p.valid[p.valid_n == 1 ? 0 : b];
