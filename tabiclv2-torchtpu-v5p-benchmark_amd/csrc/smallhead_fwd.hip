@@ -58,6 +58,8 @@ struct ShParams {
   int nqb, qbpw, nwg_b;
   int exact_scale;  // fold scale and log2e into the K operand: scale is a power of two (bf16(q * scale)
                     // needs no rounding) and the runs are long enough to amortise the K split
+  int pow2_scale;   // scale is a power of two
+  float qc;         // scale * log2e (exact for a power-of-two scale)
   int half_last;    // the last 32-key group's upper 16 keys are all past Lk (resident kernel, 4 groups)
   // RoPE tables: element (position, dim d) at position * tab_sr + (d & tab_cm); [L, E] tables give
   // (E, E - 1), tables of one head's columns shared by every head give (16, 15)
@@ -363,19 +365,20 @@ __device__ __forceinline__ bf16x8 rs_ksplit(bf16x8 k, float c, int G) {
   return op;
 }
 
-// q' log2e operand from this lane's 4 values of q' = bf16(rope(q) * scale) (the reference's packed
-// kernels, :498-502), held as floats. Each lane splits its 4 into bf16 high parts (vdst) and bf16
-// remainders (vsrc); one v_permlane32_swap per word (upper lanes' vdst <-> lower lanes' vsrc) leaves
-// lanes G < 2 with the 8 high parts and lanes G >= 2 with the 8 remainders of the shared dims, in
-// k-slot order, with no selects.
-__device__ __forceinline__ bf16x8 rs_qsplit(f32x4 qs, int G) {
+// q' log2e operand from this lane's 4 values v (v c = q' log2e: v = q' = bf16(rope(q) * scale) and c =
+// log2e, or, for a power-of-two scale, v = bf16(rope(q)) and c = scale log2e, the same product
+// exactly; the reference's packed kernels, :498-502). Each lane splits its 4 values of x = v c into
+// bf16 high parts (vdst) and bf16 remainders fma(v, c, -hi) (vsrc); one v_permlane32_swap per word
+// (upper lanes' vdst <-> lower lanes' vsrc) leaves lanes G < 2 with the 8 high parts and lanes
+// G >= 2 with the 8 remainders of the shared dims, in k-slot order, with no selects.
+__device__ __forceinline__ bf16x8 rs_qsplit(f32x4 v, float c, int G) {
   (void)G;
   f32x4 x, rem;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = qs[j] * TA_LOG2E;
+  for (int j = 0; j < 4; ++j) x[j] = v[j] * c;
   const bf16x4 hi = cvt_bf16x4(x);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) rem[j] = x[j] - (float)hi[j];
+  for (int j = 0; j < 4; ++j) rem[j] = __builtin_fmaf(v[j], c, -(float)hi[j]);
   const bf16x4 lo = cvt_bf16x4(rem);
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
   typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
@@ -460,6 +463,10 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 // positions 4 (G >> 1)) and the prefetched cos / sin of those 4 dims, for the two full-width forms
 // (rot = 16) this kernel takes: pairs in-lane; halves with the partner dims d4 ^ 8 from lane l ^ 16,
 // whose qr holds the other 8 dims of the head at the same positions (v_permlane16_swap).
+// y = fma(x, cos, partner sin): RF = 0 takes the form from p.rope and signs the partner (pairs: -x[d+1]
+// on even dims, +x[d-1] on odd; halves: -x[d+8] on dims 0..7, +x[d-8] on 8..15); RF = 1 (pairs) / 2
+// (halves) take tables whose sin already carries that sign (the same products exactly).
+template <int RF = 0>
 __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 cs, f32x4 sn, int G) {
   typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
   typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
@@ -468,11 +475,11 @@ __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 c
   const u32x2v ow = {upper ? w[2] : w[0], upper ? w[3] : w[1]};
   const bf16x4 own = __builtin_bit_cast(bf16x4, ow);
   f32x4 y;
-  if (p.rope == 1) {
+  if (RF == 1 || (RF == 0 && p.rope == 1)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float xp = (float)own[r ^ 1];
-      y[r] = (float)own[r] * cs[r] + ((r & 1) ? xp : -xp) * sn[r];
+      y[r] = __builtin_fmaf((float)own[r], cs[r], (RF != 0 || (r & 1) ? xp : -xp) * sn[r]);
     }
   } else {
     u32x2v pw;
@@ -482,28 +489,39 @@ __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 c
       pw[k] = (G & 1) ? r[0] : r[1];
     }
     const bf16x4 pt = __builtin_bit_cast(bf16x4, pw);
-    const float sg = (G & 1) ? 1.f : -1.f;  // dims 8..15 of the head: +x[jd - 8]; 0..7: -x[jd + 8]
+    const float sg = (RF != 0 || (G & 1)) ? 1.f : -1.f;  // dims 8..15 of the head: +x[jd - 8]; 0..7: -x[jd + 8]
 #pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = (float)own[r] * cs[r] + sg * (float)pt[r] * sn[r];
+    for (int r = 0; r < 4; ++r) y[r] = __builtin_fmaf((float)own[r], cs[r], sg * (float)pt[r] * sn[r]);
   }
   return y;
 }
 
 // q' log2e operand for scales that are not folded into K (or short runs): q' = bf16(rope(q) scale)
 // rounded here from the raw q (with RoPE: this block's cos / sin of the lane's 4 dims), split over
-// the two k-halves.
-template <bool ROPE>
+// the two k-halves. FOLD (a power-of-two scale): bf16(rope(q)) (pairs rounded together) times
+// scale log2e, the same operand with one multiply per value less.
+template <bool ROPE, int RF = 0, bool FOLD = false>
 __device__ __forceinline__ bf16x8 rs_qop_split(const ShParams& p, bf16x8 qr, f32x4 cs, f32x4 sn, int G) {
-  f32x4 qs;
+  f32x4 y;
   if constexpr (!ROPE) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)((float)qr[(G >> 1) * 4 + j] * p.scale);
+    for (int j = 0; j < 4; ++j) y[j] = (float)qr[(G >> 1) * 4 + j];
   } else {
-    const f32x4 y = rs_rope_q(p, qr, cs, sn, G);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) qs[j] = (float)(bf16)(y[j] * p.scale);
+    y = rs_rope_q<RF>(p, qr, cs, sn, G);
   }
-  return rs_qsplit(qs, G);
+  f32x4 v;
+  if constexpr (FOLD) {
+    if constexpr (ROPE) {
+      const bf16x4 yb = cvt_bf16x4(y);  // raw q needs no rounding
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = (float)yb[j];
+    }
+    return rs_qsplit(y, p.qc, G);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (float)(bf16)(y[j] * p.scale);
+    return rs_qsplit(v, TA_LOG2E, G);
+  }
 }
 
 // The sweep of one 16-query block over all keys from its q' operand, the exact-maximum recompute
@@ -797,14 +815,29 @@ __device__ __forceinline__ int rp_kchunk(int r, int c) { return r * 16 + (c ^ (r
 __device__ __forceinline__ int rp_vchunk(int r, int c) { return r * 16 + (c ^ ((r & 3) << 1)); }
 
 // LDS bytes of the persistent kernel for NK key rows (the tables only with RoPE).
+// Chunk c (0..7) of a staged table row: c < 4 cos of dims 4c..4c+3, else sin of dims 4(c-4)..; the
+// sin values carry the sign of the rotation's partner term for form RF (1 pairs, 2 halves).
+template <int RF>
+__device__ __forceinline__ f32x4 rp_sign_tab(f32x4 t, int c) {
+  if (c >= 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 4 * (c - 4) + j;
+      if (RF == 1 ? (d & 1) == 0 : d < 8) t[j] = -t[j];
+    }
+  }
+  return t;
+}
+
 __host__ __device__ inline int rp_lds_bytes(int NK, bool rope, int Lk, int Lq, bool qsep) {
   return 2 * NK * 256 + 2 * NK * 4 + (rope ? 128 * (Lk + (qsep ? Lq : 0)) : 0);
 }
 
-template <int NG, int MF, bool ROPE, bool HALF, int NB>
+template <int NG, int MF, int RF, bool HALF, int NB>
 __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
   constexpr int NT = SH_H * 64;
   constexpr int NK = NG * 32;
+  constexpr bool ROPE = RF != 0;
   extern __shared__ __attribute__((aligned(16))) unsigned char rp_lds[];
   bf16* const lds_k = (bf16*)rp_lds;
   bf16* const lds_v = (bf16*)(rp_lds + NK * 256);
@@ -873,16 +906,18 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
   if (lk > 0) issue(b, lk);
   if constexpr (ROPE) {
     // tables of the key rows (and of the query rows when they are other tensors), once per workgroup
+    // the sin columns take the sign of the partner term (pairs: - on even dims; halves: - on dims
+    // 0..7), so that the rotations multiply the unsigned partner (the same products exactly)
     for (int u = tid; u < 8 * p.Lk; u += NT) {
       const int r = u >> 3, c = u & 7;
       const float* src = (c < 4 ? p.ck : p.sk) + (int64_t)r * p.tab_sr + 4 * (c & 3);
-      *(f32x4*)(lds_tk + 32 * r + 4 * c) = *(const f32x4*)src;
+      *(f32x4*)(lds_tk + 32 * r + 4 * c) = rp_sign_tab<RF>(*(const f32x4*)src, c);
     }
     if (p.rp_qsep) {
       for (int u = tid; u < 8 * p.Lq; u += NT) {
         const int r = u >> 3, c = u & 7;
         const float* src = (c < 4 ? p.cq : p.sq) + (int64_t)r * p.tab_sr + 4 * (c & 3);
-        *(f32x4*)(lds_tq + 32 * r + 4 * c) = *(const f32x4*)src;
+        *(f32x4*)(lds_tq + 32 * r + 4 * c) = rp_sign_tab<RF>(*(const f32x4*)src, c);
       }
     }
   }
@@ -928,8 +963,8 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
         }
 #pragma unroll
         for (int d = 0; d < SH_D; ++d) {
-          const float xp = p.rope == 1 ? ((d & 1) ? x[d - 1] : -x[d + 1]) : (d < 8 ? -x[d + 8] : x[d - 8]);
-          y[d] = rs_rot(x[d], xp, tc[d], tc[16 + d]);
+          const float xp = RF == 1 ? ((d & 1) ? x[d - 1] : x[d + 1]) : (d < 8 ? x[d + 8] : x[d - 8]);
+          y[d] = rs_rot(x[d], xp, tc[d], tc[16 + d]);  // signed sin
         }
         bf16x8 o0, o1;
 #pragma unroll
@@ -980,7 +1015,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
       cs = *(const f32x4*)(lds_tq + 32 * row + (d4 & 15));
       sn = *(const f32x4*)(lds_tq + 32 * row + 16 + (d4 & 15));
     }
-    const bf16x8 qop = rs_qop_split<ROPE>(p, qr, cs, sn, G);
+    const bf16x8 qop = rs_qop_split<ROPE, RF, true>(p, qr, cs, sn, G);
     // b2 is read inside each block, not hoisted over the element's blocks (registers)
     int bo = b2off;
     asm volatile("" : "+s"(bo));
@@ -1085,34 +1120,44 @@ int rp_cus(int dev) {
 // LDS bytes that still let two persistent workgroups share a CU (160 KB of LDS per CU).
 constexpr int RP_LDS_MAX = 80 * 1024;
 
-template <int MF, bool ROPE, int NB>
+template <int MF, int RF, int NB>
 int launch_persist_inst(const ShParams& p, int dev, int nwg, int lds, hipStream_t stream) {
   // the dynamic-LDS limit of this instance, raised once per device
   static std::atomic<bool> raised[RP_DEV_CACHE];
   if (dev >= 0 && dev < RP_DEV_CACHE && !raised[dev].load(std::memory_order_relaxed)) {
-    (void)hipFuncSetAttribute((const void*)sh_persist_kernel<4, MF, ROPE, true, NB>,
+    (void)hipFuncSetAttribute((const void*)sh_persist_kernel<4, MF, RF, true, NB>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, RP_LDS_MAX);
     raised[dev].store(true, std::memory_order_relaxed);
   }
-  hipLaunchKernelGGL((sh_persist_kernel<4, MF, ROPE, true, NB>), dim3((unsigned)nwg), dim3(SH_H * 64),
+  hipLaunchKernelGGL((sh_persist_kernel<4, MF, RF, true, NB>), dim3((unsigned)nwg), dim3(SH_H * 64),
                      (unsigned)lds, stream, p);
   return (int)hipGetLastError();
 }
 
-template <bool ROPE, int NB>
+template <int RF, int NB>
 int launch_persist_nb(const ShParams& p, int dev, int mode, int nwg, int lds, hipStream_t stream) {
-  return mode == 0 ? launch_persist_inst<0, ROPE, NB>(p, dev, nwg, lds, stream)
-                   : launch_persist_inst<3, ROPE, NB>(p, dev, nwg, lds, stream);
+  return mode == 0 ? launch_persist_inst<0, RF, NB>(p, dev, nwg, lds, stream)
+                   : launch_persist_inst<3, RF, NB>(p, dev, nwg, lds, stream);
+}
+
+template <int NB>
+int launch_persist_rf(const ShParams& p, int dev, int mode, int nwg, int lds, hipStream_t stream) {
+  switch (p.rope) {
+    case 0: return launch_persist_nb<0, NB>(p, dev, mode, nwg, lds, stream);
+    case 1: return launch_persist_nb<1, NB>(p, dev, mode, nwg, lds, stream);
+    default: return launch_persist_nb<2, NB>(p, dev, mode, nwg, lds, stream);
+  }
 }
 
 // The persistent kernel for a resident-keys call, or -1 when the call does not suit it (then the
 // one-element-per-workgroup kernel runs): 97..112 keys (the row stage's 104 tokens), 1 or 7 query
 // blocks per element (CLS queries, the row stage's self attention), no per-batch row counts, the
-// shared one-head RoPE tables (q tables equal to the key tables, or staged separately), 16-byte
-// aligned K / V rows, LDS for two workgroups per CU and at least two elements per workgroup.
+// shared one-head RoPE tables (q tables equal to the key tables, or staged separately), a
+// power-of-two scale (folded into the q' operand's log2e factor), 16-byte aligned K / V rows, LDS for
+// two workgroups per CU and at least two elements per workgroup.
 int launch_persist(ShParams& p, int ngrp, int mode, hipStream_t stream) {
   if (ngrp != 4 || !p.half_last || mode == 2 || (p.nqb != 1 && p.nqb != 7) || p.qlen != nullptr ||
-      p.exact_scale)
+      p.exact_scale || !p.pow2_scale)
     return -1;
   if (p.rope && p.tab_sr != SH_D) return -1;
   if ((p.k_sr & 7) || (p.v_sr & 7) || ((uintptr_t)p.k & 15) || ((uintptr_t)p.v & 15)) return -1;
@@ -1125,11 +1170,8 @@ int launch_persist(ShParams& p, int ngrp, int mode, hipStream_t stream) {
   if (cus <= 0) return -1;
   const int nwg = 2 * cus;
   if (p.B < 2 * nwg) return -1;
-  if (p.nqb == 1)
-    return p.rope ? launch_persist_nb<true, 1>(p, dev, mode, nwg, lds, stream)
-                  : launch_persist_nb<false, 1>(p, dev, mode, nwg, lds, stream);
-  return p.rope ? launch_persist_nb<true, 7>(p, dev, mode, nwg, lds, stream)
-                : launch_persist_nb<false, 7>(p, dev, mode, nwg, lds, stream);
+  return p.nqb == 1 ? launch_persist_rf<1>(p, dev, mode, nwg, lds, stream)
+                    : launch_persist_rf<7>(p, dev, mode, nwg, lds, stream);
 }
 
 void launch_resident(const ShParams& p, int ngrp, int mode, int64_t nblk, hipStream_t stream) {
@@ -1497,6 +1539,8 @@ int tabicl_launch_smallhead(const void* q, int64_t q_sb, int64_t q_sr, const voi
   {
     int e = 0;
     p.exact_scale = scale > 0.f && frexpf(scale, &e) == 0.5f;
+    p.pow2_scale = p.exact_scale;
+    p.qc = scale * TA_LOG2E;
   }
   p.half_last = 0;
   p.qlen = qlen; p.qlen_n = (int)qlen_n;
