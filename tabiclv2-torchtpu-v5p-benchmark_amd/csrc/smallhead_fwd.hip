@@ -459,21 +459,17 @@ __device__ __forceinline__ float rs_max(const bf16x8 (&ka)[NG][2], bf16x8 qop, c
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-// RoPE of this lane's 4 dims of q (d4..d4+3) from the raw 8 dims qr of its k-slots (the lane's 4 at
-// positions 4 (G >> 1)) and the prefetched cos / sin of those 4 dims, for the two full-width forms
+// RoPE of this lane's 4 dims of q (d4..d4+3, `own`; rs_rope_q takes them from the raw 8 dims qr of its
+// k-slots, the lane's 4 at positions 4 (G >> 1)) and the prefetched cos / sin of those 4 dims, for the
+// two full-width forms
 // (rot = 16) this kernel takes: pairs in-lane; halves with the partner dims d4 ^ 8 from lane l ^ 16,
 // whose qr holds the other 8 dims of the head at the same positions (v_permlane16_swap).
 // y = fma(x, cos, partner sin): RF = 0 takes the form from p.rope and signs the partner (pairs: -x[d+1]
 // on even dims, +x[d-1] on odd; halves: -x[d+8] on dims 0..7, +x[d-8] on 8..15); RF = 1 (pairs) / 2
 // (halves) take tables whose sin already carries that sign (the same products exactly).
 template <int RF = 0>
-__device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 cs, f32x4 sn, int G) {
-  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 rs_rope_own(const ShParams& p, bf16x4 own, f32x4 cs, f32x4 sn, int G) {
   typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
-  const u32x4v w = __builtin_bit_cast(u32x4v, qr);
-  const bool upper = (G >> 1) != 0;
-  const u32x2v ow = {upper ? w[2] : w[0], upper ? w[3] : w[1]};
-  const bf16x4 own = __builtin_bit_cast(bf16x4, ow);
   f32x4 y;
   if (RF == 1 || (RF == 0 && p.rope == 1)) {
 #pragma unroll
@@ -482,6 +478,7 @@ __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 c
       y[r] = __builtin_fmaf((float)own[r], cs[r], (RF != 0 || (r & 1) ? xp : -xp) * sn[r]);
     }
   } else {
+    const u32x2v ow = __builtin_bit_cast(u32x2v, own);
     u32x2v pw;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -494,6 +491,21 @@ __device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 c
     for (int r = 0; r < 4; ++r) y[r] = __builtin_fmaf((float)own[r], cs[r], sg * (float)pt[r] * sn[r]);
   }
   return y;
+}
+
+// The lane's own 4 dims of its 8 k-slot dims qr.
+__device__ __forceinline__ bf16x4 rs_own4(bf16x8 qr, int G) {
+  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+  typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+  const u32x4v w = __builtin_bit_cast(u32x4v, qr);
+  const bool upper = (G >> 1) != 0;
+  const u32x2v ow = {upper ? w[2] : w[0], upper ? w[3] : w[1]};
+  return __builtin_bit_cast(bf16x4, ow);
+}
+
+template <int RF = 0>
+__device__ __forceinline__ f32x4 rs_rope_q(const ShParams& p, bf16x8 qr, f32x4 cs, f32x4 sn, int G) {
+  return rs_rope_own<RF>(p, rs_own4(qr, G), cs, sn, G);
 }
 
 // q' log2e operand for scales that are not folded into K (or short runs): q' = bf16(rope(q) scale)
@@ -522,6 +534,38 @@ __device__ __forceinline__ bf16x8 rs_qop_split(const ShParams& p, bf16x8 qr, f32
     for (int j = 0; j < 4; ++j) v[j] = (float)(bf16)(y[j] * p.scale);
     return rs_qsplit(v, TA_LOG2E, G);
   }
+}
+
+// The folded q' log2e operand from the lane's q dims (a power-of-two scale; sin tables signed, RF 1
+// or 2): bf16(rope(q)) (pairs of values rounded together; raw q needs no rounding) times scale log2e,
+// split.
+// Halves form: the partner dims d4 ^ 8 are the own dims of lane l ^ 16, taken with ds_swizzle (xor 16
+// within each 32 lanes; the LDS crossbar, no VALU).
+template <int RF>
+__device__ __forceinline__ bf16x8 rs_qop_own(const ShParams& p, bf16x4 q, f32x4 cs, f32x4 sn, int G) {
+  f32x4 y;
+  if constexpr (RF == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[j] = (float)q[j];
+  } else {
+    f32x4 r;
+    if constexpr (RF == 1) {
+      r = rs_rope_own<1>(p, q, cs, sn, G);
+    } else {
+      typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+      const u32x2v ow = __builtin_bit_cast(u32x2v, q);
+      u32x2v pw;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) pw[k] = (unsigned)__builtin_amdgcn_ds_swizzle((int)ow[k], 0x401F);
+      const bf16x4 pt = __builtin_bit_cast(bf16x4, pw);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = __builtin_fmaf((float)q[j], cs[j], (float)pt[j] * sn[j]);
+    }
+    const bf16x4 yb = cvt_bf16x4(r);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[j] = (float)yb[j];
+  }
+  return rs_qsplit(y, p.qc, G);
 }
 
 // The sweep of one 16-query block over all keys from its q' operand, the exact-maximum recompute
@@ -886,19 +930,19 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
   };
   const int kcol = g * SH_D + 8 * (G & 1);
   const int d4 = kcol + 4 * (G >> 1);
-  const int qoff = (l16 * (int)p.q_sr + kcol) * 2, qstep = 16 * (int)p.q_sr * 2;
+  const int qoff = (l16 * (int)p.q_sr + d4) * 2, qstep = 16 * (int)p.q_sr * 2;
   const int ooff = (l16 * (int)p.o_sr + g * SH_D + 4 * G) * 2, ostep = 16 * (int)p.o_sr * 2;
-  // q of stream block t (element t / nb of this workgroup, block t % nb); past the last element the
-  // resource is empty and the load reads zeros
-  auto qload = [&](int t) {
-    const int it = t / nb, m = t - it * nb;
+  // the lane's own 4 dims of q in block m of the workgroup's element it (the callers' it and m are
+  // compile-time offsets from the current element, so the resource is shared by its blocks); past
+  // the last element the resource is empty and the load reads zeros
+  auto qload = [&](int it, int m) {
     const int bb = (int)blockIdx.x + it * stride;
     const int rows = it < nitems ? p.Lq : 0;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (bf16*)p.q + (int64_t)(it < nitems ? bb : 0) * p.q_sb, 0, rows * (int)p.q_sr * 2, TA_BUF_WORD3);
     int so = m * qstep;
     asm volatile("" : "+s"(so));  // formed at the load, not hoisted into a register per block
-    return rs_qraw(rs, qoff + so);
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rs, qoff + so, 0, 0));
   };
 
   int b = blockIdx.x;
@@ -922,7 +966,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
     }
   }
   float braw = bias_raw(b);
-  bf16x8 qa = qload(0), qb = qload(1);
+  bf16x4 qa = qload(0, 0), qb = NB >= 2 ? qload(0, 1) : qload(1, 0);
   __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc((bf16*)p.o + (int64_t)b * p.o_sb, 0,
                                                                  p.Lq * (int)p.o_sr * 2, TA_BUF_WORD3);
   // a zero store to the first element's block 0 (which this wave rewrites later, in order): the
@@ -938,7 +982,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
   // Element set-up: its copies have landed (first element: everything; later ones: the copies are
   // older than the previous element's last q load and output store, so all but the two youngest
   // memory operations), b2, RoPE on K, operands, then the next element's copies.
-  auto setup = [&](int it, bf16x8& q0, bf16x8& q1) {
+  auto setup = [&](int it, bf16x4& q0, bf16x4& q1) {
     if (it == 0)
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     else
@@ -1007,7 +1051,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
   };
 
   // one block of the stream: q' operand (RoPE tables from LDS), sweep, store
-  auto block = [&](bf16x8 qr, int m) -> u32x2 {
+  auto block = [&](bf16x4 qr, int m) -> u32x2 {
     if (lk == 0) return u32x2{0u, 0u};
     f32x4 cs = {0.f, 0.f, 0.f, 0.f}, sn = cs;
     if constexpr (ROPE) {
@@ -1015,7 +1059,7 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
       cs = *(const f32x4*)(lds_tq + 32 * row + (d4 & 15));
       sn = *(const f32x4*)(lds_tq + 32 * row + 16 + (d4 & 15));
     }
-    const bf16x8 qop = rs_qop_split<ROPE, RF, true>(p, qr, cs, sn, G);
+    const bf16x8 qop = rs_qop_own<RF>(p, qr, cs, sn, G);
     // b2 is read inside each block, not hoisted over the element's blocks (registers)
     int bo = b2off;
     asm volatile("" : "+s"(bo));
@@ -1025,14 +1069,13 @@ __global__ __launch_bounds__(SH_H * 64, 4) void sh_persist_kernel(ShParams p) {
   // One element: set-up, then its blocks, each computing with q0 / q1 alternately and loading the
   // block two ahead into the same register. After an odd block count the next element's block 0 is in
   // q1 and block 1 in q0, so elements alternate the roles of qa and qb (no register moves).
-  auto element = [&](int it, bf16x8& q0, bf16x8& q1) {
+  auto element = [&](int it, bf16x4& q0, bf16x4& q1) {
     setup(it, q0, q1);
-    const int t0 = it * NB;
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
-      bf16x8& qr = (m & 1) ? q1 : q0;
+      bf16x4& qr = (m & 1) ? q1 : q0;
       const u32x2 ov = block(qr, m);
-      qr = qload(t0 + m + 2);
+      qr = qload(it + (m + 2) / NB, (m + 2) % NB);
       int so = m * ostep;
       asm volatile("" : "+s"(so));
       rs_store(ors, ov, ooff + so);
