@@ -874,9 +874,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       st.nm[qc] = mx > -1e4f ? -fminf(ceilf(mx), 1e4f) : 0.f;
     }
 
-    if (nfull == 1) {
-      ip_iter<true, true>(st, sA, sB, pA, pB, lds, c, 0);
-    } else if (nfull > 1) {
+    if (nfull > 1) {
       ip_iter<true, false>(st, sA, sB, pA, pB, lds, c, 0);
       int t = 1;
       for (; t + IP_NBUF < nfull; t += IP_NBUF) {  // t % IP_NBUF == 1 at the top
@@ -887,8 +885,15 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       }
       for (; t + 1 < nfull; ++t) ip_iter<false, false>(st, sA, sB, pA, pB, lds, c, t);
       ip_iter<false, true>(st, sA, sB, pA, pB, lds, c, nfull - 1);
+      ip_pv(st, pB, lds[(nfull - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
+    } else if (nfull == 1) {
+      // one full tile: the unpipelined form (the same probabilities, products and order), then the
+      // join that the pipelined iteration would make (tile 1 landed; the idle waves make it too).
+      // A pipelined instance for this case kept the first tile's probabilities live across the
+      // sweep and made the compiler spill 25 VGPRs around it.
+      ip_tail(st, lds[0], lds[0] + ICL_KT * ICL_D, t0 * ICL_KT, valid, c.sc, lane);
+      TA_WAIT_JOIN(4);
     }
-    if (nfull > 0) ip_pv(st, pB, lds[(nfull - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
     if (nfull < nt) {
       // the crossing tile landed at the last join (or before the sweep when it is the only tile)
       const bf16* lk = lds[nfull % IP_NBUF];

@@ -31,6 +31,8 @@ def _err(out, ref):
     ("valid_scalar_bf16", 2, 8, 300, 1000, 777, torch.bfloat16),
     ("valid_scalar_fp32", 2, 8, 300, 1000, 777, torch.float32),
     ("valid_tile_edge", 1, 8, 128, 256, 64, torch.bfloat16),
+    ("one_full_tile_and_tail", 2, 8, 300, 256, 100, torch.bfloat16),
+    ("two_full_tiles", 1, 8, 300, 256, 128, torch.bfloat16),
     ("valid_one_key", 1, 4, 64, 128, 1, torch.float32),
     ("odd_sizes", 3, 2, 1000, 4099, None, torch.bfloat16),
 ])

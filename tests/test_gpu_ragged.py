@@ -41,6 +41,9 @@ def _check_rows(out, ref, q_len, row_dim, untouched=False):
     ("nosplit_bf16", 4, 8, 700, 900, None, [700, 999, 256, 1], torch.bfloat16),
     ("shared_qlen_bf16", 2, 4, 600, 2000, [2000], [300], torch.bfloat16),
     ("split_fp32", 3, 2, 300, 2500, [2500, 100, 1], [129, 300, 64], torch.float32),
+    # one or two full key tiles (with and without a crossing tile) in work items whose later waves
+    # hold no live row: the idle waves' joins match the single-tile path's
+    ("short_keys_idle_waves_bf16", 3, 8, 600, 300, [100, 64, 130], [70, 200, 1], torch.bfloat16),
     # many work items (the live work-item list of the pipelined kernel, a count that is not a multiple
     # of the 8 XCDs): per-element valid lengths and row counts across work-item edges, 0 and past Tq
     ("list_bf16", 37, 8, 1024, 2500, "random", "random", torch.bfloat16),
