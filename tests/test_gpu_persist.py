@@ -49,6 +49,8 @@ def _sample(B):
 @pytest.mark.parametrize("name,B,interleaved,bias", [
     ("rope_halves", 1100, False, False),
     ("rope_pairs_bias", 1100, True, True),
+    ("rope_halves_bias", 4100, False, True),  # the row stage with padded feature slots
+    ("rope_pairs", 1100, True, False),
 ])
 def test_pk_self_row_stage(dev, name, B, interleaved, bias):
     import tabicl_mi355_attn as pk
