@@ -697,7 +697,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the workload shards by estimator with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the workload would shard by estimator, one cache per GPU, with no exchange)", file=sys.stderr)
         return 2
 
     import torch
