@@ -1,12 +1,12 @@
-"""GPU checks at BASELINE's full sizes for the row (C2) and column ISAB-2 (C3) attention, the two d = 16
-configs that the other GPU tests run at reduced batch: the fp64 oracle on sampled sequences, and over
+"""GPU checks at BASELINE's full sizes for the fp32 column attention (C1), the row attention (C2) and
+both column ISAB legs (C3), configs that the other GPU tests run at reduced batch: the fp64 oracle on sampled sequences, and over
 the whole output the size-independent properties of softmax attention: every output is finite and,
 per head and dimension, lies between the smallest and largest value of V over the keys (a convex
 combination), and a bit-identical rerun. Inputs come from a device generator (the CPU oracle gets
 copies of the sampled sequences only).
 
-Bar (written here): max abs error <= 2e-2 against the oracle (bf16 inputs); hull with 2e-2 slack for
-the bf16 rounding of the output.
+Bar (written here): max abs error <= 2e-2 against the oracle (bf16 inputs), <= 1e-4 (fp32 inputs);
+hull with 2e-2 slack for the bf16 rounding of the output (1e-4 for fp32).
 """
 import pytest
 import torch
@@ -77,3 +77,60 @@ def test_c3_isab2_full_size(dev):
         err = float(np.abs(out[b:b + 1, rows].double().cpu().numpy() - ref).max())
         assert err <= 2e-2, (b, err)
     del q, out
+
+
+def test_c3_isab1_full_size(dev):
+    # 800 sequences x 128 inducing queries over 50,000 rows of packed K|V, 45,000 valid; the rows past
+    # the valid length hold NaN (never read). Hull over the valid keys, computed in bf16 (no fp32 copy).
+    import numpy as np
+
+    import tabicl_mi355_attn as pk
+    g = torch.Generator(device=dev).manual_seed(3)
+    B, T, VALID, NI = 800, 50000, 45000, 128
+    q = (torch.randn(B, NI, E, generator=g, device=dev) * 0.25).to(torch.bfloat16)
+    kv = torch.randn(B, T, 2 * E, generator=g, device=dev).to(torch.bfloat16)
+    kv[:, VALID:] = float("nan")
+    vt = torch.tensor([VALID], dtype=torch.int32, device=dev)
+    print("[fullsize] c3 isab1", flush=True)
+    with torch.no_grad():
+        out = pk.hxq_attention(q, kv, vt, H)
+        again = pk.hxq_attention(q, kv, vt, H)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out, again)
+    vmax = kv[:, :VALID, E:].amax(dim=1, keepdim=True).float()
+    vmin = kv[:, :VALID, E:].amin(dim=1, keepdim=True).float()
+    assert bool((out.float() <= vmax + 2e-2).all()) and bool((out.float() >= vmin - 2e-2).all())
+    for b in (0, 399, B - 1):
+        ref = O.hxq_ref(q[b:b + 1].cpu(), kv[b:b + 1, :VALID].cpu(), np.array([VALID]), H)
+        err = float(np.abs(out[b:b + 1].double().cpu().numpy() - ref).max())
+        assert err <= 2e-2, (b, err)
+    del q, kv, out, again
+
+
+@pytest.mark.parametrize("leg", ["isab1", "isab2"])
+def test_c1_fp32_full_size(dev, leg):
+    # BASELINE config 1 in fp32: 400 sequences, ISAB-1 = 128 queries over 1,024 keys (the streaming
+    # kernel), ISAB-2 = 1,024 queries over 128 keys (the resident kernel), q pre-scaled by 1/4
+    import numpy as np
+
+    import tabicl_mi355_attn as pk
+    g = torch.Generator(device=dev).manual_seed(4)
+    B = 400
+    Lq, Lk = (128, 1024) if leg == "isab1" else (1024, 128)
+    q = torch.randn(B, Lq, E, generator=g, device=dev) * 0.25
+    k = torch.randn(B, Lk, E, generator=g, device=dev)
+    v = torch.randn(B, Lk, E, generator=g, device=dev)
+    print(f"[fullsize] c1 {leg}", flush=True)
+    with torch.no_grad():
+        out = pk.hx_attention(q, k, v, H)
+        again = pk.hx_attention(q, k, v, H)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32 and torch.isfinite(out).all()
+    assert torch.equal(out, again)
+    assert bool((out <= v.amax(dim=1, keepdim=True) + 1e-4).all())
+    assert bool((out >= v.amin(dim=1, keepdim=True) - 1e-4).all())
+    for b in (0, 199, B - 1):
+        ref = O.hx_ref(q[b:b + 1].cpu(), k[b:b + 1].cpu(), v[b:b + 1].cpu(), H)
+        err = float(np.abs(out[b:b + 1].double().cpu().numpy() - ref).max())
+        assert err <= 1e-4, (b, err)
