@@ -134,3 +134,70 @@ def test_c1_fp32_full_size(dev, leg):
         ref = O.hx_ref(q[b:b + 1].cpu(), k[b:b + 1].cpu(), v[b:b + 1].cpu(), H)
         err = float(np.abs(out[b:b + 1].double().cpu().numpy() - ref).max())
         assert err <= 1e-4, (b, err)
+
+
+def test_c5_ragged_buckets_full_size(dev):
+    # BASELINE config 5 as bench.py draws it (64 tables, seed-fixed sizes): every ICL bucket at its full
+    # shape (8 estimators x 8 heads per table, test rows padded to 1k over the train bucket, per-table
+    # valid and test-row counts), and the column ISAB-2 buckets up to 4k rows (8 estimators x 100
+    # features per table, per-sequence row counts). The ragged call's live rows equal the padded call's
+    # bit for bit; sampled tables match the oracle; live outputs are finite.
+    import numpy as np
+
+    import bench
+    import tabicl_mi355_attn as pk
+    import tabicl_mi355_icl as icl
+    n_train, n_test = bench.c5_tables()
+    groups = {}
+    for i in range(64):
+        groups.setdefault(("isab", bench.c5_bucket(int(n_train[i] + n_test[i]))), []).append(i)
+        groups.setdefault(("icl", bench.c5_bucket(int(n_train[i]))), []).append(i)
+    g = torch.Generator(device=dev).manual_seed(5)
+    for (kind, L), tabs in sorted(groups.items()):
+        nt = [int(n_train[i]) for i in tabs]
+        ns = [int(n_test[i]) for i in tabs]
+        print(f"[fullsize] c5 {kind} bucket {L}: {len(tabs)} tables", flush=True)
+        if kind == "icl":
+            N, Tq = len(tabs) * 8, 1024
+            valid = torch.tensor(nt, dtype=torch.int32).repeat_interleave(8).to(dev)
+            qlen = torch.tensor(ns, dtype=torch.int32).repeat_interleave(8).to(dev)
+            k = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
+            q = torch.randn(N, H, Tq, 64, generator=g, device=dev, dtype=torch.bfloat16)
+            padded, ragged = torch.empty_like(q), torch.zeros_like(q)
+            with torch.no_grad():
+                icl.ICL_FWD_OUT(q, k, v, valid, 64 ** -0.5, padded)
+                icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, ragged)
+            torch.cuda.synchronize()
+            for n in range(N):
+                m = ns[n // 8]
+                assert torch.equal(ragged[n, :, :m], padded[n, :, :m]), (L, n)
+                assert torch.isfinite(ragged[n, :, :m].float()).all()
+            for n in (0, N - 1):
+                m, vl = ns[n // 8], nt[n // 8]
+                ref = O.splash_sdpa_ref(q[n:n + 1, :2, :m].cpu(), k[n:n + 1, :2].cpu(), v[n:n + 1, :2].cpu(),
+                                        np.array([vl]))
+                err = float(np.abs(ragged[n:n + 1, :2, :m].double().cpu().numpy() - ref).max())
+                assert err <= 2e-2, (L, n, err)
+            del k, v, q, padded, ragged
+        elif L <= 4096:
+            B = len(tabs) * 800
+            rows = [a + b for a, b in zip(nt, ns)]
+            qlen = torch.tensor(rows, dtype=torch.int32).repeat_interleave(800).to(dev)
+            q2 = torch.randn(B, L, E, generator=g, device=dev, dtype=torch.bfloat16)
+            kv2 = torch.randn(B, 128, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
+            with torch.no_grad():
+                padded = pk.pk_cross_attention(q2, kv2, H, None, None, 0.25)
+                ragged = pk.pk_cross_attention(q2, kv2, H, None, None, 0.25, q_len=qlen)
+            torch.cuda.synchronize()
+            for t, r in enumerate(rows):
+                sl = slice(800 * t, 800 * (t + 1))
+                assert torch.equal(ragged[sl, :r], padded[sl, :r]), (L, t)
+            for b in (0, B - 1):
+                r = rows[b // 800]
+                sel = torch.arange(0, r, 7)
+                ref = O.pk_cross_ref(q2[b:b + 1, sel].cpu(), kv2[b:b + 1].cpu(), H, None, None, None, 0.25)
+                err = float(np.abs(ragged[b:b + 1, sel].double().cpu().numpy() - ref).max())
+                assert err <= 2e-2, (L, b, err)
+            del q2, kv2, padded, ragged
+        torch.cuda.empty_cache()
