@@ -463,6 +463,46 @@ def test_resident_long_runs_rope(dev):
         assert _err(out[b:b + 1], ref) <= 2e-2
 
 
+@pytest.mark.parametrize("name,Lk,bias,hot", [
+    ("four_groups", 128, False, False),              # no b2 term
+    ("four_groups_key_bias", 128, True, False),      # b2 on every group (key bias, masked tail)
+    ("four_groups_last_partial", 120, False, False),  # b2 on the last group only
+    ("two_groups_last_partial", 60, False, False),
+    ("one_group", 32, False, False),
+    ("sums_out_of_range", 128, True, True),          # exact-maximum recompute, mixed waves
+])
+def test_resident_exact_scale_long_runs(dev, name, Lk, bias, hot):
+    # runs of more than 8 16-query blocks per workgroup with a power-of-two scale: the K operand
+    # carries scale log2e as bf16 high parts and remainders (the exact-scale form the column ISAB-2
+    # takes at C3 / C5 sizes), under every b2 mode and the exact-maximum recompute.
+    # 70 x 16000 queries: odd runs of 9 blocks, and the last run of each element holds 10 rows
+    pk = _attn()
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    B, Lq = 70, 16000
+    q = torch.randn(B, Lq, E, generator=g, device=dev) * 0.25
+    if hot:
+        q[1, 0::2] *= 120.0  # sums past 2^64 on every other query
+    q = q.to(torch.bfloat16)
+    k = torch.randn(B, Lk, E, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, Lk, E, generator=g, device=dev).to(torch.bfloat16)
+    kb = None
+    if bias:
+        kb = torch.randn(B, Lk, generator=g, device=dev) * 2.0
+        kb[:, Lk - 5:] = -1e30
+        if hot:
+            kb[0] = -60.0  # sums below 2^-64
+    print(f"[resident exact] {name}", flush=True)
+    out = pk.hx_attention(q, k, v, H, kb).cpu()
+    assert torch.isfinite(out.float()).all()
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    kbc = None if kb is None else kb.cpu()
+    for b in (0, 1, 69):
+        rows = np.r_[0:200, Lq - 300:Lq]
+        ref = O.hx_ref(qc[b:b + 1, rows], kc[b:b + 1], vc[b:b + 1], H, None if kbc is None else kbc[b:b + 1])
+        assert _err(out[b:b + 1, rows], ref) <= 2e-2, f"{name}: element {b}"
+
+
 @pytest.mark.parametrize("interleaved", [False, True])
 def test_resident_long_runs_cross_rope(dev, interleaved):
     # pk_cross with RoPE (positions 0..L-1 on both sides) and runs of several 16-query blocks per
