@@ -13,6 +13,9 @@
  * ops, rows are E (q/k/v), 2E (packed K|V) or 3E (packed Q|K|V) wide, heads are contiguous d-wide
  * column blocks. Softmax is fp32; scores accumulate in fp32; probabilities are cast to the value
  * dtype before the PV product; outputs are written in the query dtype.
+ *
+ * Empty calls: a batch of 0 elements or 0 query rows returns 0 without any launch (the key count may
+ * then be 0 too, e.g. an empty self-attention); otherwise at least one key is required.
  */
 #ifndef TABICL_ATTN_H
 #define TABICL_ATTN_H

@@ -38,7 +38,10 @@ int smallhead_shape(const char* op, int64_t B, int64_t Lq, int64_t Lk, int64_t E
   if (E != 128 || h != 8)
     return fail(1, "%s: needs E == 128 and h == 8 (head dim 16), got E=%lld h=%d", op,
                 (long long)E, h);
-  if (B < 0 || Lq < 0 || Lk < 1 || B > (1LL << 30) || Lq > (1LL << 30) || Lk > (1LL << 30))
+  // no keys only where there is nothing to compute (no batch element or no query row: an empty
+  // self-attention); the entry points return before any launch then
+  const int64_t lk_min = B > 0 && Lq > 0 ? 1 : 0;
+  if (B < 0 || Lq < 0 || Lk < lk_min || B > (1LL << 30) || Lq > (1LL << 30) || Lk > (1LL << 30))
     return fail(1, "%s: bad sizes B=%lld Lq=%lld Lk=%lld", op, (long long)B, (long long)Lq,
                 (long long)Lk);
   return 0;
@@ -86,7 +89,7 @@ int bwd_common(const char* op, int64_t B, int64_t Lq, int64_t Lk, int64_t E, int
   if (st) return st;
   if (bias && bias_b != 1 && bias_b != B)
     return fail(1, "%s: bias batch %lld must be 1 or B=%lld", op, (long long)bias_b, (long long)B);
-  if (!o || !dout || !aligned16(o) || !aligned16(dout))
+  if (B > 0 && Lq > 0 && (!o || !dout || !aligned16(o) || !aligned16(dout)))
     return fail(1, "%s: o and dout must be 16-byte aligned device pointers", op);
   if (B > 0 && Lq > 0 && (!ws || !aligned16(ws) || ws_bytes < tabicl_launch_smallhead_bwd_ws_bytes(B, Lq)))
     return fail(1, "%s: workspace of %lld bytes (16-byte aligned) required", op,
@@ -290,7 +293,7 @@ int tabicl_hx_bwd(const void* q, const void* k, const void* v, const float* bias
   if (st) return st;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
     return fail(1, "hx_bwd: pointers must be 16-byte aligned");
-  if (B == 0) return 0;
+  if (B == 0 || Lk == 0) return 0;
   return launch_status(
       tabicl_launch_smallhead_bwd(q, Lq * E, E, k, Lk * E, E, v, Lk * E, E, o, dout, dq, Lq * E, E, dk, Lk * E, E,
                                   dv, Lk * E, E, bias, bias && bias_b == B ? Lk : 0, nullptr, nullptr, nullptr,
@@ -336,7 +339,7 @@ int tabicl_pk_cross_bwd(const void* q, int64_t q_b, const void* kv, const float*
     return fail(1, "pk_cross_bwd: rope tables must be 16-byte aligned");
   if (!aligned16(q) || !aligned16(kv) || !aligned16(dq) || !aligned16(dkv))
     return fail(1, "pk_cross_bwd: pointers must be 16-byte aligned");
-  if (B == 0) return 0;
+  if (B == 0 || Lk == 0) return 0;
   const char* kvb = (const char*)kv;
   char* dkvb = (char*)dkv;
   const size_t es = esize(dtype);

@@ -17,6 +17,7 @@ Replaces the reference's Splash path for the ICL stage:
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 from typing import Callable, Optional, Union
 
@@ -155,9 +156,10 @@ def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, 
     lead = q.shape[:-3]
     H, Tq = q.shape[-3], q.shape[-2]
     Tkv = k.shape[-2]
-    q4 = q.reshape(-1, H, Tq, D)
-    k4 = k.reshape(-1, H, Tkv, D)
-    v4 = v.reshape(-1, H, Tkv, D)
+    n = math.prod(lead)  # explicit: reshape(-1, ...) is ambiguous with no query rows
+    q4 = q.reshape(n, H, Tq, D)
+    k4 = k.reshape(n, H, Tkv, D)
+    v4 = v.reshape(n, H, Tkv, D)
     valid = None
     if isinstance(valid_kv_len, Tensor):
         valid = valid_kv_len.to(device=q.device, dtype=torch.int32).reshape(-1).contiguous()

@@ -36,6 +36,7 @@ torch math run on CPU tensors in tests; the HIP kernels never run on CPU tensors
 """
 from __future__ import annotations
 
+import math
 import os
 from dataclasses import dataclass
 from typing import Optional
@@ -236,7 +237,7 @@ def _ssmax(ssmax_layer, q: Tensor, h: int, n) -> Tensor:  # noqa: ANN001
     (results/tpu_patch.diff:251-254)."""
     qh = _heads(q, h)
     lead = qh.shape[:-3]
-    return _merge(ssmax_layer(qh.reshape(-1, *qh.shape[-3:]), n).reshape(*lead, *qh.shape[-3:]))
+    return _merge(ssmax_layer(qh.reshape(math.prod(lead), *qh.shape[-3:]), n).reshape(*lead, *qh.shape[-3:]))
 
 
 # ---------------------------------------------------------------------------------------------
@@ -518,10 +519,11 @@ def icl_hook(upstream_sdpa):  # noqa: ANN001
                 and q.dtype in (torch.bfloat16, torch.float32) and q.dtype == k.dtype == v.dtype
                 and _ICL.icl_supported(q.shape[-2], Tkv, q.shape[-1], q.dtype)):
             lead = q.shape[:-3]
-            q3 = q.reshape(-1, *q.shape[-3:])
+            q3 = q.reshape(math.prod(lead), *q.shape[-3:])
             if ssmax_layer is not None:
                 q3 = ssmax_layer(q3, src_len_override if src_len_override is not None else Tkv)
-            out = _ICL.icl_sdpa(q3, k.reshape(-1, *k.shape[-3:]), v.reshape(-1, *v.shape[-3:]), valid_kv_len, kb)
+            out = _ICL.icl_sdpa(q3, k.reshape(q3.shape[0], *k.shape[-3:]), v.reshape(q3.shape[0], *v.shape[-3:]),
+                                valid_kv_len, kb)
             return out.reshape(*lead, *out.shape[-3:])
         return upstream_sdpa(q, k, v, attn_mask, dropout_p, ssmax_layer=ssmax_layer,
                              src_len_override=src_len_override, valid_kv_len=valid_kv_len)

@@ -89,6 +89,19 @@ def test_bad_arguments_rejected_before_launch():
         nat.check(1, "x")
 
 
+def test_empty_calls_return_before_launch():
+    # no batch element or no query row: status 0 with nothing dereferenced or launched (NULL pointers,
+    # no stream), the key count then allowed to be 0 (an empty self-attention); keys are still required
+    # when there is work
+    import tabicl_mi355_native as nat
+    lib = nat.load()
+    assert lib.tabicl_pk_self_fwd(None, None, 1, None, None, None, 3, 0, 128, 8, 0, 8, 16, 0.25, 0, None) == 0
+    assert lib.tabicl_hx_fwd(None, None, None, None, 1, None, 3, 0, 0, 128, 8, 0, None) == 0
+    assert lib.tabicl_hx_fwd(None, None, None, None, 1, None, 0, 40, 0, 128, 8, 0, None) == 0
+    st = lib.tabicl_hx_fwd(None, None, None, None, 1, None, 3, 40, 0, 128, 8, 0, None)
+    assert st == 1 and "bad sizes" in nat.last_error()
+
+
 @pytest.mark.parametrize("shared", [False, True])
 def test_rope_table_shapes_refused_before_launch(shared):
     # a table of the wrong width, length or dtype is refused before any pointer reaches the library
