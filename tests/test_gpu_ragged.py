@@ -47,6 +47,8 @@ def _check_rows(out, ref, q_len, row_dim, untouched=False):
     # many work items (the live work-item list of the pipelined kernel, a count that is not a multiple
     # of the 8 XCDs): per-element valid lengths and row counts across work-item edges, 0 and past Tq
     ("list_bf16", 37, 8, 1024, 2500, "random", "random", torch.bfloat16),
+    # heads not a multiple of 8: one list section, each XCD an equal contiguous share (with remainders)
+    ("list_h12_bf16", 21, 12, 1024, 2500, "random", "random", torch.bfloat16),
 ])
 def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
     import tabicl_mi355_icl as icl
