@@ -8,12 +8,12 @@
 //
 // Work decomposition. A workgroup = (batch b, key split s, head group hg of 4 heads, 128 queries);
 // 8 waves = 4 heads x 2 halves of 64 queries, each wave four 16-query blocks of one head (<= 128
-// VGPRs, two workgroups per CU). Its key range streams through LDS in 32-key tiles holding K and V
-// of its 4 heads (two whole 128-byte lines per key), copied by the load unit itself
-// (global_load_lds_dwordx4) seven tiles ahead, with 16-byte chunks XOR-swizzled per key so that
-// the LDS operand reads below do not conflict on banks.
+// VGPRs, two workgroups per CU). Its key range streams through LDS in 64-key tiles (two 32-key
+// sub-tiles, one workgroup join per tile) holding K and V of its 4 heads (two whole 128-byte lines
+// per key), copied by the load unit itself (global_load_lds_dwordx4) three tiles ahead, with 16-byte
+// chunks XOR-swizzled per key so that the LDS operand reads below do not conflict on banks.
 //
-// Per (16-query block, 32-key tile) a wave runs four v_mfma_f32_16x16x32_bf16:
+// Per (16-query block, 32-key sub-tile) a wave runs four v_mfma_f32_16x16x32_bf16:
 //   x  = K (q log2e) - m    two MFMAs; the 32-deep contraction holds q*log2e split in a bf16 high
 //                           part (k-slots 0..15) and the bf16 rounding remainder (slots 16..31)
 //                           against the same K, and the accumulator starts at -m: the MFMA output
@@ -23,11 +23,11 @@
 // so the VALU work per score is one v_exp_f32 and half a conversion.
 //
 // Softmax reference m (per query and head). The sweep over a split's keys does not track the
-// running maximum: m is the (ceiled) maximum over the split's first tile and stays fixed, so p =
-// exp2(x) may exceed 1. The row sum l > 1/2 from the first tile on; if at the end of the sweep l <=
+// running maximum: m is the (ceiled) maximum over the split's first 32 keys and stays fixed, so p =
+// exp2(x) may exceed 1. The row sum l > 1/2 from the first sub-tile on; if at the end of the sweep l <=
 // 2^96 and O is finite, every p stayed far inside the bf16/fp32 range and the result equals the
 // max-subtracted softmax to rounding (fp32/bf16 relative precision does not depend on scale). A
-// score more than ~66 nats above the first tile's maximum (or a NaN / inf) breaks that test; the
+// score more than ~66 nats above the first sub-tile's maximum (or a NaN / inf) breaks that test; the
 // workgroup then sweeps the split again in exact mode, a classic online softmax that moves m by
 // exact powers of two. No test or branch runs per tile in the fast sweep.
 //
@@ -45,13 +45,15 @@ constexpr int SS_NHG = SS_H / SS_HPW;    // head groups
 constexpr int SS_NW = 2 * SS_HPW;        // waves per workgroup: heads x 2 query halves
 constexpr int SS_NB = 4;                 // 16-query blocks per wave
 constexpr int SS_QG = 2 * 16 * SS_NB;    // queries per workgroup
-constexpr int SS_KT = 32;                // keys per tile
+constexpr int SS_KT = 64;                // keys per tile (one LDS buffer, one join of the sweep)
+constexpr int SS_ST = 32;                // keys per sub-tile (one operand set of the products)
 constexpr int SS_ROW = 32 * SS_HPW * 2;  // tile row bytes: K then V of the heads, bf16 (256)
 constexpr int SS_CPR = SS_ROW / 16;      // 16-byte chunks per row (16)
-constexpr int SS_TILE = SS_KT * SS_ROW;  // 8 KB
-constexpr int SS_NBUF = 8;
+constexpr int SS_STILE = SS_ST * SS_ROW;  // 8 KB
+constexpr int SS_TILE = SS_KT * SS_ROW;   // 16 KB
+constexpr int SS_NBUF = 4;
 constexpr int SS_MAX_SPLIT = 8;
-constexpr int SS_MIN_TILES = 16;         // per key split
+constexpr int SS_MIN_TILES = 8;          // per key split
 constexpr float SS_L_HI = 0x1p96f;   // row-sum bound of the fast sweep
 
 struct SsParams {
@@ -83,12 +85,13 @@ struct SsParams {
 __device__ __forceinline__ int ss_swz(int r) { return ((2 * (r & 7)) | ((r >> 2) & 1)) ^ ((r >> 3) & 1); }
 static_assert(SS_CPR == 16, "swizzle above is for 16 chunks per row");
 
-// Every sweep iteration issues exactly one copy per wave (past the end of the range the last tile
-// is copied again into a buffer nobody reads), so the wait for tile t is always "all but the
-// SS_NBUF - 2 newest copies". The join also waits for this wave's LDS operations (the restart flag).
+// Every sweep iteration issues exactly one tile per wave, one copy per sub-tile (past the end of the
+// range the last tile is copied again into a buffer nobody reads), so the wait for tile t is always
+// "all but the newest SS_NBUF - 2 tiles' copies". The join also waits for this wave's LDS
+// operations (the restart flag).
 __device__ __forceinline__ void ss_wait_join() {
-  static_assert(SS_NBUF - 2 == 6, "vmcnt below");
-  TA_WAIT_JOIN(6);
+  static_assert((SS_NBUF - 2) * (SS_KT / SS_ST) == 4, "vmcnt below");
+  TA_WAIT_JOIN(4);
 }
 __device__ __forceinline__ void ss_drain_join() {
   TA_WAIT_JOIN(0);
@@ -115,13 +118,17 @@ __device__ __forceinline__ SsSrc ss_src(const SsParams& p, int b, int hg, int wa
   return s;
 }
 
-// Copy the tile starting at key k0 (rows clamped to lk - 1: no key past the valid length is read).
+// Copy the tile starting at key k0, sub-tile by sub-tile (rows clamped to lk - 1: no key past the
+// valid length is read).
 __device__ __forceinline__ void ss_issue(const SsSrc& s, uint32_t buf, int k0, int lk, int wave) {
-  const uint32_t key = (uint32_t)min(k0 + s.row, lk - 1);
-  lds_dma16(s.base + (uint64_t)key * s.stride, buf + 1024 * wave);
+#pragma unroll
+  for (int h = 0; h < SS_KT / SS_ST; ++h) {
+    const uint32_t key = (uint32_t)min(k0 + SS_ST * h + s.row, lk - 1);
+    lds_dma16(s.base + (uint64_t)key * s.stride, buf + SS_STILE * h + 1024 * wave);
+  }
 }
 
-// Scores x = K (q log2e) - m of one 16-query block over a 32-key tile. Lane (l16, G) holds keys
+// Scores x = K (q log2e) - m of one 16-query block over a 32-key sub-tile. Lane (l16, G) holds keys
 // key0 + r (x0) and key0 + 16 + r (x1), key0 = tile start + 4G, r = 0..3, of query l16, which is the
 // k-slot order 8G + j of the B operand of the 16x16x32 products.
 template <bool MASK>
@@ -236,9 +243,14 @@ __device__ __forceinline__ void ss_step(SsState& st, char* lds, uint32_t lds0, c
   ss_wait_join();
   ss_issue(src, lds0 + ((t + SS_NBUF - 1) % SS_NBUF) * SS_TILE, min(t0 + t + SS_NBUF - 1, tlast) * SS_KT, lk,
            wave);
-  bf16x8 ka0, ka1, va;
-  ss_operands(lds + (t % SS_NBUF) * SS_TILE, koff, voff, ka0, ka1, va);
-  ss_tile<EXACT, MASK>(st, ka0, ka1, va, (t0 + t) * SS_KT + 4 * G, lk);
+#pragma unroll
+  for (int h = 0; h < SS_KT / SS_ST; ++h) {
+    const int k0 = (t0 + t) * SS_KT + SS_ST * h;
+    if (MASK && k0 >= lk) break;  // a last tile's sub-tiles past the valid length (uniform)
+    bf16x8 ka0, ka1, va;
+    ss_operands(lds + (t % SS_NBUF) * SS_TILE + SS_STILE * h, koff, voff, ka0, ka1, va);
+    ss_tile<EXACT, MASK>(st, ka0, ka1, va, k0 + 4 * G, lk);
+  }
 }
 
 // One sweep over the split's tiles [t0, t0 + nt), nt >= 1; the last one masks keys past the valid
@@ -323,7 +335,7 @@ __global__ __launch_bounds__(SS_NW * 64, 2) void ss_stream_kernel(SsParams p) {
   const uint32_t lds0 = lds_addr(lds);
 
   if (nt > 0) {
-    // reference m: ceiled maximum over the split's first tile
+    // reference m: ceiled maximum over the split's first 32 keys
     ss_issue(src, lds0, t0 * SS_KT, lk, wave);
     ss_drain_join();
     bf16x8 ka0, ka1, va;
