@@ -73,8 +73,8 @@ def _bias3(key_bias: Optional[Tensor], lead, Lk: int, device) -> Tensor:
     if missing > 0:
         kb = kb.reshape((1,) * missing + tuple(kb.shape))
     if math.prod(kb.shape[:-1]) == 1:
-        return kb.reshape(1, 1, Lk).contiguous()
-    return kb.expand(*lead, Lk).reshape(math.prod(lead), 1, Lk).contiguous()
+        return _nat.aligned16(kb.reshape(1, 1, Lk))
+    return _nat.aligned16(kb.expand(*lead, Lk).reshape(math.prod(lead), 1, Lk))
 
 
 def rope_tables(rope_mod, L: int, E: int, h: int, device) -> tuple:  # noqa: ANN001

@@ -170,8 +170,7 @@ def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, 
         kb = key_bias.to(device=q.device, dtype=torch.float32).reshape(-1, Tkv)
         if kb.shape[0] not in (1, q4.shape[0]):
             raise ValueError(f"key_bias rows {kb.shape[0]} must be 1 or the flattened batch {q4.shape[0]}")
-        if kb.stride(-1) != 1 or (kb.data_ptr() % 16):
-            kb = kb.contiguous()
+        kb = _nat.aligned16(kb)
     out = ICL_FWD(q4, k4, v4, valid, float(D) ** -0.5, kb)
     return out.reshape(*lead, H, Tq, D)
 

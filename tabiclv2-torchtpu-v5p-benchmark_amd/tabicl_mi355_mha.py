@@ -273,8 +273,9 @@ def folded_mab1(query: Tensor, key: Tensor, valid_kv_len: Optional[Tensor], num_
     b_q = None if in_proj_bias is None else in_proj_bias[:E]
     b_v = None if in_proj_bias is None else in_proj_bias[2 * E:]
     q = F.linear(ind, w_q, b_q)
-    if ssmax_layer is not None:
-        q = _ssmax(ssmax_layer, q, num_heads, src_len_override if src_len_override is not None else valid_kv_len)
+    if ssmax_layer is not None:  # source length: the override, else the valid length, else every key
+        n = src_len_override if src_len_override is not None else valid_kv_len
+        q = _ssmax(ssmax_layer, q, num_heads, key.shape[-2] if n is None else n)
     q = q * d ** -0.5
     # Qf[.., g, i, :] = q[.., i, g d:(g + 1) d] @ W_k[g d:(g + 1) d, :]   (both operands contiguous)
     qf = torch.matmul(_heads(q, num_heads).contiguous(), w_k.reshape(num_heads, d, E).contiguous())

@@ -132,6 +132,15 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def aligned16(t: torch.Tensor) -> torch.Tensor:
+    """t when it is contiguous and starts on a 16-byte boundary (what the entry points require of a
+    key bias), else a contiguous copy in a fresh allocation (the caching allocator aligns those).
+    `.contiguous()` alone returns a contiguous view that starts off the boundary unchanged."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def check(status: int, what: str) -> None:
     if status == 0:
         return

@@ -214,6 +214,25 @@ def test_bias3_forms():
     assert torch.equal(out[3], b2[1])
 
 
+def test_key_bias_alignment_fixup():
+    # a contiguous view that starts off a 16-byte boundary (here 1 float in) is copied into a fresh,
+    # aligned allocation by _bias3 and by the ICL wrapper's helper; aligned contiguous rows pass through
+    import tabicl_mi355_attn as pk
+    import tabicl_mi355_native as nat
+    base = torch.randn(1, 66)
+    view = base[:, 1:65]
+    assert view.is_contiguous() and view.data_ptr() % 16 != 0
+    fixed = nat.aligned16(view)
+    assert fixed.data_ptr() % 16 == 0 and torch.equal(fixed, view)
+    out = pk._bias3(view[0], (3,), 64, "cpu")
+    assert out.data_ptr() % 16 == 0 and torch.equal(out[0, 0], view[0])
+    rows = torch.randn(3, 65)[:, 1:]  # non-contiguous rows
+    out = pk._bias3(rows, (3,), 64, "cpu")
+    assert out.is_contiguous() and out.data_ptr() % 16 == 0 and torch.equal(out[:, 0], rows)
+    ok = torch.randn(64)
+    assert nat.aligned16(ok) is ok
+
+
 class _Rope:
     def __init__(self, interleaved):
         self.interleaved = interleaved

@@ -5,13 +5,16 @@ per head and dimension, lies between the smallest and largest value of V over th
 combination), and a bit-identical rerun. Inputs come from a device generator (the CPU oracle gets
 copies of the sampled sequences only).
 
-Bar (written here): max abs error <= 2e-2 against the oracle (bf16 inputs), <= 1e-4 (fp32 inputs);
-hull with 2e-2 slack for the bf16 rounding of the output (1e-4 for fp32).
+Bars (tests/parity.py): max abs error <= 2e-2 against the oracle (bf16 inputs), <= 1e-4 (fp32 inputs),
+and <= 2e-2 (bf16) / 1e-3 (fp32) times max |ref|; hull with 2e-2 slack for the bf16 rounding of the
+output (1e-4 for fp32). The long-key legs (C3 ISAB-1 over 45,000 rows, C5's ISAB-1 and ICL buckets)
+also run with sharpened queries (q x 4: outputs O(1) instead of ~0.03).
 """
 import pytest
 import torch
 
 from oracle import attention as O
+from parity import check
 
 pytestmark = pytest.mark.gpu
 H, E = 8, 128
@@ -35,8 +38,6 @@ def _hull_ok(out, v, tol=2e-2):
 
 
 def test_c2_row_stage_full_size(dev):
-    import numpy as np
-
     import tabicl_mi355_attn as pk
     g = torch.Generator(device=dev).manual_seed(1)
     B, L = 16384, 104
@@ -53,13 +54,10 @@ def test_c2_row_stage_full_size(dev):
     tables = O.rope_tables_ref(rope.freqs.double().numpy(), L, E, H, False)
     for b in (0, 1, 4097, 9999, B - 1):
         ref = O.pk_self_ref(qkv[b:b + 1].cpu(), H, None, tables, 0.25)
-        err = float(np.abs(out[b:b + 1].double().cpu().numpy() - ref).max())
-        assert err <= 2e-2, (b, err)
+        check(out[b:b + 1], ref, torch.bfloat16, f"c2 seq {b}")
 
 
 def test_c3_isab2_full_size(dev):
-    import numpy as np
-
     import tabicl_mi355_attn as pk
     g = torch.Generator(device=dev).manual_seed(2)
     B, T, NI = 800, 50000, 128
@@ -74,24 +72,25 @@ def test_c3_isab2_full_size(dev):
     rows = torch.arange(0, T, 997)
     for b in (0, 399, B - 1):
         ref = O.pk_cross_ref(q[b:b + 1, rows].cpu(), kv[b:b + 1].cpu(), H, None, None, None, 0.25)
-        err = float(np.abs(out[b:b + 1, rows].double().cpu().numpy() - ref).max())
-        assert err <= 2e-2, (b, err)
+        check(out[b:b + 1, rows], ref, torch.bfloat16, f"c3 isab2 seq {b}")
     del q, out
 
 
-def test_c3_isab1_full_size(dev):
+@pytest.mark.parametrize("qscale", [1.0, 4.0], ids=["normal_q", "sharp_q"])
+def test_c3_isab1_full_size(dev, qscale):
     # 800 sequences x 128 inducing queries over 50,000 rows of packed K|V, 45,000 valid; the rows past
     # the valid length hold NaN (never read). Hull over the valid keys, computed in bf16 (no fp32 copy).
+    # q = N(0,1) x 0.25 as BASELINE draws it (scores ~N(0,1), outputs ~0.04), and x 4 of that
     import numpy as np
 
     import tabicl_mi355_attn as pk
     g = torch.Generator(device=dev).manual_seed(3)
     B, T, VALID, NI = 800, 50000, 45000, 128
-    q = (torch.randn(B, NI, E, generator=g, device=dev) * 0.25).to(torch.bfloat16)
+    q = (torch.randn(B, NI, E, generator=g, device=dev) * (0.25 * qscale)).to(torch.bfloat16)
     kv = torch.randn(B, T, 2 * E, generator=g, device=dev).to(torch.bfloat16)
     kv[:, VALID:] = float("nan")
     vt = torch.tensor([VALID], dtype=torch.int32, device=dev)
-    print("[fullsize] c3 isab1", flush=True)
+    print(f"[fullsize] c3 isab1 qscale={qscale}", flush=True)
     with torch.no_grad():
         out = pk.hxq_attention(q, kv, vt, H)
         again = pk.hxq_attention(q, kv, vt, H)
@@ -103,8 +102,7 @@ def test_c3_isab1_full_size(dev):
     assert bool((out.float() <= vmax + 2e-2).all()) and bool((out.float() >= vmin - 2e-2).all())
     for b in (0, 399, B - 1):
         ref = O.hxq_ref(q[b:b + 1].cpu(), kv[b:b + 1, :VALID].cpu(), np.array([VALID]), H)
-        err = float(np.abs(out[b:b + 1].double().cpu().numpy() - ref).max())
-        assert err <= 2e-2, (b, err)
+        check(out[b:b + 1], ref, torch.bfloat16, f"c3 isab1 seq {b} qscale={qscale}")
     del q, kv, out, again
 
 
@@ -112,8 +110,6 @@ def test_c3_isab1_full_size(dev):
 def test_c1_fp32_full_size(dev, leg):
     # BASELINE config 1 in fp32: 400 sequences, ISAB-1 = 128 queries over 1,024 keys (the streaming
     # kernel), ISAB-2 = 1,024 queries over 128 keys (the resident kernel), q pre-scaled by 1/4
-    import numpy as np
-
     import tabicl_mi355_attn as pk
     g = torch.Generator(device=dev).manual_seed(4)
     B = 400
@@ -132,72 +128,128 @@ def test_c1_fp32_full_size(dev, leg):
     assert bool((out >= v.amin(dim=1, keepdim=True) - 1e-4).all())
     for b in (0, 199, B - 1):
         ref = O.hx_ref(q[b:b + 1].cpu(), k[b:b + 1].cpu(), v[b:b + 1].cpu(), H)
-        err = float(np.abs(out[b:b + 1].double().cpu().numpy() - ref).max())
-        assert err <= 1e-4, (b, err)
+        check(out[b:b + 1], ref, torch.float32, f"c1 {leg} seq {b}")
 
 
-def test_c5_ragged_buckets_full_size(dev):
-    # BASELINE config 5 as bench.py draws it (64 tables, seed-fixed sizes): every ICL bucket at its full
-    # shape (8 estimators x 8 heads per table, test rows padded to 1k over the train bucket, per-table
-    # valid and test-row counts), and the column ISAB-2 buckets up to 4k rows (8 estimators x 100
-    # features per table, per-sequence row counts). The ragged call's live rows equal the padded call's
-    # bit for bit; sampled tables match the oracle; live outputs are finite.
-    import numpy as np
-
+def _c5_groups():
+    # BASELINE config 5 as bench.py draws it (64 tables, seed-fixed sizes): the column stage's row
+    # bucket (train + test rows) and the ICL stage's train bucket per table
     import bench
-    import tabicl_mi355_attn as pk
-    import tabicl_mi355_icl as icl
     n_train, n_test = bench.c5_tables()
     groups = {}
     for i in range(64):
         groups.setdefault(("isab", bench.c5_bucket(int(n_train[i] + n_test[i]))), []).append(i)
         groups.setdefault(("icl", bench.c5_bucket(int(n_train[i]))), []).append(i)
-    g = torch.Generator(device=dev).manual_seed(5)
-    for (kind, L), tabs in sorted(groups.items()):
-        nt = [int(n_train[i]) for i in tabs]
-        ns = [int(n_test[i]) for i in tabs]
-        print(f"[fullsize] c5 {kind} bucket {L}: {len(tabs)} tables", flush=True)
-        if kind == "icl":
-            N, Tq = len(tabs) * 8, 1024
-            valid = torch.tensor(nt, dtype=torch.int32).repeat_interleave(8).to(dev)
-            qlen = torch.tensor(ns, dtype=torch.int32).repeat_interleave(8).to(dev)
-            k = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
-            v = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
-            q = torch.randn(N, H, Tq, 64, generator=g, device=dev, dtype=torch.bfloat16)
-            padded, ragged = torch.empty_like(q), torch.zeros_like(q)
-            with torch.no_grad():
-                icl.ICL_FWD_OUT(q, k, v, valid, 64 ** -0.5, padded)
-                icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, ragged)
-            torch.cuda.synchronize()
-            for n in range(N):
-                m = ns[n // 8]
-                assert torch.equal(ragged[n, :, :m], padded[n, :, :m]), (L, n)
-                assert torch.isfinite(ragged[n, :, :m].float()).all()
-            for n in (0, N - 1):
-                m, vl = ns[n // 8], nt[n // 8]
-                ref = O.splash_sdpa_ref(q[n:n + 1, :2, :m].cpu(), k[n:n + 1, :2].cpu(), v[n:n + 1, :2].cpu(),
-                                        np.array([vl]))
-                err = float(np.abs(ragged[n:n + 1, :2, :m].double().cpu().numpy() - ref).max())
-                assert err <= 2e-2, (L, n, err)
-            del k, v, q, padded, ragged
-        elif L <= 4096:
-            B = len(tabs) * 800
-            rows = [a + b for a, b in zip(nt, ns)]
-            qlen = torch.tensor(rows, dtype=torch.int32).repeat_interleave(800).to(dev)
-            q2 = torch.randn(B, L, E, generator=g, device=dev, dtype=torch.bfloat16)
-            kv2 = torch.randn(B, 128, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
-            with torch.no_grad():
-                padded = pk.pk_cross_attention(q2, kv2, H, None, None, 0.25)
-                ragged = pk.pk_cross_attention(q2, kv2, H, None, None, 0.25, q_len=qlen)
-            torch.cuda.synchronize()
-            for t, r in enumerate(rows):
-                sl = slice(800 * t, 800 * (t + 1))
-                assert torch.equal(ragged[sl, :r], padded[sl, :r]), (L, t)
-            for b in (0, B - 1):
-                r = rows[b // 800]
-                sel = torch.arange(0, r, 7)
-                ref = O.pk_cross_ref(q2[b:b + 1, sel].cpu(), kv2[b:b + 1].cpu(), H, None, None, None, 0.25)
-                err = float(np.abs(ragged[b:b + 1, sel].double().cpu().numpy() - ref).max())
-                assert err <= 2e-2, (L, b, err)
-            del q2, kv2, padded, ragged
+    return n_train, n_test, groups
+
+
+def _c5_buckets(kind):
+    n_train, n_test, groups = _c5_groups()
+    return [(L, [int(n_train[i]) for i in tabs], [int(n_test[i]) for i in tabs])
+            for (k, L), tabs in sorted(groups.items()) if k == kind]
+
+
+@pytest.mark.parametrize("L", [1024, 2048, 4096, 8192, 16384])
+def test_c5_icl_bucket_full_size(dev, L):
+    # every ICL bucket at its full shape (8 estimators x 8 heads per table, test rows padded to 1k over
+    # the train bucket, per-table valid and test-row counts): the ragged call's live rows equal the
+    # padded call's bit for bit and are finite; sampled tables match the oracle, with N(0,1) queries
+    # (outputs ~0.03-0.1 over 500-10,000 keys) and with q x 4
+    import numpy as np
+
+    import tabicl_mi355_icl as icl
+    (nt, ns), = [(a, b) for LL, a, b in _c5_buckets("icl") if LL == L]
+    g = torch.Generator(device=dev).manual_seed(5 + L)
+    N, Tq = len(nt) * 8, 1024
+    valid = torch.tensor(nt, dtype=torch.int32).repeat_interleave(8).to(dev)
+    qlen = torch.tensor(ns, dtype=torch.int32).repeat_interleave(8).to(dev)
+    k = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(N, H, L, 64, generator=g, device=dev, dtype=torch.bfloat16)
+    q0 = torch.randn(N, H, Tq, 64, generator=g, device=dev, dtype=torch.bfloat16)
+    for qscale in (1.0, 4.0):
+        q = q0 * qscale
+        print(f"[fullsize] c5 icl bucket {L}: {len(nt)} tables, qscale={qscale}", flush=True)
+        padded, ragged = torch.empty_like(q), torch.zeros_like(q)
+        with torch.no_grad():
+            icl.ICL_FWD_OUT(q, k, v, valid, 64 ** -0.5, padded)
+            icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, ragged)
+        torch.cuda.synchronize()
+        for n in range(N):
+            m = ns[n // 8]
+            assert torch.equal(ragged[n, :, :m], padded[n, :, :m]), (L, n)
+            assert torch.isfinite(ragged[n, :, :m].float()).all()
+        for n in (0, N // 2 + 3, N - 1):
+            m, vl = ns[n // 8], nt[n // 8]
+            ref = O.splash_sdpa_ref(q[n:n + 1, :2, :m].cpu(), k[n:n + 1, :2].cpu(), v[n:n + 1, :2].cpu(),
+                                    np.array([vl]))
+            check(ragged[n:n + 1, :2, :m], ref, torch.bfloat16, f"c5 icl {L} n={n} valid={vl} qscale={qscale}")
+        del padded, ragged
+
+
+@pytest.mark.parametrize("L", [1024, 2048, 4096, 8192, 16384])
+def test_c5_isab1_bucket_full_size(dev, L):
+    # the column ISAB-1 leg of every row bucket as bench.py times it: hxq of 128 inducing queries over
+    # the bucket's rows for 8 estimators x 100 features per table (one call per bucket), valid = the
+    # table's train rows; the rows past valid hold NaN (never read). Sampled sequences of the first,
+    # a middle and the last table match the oracle, with q = N(0,1) x 0.25 as bench draws it and x 4
+    import numpy as np
+
+    import tabicl_mi355_attn as pk
+    (nt, ns), = [(a, b) for LL, a, b in _c5_buckets("isab") if LL == L]
+    g = torch.Generator(device=dev).manual_seed(6 + L)
+    per = 800
+    B = len(nt) * per
+    valid = torch.tensor(nt, dtype=torch.int32).repeat_interleave(per).to(dev)
+    kv = torch.randn(B, L, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
+    for t, n in enumerate(nt):
+        kv[t * per:(t + 1) * per, n:] = float("nan")
+    q0 = torch.randn(B, 128, E, generator=g, device=dev, dtype=torch.bfloat16)
+    for qscale in (0.25, 1.0):
+        q = q0 * qscale
+        print(f"[fullsize] c5 isab1 bucket {L}: {len(nt)} tables, qscale={qscale}", flush=True)
+        with torch.no_grad():
+            out = pk.hxq_attention(q, kv, valid, H)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all()
+        for t in (0, len(nt) // 2, len(nt) - 1):
+            for b in (t * per, t * per + per - 1):
+                ref = O.hxq_ref(q[b:b + 1].cpu(), kv[b:b + 1, :nt[t]].cpu(), np.array([nt[t]]), H)
+                check(out[b:b + 1], ref, torch.bfloat16, f"c5 isab1 {L} seq {b} valid={nt[t]} qscale={qscale}")
+        del out
+    del kv, q0
+
+
+@pytest.mark.parametrize("L", [1024, 2048, 4096, 8192, 16384])
+def test_c5_isab2_bucket_full_size(dev, L):
+    # the column ISAB-2 leg of every row bucket: every row of the bucket (padded to L) over 128 inducing
+    # keys, per-sequence live row counts (train + test rows of the table), 8 estimators x 100 features
+    # per table; calls of at most 4 tables (the 8k and 16k buckets hold 10 and 15 tables: 4 tables of
+    # 16k rows are 17 GB of queries). The ragged call's live rows equal the padded call's bit for bit;
+    # sampled rows of the first and last sequence of each call match the oracle.
+    import tabicl_mi355_attn as pk
+    (nt, ns), = [(a, b) for LL, a, b in _c5_buckets("isab") if LL == L]
+    g = torch.Generator(device=dev).manual_seed(7 + L)
+    per, chunk = 800, 4
+    rows_all = [a + b for a, b in zip(nt, ns)]
+    for c0 in range(0, len(nt), chunk):
+        rows = rows_all[c0:c0 + chunk]
+        B = len(rows) * per
+        print(f"[fullsize] c5 isab2 bucket {L}: tables {c0}..{c0 + len(rows) - 1}", flush=True)
+        qlen = torch.tensor(rows, dtype=torch.int32).repeat_interleave(per).to(dev)
+        q2 = torch.randn(B, L, E, generator=g, device=dev, dtype=torch.bfloat16)
+        kv2 = torch.randn(B, 128, 2 * E, generator=g, device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            padded = pk.pk_cross_attention(q2, kv2, H, None, None, 0.25)
+            ragged = pk.pk_cross_attention(q2, kv2, H, None, None, 0.25, q_len=qlen)
+        torch.cuda.synchronize()
+        for t, r in enumerate(rows):
+            sl = slice(per * t, per * (t + 1))
+            assert torch.equal(ragged[sl, :r], padded[sl, :r]), (L, c0 + t)
+            assert torch.isfinite(ragged[sl, :r].float()).all()
+        for b in (0, B - 1):
+            r = rows[b // per]
+            sel = torch.arange(0, r, 7)
+            ref = O.pk_cross_ref(q2[b:b + 1, sel].cpu(), kv2[b:b + 1].cpu(), H, None, None, None, 0.25)
+            check(ragged[b:b + 1, sel], ref, torch.bfloat16, f"c5 isab2 {L} seq {b} rows={r}")
+        del q2, kv2, padded, ragged
         torch.cuda.empty_cache()

@@ -1,28 +1,26 @@
 """GPU parity of the cached-KV in-context attention (head dim 64) against the CPU oracle.
 
-Bar (written here): max abs error <= 2e-2 for bf16 inputs with fp32 accumulation and <= 1e-4 in
-the fp32-input validation mode, against the fp64 restatement of the reference's Splash hook.
+Bars (tests/parity.py, written there): max abs error <= 2e-2 for bf16 inputs with fp32 accumulation
+and <= 1e-4 in the fp32-input validation mode, and max abs error <= 2e-2 (bf16) / 1e-3 (fp32) times
+max |ref|, against the fp64 restatement of the reference's Splash hook. The scale-aware bar is what
+discriminates at 45,000 keys, where N(0,1) inputs give outputs ~0.03; the full C4 shape also runs
+with sharpened queries (q x 4, outputs O(1)).
 At the full C4 shape a subset of (estimator, head) slices and query rows is compared and the whole
 output is checked for NaN/Inf and for the convex-hull property (every output lies within the
 per-dim range of the visible values).
 """
-import numpy as np
 import pytest
 import torch
 
 from oracle import attention as O
+from parity import check
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
 
 
 def _icl():
     import tabicl_mi355_icl as icl
     return icl
-
-
-def _err(out, ref):
-    return float(np.abs(out.detach().double().cpu().numpy() - ref).max())
 
 
 @pytest.mark.parametrize("name,N,H,Tq,Tkv,valid,dtype", [
@@ -48,7 +46,7 @@ def test_icl_parity(dev, name, N, H, Tq, Tkv, valid, dtype):
     torch.cuda.synchronize()
     ref = O.splash_sdpa_ref(q, k, v, valid)
     assert out.shape == q.shape and out.dtype == dtype
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, name)
 
 
 def test_icl_int_valid_and_per_batch_valid(dev):
@@ -58,10 +56,10 @@ def test_icl_int_valid_and_per_batch_valid(dev):
     k = torch.randn(3, 2, 500, 64, generator=g).to(torch.bfloat16)
     v = torch.randn(3, 2, 500, 64, generator=g).to(torch.bfloat16)
     out = icl.icl_sdpa(q.to(dev), k.to(dev), v.to(dev), 321)
-    assert _err(out, O.splash_sdpa_ref(q, k, v, 321)) <= 2e-2
+    check(out, O.splash_sdpa_ref(q, k, v, 321), torch.bfloat16, "int valid")
     vn = torch.tensor([500, 17, 0], dtype=torch.int32)
     out = icl.icl_sdpa(q.to(dev), k.to(dev), v.to(dev), vn.to(dev))
-    assert _err(out, O.splash_sdpa_ref(q, k, v, vn.numpy())) <= 2e-2
+    check(out, O.splash_sdpa_ref(q, k, v, vn.numpy()), torch.bfloat16, "per-batch valid")
     assert torch.all(out[2] == 0)
 
 
@@ -80,7 +78,7 @@ def test_icl_strided_cache_views_and_padding_garbage(dev):
         out = icl.icl_sdpa(qd[:, blk], kd[:, blk], vd[:, blk], torch.tensor(450, dtype=torch.int32).to(dev))
         ref = O.splash_sdpa_ref(qa[:, blk], kc[:, blk], vc[:, blk], 450)
         assert torch.isfinite(out.float()).all()
-        assert _err(out, ref) <= 2e-2
+        check(out, ref, torch.bfloat16, f"strided block {blk}")
 
 
 def test_icl_cache_append_and_query(dev):
@@ -101,7 +99,7 @@ def test_icl_cache_append_and_query(dev):
         assert torch.equal(cache.values[:, b, :, :700].cpu(), vs[b])
     q = torch.randn(E_, H, 200, D, generator=g).to(torch.bfloat16)
     out = cache.query(1, q.to(dev), torch.tensor(700, dtype=torch.int32).to(dev))
-    assert _err(out, O.splash_sdpa_ref(q, ks[1], vs[1], 700)) <= 2e-2
+    check(out, O.splash_sdpa_ref(q, ks[1], vs[1], 700), torch.bfloat16, "cache query")
     with pytest.raises(ValueError):
         cache.append(0, ks[0].to(dev), vs[0].to(dev), row0=400)  # past capacity
 
@@ -144,29 +142,31 @@ def test_icl_split_matches_unsplit(dev):
     torch.cuda.synchronize()
     assert float((split.float() - single.float()).abs().max()) <= 1e-2
     ref = O.splash_sdpa_ref(q.cpu(), k.cpu(), v.cpu(), valid.cpu().numpy())
-    assert _err(split, ref) <= 2e-2
+    check(split, ref, torch.bfloat16, "split")
 
 
-def test_icl_full_c4_slice(dev):
+@pytest.mark.parametrize("qscale", [1.0, 4.0], ids=["normal_q", "sharp_q"])
+def test_icl_full_c4_slice(dev, qscale):
     # BASELINE config 4 at full size for one block: 8 est x 8 heads, 5000 q over 45000 cached keys.
     # Oracle on 2 (est, head) slices x 256 query rows; whole output finite and in the value hull.
+    # qscale 4: scores ~N(0, 16), a few hundred keys carry the weight and outputs are O(1)
     icl = _icl()
     g = torch.Generator(device="cpu").manual_seed(3)
     N, H, Tq, Tkv, D = 8, 8, 5000, 45000, 64
-    q = torch.randn(N, H, Tq, D, generator=g).to(torch.bfloat16)
+    q = (torch.randn(N, H, Tq, D, generator=g) * qscale).to(torch.bfloat16)
     k = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16)
     v = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    print(f"[icl] full c4 qscale={qscale}", flush=True)
     out = icl.icl_sdpa(qd, kd, vd, torch.tensor(Tkv, dtype=torch.int32).to(dev))
     assert torch.isfinite(out.float()).all()
     vmax = vd.float().amax(dim=2, keepdim=True)
     vmin = vd.float().amin(dim=2, keepdim=True)
     assert bool((out.float() <= vmax + 1e-2).all()) and bool((out.float() >= vmin - 1e-2).all())
     rows = torch.arange(0, Tq, Tq // 256)[:256]
-    for n, h in ((0, 0), (7, 5)):
-        ref = O.splash_sdpa_torch(q[n:n + 1, h:h + 1, rows], k[n:n + 1, h:h + 1], v[n:n + 1, h:h + 1])
-        err = float((out[n, h, rows].float().cpu() - ref[0, 0]).abs().max())
-        assert err <= 2e-2, err
+    for n, h in ((0, 0), (3, 2), (7, 5)):
+        ref = O.splash_sdpa_ref(q[n:n + 1, h:h + 1, rows], k[n:n + 1, h:h + 1], v[n:n + 1, h:h + 1])
+        check(out[n:n + 1, h:h + 1, rows], ref, torch.bfloat16, f"c4 ({n},{h}) qscale={qscale}")
 
 
 def _native_icl(q, k, v, valid, ws):
@@ -203,4 +203,4 @@ def test_icl_fixed_reference_and_exact_recompute(dev, name, qscale, expect_flag)
     assert bool((flags != 0).any()) == expect_flag, flags
     assert torch.isfinite(out.float()).all()
     ref = O.splash_sdpa_ref(q, k, v, valid.numpy())
-    assert _err(out, ref) <= 2e-2
+    check(out, ref, torch.bfloat16, name)

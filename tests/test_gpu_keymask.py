@@ -8,22 +8,19 @@ for bit on the pipelined / streaming kernels (the device reads it as that length
 (random finite terms, scattered masked keys, a row masked everywhere) runs on the kernels that add it
 term by term. Rows past the prefix hold NaN where the test says so: they must never be read.
 
-Bar (written here): max abs error <= 2e-2 for bf16 inputs, <= 1e-4 for fp32 inputs.
+Bars (tests/parity.py): max abs error <= 2e-2 for bf16 inputs, <= 1e-4 for fp32 inputs, and <= 2e-2
+(bf16) / 1e-3 (fp32) times max |ref|.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import attention as O
+from parity import check
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
 FMIN = float(torch.finfo(torch.float32).min)
 H, E = 8, 128
-
-
-def _err(out, ref):
-    return float(np.abs(out.detach().double().cpu().numpy() - ref).max())
 
 
 def _bias(kind, rows, L, g):
@@ -65,7 +62,7 @@ def test_icl_key_mask(dev, name, N, Hh, Tq, Tkv, kind, rows, dtype):
     out = icl.icl_sdpa(q.to(dev), k.to(dev), v.to(dev), None, b.to(dev))
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    assert _err(out, O.splash_sdpa_ref(q, k, v, None, b)) <= TOL[dtype]
+    check(out, O.splash_sdpa_ref(q, k, v, None, b), dtype, "icl_key_mask")
 
 
 def test_icl_prefix_mask_is_the_valid_length(dev):
@@ -106,7 +103,7 @@ def test_icl_masked_view_of_block_output(dev):
     b = _bias("random", 2, 700, g)
     buf = torch.zeros(2, 3, 8, 90, 64, dtype=torch.bfloat16, device=dev)
     icl.ICL_FWD_OUT(q.to(dev), k.to(dev), v.to(dev), None, 0.125, buf[:, 1], b.to(dev))
-    assert _err(buf[:, 1], O.splash_sdpa_ref(q, k, v, None, b)) <= 2e-2
+    check(buf[:, 1], O.splash_sdpa_ref(q, k, v, None, b), torch.bfloat16, "icl_masked_view_of_block_output")
     assert float(buf[:, 0].abs().max()) == 0.0 and float(buf[:, 2].abs().max()) == 0.0
 
 
@@ -125,7 +122,7 @@ def test_icl_cache_default_length(dev):
     out = cache.query(1, q.to(dev))
     assert cache.length(1) == 300
     assert torch.isfinite(out.float()).all()
-    assert _err(out, O.splash_sdpa_ref(q, k, v)) <= 2e-2
+    check(out, O.splash_sdpa_ref(q, k, v), torch.bfloat16, "icl_cache_default_length")
     with pytest.raises(ValueError):
         cache.query(0, q.to(dev))  # nothing appended to block 0
 
@@ -154,7 +151,7 @@ def test_hxq_key_mask(dev, name, B, Lq, Lk, kind, rows, valid, dtype):
     ref = O.attention_f64(q.double().numpy(), kv[..., :E].double().numpy(), kv[..., E:].double().numpy(), H,
                           np.broadcast_to(b.double().numpy(), (B, Lk)), valid=None if valid is None else np.array(valid))
     assert torch.isfinite(out.float()).all()
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "hxq_key_mask")
 
 
 def test_hxq_prefix_mask_is_the_valid_length(dev):
@@ -184,4 +181,4 @@ def test_hxf_key_mask(dev, dtype, kind):
     out = pk.hxf_attention(qf[0].to(dev), x.to(dev), None, b.to(dev))
     ref = O.attention_f64(np.broadcast_to(qf.double().numpy(), (B, hq, E)), x.double().numpy(), x.double().numpy(),
                           1, b.double().numpy())
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "hxf_key_mask")

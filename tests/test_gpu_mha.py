@@ -6,7 +6,11 @@ the HIP op of the route ran, and the output is compared with the same upstream s
 running torch math on the same GPU from the same inputs (the projections are the same GEMMs on both
 sides, so the difference is the kernel's).
 
-Bar (written here): max abs error <= 2e-2 with bf16 activations, <= 1e-4 with fp32.
+Bar (written here): max abs error <= 2e-2 with bf16 activations, <= 1e-4 with fp32. The long-key routes
+(cached ICL over 45,000 / 5,000 keys, ISAB-1 over 50,000 rows) also take the scale-aware bar of
+tests/parity.py on the attention's part of the block output (output minus the out-projection bias):
+max abs error <= 2e-2 (bf16) / 1e-3 (fp32) times its max. The SSMax stand-in scales q by s_h log n
+(5-11 at these key counts), so the attention is sharp there and that part is O(1) (~3.4).
 The small_head_attention "pk" branch (mask -> key bias -> hx kernel) is compared with the fp64 oracle.
 """
 import numpy as np
@@ -15,6 +19,7 @@ import torch
 
 import upstream_stub as U
 from oracle import attention as O
+from parity import check
 
 pytestmark = pytest.mark.gpu
 H, E = 8, 128
@@ -87,7 +92,7 @@ def test_block_cached_icl_tensor_train_size(dev, mha, monkeypatch, T, train):
                       cached_kv=U.KVEntry(kr, vr), src_len_override=ts, ssmax_layer=U.SSMaxStub(nh))
     assert seen == ["icl_sdpa"], seen
     assert torch.isfinite(got.float()).all()
-    assert _err(got, want) <= TOL[torch.bfloat16]
+    check(got.double() - bo.double(), want.double() - bo.double(), torch.bfloat16, f"cached icl T={T}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -105,7 +110,7 @@ def test_block_isab1_50k_rows_few_query_route(dev, mha, monkeypatch, dtype):
     got, want = _run(mod, ref_mod, ind, w, b, wo, bo, k=rows, v=rows, src_len_override=ts, valid_kv_len=ts,
                      ssmax_layer=U.SSMaxStub(H))
     assert seen == ["hxq_attention"], seen
-    assert _err(got, want) <= TOL[dtype]
+    check(got.double() - bo.double(), want.double() - bo.double(), dtype, f"isab1 50k {dtype}")
 
 
 def test_block_isab1_folded_route(dev, mha, monkeypatch):

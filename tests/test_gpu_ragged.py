@@ -2,7 +2,8 @@
 
 A ragged call takes per-batch query-row counts q_len. Bar (written here): rows below q_len[b] are
 bit-identical to the plain call on the same inputs (same kernels, same key splits), and the plain
-call itself is checked against the fp64 oracle on a subset of rows (2e-2 bf16, 1e-4 fp32), so the
+call itself is checked against the fp64 oracle on a subset of rows (tests/parity.py bars: 2e-2 bf16,
+1e-4 fp32, and 2e-2 / 1e-3 times max |ref|), so the
 ragged rows are pinned to the oracle through it. The ICL kernels never write the rows at or past
 q_len (checked with a NaN sentinel); for pk_cross their contents are unspecified (the resident
 kernel skips them, the others compute them). Cases: whole work items past q_len, a work item cut
@@ -16,9 +17,9 @@ import pytest
 import torch
 
 from oracle import attention as O
+from parity import check
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
 
 
 def _check_rows(out, ref, q_len, row_dim, untouched=False):
@@ -75,8 +76,7 @@ def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
     if n0 > 0:
         vl = Tkv if valid is None else valid[0]
         exp = O.splash_sdpa_ref(q[:1, :1], k[:1, :1], v[:1, :1], [vl])
-        err = float(np.abs(out[0, 0, :n0].double().cpu().numpy() - exp[0, 0, :n0]).max())
-        assert err <= TOL[dtype], f"{name}: max abs err {err}"
+        check(out[0, 0, :n0], exp[0, 0, :n0], dtype, name)
 
 
 def _pk_cross_case(dev, B, Lq, Lk, dtype, seed):
@@ -114,5 +114,4 @@ def test_pk_cross_ragged(dev, name, B, Lq, Lk, dtype, q_len):
     n0 = min(q_len[0], Lq, 64)
     if n0 > 0:
         exp = O.pk_cross_ref(q[:1, :n0], kv[:1], 8, None, None, None, 0.25)
-        err = float(np.abs(out[:1, :n0].double().cpu().numpy() - exp).max())
-        assert err <= TOL[dtype], f"{name}: max abs err {err}"
+        check(out[:1, :n0], exp, dtype, name)

@@ -1,18 +1,19 @@
 """GPU parity of the small-head kernels (hx, hxq, pk_self, pk_cross) against the CPU oracle.
 
 Shapes follow the reference's own test matrix (scripts/tests/test_pallas_attn.py:371-403) plus edge
-cases. Tolerance (written here): max abs error <= 2e-2 for bf16 inputs
-with fp32 accumulation, <= 1e-4 for fp32 inputs, against the fp32/fp64 oracle on the same inputs.
+cases. Bars (tests/parity.py): max abs error <= 2e-2 for bf16 inputs with
+fp32 accumulation, <= 1e-4 for fp32 inputs, and <= 2e-2 (bf16) / 1e-3 (fp32) times max |ref|, against
+the fp32/fp64 oracle on the same inputs.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import attention as O
+from parity import check
 
 H = 8
 E = 128
-TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
 
 pytestmark = pytest.mark.gpu
 
@@ -24,10 +25,6 @@ def _attn():
 
 def _gen(seed):
     return torch.Generator().manual_seed(seed)
-
-
-def _err(out, ref):
-    return float(np.abs(out.detach().double().cpu().numpy() - ref).max())
 
 
 class _Rope:
@@ -76,7 +73,7 @@ def test_hx(dev, name, B, Lq, Lk, dtype, bias):
     torch.cuda.synchronize()
     ref = O.hx_ref(q, k, v, H, kb)
     assert out.shape == q.shape and out.dtype == dtype
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "hx")
 
 
 def test_hx_fp32_long_queries(dev):
@@ -87,7 +84,7 @@ def test_hx_fp32_long_queries(dev):
     v = torch.randn(2, 128, E, generator=g)
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H)
     ref = O.ref_attn(q, k, v, H).double().numpy()
-    assert _err(out, ref) <= 1e-4
+    check(out, ref, torch.float32, "hx_fp32_long_queries")
 
 
 def test_hx_shared_bias_matches_broadcast(dev):
@@ -119,7 +116,7 @@ def test_hxq(dev, name, B, Lq, Lk, valid, dtype):
     print(f"[hxq] {name}", flush=True)
     out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(valid, dtype=torch.int32).to(dev), H)
     ref = O.hxq_ref(q, kv, np.array([min(valid, Lk)]), H)
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "hxq")
 
 
 def test_hxq_ragged_valid_and_empty(dev):
@@ -131,7 +128,7 @@ def test_hxq_ragged_valid_and_empty(dev):
     valid = torch.tensor([2048, 1, 0, 1000], dtype=torch.int32)
     out = pk.hxq_attention(q.to(dev), kv.to(dev), valid.to(dev), H)
     ref = O.hxq_ref(q, kv, valid.numpy(), H)
-    assert _err(out, ref) <= 2e-2
+    check(out, ref, torch.bfloat16, "hxq_ragged_valid_and_empty")
     assert torch.all(out[2] == 0)
 
 
@@ -145,7 +142,7 @@ def test_hxq_ragged_valid_and_empty_fp32(dev):
     valid = torch.tensor([2048, 1, 0, 1000], dtype=torch.int32)
     out = pk.hxq_attention(q.to(dev), kv.to(dev), valid.to(dev), H)
     ref = O.hxq_ref(q, kv, valid.numpy(), H)
-    assert _err(out, ref) <= 1e-4
+    check(out, ref, torch.float32, "hxq_ragged_valid_and_empty_fp32")
     assert torch.all(out[2] == 0)
 
 
@@ -163,7 +160,7 @@ def test_fp32_stream_long_runs_with_bias(dev):
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev)).cpu()
     for b in (0, 255, 511):
         ref = O.hx_ref(q[b:b + 1], k[b:b + 1], v[b:b + 1], H, kb[b:b + 1])
-        assert _err(out[b:b + 1], ref) <= 1e-4
+        check(out[b:b + 1], ref, torch.float32, "fp32_stream_long_runs_with_bias")
 
 
 def test_hxq_inference_tile_subset(dev):
@@ -176,7 +173,7 @@ def test_hxq_inference_tile_subset(dev):
     kv = torch.randn(B, Lk, 2 * E, generator=g).to(torch.bfloat16)
     out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(valid).to(dev), H)
     ref = O.ref_attn(q.float(), kv[:, :valid, :E].float(), kv[:, :valid, E:].float(), H).double().numpy()
-    assert _err(out, ref) <= 2e-2
+    check(out, ref, torch.bfloat16, "hxq_inference_tile_subset")
 
 
 @pytest.mark.parametrize("name,B,L,dtype,interleaved,bias", [
@@ -199,7 +196,7 @@ def test_pk_self(dev, name, B, L, dtype, interleaved, bias):
     out = pk.pk_self_attention(x.to(dev), H, None if kb is None else kb.to(dev), rope, 16 ** -0.5)
     ref = O.pk_self_ref(x, H, kb, None if rope is None else _rope_np(rope, L), 16 ** -0.5)
     assert out.shape == (B, L, E)
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "pk_self")
 
 
 @pytest.mark.parametrize("name,B,L,dtype,interleaved", [
@@ -217,7 +214,7 @@ def test_pk_self_partial_rotary(dev, name, B, L, dtype, interleaved):
     print(f"[pk_self partial rotary] {name}", flush=True)
     out = pk.pk_self_attention(x.to(dev), H, None, rope, 16 ** -0.5)
     ref = O.pk_self_ref(x, H, None, _rope_np(rope, L), 16 ** -0.5)
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "pk_self_partial_rotary")
 
 
 @pytest.mark.parametrize("name,B,Lq,Lk,dtype,interleaved", [
@@ -238,7 +235,7 @@ def test_pk_cross(dev, name, B, Lq, Lk, dtype, interleaved):
     rq = None if rope is None else _rope_np(rope, Lq)
     rk = None if rope is None else _rope_np(rope, Lk)
     ref = O.pk_cross_ref(x, y, H, None, rq, rk, 16 ** -0.5)
-    assert _err(out, ref) <= TOL[dtype]
+    check(out, ref, dtype, "pk_cross")
 
 
 def test_pk_cross_broadcast_query_no_copy(dev):
@@ -251,7 +248,7 @@ def test_pk_cross_broadcast_query_no_copy(dev):
     out = pk.pk_cross_attention(q_exp, kv.to(dev), H, None, None, 0.25)
     ref = O.pk_cross_ref(ind, kv, H, None, None, None, 0.25)
     assert out.shape == (5, 128, E)
-    assert _err(out, ref) <= 2e-2
+    check(out, ref, torch.bfloat16, "pk_cross_broadcast_query_no_copy")
 
 
 def test_all_keys_masked_by_bias_is_uniform(dev):
@@ -282,7 +279,7 @@ def test_fp32_sharp_key_far_above_first_keys(dev, Lk):
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H)
     ref = O.hx_ref(q, k, v, H)
     assert torch.isfinite(out).all()
-    assert _err(out, ref) <= 1e-4
+    check(out, ref, torch.float32, "fp32_sharp_key_far_above_first_keys")
 
 
 def test_no_nan_with_garbage_past_valid(dev):
@@ -295,7 +292,7 @@ def test_no_nan_with_garbage_past_valid(dev):
     out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(300).to(dev), H)
     assert torch.isfinite(out.float()).all()
     ref = O.hxq_ref(q, kv[:, :300], np.array([300]), H)
-    assert _err(out, ref) <= 2e-2
+    check(out, ref, torch.bfloat16, "no_nan_with_garbage_past_valid")
 
 
 # --- streaming kernel (bf16, Lk > 128, no RoPE / key bias): reference-point moves, key splits ---
@@ -313,7 +310,7 @@ def test_stream_shapes(dev, name, B, Lq, Lk):
     v = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
     print(f"[stream] {name}", flush=True)
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H)
-    assert _err(out, O.hx_ref(q, k, v, H)) <= 2e-2
+    check(out, O.hx_ref(q, k, v, H), torch.bfloat16, "stream_shapes")
 
 
 @pytest.mark.parametrize("name,qscale,kshift", [
@@ -334,7 +331,7 @@ def test_stream_reference_moves(dev, name, qscale, kshift):
     print(f"[stream] {name}", flush=True)
     out = pk.hxq_attention(q.to(dev), kv.to(dev), torch.tensor(2900, dtype=torch.int32).to(dev), H)
     assert torch.isfinite(out.float()).all()
-    assert _err(out, O.hxq_ref(q, kv, np.array([2900]), H)) <= 2e-2
+    check(out, O.hxq_ref(q, kv, np.array([2900]), H), torch.bfloat16, "stream_reference_moves")
 
 
 def test_stream_split_matches_unsplit(dev):
@@ -356,8 +353,8 @@ def test_stream_split_matches_unsplit(dev):
     torch.cuda.synchronize()
     assert float((split.float() - one.float()).abs().max()) <= 1e-2
     ref = O.hxq_ref(q[:, :16].cpu(), kv.cpu(), valid.cpu().numpy(), H)
-    assert _err(split[:, :16], ref) <= 2e-2
-    assert _err(one[:, :16], ref) <= 2e-2
+    check(split[:, :16], ref, torch.bfloat16, "stream_split_matches_unsplit")
+    check(one[:, :16], ref, torch.bfloat16, "stream_split_matches_unsplit")
 
 
 def test_c5_style_bucket_group(dev):
@@ -372,12 +369,12 @@ def test_c5_style_bucket_group(dev):
     q = (torch.randn(B, 128, E, generator=g) * 0.25).to(torch.bfloat16)
     kv = torch.randn(B, L, 2 * E, generator=g).to(torch.bfloat16)
     out = pk.hxq_attention(q.to(dev), kv.to(dev), valid.to(dev), H)
-    assert _err(out, O.hxq_ref(q, kv, valid.numpy(), H)) <= 2e-2
+    check(out, O.hxq_ref(q, kv, valid.numpy(), H), torch.bfloat16, "c5_style_bucket_group")
     rows = torch.randn(B, L, E, generator=g).to(torch.bfloat16)
     ind = torch.randn(B, 128, 2 * E, generator=g).to(torch.bfloat16)
     out2 = pk.pk_cross_attention(rows.to(dev), ind.to(dev), H, None, None, 0.25)
     sub = slice(0, 300)
-    assert _err(out2[:, sub], O.pk_cross_ref(rows[:, sub], ind, H, None, None, None, 0.25)) <= 2e-2
+    check(out2[:, sub], O.pk_cross_ref(rows[:, sub], ind, H, None, None, None, 0.25), torch.bfloat16, "c5_style_bucket_group")
 
 
 # --- resident kernel (bf16, Lk <= 128): key-group counts, masking modes, recompute, long runs ---
@@ -401,7 +398,7 @@ def test_resident_key_groups(dev, name, B, Lq, Lk, bias):
         kb[:, Lk - 5:] = -1e30
     print(f"[resident] {name}", flush=True)
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, None if kb is None else kb.to(dev))
-    assert _err(out, O.hx_ref(q, k, v, H, kb)) <= 2e-2
+    check(out, O.hx_ref(q, k, v, H, kb), torch.bfloat16, "resident_key_groups")
 
 
 def test_resident_sums_out_of_range(dev):
@@ -420,7 +417,7 @@ def test_resident_sums_out_of_range(dev):
     kb[0] = -60.0
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev))
     assert torch.isfinite(out.float()).all()
-    assert _err(out, O.hx_ref(q, k, v, H, kb)) <= 2e-2
+    check(out, O.hx_ref(q, k, v, H, kb), torch.bfloat16, "resident_sums_out_of_range")
 
 
 def test_resident_all_keys_masked_bf16_is_uniform(dev):
@@ -432,7 +429,7 @@ def test_resident_all_keys_masked_bf16_is_uniform(dev):
     kb = torch.full((2, 20), -1e30)
     out = pk.hx_attention(q.to(dev), k.to(dev), v.to(dev), H, kb.to(dev))
     want = v.double().mean(dim=1, keepdim=True).expand(2, 24, E).numpy()
-    assert _err(out, want) <= 2e-2
+    check(out, want, torch.bfloat16, "resident_all_keys_masked_bf16_is_uniform")
 
 
 def test_resident_long_query_runs(dev):
@@ -446,7 +443,7 @@ def test_resident_long_query_runs(dev):
     out = pk.pk_cross_attention(x.to(dev), y.to(dev), H, None, None, 0.25).cpu()
     for b in (0, 41, 79):
         ref = O.pk_cross_ref(x[b:b + 1], y[b:b + 1], H, None, None, None, 0.25)
-        assert _err(out[b:b + 1], ref) <= 2e-2
+        check(out[b:b + 1], ref, torch.bfloat16, "resident_long_query_runs")
 
 
 def test_resident_long_runs_rope(dev):
@@ -460,7 +457,7 @@ def test_resident_long_runs_rope(dev):
     tabs = _rope_np(rope, L)
     for b in (0, 1023, 2047):
         ref = O.pk_self_ref(x[b:b + 1], H, None, tabs, 16 ** -0.5)
-        assert _err(out[b:b + 1], ref) <= 2e-2
+        check(out[b:b + 1], ref, torch.bfloat16, "resident_long_runs_rope")
 
 
 @pytest.mark.parametrize("name,Lk,bias,hot", [
@@ -500,7 +497,7 @@ def test_resident_exact_scale_long_runs(dev, name, Lk, bias, hot):
     for b in (0, 1, 69):
         rows = np.r_[0:200, Lq - 300:Lq]
         ref = O.hx_ref(qc[b:b + 1, rows], kc[b:b + 1], vc[b:b + 1], H, None if kbc is None else kbc[b:b + 1])
-        assert _err(out[b:b + 1, rows], ref) <= 2e-2, f"{name}: element {b}"
+        check(out[b:b + 1, rows], ref, torch.bfloat16, "resident_exact_scale_long_runs")
 
 
 @pytest.mark.parametrize("interleaved", [False, True])
@@ -517,4 +514,4 @@ def test_resident_long_runs_cross_rope(dev, interleaved):
     rq, rk = _rope_np(rope, Lq), _rope_np(rope, Lk)
     for b in (0, 41, 79):
         ref = O.pk_cross_ref(x[b:b + 1], y[b:b + 1], H, None, rq, rk, 16 ** -0.5)
-        assert _err(out[b:b + 1], ref) <= 2e-2
+        check(out[b:b + 1], ref, torch.bfloat16, "resident_long_runs_cross_rope")

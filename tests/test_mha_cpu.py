@@ -306,6 +306,26 @@ def test_isab1_folded_route_takes_the_train_mask(routed, mha, monkeypatch):
     torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
 
 
+def test_isab1_folded_route_key_mask_and_ssmax_without_override(routed, mha, monkeypatch):
+    # a key-padding mask and SSMax with neither src_len_override nor valid_kv_len: SSMax takes the key
+    # count, as upstream's sdpa does (k.size(-2), results/tpu_patch.diff:251-254)
+    mod, ref_mod, seen = routed
+    monkeypatch.setattr(mha.KNOBS, "folded", True)
+    g = torch.Generator().manual_seed(9)
+    w, b, wo, bo = U.weights(E, 9)
+    ind = torch.randn(16, E, generator=g).expand(2, 16, E)
+    rows = torch.randn(2, 300, E, generator=g)
+    kpm = torch.zeros(2, 300)
+    kpm[:, 270:] = torch.finfo(torch.float32).min
+    mod2 = U.make_module()
+    assert mha.install(mod2, None, mode="pk")
+    kw = dict(k=rows, v=rows, key_padding_mask=kpm, ssmax_layer=U.SSMaxStub(H))
+    got = _block(mod2, ind, w, b, wo, bo, **kw)
+    want = _block(ref_mod, ind, w, b, wo, bo, **kw)
+    assert seen == ["hxf_attention"]
+    torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
+
+
 def test_isab1_reference_device_semantics_tensor_length(routed):
     # the caller hands over a tensor valid_kv_len and no mask (what upstream does on the reference's device)
     mod, ref_mod, seen = routed
