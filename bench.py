@@ -682,6 +682,108 @@ def bench_icl_stage(steps: int, warmup: int) -> list:
                         "cached-KV query 938.49 ms (best_model_forward_and_e2e.jsonl:2); not the same workload"}]
 
 
+def bench_query(steps: int, warmup: int) -> list:
+    """The whole cached-KV query at the headline workload (tabicl_mi355_query.cached_query: the reference
+    runner's _make_query_fn, scripts/tabicl_tpu_bucketed.py:768-834): 8 estimators x 5,000 test rows x 100
+    features through 3 column blocks over their cached K|V of 128 inducing points (pk_cross), the row
+    interactor (104 tokens per row: 2 RoPE self-attention blocks on pk_self, the CLS block on pk_cross), 12
+    ICL blocks over 45,000 cached train rows and the decoder (10 classes). Width 128 (column, row) and 512
+    (ICL), 8 heads, feed-forward x2, GELU; random weights and inputs (seed 7), caches filled before the
+    timed region. Two precisions: the column and row stages in fp32 (the reference's headline knobs run
+    them without autocast, best_model_forward_and_e2e.jsonl:2) or in bf16; the ICL stage in bf16 GEMMs
+    (its autocast) either way. Per-stage times are each stage alone on its own input. The reference's
+    938.49 ms for this query (TPU v5p, test rows padded to 8,192) is context, not the same weights."""
+    import torch
+    import torch.nn.functional as F
+
+    import tabicl_mi355_icl as icl
+    import tabicl_mi355_query as Q
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(7)
+    Ec, NF, NI, C, W, NCLS = 128, 100, 128, 4, HEADS * D, 10
+
+    def lin(o, i, dt):
+        return ((torch.randn(o, i, generator=g, device=dev) * i ** -0.5).to(dt),
+                (torch.randn(o, generator=g, device=dev) * 0.02).to(dt))
+
+    def block(width, dt):
+        ln = lambda: (1 + 0.05 * torch.randn(width, generator=g, device=dev),  # noqa: E731
+                      0.05 * torch.randn(width, generator=g, device=dev))
+        (l1w, l1b), (inw, inb), (ow, ob), (l2w, l2b), (f1w, f1b), (f2w, f2b) = \
+            ln(), lin(3 * width, width, dt), lin(width, width, dt), ln(), lin(2 * width, width, dt), lin(width, 2 * width, dt)
+        return Q.BlockWeights(l1w, l1b, inw, inb, ow, ob, l2w, l2b, f1w, f1b, f2w, f2b)
+
+    class Rope:
+        interleaved = False
+        freqs = 100000.0 ** (-torch.arange(0, 16, 2, dtype=torch.float32) / 16)
+
+        def get_seq_pos(self, n, device=None, dtype=torch.float32):
+            return torch.arange(n, device=device, dtype=dtype)
+
+    rope = Rope()
+    icl_blocks = [block(W, torch.bfloat16) for _ in range(BLOCKS)]
+    (d1w, d1b), (d2w, d2b) = lin(2 * W, W, torch.bfloat16), lin(NCLS, 2 * W, torch.bfloat16)
+    dec = Q.DecoderWeights(1 + 0.05 * torch.randn(W, generator=g, device=dev), 0.05 * torch.randn(W, generator=g, device=dev),
+                           d1w, d1b, d2w, d2b)
+    icl_cache = icl.IclKVCache(EST, BLOCKS, HEADS, TRAIN, D, torch.bfloat16, dev)
+    xtr = torch.randn(EST, TRAIN, W, generator=g, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        for b, w in enumerate(icl_blocks):
+            icl_cache.append_projected(b, xtr, w.in_w, w.in_b)
+    del xtr
+    X = torch.randn(EST, TEST, NF, generator=g, device=dev)
+    d = torch.full((EST,), NF, dtype=torch.int64, device=dev)
+    valid = torch.tensor([TRAIN], dtype=torch.int32, device=dev)
+    a = 0.05 * torch.randn(HEADS, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    logn = float(torch.log(torch.tensor(float(TRAIN))))
+    ssmax = (lambda q: q * (1.0 + a * logn))  # stand-in for upstream's elementwise SSMax on q (n = train rows)
+    recs = []
+    for dt, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        col = Q.ColumnWeights(*lin(Ec, 3, dt), [block(Ec, dt) for _ in range(3)])
+        row = Q.RowWeights((0.5 * torch.randn(C, Ec, generator=g, device=dev)).to(dt), [block(Ec, dt) for _ in range(3)],
+                           1 + 0.05 * torch.randn(Ec, generator=g, device=dev), 0.05 * torch.randn(Ec, generator=g, device=dev))
+        weights = Q.QueryWeights(col, row, icl_blocks, dec)
+        col_cache = Q.ColumnKVCache(3, EST, NF + C, NI, Ec, dt, dev)
+        with torch.no_grad():
+            for b in range(3):
+                col_cache.append_projected(b, torch.randn(EST, NF + C, NI, Ec, generator=g, device=dev).to(dt),
+                                           col.blocks[b])
+            src = Q.column_stage(X, d, col_cache, col)
+            reprs = Q.row_stage(src, d, row, rope).float()
+
+            def whole():
+                return Q.cached_query(X, d, col_cache, icl_cache, weights, valid, rope, ssmax)
+
+            ms = _time(whole, steps, warmup)
+            ms_col = _time(lambda: Q.column_stage(X, d, col_cache, col), steps, warmup)
+            ms_row = _time(lambda: Q.row_stage(src, d, row, rope), steps, warmup)
+            ms_icl = _time(lambda: Q.decode(icl_cache.query_blocks(reprs, icl_blocks, valid, ssmax), dec), steps, warmup)
+            out = whole()
+            finite = bool(torch.isfinite(out).all())
+        del src, reprs, col_cache, out
+        torch.cuda.empty_cache()
+        tokens_col = EST * (NF + C) * TEST
+        attn_flops = (3 * 4.0 * tokens_col * NI * Ec                              # column blocks over 128 keys
+                      + 2 * 4.0 * EST * TEST * (NF + C) ** 2 * Ec                 # row self-attention
+                      + 4.0 * EST * TEST * C * (NF + C) * Ec                      # CLS rows
+                      + BLOCKS * 4.0 * EST * TEST * TRAIN * W)                     # ICL
+        recs.append({"metric": f"ms per whole cached-KV query (column + row stages in {tag}, ICL stage bf16)",
+                     "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup,
+                     "higher_is_better": False, "vs_baseline": None, "dtype": f"{tag} column/row, bf16 ICL",
+                     "data": "synthetic test rows, random weights and caches (seed 7)",
+                     "config": {"workload": "C4 headline query: 8 est x 5000 test rows x 100 features; 3 column "
+                                            "blocks over 128 cached inducing keys, 3 row blocks over 104 tokens, 12 "
+                                            "ICL blocks over 45000 cached train rows, decoder to 10 classes"},
+                     "column_stage_ms": round(ms_col, 3), "row_stage_ms": round(ms_row, 3),
+                     "icl_stage_ms": round(ms_icl, 3), "attention_gflop": round(attn_flops / 1e9, 1),
+                     "finite": finite,
+                     "context": "reference (TPU v5p, one chip): 938.49 ms p50 for the cached-KV query of this "
+                                "workload, test rows padded to 8192 (best_model_forward_and_e2e.jsonl:2); not the "
+                                "same weights"})
+    return recs
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -690,10 +792,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-c3", action="store_true", help="default run: skip the C3 line printed before the headline")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer, icl_stage "
+                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer, icl_stage, query "
                          "(comma-separated) or all print the other BASELINE configs' lines, the fwd+bwd training "
-                         "lines, the folded first-ISAB lines, the ICL cache build / attention sub-layer lines and the "
-                         "cached ICL query stage (12 blocks with norms and feed-forward)")
+                         "lines, the folded first-ISAB lines, the ICL cache build / attention sub-layer lines, the "
+                         "cached ICL query stage (12 blocks with norms and feed-forward) and the whole cached-KV "
+                         "query (column, row and ICL stages, decoder)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -703,7 +806,7 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "query", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
@@ -720,6 +823,8 @@ def main() -> int:
             recs += bench_icl_layer(args.steps, args.warmup)
         if configs & {"icl_stage", "all"}:
             recs += bench_icl_stage(args.steps, args.warmup)
+        if configs & {"query", "all"}:
+            recs += bench_query(args.steps, args.warmup)
         for rec in recs:
             print(json.dumps(rec), flush=True)
         return 0

@@ -6,7 +6,11 @@ and the HIP kernels of libtabicl_attn.so.
 modules: layers.py imports it by name) and, for the 8 x 64 ICL attention, the module's
 `sdpa_with_flattened_batch` (whose Splash branch the reference hooks, results/tpu_patch.diff:261-281).
 
-Routing contract kept from the reference (same knobs, same order, same fallbacks):
+Routing contract kept from the reference (same knobs, same order, same fallbacks), with one route
+ahead of it:
+  0. small heads over cached K/V            TABICL_TPU_MHA_CACHED (default 1; no counterpart in the
+     reference, whose route 3 sends these calls to upstream torch): the column blocks' second
+     attention at query time (test rows over the cached inducing-point K/V)
   1. folded first-ISAB attention            TABICL_TPU_MHA_HXF=1      (reference :319-327)
   2. few queries over the train rows        TABICL_TPU_MHA_HXQ=1      (reference :328-342)
   3. upstream for: cached K/V (its attention reaches the ICL hook below), K/V requested back,
@@ -30,7 +34,7 @@ Where this differs from the reference, and why:
 
 Knobs (names of the reference): TABICL_TPU_MHA=hxq|hxk|thl|std|pk|hx|auto|<rules>,
 TABICL_TPU_MHA_MAX_HEAD_DIM (32), TABICL_TPU_MHA_PROJ (accepted; every form computes the same
-projections here), TABICL_TPU_MHA_HXF, _HXQ, _PACKED, TABICL_TPU_MHA_ANY_DEVICE (lets route 5's
+projections here), TABICL_TPU_MHA_HXF, _HXQ, _PACKED, _CACHED, TABICL_TPU_MHA_ANY_DEVICE (lets route 5's
 torch math run on CPU tensors in tests; the HIP kernels never run on CPU tensors), TABICL_MI355_ICL
 (default 1: install the ICL hook).
 """
@@ -58,6 +62,7 @@ class Knobs:
     folded: bool = _env_flag("TABICL_TPU_MHA_HXF")
     few_queries: bool = _env_flag("TABICL_TPU_MHA_HXQ")
     packed: bool = _env_flag("TABICL_TPU_MHA_PACKED")
+    cached: bool = _env_flag("TABICL_TPU_MHA_CACHED", "1")
     any_device: bool = _env_flag("TABICL_TPU_MHA_ANY_DEVICE")
     icl_hook: bool = _env_flag("TABICL_MI355_ICL", "1")
 
@@ -347,6 +352,45 @@ class _Call:
         return F.linear(merged, self.wo, self.bo)
 
 
+def _route_cached(c: _Call, knobs: Knobs) -> Optional[Tensor]:
+    """Small heads over cached K/V: the column blocks' second attention at query time, test rows over
+    the cached K/V of the 128 inducing points (scripts/tabicl_tpu_bucketed.py:788-792). Upstream's cached
+    branch (results/tpu_patch.diff:305-318) projects q only, promotes q and the cache to one dtype and
+    attends over the cache's head-split K/V [..., h, Lk, d]; the reference's TPU path leaves these calls
+    to it (scripts/tabicl_tpu_mha.py:343-347), which on this GPU would be torch SDPA (the ICL hook takes
+    the 64-wide heads only). Here the cache's K and V are written once per call into the packed
+    [.., Lk, 2E] rows pk_cross reads (one copy of the Lk cached rows, 128 here) and pk_cross runs; SSMax
+    takes n = src_len_override or the cached key count (diff:251-254). Declines RoPE (the cache holds
+    keys rotated at fit time), a valid length, K/V requested back, gradients and dropout."""
+    e = c.cached_kv
+    if not (knobs.cached and e is not None and c.on_gpu and not c.need_kv and c.rope is None
+            and c.valid_kv_len is None and c.d <= knobs.max_head_dim and not torch.is_grad_enabled()
+            and not (c.training and c.dropout_p > 0.0)):
+        return None
+    k, v = e.key, e.value
+    if (k.dim() < 3 or k.shape != v.shape or k.shape[-3] != c.h or k.shape[-1] != c.d
+            or tuple(k.shape[:-3]) != c.batch_shape):
+        return None
+    Lk = k.shape[-2]
+    if pick_impl(knobs.mode, c.Lq, Lk) != "pk":
+        return None
+    q = _linear_rows(c.query, c.w, c.b, slice(0, c.E))
+    dt = torch.promote_types(q.dtype, k.dtype)
+    if not _PK.packed_supported(c.Lq, Lk, c.E, c.h, False, dt):
+        return None
+    m = _combined_mask(c.attn_mask, c.key_padding_mask, c.batch_shape, c.h, c.Lq, Lk, dt)
+    kb = None if m is None or m is False else _key_only(m, Lk)
+    if m is False or kb is False:
+        return None
+    kv = torch.empty(*c.batch_shape, Lk, 2, c.h, c.d, dtype=dt, device=q.device)
+    kv[..., 0, :, :] = k.transpose(-3, -2)
+    kv[..., 1, :, :] = v.transpose(-3, -2)
+    q = q.to(dt)
+    if c.ssmax is not None:
+        q = _ssmax(c.ssmax, q, c.h, c.ssmax_n(Lk))
+    return c.out(_PK.pk_cross_attention(q, kv.flatten(-3), c.h, kb, None, c.d ** -0.5))
+
+
 def _route_folded(c: _Call, knobs: Knobs) -> Optional[Tensor]:
     if not (knobs.folded and c.inducing_over_rows(knobs.max_head_dim)):
         return None
@@ -444,7 +488,9 @@ def install(att_module, layers_module=None, mode: Optional[str] = None, proj: Op
         c = _Call(query, num_heads, in_proj_weight, in_proj_bias, dropout_p, out_proj_weight, out_proj_bias, key,
                   value, cached_kv, training, key_padding_mask, attn_mask, rope, ssmax_layer, need_kv,
                   src_len_override, valid_kv_len)
-        out = _route_folded(c, knobs)
+        out = _route_cached(c, knobs)
+        if out is None:
+            out = _route_folded(c, knobs)
         if out is None:
             out = _route_few_queries(c, knobs)
         if out is None and not _defers(c, knobs, att_module, splash_min_kv):

@@ -1,0 +1,237 @@
+"""The whole cached-KV query of TabICLv2 on MI355X: test rows through the column blocks over their
+cached inducing-point K/V, the row interactor, the cached ICL blocks and the decoder, every attention
+on the HIP kernels of libtabicl_attn.so.
+
+This is the body of the reference runner's query function (`_make_query_fn`,
+scripts/tabicl_tpu_bucketed.py:768-834), the step its published 938.49 ms cached-KV query times
+(results/inference/best_model_forward_and_e2e.jsonl:2):
+  * column stage (:777-797): circular feature grouping of the test rows (group size 3, the reference's
+    restatement at :362-372), `reserve_cls_tokens` leading feature slots filled with the skip value -100,
+    the in-linear (a group of 3 values -> width 128; rows whose inputs are all the skip value stay the
+    skip value), then per column block the block's second attention `multihead_attn2(src,
+    cached_kv=...)` (a pre-norm encoder layer whose attention reads the cached K/V of the 128 inducing
+    points) with the skip-column refill of results/tpu_patch.diff:1749-1757;
+  * row interactor (`_train_forward`, diff:1276-1307 and :169-190): the CLS tokens replace the reserved
+    slots, an additive key mask hides the padded feature slots (finfo.min past d + num_cls), every
+    block but the last is RoPE self-attention over the row's tokens, the last block computes the CLS
+    rows only (4 queries over all tokens, RoPE), then the out-LayerNorm (SafeLayerNorm) and the CLS rows
+    flattened into the row representation [B, T, num_cls width];
+  * ICL stage (:803-823): the cached ICL blocks (tabicl_mi355_icl.IclKVCache.query_blocks), the final
+    LayerNorm (norm_first) and the decoder MLP.
+Upstream tabicl (2.2.0) is not in the reference tree; the layers around the attention are restated from
+these call sites. The weights are the caller's (random in the benchmark and tests: no checkpoint is
+available); upstream's SSMax and RoPE modules come in as the caller's q transforms and rope object.
+
+Attention kernels per stage: column blocks `pk_cross` over 128 cached keys (fp32: sf_kernel; bf16:
+sh_resident_kernel), row blocks `pk_self` with in-kernel RoPE and the key mask (sh_persist_kernel for
+104 tokens in bf16), the CLS block `pk_cross` with RoPE, ICL `icl_pipe_kernel`. The GEMMs, norms and
+activations are torch (hipBLASLt / MIOpen-free elementwise kernels). Precision follows the weights:
+the reference runs the column and row stages in fp32 and the ICL stage under bf16 autocast (its
+headline knobs, best_model_forward_and_e2e.jsonl:2: no column / row autocast)."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, Optional, Union
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+import tabicl_mi355_attn as _pk
+import tabicl_mi355_icl as _icl
+import tabicl_mi355_native as _nat
+
+BlockWeights = _icl.IclBlockWeights  # one pre-norm encoder layer (norms, packed in-projection, out-projection, FFN)
+SKIP_VALUE = -100.0  # the column stage's skip value (scripts/tabicl_tpu_bucketed.py:708, 780)
+
+
+@dataclass
+class ColumnWeights:
+    """Column embedder at query time: the in-linear [width, group] + bias, and for every column block the
+    weights of its second attention layer (`multihead_attn2`; the first one only runs at fit time)."""
+    in_w: Tensor
+    in_b: Optional[Tensor]
+    blocks: list
+    heads: int = 8
+    reserve_cls: int = 4
+
+
+@dataclass
+class RowWeights:
+    """Row interactor: the CLS tokens [num_cls, width], the tf_row blocks (the last one computes the CLS
+    rows only) and the out-LayerNorm."""
+    cls_tokens: Tensor
+    blocks: list
+    out_ln_w: Tensor
+    out_ln_b: Optional[Tensor]
+    heads: int = 8
+    eps: float = 1e-5
+
+
+@dataclass
+class DecoderWeights:
+    """The ICL predictor's final LayerNorm (norm_first) and decoder MLP width -> ff -> classes."""
+    ln_w: Tensor
+    ln_b: Optional[Tensor]
+    w1: Tensor
+    b1: Optional[Tensor]
+    w2: Tensor
+    b2: Optional[Tensor]
+    eps: float = 1e-5
+
+
+def _ln(x: Tensor, w: Tensor, b: Optional[Tensor], eps: float, out_dtype: torch.dtype) -> Tensor:
+    return _icl._safe_layer_norm(x, w, b, eps, out_dtype)
+
+
+def _ffn(x: Tensor, blk, activation) -> Tensor:  # noqa: ANN001
+    """x + W2 act(W1 LN2(x) + b1) + b2 (the feed-forward half of a pre-norm encoder layer)."""
+    h = _ln(x, blk.ln2_w, blk.ln2_b, blk.eps, blk.ff1_w.dtype)
+    return x + F.linear(activation(F.linear(h, blk.ff1_w, blk.ff1_b)), blk.ff2_w, blk.ff2_b).to(x.dtype)
+
+
+def feature_grouping(X: Tensor, real_features: Optional[Tensor] = None, group_size: int = 3) -> Tensor:
+    """Circular feature grouping ("same" mode) of X [B, T, H]: slot j of the result holds the values of
+    features (j mod rf + 2^i) mod rf for i < group_size, rf = the table's real feature count
+    (real_features [B], default H): [B, T, H, group_size]. The reference's restatement of upstream's
+    grouping, indices computed once per table (scripts/tabicl_tpu_bucketed.py:362-372)."""
+    B, T, H = X.shape
+    idx = torch.arange(H, dtype=torch.long, device=X.device).view(1, 1, H)
+    rf = torch.full((B, 1, 1), H, dtype=torch.long, device=X.device) if real_features is None \
+        else real_features.to(device=X.device, dtype=torch.long).view(B, 1, 1)
+    base = idx % rf
+    return torch.stack([torch.gather(X, 2, ((base + 2 ** i) % rf).expand(B, T, H)) for i in range(group_size)],
+                       dim=-1)
+
+
+class ColumnKVCache:
+    """Fit-time K|V of every column block's second attention: [blocks, B, columns, inducing, 2 width],
+    the packed rows (K columns [0, width), V [width, 2 width)) that pk_cross reads, so the query makes no
+    copy. Upstream's need_kv returns the same K/V head-split (diff:1569-1575, cached at
+    scripts/tabicl_tpu_bucketed.py:719-724); the dispatch route for that form merges them per call."""
+
+    def __init__(self, blocks: int, batch: int, columns: int, inducing: int, width: int,
+                 dtype: torch.dtype = torch.float32, device: Union[str, torch.device] = "cuda"):
+        self.kv = torch.empty(blocks, batch, columns, inducing, 2 * width, dtype=dtype, device=device)
+        self.width = width
+        self.filled = [False] * blocks
+
+    def append_projected(self, block: int, hidden: Tensor, blk) -> None:  # noqa: ANN001
+        """K|V of block `block` from the first attention's output hidden [B, columns, inducing, width]:
+        the layer's pre-norm (norm1 normalises the keys too, diff:505-508), then the K|V thirds of its
+        packed in-projection (one GEMM)."""
+        E = self.width
+        if tuple(hidden.shape) != tuple(self.kv.shape[1:-1]) + (E,):
+            raise ValueError(f"hidden must be {tuple(self.kv.shape[1:-1]) + (E,)}, got {tuple(hidden.shape)}")
+        h = _ln(hidden, blk.ln1_w, blk.ln1_b, blk.eps, blk.in_w.dtype)
+        self.kv[block] = F.linear(h, blk.in_w[E:], None if blk.in_b is None else blk.in_b[E:]).to(self.kv.dtype)
+        self.filled[block] = True
+
+
+def _skippable_linear(x: Tensor, w: Tensor, b: Optional[Tensor], skip: float) -> Tensor:
+    """x W^T + b, with rows whose inputs all equal the skip value left at the skip value."""
+    out = F.linear(x, w, b)
+    return torch.where((x == skip).all(dim=-1, keepdim=True), torch.full((), skip, dtype=out.dtype, device=out.device),
+                       out)
+
+
+def column_stage(X: Tensor, real_features: Optional[Tensor], cache: ColumnKVCache, w: ColumnWeights,
+                 group_size: int = 3, activation: Callable[[Tensor], Tensor] = F.gelu,
+                 q_transform: Optional[Callable[[int, Tensor], Tensor]] = None) -> Tensor:
+    """Test rows X [B, T, H] through the column embedder with cached K/V: [B, H + reserve, T, width]
+    in the weights' dtype (scripts/tabicl_tpu_bucketed.py:777-792). Each block:
+        x = x + out_proj(pk_cross(LN1(x) W_q^T + b_q, cached K|V)),  x = x + FFN(LN2(x)),
+    then columns whose input was all skip value are refilled with it. q_transform(block, q) stands for a
+    module applied to the block's q (none in upstream's second attention)."""
+    _nat.require_device(X, cache.kv)
+    E, h = cache.width, w.heads
+    dt = w.in_w.dtype
+    x = feature_grouping(X, real_features, group_size)
+    if w.reserve_cls:
+        x = F.pad(x, (0, 0, w.reserve_cls, 0), value=SKIP_VALUE)
+    src = _skippable_linear(x.transpose(1, 2).to(dt), w.in_w, w.in_b, SKIP_VALUE)  # [B, HC, T, E]
+    skip = torch.full((), SKIP_VALUE, dtype=src.dtype, device=src.device)
+    for b, blk in enumerate(w.blocks):
+        if not cache.filled[b]:
+            raise ValueError(f"column block {b} of the cache was never filled")
+        skip_mask = (src == skip).all(dim=-1, keepdim=True).all(dim=-2, keepdim=True)
+        q = F.linear(_ln(src, blk.ln1_w, blk.ln1_b, blk.eps, blk.in_w.dtype), blk.in_w[:E],
+                     None if blk.in_b is None else blk.in_b[:E])
+        if q_transform is not None:
+            q = q_transform(b, q)
+        kv = cache.kv[b]
+        if kv.dtype != q.dtype:
+            kv = kv.to(q.dtype)
+        a = _pk.pk_cross_attention(q, kv, h, None, None, (E // h) ** -0.5)
+        out = src + F.linear(a, blk.out_w, blk.out_b).to(src.dtype)
+        src = torch.where(skip_mask, skip, _ffn(out, blk, activation))
+    return src
+
+
+def feature_key_mask(B: int, HC: int, real_features: Optional[Tensor], num_cls: int, device,  # noqa: ANN001
+                     dtype: torch.dtype) -> Optional[Tensor]:
+    """Additive key mask [B, 1, HC] over a row's tokens: 0 for the CLS slots and the table's real
+    features (token index < d + num_cls), finfo(dtype).min after (diff:172-190); None without d."""
+    if real_features is None:
+        return None
+    cond = torch.arange(HC, device=device).view(1, 1, HC) < (real_features.to(device).view(B, 1, 1) + num_cls)
+    return torch.where(cond, torch.zeros((), dtype=dtype, device=device),
+                       torch.full((), torch.finfo(dtype).min, dtype=dtype, device=device))
+
+
+def row_stage(src: Tensor, real_features: Optional[Tensor], w: RowWeights, rope,  # noqa: ANN001
+              activation: Callable[[Tensor], Tensor] = F.gelu) -> Tensor:
+    """The column output src [B, HC, T, width] as rows of HC tokens through the row interactor:
+    [B, T, num_cls width] (diff:1276-1307). Every block but the last: x = x + out_proj(pk_self(LN1(x)
+    W^T + b, RoPE, key mask)), x = x + FFN(LN2(x)); the last block takes the CLS rows as queries over
+    all tokens (keys normalised by the same norm1), pk_cross with RoPE on both sides; then the
+    out-LayerNorm and the CLS rows flattened."""
+    B, HC, T, E = src.shape
+    C, h = w.cls_tokens.shape[0], w.heads
+    x = src.transpose(1, 2)  # [B, T, HC, E]
+    x = torch.cat([w.cls_tokens.to(device=x.device, dtype=x.dtype).expand(B, T, C, E), x[:, :, C:]], dim=2)
+    kb = feature_key_mask(B, HC, real_features, C, x.device, x.dtype)
+    kb = None if kb is None else kb.view(B, 1, HC).float()
+    scale = (E // h) ** -0.5
+    for blk in w.blocks[:-1]:
+        qkv = F.linear(_ln(x, blk.ln1_w, blk.ln1_b, blk.eps, blk.in_w.dtype), blk.in_w, blk.in_b)
+        a = _pk.pk_self_attention(qkv, h, kb, rope, scale)
+        x = _ffn(x + F.linear(a, blk.out_w, blk.out_b).to(x.dtype), blk, activation)
+    blk = w.blocks[-1]
+    hk = _ln(x, blk.ln1_w, blk.ln1_b, blk.eps, blk.in_w.dtype)
+    q = F.linear(hk[:, :, :C], blk.in_w[:E], None if blk.in_b is None else blk.in_b[:E])
+    kv = F.linear(hk, blk.in_w[E:], None if blk.in_b is None else blk.in_b[E:])
+    a = _pk.pk_cross_attention(q, kv, h, kb, rope, scale)
+    cls = _ffn(x[:, :, :C] + F.linear(a, blk.out_w, blk.out_b).to(x.dtype), blk, activation)
+    cls = _ln(cls, w.out_ln_w, w.out_ln_b, w.eps, cls.dtype)
+    return cls.flatten(-2)
+
+
+def decode(x: Tensor, w: DecoderWeights, activation: Callable[[Tensor], Tensor] = F.gelu) -> Tensor:
+    """Final LayerNorm and decoder MLP of the ICL predictor, logits in fp32 (scripts/tabicl_tpu_bucketed.py
+    :819-823)."""
+    h = _ln(x, w.ln_w, w.ln_b, w.eps, w.w1.dtype)
+    return F.linear(activation(F.linear(h, w.w1, w.b1)), w.w2, w.b2).float()
+
+
+@dataclass
+class QueryWeights:
+    column: ColumnWeights
+    row: RowWeights
+    icl_blocks: list
+    decoder: DecoderWeights
+
+
+def cached_query(X: Tensor, real_features: Optional[Tensor], col_cache: ColumnKVCache, icl_cache,  # noqa: ANN001
+                 w: QueryWeights, train_size: Union[int, Tensor], rope,
+                 icl_q_transform: Optional[Callable[[Tensor], Tensor]] = None,
+                 activation: Callable[[Tensor], Tensor] = F.gelu) -> Tensor:
+    """Logits [B, T, classes] of test rows X [B, T, H] (B = estimators) from the fit-time caches: column
+    stage, row interactor, the ICL blocks over the cached train rows (keys >= train_size masked) and the
+    decoder (scripts/tabicl_tpu_bucketed.py:768-834). The ICL stage's GEMMs run in its weights' dtype
+    (bf16: the reference's autocast of that stage) around an fp32 residual stream (the row representation
+    in fp32)."""
+    src = column_stage(X, real_features, col_cache, w.column, activation=activation)
+    reprs = row_stage(src, real_features, w.row, rope, activation)
+    x = icl_cache.query_blocks(reprs.float(), w.icl_blocks, train_size, icl_q_transform, activation)
+    return decode(x, w.decoder, activation)

@@ -113,6 +113,25 @@ def test_block_isab1_50k_rows_few_query_route(dev, mha, monkeypatch, dtype):
     check(got.double() - bo.double(), want.double() - bo.double(), dtype, f"isab1 50k {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_block_cached_column_attention(dev, mha, monkeypatch, dtype):
+    # the column blocks' second attention at query time (scripts/tabicl_tpu_bucketed.py:788-792): test rows
+    # of each (estimator, column) over that column's cached K/V of the 128 inducing points, head-split as
+    # upstream's need_kv returns them; the route writes them as packed K|V rows and runs pk_cross
+    seen = _spy(monkeypatch)
+    g = torch.Generator().manual_seed(54)
+    w, b, wo, bo = _weights(E, 16, dev, dtype)
+    mod, ref_mod = U.make_module(), U.make_module()
+    assert mha.install(mod, None, mode="col1=pk,col2=pk,row=pk,cls=pk")
+    rows = torch.randn(2, 13, 5000, E, generator=g).to(dev, dtype)  # [est, column, test row, E]
+    kc = torch.randn(2, 13, H, 128, E // H, generator=g).to(dev, dtype)
+    vc = torch.randn(2, 13, H, 128, E // H, generator=g).to(dev, dtype)
+    print(f"[mha] cached column attention {dtype}", flush=True)
+    got, want = _run(mod, ref_mod, rows, w, b, wo, bo, cached_kv=U.KVEntry(kc, vc))
+    assert seen == ["pk_cross_attention"], seen
+    check(got.double() - bo.double(), want.double() - bo.double(), dtype, f"cached column {dtype}")
+
+
 def test_block_isab1_folded_route(dev, mha, monkeypatch):
     monkeypatch.setattr(mha.KNOBS, "folded", True)
     seen = _spy(monkeypatch)

@@ -384,6 +384,49 @@ def test_cached_icl_with_tensor_train_size_reaches_the_icl_kernel(routed, T, tra
     torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_cached_column_attention_takes_pk_cross(routed, with_mask):
+    # the column blocks' second attention at query time: test rows over the cached head-split K/V of
+    # the 128 inducing points (scripts/tabicl_tpu_bucketed.py:788-792) -> pk_cross on packed K|V rows;
+    # with a key-padding mask over the inducing keys it becomes the key bias
+    mod, ref_mod, seen = routed
+    g = torch.Generator().manual_seed(12)
+    w, b, wo, bo = U.weights(E, 12)
+    rows = torch.randn(2, 3, 40, E, generator=g)  # [est, column, test row, E]
+    kc = torch.randn(2, 3, H, 128, E // H, generator=g)
+    vc = torch.randn(2, 3, H, 128, E // H, generator=g)
+    kw = dict(cached_kv=U.KVEntry(kc, vc))
+    if with_mask:
+        kpm = torch.zeros(2, 3, 128)
+        kpm[:, :, 100:] = torch.finfo(torch.float32).min
+        kw["key_padding_mask"] = kpm
+    got = _block(mod, rows, w, b, wo, bo, **kw)
+    want = _block(ref_mod, rows, w, b, wo, bo, **kw)
+    assert seen == ["pk_cross_attention"]
+    torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
+
+
+def test_cached_column_attention_declines(routed, mha, monkeypatch):
+    # RoPE (the cache holds keys rotated at fit time), K/V whose batch differs from the query's, and the
+    # knob off all leave the call to upstream
+    mod, ref_mod, seen = routed
+    g = torch.Generator().manual_seed(13)
+    w, b, wo, bo = U.weights(E, 13)
+    rows = torch.randn(2, 40, E, generator=g)
+    kc = torch.randn(2, H, 128, E // H, generator=g)
+    vc = torch.randn(2, H, 128, E // H, generator=g)
+    _block(mod, rows, w, b, wo, bo, cached_kv=U.KVEntry(kc, vc), rope=U.RopeStub())
+    _block(mod, rows, w, b, wo, bo, cached_kv=U.KVEntry(kc[:1], vc[:1]))
+    assert seen == []
+    monkeypatch.setattr(mha.KNOBS, "cached", False)
+    mod2 = U.make_module()
+    assert mha.install(mod2, None, mode="col1=pk,col2=pk,row=pk,cls=pk")
+    got = _block(mod2, rows, w, b, wo, bo, cached_kv=U.KVEntry(kc, vc))
+    want = _block(ref_mod, rows, w, b, wo, bo, cached_kv=U.KVEntry(kc, vc))
+    assert seen == []
+    torch.testing.assert_close(got, want, atol=1e-6, rtol=1e-6)
+
+
 def test_fallbacks_to_upstream(routed):
     mod, ref_mod, seen = routed
     g = torch.Generator().manual_seed(11)
