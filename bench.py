@@ -291,7 +291,11 @@ TRAIN_SHAPES = (
 def bench_train(steps: int, warmup: int) -> list:
     """fwd+bwd step of the small-head ops on the reference's training shapes. Algorithmic FLOPs:
     the forward's 4 Lq Lk d per (sequence, head) times 3.5 (backward = 2.5 forwards: dP, dq, dk, dv
-    and the score recompute)."""
+    and the score recompute). These kernels are bound by HBM and VALU issue, not the matrix core, so the
+    roofline is HBM: algorithmic bytes per batch element (bf16) = forward (read q, k, v, write o) +
+    backward (read q, k, v, o, dO, write dq, dk, dv): hx 2 E (6 Lq + 6 Lk), pk_self (packed q|k|v, one
+    length L) 2 E 12 L; over the kernels' time alone (forward and backward ops from a given upstream
+    gradient, `kernels_ms`)."""
     import torch
 
     import tabicl_mi355_attn as pk
@@ -343,6 +347,8 @@ def bench_train(steps: int, warmup: int) -> list:
 
         ms_k = _time(step_kernels, steps, warmup)
         tf = 3.5 * 4.0 * Lq * Lk * 16 * H * B / (ms * 1e-3) / 1e12
+        nbytes = 2.0 * E * B * (12 * Lq if op == "pk_self" else 6 * Lq + 6 * Lk)
+        gbs = nbytes / (ms_k * 1e-3) / 1e9
         recs.append({"metric": f"ms per fwd+bwd {name} step", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
                      "steps": steps, "warmup": warmup, "higher_is_better": False,
                      "vs_baseline": None if published is None else round(ms / published, 4),
@@ -351,8 +357,9 @@ def bench_train(steps: int, warmup: int) -> list:
                      "attn_tflops": round(tf, 2),
                      "kernels_ms": round(ms_k, 4),
                      "kernels_note": "forward + backward ops from a given bf16 upstream gradient, no loss",
-                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
-                                  "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                                  "over": "kernels_ms"}})
     return recs
 
 

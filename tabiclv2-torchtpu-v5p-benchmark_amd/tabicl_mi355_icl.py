@@ -140,6 +140,39 @@ ICL_FWD_OUT = torch.ops.tabicl.icl_cached_attn_out
 ICL_FWD_RAGGED_OUT = torch.ops.tabicl.icl_cached_attn_ragged_out
 
 
+@torch.library.custom_op("tabicl::tpu_splash_sdpa_seg", mutates_args=())
+def splash_sdpa_seg_op(q_in: Tensor, k_in: Tensor, v_in: Tensor, valid_kv_t: Tensor, bq: int, bkv: int) -> Tensor:
+    """The reference's Splash op under its own name and schema (results/tpu_patch.diff:95-102), on the
+    HIP ICL kernel: q_in [N, H, Tq, D] already scaled by D^-0.5 (the caller pads and scales,
+    diff:133-139), k_in / v_in [N, H, Tkv, D], keys >= valid_kv_t (an int32 scalar tensor) masked. bq and
+    bkv are the TPU kernel's block sizes and are ignored: the library picks its own tiling, and needs no
+    padding of Tq or Tkv. Bound to the upstream attention module's `_tpu_splash_sdpa_seg_op` by
+    install(), so code that calls that attribute (the reference's knob hook,
+    scripts/tabicl_tpu_bucketed.py:236-242) reaches this kernel."""
+    valid = valid_kv_t.to(device=q_in.device, dtype=torch.int32).reshape(1).contiguous()
+    out = torch.empty(q_in.shape, device=q_in.device, dtype=q_in.dtype)
+    _launch(q_in, k_in, v_in, valid, 1.0, out)
+    return out
+
+
+@splash_sdpa_seg_op.register_fake
+def _(q_in, k_in, v_in, valid_kv_t, bq, bkv):  # noqa: ANN001
+    return torch.empty_like(q_in)
+
+
+@torch.library.custom_op("tabicl::tpu_splash_sdpa_full", mutates_args=())
+def splash_sdpa_full_op(q_in: Tensor, k_in: Tensor, v_in: Tensor, bq: int, bkv: int) -> Tensor:
+    """tpu_splash_sdpa_seg with every key valid (results/tpu_patch.diff:110-115)."""
+    out = torch.empty(q_in.shape, device=q_in.device, dtype=q_in.dtype)
+    _launch(q_in, k_in, v_in, None, 1.0, out)
+    return out
+
+
+@splash_sdpa_full_op.register_fake
+def _(q_in, k_in, v_in, bq, bkv):  # noqa: ANN001
+    return torch.empty_like(q_in)
+
+
 def icl_supported(Tq: int, Tkv: int, D: int, dtype: torch.dtype) -> bool:
     return dtype in (torch.bfloat16, torch.float32) and _nat.supported(_nat.OP_ICL, Tq, Tkv, D, 1, dtype)
 

@@ -20,7 +20,9 @@ ahead of it:
                                                                        (reference :350-371)
   5. the mode's small-head implementation   TABICL_TPU_MHA=<mode>     (reference :372-385)
 The ICL hook sends every d = 64 attention without gradient, dropout or a non-key mask to the HIP
-kernel (the reference: keys >= TABICL_TPU_SPLASH_MIN_KV without a mask, diff:263-265).
+kernel (the reference: keys >= TABICL_TPU_SPLASH_MIN_KV without a mask, diff:263-265), and the
+module's `_tpu_splash_sdpa_seg_op` / `_tpu_splash_sdpa_full_op` attributes (the reference's Splash
+ops, diff:95-115) are bound to the same kernel under the reference's op names.
 
 Where this differs from the reference, and why:
   * A key-validity length reaches routes 1, 2 and the ICL hook either as a tensor `valid_kv_len`
@@ -34,12 +36,14 @@ Where this differs from the reference, and why:
 
 Knobs (names of the reference): TABICL_TPU_MHA=hxq|hxk|thl|std|pk|hx|auto|<rules>,
 TABICL_TPU_MHA_MAX_HEAD_DIM (32), TABICL_TPU_MHA_PROJ (accepted; every form computes the same
-projections here), TABICL_TPU_MHA_HXF, _HXQ, _PACKED, _CACHED, TABICL_TPU_MHA_ANY_DEVICE (lets route 5's
+projections here), TABICL_TPU_MHA_HXF, _HXQ, _PACKED, _CACHED, TABICL_MI355_HXF_FORCE (route 1 runs the
+folded kernel even where projection + hxq takes the call, which is faster here), TABICL_TPU_MHA_ANY_DEVICE (lets route 5's
 torch math run on CPU tensors in tests; the HIP kernels never run on CPU tensors), TABICL_MI355_ICL
 (default 1: install the ICL hook).
 """
 from __future__ import annotations
 
+import dataclasses
 import math
 import os
 from dataclasses import dataclass
@@ -63,6 +67,7 @@ class Knobs:
     few_queries: bool = _env_flag("TABICL_TPU_MHA_HXQ")
     packed: bool = _env_flag("TABICL_TPU_MHA_PACKED")
     cached: bool = _env_flag("TABICL_TPU_MHA_CACHED", "1")
+    folded_force: bool = _env_flag("TABICL_MI355_HXF_FORCE")
     any_device: bool = _env_flag("TABICL_TPU_MHA_ANY_DEVICE")
     icl_hook: bool = _env_flag("TABICL_MI355_ICL", "1")
 
@@ -392,6 +397,12 @@ def _route_cached(c: _Call, knobs: Knobs) -> Optional[Tensor]:
 
 
 def _route_folded(c: _Call, knobs: Knobs) -> Optional[Tensor]:
+    """Route 1. The folded kernel computes softmax(Qf x^T) x with h Lq folded queries of width E: 4x
+    the attention FLOPs of projection + hxq (4 h Lq Lk E against 2 Lk E 2E + 4 Lq Lk E per batch
+    element), to save the [.., Lk, 2E] projection that the reference avoids on its TPU for memory. On
+    this GPU that trade loses at every shape measured (bf16 1.67 vs 0.94 ms, fp32 10.9 vs 4.3 ms at
+    54 x 128 queries over 45k rows), so where the hxq kernel takes the call it runs as route 2 does,
+    the same math to rounding; TABICL_MI355_HXF_FORCE=1 keeps the folded kernel."""
     if not (knobs.folded and c.inducing_over_rows(knobs.max_head_dim)):
         return None
     kc = c.key_constraint()
@@ -400,6 +411,8 @@ def _route_folded(c: _Call, knobs: Knobs) -> Optional[Tensor]:
     valid, kb = kc
     if valid is not None and valid.numel() != 1:
         return None
+    if not knobs.folded_force and _PK.hxq_supported(c.Lq, c.Lk, c.E, c.h, c.query.dtype):
+        return _route_few_queries(c, dataclasses.replace(knobs, few_queries=True))
     o = folded_mab1(c.query, c.key, valid, c.h, c.w, c.b, c.ssmax, c.src_len_override, key_bias=kb)
     return None if o is None else c.out(o)
 
@@ -509,6 +522,11 @@ def install(att_module, layers_module=None, mode: Optional[str] = None, proj: Op
         layers_module.multi_head_attention_forward = multi_head_attention_forward
     if knobs.icl_hook and hasattr(att_module, "sdpa_with_flattened_batch"):
         att_module.sdpa_with_flattened_batch = icl_hook(att_module.sdpa_with_flattened_batch)
+    if knobs.icl_hook:  # the reference's Splash op attributes (diff:95-115), for code that calls them directly
+        for form in ("seg", "full"):
+            op = getattr(_ICL, f"splash_sdpa_{form}_op", None)
+            if op is not None:
+                setattr(att_module, f"_tpu_splash_sdpa_{form}_op", op)
     att_module._mi355_mha_installed = True
     att_module._mi355_mha_mode = knobs.mode
     att_module._mi355_mha_proj = knobs.proj

@@ -169,6 +169,38 @@ def test_icl_full_c4_slice(dev, qscale):
         check(out[n:n + 1, h:h + 1, rows], ref, torch.bfloat16, f"c4 ({n},{h}) qscale={qscale}")
 
 
+@pytest.mark.parametrize("form", ["seg", "full"])
+def test_reference_splash_op_names(dev, form):
+    # the reference's call pattern around its Splash ops (results/tpu_patch.diff:123-155): q scaled by
+    # D^-0.5 in the input dtype and padded to a multiple of bq, k/v padded with zeros to a multiple of
+    # bkv, then tabicl::tpu_splash_sdpa_seg with the valid length (or _full when every padded key is
+    # valid), the padded query rows sliced off
+    import torch.nn.functional as F
+
+    import tabicl_mi355_icl as icl
+    g = torch.Generator().manual_seed(14)
+    N, H, Tq, Tkv, D = 2, 8, 700, 3000 if form == "seg" else 4096, 64
+    bq, bkv = 512, 1024
+    q = torch.randn(N, H, Tq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(N, H, Tkv, D, generator=g).to(torch.bfloat16)
+    tq, tk = -(-Tq // bq) * bq, -(-Tkv // bkv) * bkv
+    q_in = F.pad((q.to(dev) * D ** -0.5).contiguous(), (0, 0, 0, tq - Tq))
+    k_in = F.pad(k.to(dev), (0, 0, 0, tk - Tkv))
+    v_in = F.pad(v.to(dev), (0, 0, 0, tk - Tkv))
+    if form == "seg":
+        out = torch.ops.tabicl.tpu_splash_sdpa_seg(q_in, k_in, v_in, torch.tensor(2500, dtype=torch.int32, device=dev),
+                                                   bq, bkv)
+        ref = O.splash_sdpa_ref(q, k, v, 2500)
+    else:
+        assert tk == Tkv
+        out = icl.splash_sdpa_full_op(q_in, k_in, v_in, bq, bkv)
+        ref = O.splash_sdpa_ref(q, k, v)
+    torch.cuda.synchronize()
+    assert out.shape == q_in.shape
+    check(out[:, :, :Tq], ref, torch.bfloat16, f"splash op {form}")
+
+
 def _native_icl(q, k, v, valid, ws):
     import tabicl_mi355_native as nat
     out = torch.empty_like(q)

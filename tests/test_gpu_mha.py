@@ -134,6 +134,7 @@ def test_block_cached_column_attention(dev, mha, monkeypatch, dtype):
 
 def test_block_isab1_folded_route(dev, mha, monkeypatch):
     monkeypatch.setattr(mha.KNOBS, "folded", True)
+    monkeypatch.setattr(mha.KNOBS, "folded_force", True)  # the folded kernel, not projection + hxq
     seen = _spy(monkeypatch)
     g = torch.Generator().manual_seed(51)
     w, b, wo, bo = _weights(E, 14, dev, torch.float32)

@@ -292,6 +292,7 @@ def test_isab1_train_mask_from_tensor_train_size_takes_few_query_route(routed):
 def test_isab1_folded_route_takes_the_train_mask(routed, mha, monkeypatch):
     mod, ref_mod, seen = routed
     monkeypatch.setattr(mha.KNOBS, "folded", True)  # install() copies the knobs: a new install sees it
+    monkeypatch.setattr(mha.KNOBS, "folded_force", True)  # the folded kernel itself, not projection + hxq
     g = torch.Generator().manual_seed(6)
     w, b, wo, bo = U.weights(E, 6)
     ind = torch.randn(16, E, generator=g).expand(3, 16, E)
@@ -311,6 +312,7 @@ def test_isab1_folded_route_key_mask_and_ssmax_without_override(routed, mha, mon
     # count, as upstream's sdpa does (k.size(-2), results/tpu_patch.diff:251-254)
     mod, ref_mod, seen = routed
     monkeypatch.setattr(mha.KNOBS, "folded", True)
+    monkeypatch.setattr(mha.KNOBS, "folded_force", True)
     g = torch.Generator().manual_seed(9)
     w, b, wo, bo = U.weights(E, 9)
     ind = torch.randn(16, E, generator=g).expand(2, 16, E)
@@ -323,6 +325,26 @@ def test_isab1_folded_route_key_mask_and_ssmax_without_override(routed, mha, mon
     got = _block(mod2, ind, w, b, wo, bo, **kw)
     want = _block(ref_mod, ind, w, b, wo, bo, **kw)
     assert seen == ["hxf_attention"]
+    torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
+
+
+def test_isab1_folded_knob_runs_projection_and_hxq_where_it_applies(routed, mha, monkeypatch):
+    # TABICL_TPU_MHA_HXF=1 alone (not forced): the call goes to projection + hxq, faster on this GPU, with
+    # the HXQ knob off too; the result is the same attention
+    mod, ref_mod, seen = routed
+    monkeypatch.setattr(mha.KNOBS, "folded", True)
+    monkeypatch.setattr(mha.KNOBS, "few_queries", False)
+    g = torch.Generator().manual_seed(10)
+    w, b, wo, bo = U.weights(E, 10)
+    ind = torch.randn(16, E, generator=g).expand(2, 16, E)
+    rows = torch.randn(2, 300, E, generator=g)
+    ts = torch.tensor(250)
+    mod2 = U.make_module()
+    assert mha.install(mod2, None, mode="pk")
+    kw = dict(k=rows, v=rows, src_len_override=ts, valid_kv_len=ts, ssmax_layer=U.SSMaxStub(H))
+    got = _block(mod2, ind, w, b, wo, bo, **kw)
+    want = _block(ref_mod, ind, w, b, wo, bo, **kw)
+    assert seen == ["hxq_attention"]
     torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
 
 
@@ -448,6 +470,21 @@ def test_fallbacks_to_upstream(routed):
     with torch.no_grad():
         U.call(mod.multi_head_attention_forward, x, x, x, H, w, b, wo, bo, need_kv=True)
     assert seen == []
+
+
+def test_install_binds_the_reference_splash_ops(mha):
+    # the upstream module's _tpu_splash_sdpa_{seg,full}_op attributes (the reference's op objects,
+    # results/tpu_patch.diff:95-115) become the HIP ICL ops under the reference's op names
+    import tabicl_mi355_icl as icl
+    mod = U.make_module()
+    assert mha.install(mod, None, mode="pk")
+    assert mod._tpu_splash_sdpa_seg_op is icl.splash_sdpa_seg_op
+    assert mod._tpu_splash_sdpa_full_op is icl.splash_sdpa_full_op
+    assert torch.ops.tabicl.tpu_splash_sdpa_seg is not None and torch.ops.tabicl.tpu_splash_sdpa_full is not None
+    q = torch.zeros(2, 8, 1024, 64, device="meta", dtype=torch.bfloat16)
+    k = torch.zeros(2, 8, 4096, 64, device="meta", dtype=torch.bfloat16)
+    out = torch.ops.tabicl.tpu_splash_sdpa_seg(q, k, k, torch.zeros((), dtype=torch.int32, device="meta"), 1024, 4096)
+    assert out.shape == q.shape and out.dtype == q.dtype
 
 
 def test_install_is_idempotent_and_off(mha):
