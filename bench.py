@@ -689,6 +689,43 @@ def bench_icl_stage(steps: int, warmup: int) -> list:
                         "cached-KV query 938.49 ms (best_model_forward_and_e2e.jsonl:2); not the same workload"}]
 
 
+def bench_icl_masked(steps: int, warmup: int) -> list:
+    """Key-masked ICL attention at one C4 block launch (8 est x 8 heads x 5000 q over 45000 keys, bf16),
+    icl_sdpa with an additive fp32 key mask, one row per estimator: a prefix mask (0 on the first 44000
+    keys, finfo.min after: the train mask upstream builds from a tensor train size) runs on the
+    pipelined kernel as a valid length; a scattered mask (finfo.min on a random 10% of the keys, 0
+    elsewhere) runs on the exact kernel, which adds it term by term. TFLOP/s over the keys each kernel
+    sweeps (44000 and 45000)."""
+    import torch
+
+    import tabicl_mi355_icl as icl
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(8)
+    q = torch.randn(EST, HEADS, TEST, D, generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(EST, HEADS, TRAIN, D, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(EST, HEADS, TRAIN, D, generator=g, device=dev, dtype=torch.bfloat16)
+    fmin = torch.finfo(torch.float32).min
+    prefix = torch.zeros(EST, TRAIN, device=dev)
+    prefix[:, TRAIN - 1000:] = fmin
+    scattered = torch.where(torch.rand(EST, TRAIN, generator=g, device=dev) < 0.1, fmin, 0.0)
+    recs = []
+    for name, mask, keys in (("prefix mask (pipelined kernel)", prefix, TRAIN - 1000),
+                             ("scattered mask (exact kernel)", scattered, TRAIN)):
+        with torch.no_grad():
+            ms = _time(lambda: icl.icl_sdpa(q, k, v, None, mask), steps, warmup)
+        tf = 4.0 * TEST * keys * D * HEADS * EST / (ms * 1e-3) / 1e12
+        recs.append({"metric": f"ms per key-masked ICL attention launch, {name}", "value": round(ms, 4),
+                     "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
+                     "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) (seed 8)",
+                     "config": {"workload": "one C4 block: 8 est x 8 heads x 5000 q over 45000 keys, d=64, "
+                                            "fp32 key mask [8, 45000]"},
+                     "attn_tflops": round(tf, 1),
+                     "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                  "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}})
+    return recs
+
+
 def bench_query(steps: int, warmup: int) -> list:
     """The whole cached-KV query at the headline workload (tabicl_mi355_query.cached_query: the reference
     runner's _make_query_fn, scripts/tabicl_tpu_bucketed.py:768-834): 8 estimators x 5,000 test rows x 100
@@ -799,11 +836,12 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-c3", action="store_true", help="default run: skip the C3 line printed before the headline")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer, icl_stage, query "
+                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer, icl_stage, "
+                         "icl_masked, query "
                          "(comma-separated) or all print the other BASELINE configs' lines, the fwd+bwd training "
                          "lines, the folded first-ISAB lines, the ICL cache build / attention sub-layer lines, the "
-                         "cached ICL query stage (12 blocks with norms and feed-forward) and the whole cached-KV "
-                         "query (column, row and ICL stages, decoder)")
+                         "cached ICL query stage (12 blocks with norms and feed-forward), key-masked ICL launches "
+                         "and the whole cached-KV query (column, row and ICL stages, decoder)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -813,7 +851,8 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "query", "all"}:
+    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "icl_masked", "query",
+                       "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
@@ -830,6 +869,8 @@ def main() -> int:
             recs += bench_icl_layer(args.steps, args.warmup)
         if configs & {"icl_stage", "all"}:
             recs += bench_icl_stage(args.steps, args.warmup)
+        if configs & {"icl_masked", "all"}:
+            recs += bench_icl_masked(args.steps, args.warmup)
         if configs & {"query", "all"}:
             recs += bench_query(args.steps, args.warmup)
         for rec in recs:

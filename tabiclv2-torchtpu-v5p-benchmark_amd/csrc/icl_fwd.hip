@@ -208,11 +208,94 @@ struct BiasStage {
   }
 };
 
+// One 32-key half kb of a key tile with the tile's key mask lb: S^T = K Q^T + mask, the online softmax
+// update (the running max moves per half), O^T += V^T P^T. The masked instance of the kernel takes a
+// tile in two such halves: only one half's scores and probabilities are live at a time, which keeps it
+// within 256 VGPRs (two waves per SIMD; a whole-tile pass needed 264 registers, one wave per SIMD).
+template <typename T, int QC, bool MASK, int D>
+__device__ __forceinline__ void icl_half_bias(IclState<T, QC, D>& st, const T* lk, const T* lv, const float* lb,
+                                              int k0, int valid, float sc, int lr, int hh, int kb) {
+  typedef IclLds<T, D> L;
+  typedef typename OpVec<T, 8>::type Op8;
+  f32x16 s[QC];
+#pragma unroll
+  for (int qc = 0; qc < QC; ++qc)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[qc][r] = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < D / 16; ++sl) {
+    const Op8 a = *(const Op8*)(lk + (kb * 32 + lr) * L::KSTR + 16 * sl + 8 * hh);
+#pragma unroll
+    for (int qc = 0; qc < QC; ++qc) s[qc] = mfma32x32x16(a, st.qop[qc][sl], s[qc]);
+  }
+  // S^T row of reg r = key 8 (r / 4) + 4 hh + r % 4 of the 32-key block
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 bb = *(const float4*)(lb + kb * 32 + 8 * g + 4 * hh);
+#pragma unroll
+    for (int qc = 0; qc < QC; ++qc) {
+      s[qc][4 * g] += bb.x;
+      s[qc][4 * g + 1] += bb.y;
+      s[qc][4 * g + 2] += bb.z;
+      s[qc][4 * g + 3] += bb.w;
+    }
+  }
+  if (MASK) {
+#pragma unroll
+    for (int qc = 0; qc < QC; ++qc)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (k0 + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3) >= valid) s[qc][r] = TA_NEG_INF;
+  }
+  Op8 pop[QC][2];
+#pragma unroll
+  for (int qc = 0; qc < QC; ++qc) {
+    float mx = s[qc][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[qc][r]);
+    mx = lane_pair_max(mx);
+    const float m_new = fmaxf(st.m_run[qc], mx);
+    if (wave_any((m_new - st.m_run[qc]) * sc > ICL_LAZY)) {
+      const float alpha = __builtin_amdgcn_exp2f((st.m_run[qc] - m_new) * sc);
+      st.l_run[qc] *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st.o[qc][db][r] *= alpha;
+      st.m_run[qc] = m_new;
+    }
+    const float mr = st.m_run[qc];
+    float lsum = 0.f;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)  // the difference first: scores reach the -1e30 floor (see icl_tile)
+        pop[qc][m][j] = from_f32<T>(__builtin_amdgcn_exp2f((s[qc][8 * m + j] - mr) * sc));
+      lsum = psum8(pop[qc][m], lsum);
+    }
+    st.l_run[qc] += lsum;
+  }
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const Op8 a = *(const Op8*)(lv + vt_off(db * 32 + lr, kb * 32 + 16 * m + 8 * hh, L::VSTR));
+#pragma unroll
+      for (int qc = 0; qc < QC; ++qc) st.o[qc][db] = mfma32x32x16(a, pop[qc][m], st.o[qc][db]);
+    }
+}
+
 // One key tile: S^T = K Q^T (+ the tile's key mask lb when BIAS), online softmax, O^T += V^T P^T.
-// MASK: the tile crosses `valid`.
+// MASK: the tile crosses `valid`. With BIAS the tile goes through icl_half_bias twice.
 template <typename T, int QC, bool MASK, int D, bool BIAS = false>
 __device__ __forceinline__ void icl_tile(IclState<T, QC, D>& st, const T* lk, const T* lv, const float* lb,
                                          int k0, int valid, float sc, int lr, int hh) {
+  if constexpr (BIAS) {
+    icl_half_bias<T, QC, MASK, D>(st, lk, lv, lb, k0, valid, sc, lr, hh, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the second half's products start after the first half's PV
+    icl_half_bias<T, QC, MASK, D>(st, lk, lv, lb, k0, valid, sc, lr, hh, 1);
+    return;
+  }
   typedef IclLds<T, D> L;
   typedef typename OpVec<T, 8>::type Op8;
   f32x16 s[QC][2];
