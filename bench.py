@@ -503,9 +503,10 @@ def bench_c5(steps: int, warmup: int) -> list:
                 for _ in range(BLOCKS):  # one block's cache stands for each of the 12 blocks
                     icl.ICL_FWD_OUT(q, k, v, valid, 64 ** -0.5, out)
 
-            def step():
+            def step():  # the live work-item list once per bucket, then every block's call takes it
+                plan = icl.IclRaggedPlan(qlen, N, H, Tq, L, 64, torch.bfloat16)
                 for _ in range(BLOCKS):
-                    icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, out)
+                    icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, qlen, 64 ** -0.5, out, None, plan.workspace)
 
             parts["icl"][3] += _time(step_padded, steps, warmup)
             ms = _time(step, steps, warmup)

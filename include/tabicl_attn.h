@@ -244,6 +244,34 @@ int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int
                           void* stream);
 
 /*
+ * Plan of a ragged ICL call: writes the list of live work items (those holding a row below q_len)
+ * into `workspace` (at least tabicl_icl_workspace_bytes(N, H, Tq, Tkv, D, dtype) bytes) on `stream`,
+ * and nothing else. tabicl_icl_fwd_ragged_listed then takes the list from that workspace instead of
+ * computing it, so a caller that repeats one ragged call shape (the 12 ICL blocks of a bucket, one
+ * call per block) computes the list once. No counterpart in the reference, whose bucketed runner has
+ * no ragged calls. Only bf16 with D = 64 uses a list; for fp32 the call does nothing.
+ */
+int tabicl_icl_ragged_plan(const int32_t* q_len, int64_t q_len_n, int64_t N, int64_t H, int64_t Tq,
+                           int64_t Tkv, int64_t D, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/*
+ * tabicl_icl_fwd_ragged with the live work-item list taken from `workspace`, where an earlier
+ * tabicl_icl_ragged_plan call on the same stream left it for the same N, H, Tq, Tkv, D, dtype, q_len
+ * contents and workspace_bytes (the workspace is otherwise used as by tabicl_icl_fwd_ragged: each
+ * call writes the parts it reads, so calls that follow each other on one stream may share it; calls
+ * that overlap race). A stale list (q_len changed since the plan) leaves rows unwritten. Results equal
+ * tabicl_icl_fwd_ragged's bit for bit. No counterpart in the reference.
+ */
+int tabicl_icl_fwd_ragged_listed(const void* q, const void* k, const void* v, const int32_t* valid,
+                                 int64_t valid_n, const int32_t* q_len, int64_t q_len_n, void* out, int64_t N,
+                                 int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh,
+                                 int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st, int64_t v_sn,
+                                 int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                                 float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+
+/*
  * tabicl_icl_fwd_ragged with an additive fp32 key mask (NULL: none): key_bias [bias_n, Tkv] with
  * bias_n in {1, N}, row stride bias_sn elements, keys contiguous, added to the scaled scores
  * (softmax(scale q k^T + mask) v, the reference's attn_mask path, results/tpu_patch.diff:263-270,

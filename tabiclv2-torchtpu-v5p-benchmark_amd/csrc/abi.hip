@@ -375,6 +375,42 @@ int tabicl_icl_fwd_ragged(const void* q, const void* k, const void* v, const int
                                workspace, workspace_bytes, stream);
 }
 
+int tabicl_icl_fwd_ragged_listed(const void* q, const void* k, const void* v, const int32_t* valid,
+                                 int64_t valid_n, const int32_t* q_len, int64_t q_len_n, void* out, int64_t N,
+                                 int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int64_t q_sn, int64_t q_sh,
+                                 int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st, int64_t v_sn,
+                                 int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                                 float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  const int64_t strides[12] = {q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st};
+  int st = icl_args("icl_fwd_ragged_listed", q, k, v, valid, valid_n, nullptr, 0, 0, q_len, q_len_n, out, N, H, Tq,
+                    Tkv, D, strides, scale, dtype);
+  if (st || N == 0 || H == 0 || Tq == 0) return st;
+  if (!q_len) return fail(1, "icl_fwd_ragged_listed: q_len is required");
+  return launch_status(
+      tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, 64, q_sn, q_sh, q_st, k_sn,
+                            k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype,
+                            workspace && aligned16(workspace) ? workspace : nullptr, workspace_bytes,
+                            (hipStream_t)stream, q_len, q_len_n, nullptr, 0, 0, 1),
+      "icl_fwd_ragged_listed");
+}
+
+int tabicl_icl_ragged_plan(const int32_t* q_len, int64_t q_len_n, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                           int64_t D, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (N < 0 || H < 0 || Tq < 0 || Tkv < 0) return fail(1, "icl_ragged_plan: negative size");
+  if (D != 64) return fail(1, "icl_ragged_plan: D must be 64");
+  if (dtype != 0 && dtype != 1) return fail(1, "icl_ragged_plan: dtype must be 0 (bf16) or 1 (fp32)");
+  if (!q_len || (q_len_n != 1 && q_len_n != N)) return fail(1, "icl_ragged_plan: q_len [1 or N] is required");
+  if (N == 0 || H == 0 || Tq == 0 || Tkv == 0) return 0;
+  if (workspace && !aligned16(workspace)) return fail(1, "icl_ragged_plan: workspace must be 16-byte aligned");
+  // the list goes where the call puts it: the kernels need no q / k / v / out here, only their sizes
+  return launch_status(
+      tabicl_launch_icl_fwd(nullptr, nullptr, nullptr, nullptr, 0, nullptr, N, H, Tq, Tkv, 64, 0, 0, 0, 0, 0, 0, 0,
+                            0, 0, 0, 0, 0, 1.0f, dtype, workspace, workspace ? workspace_bytes : 0,
+                            (hipStream_t)stream, q_len, q_len_n, nullptr, 0, 0, 2),
+      "icl_ragged_plan");
+}
+
 int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
                           const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,
                           int64_t q_len_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,

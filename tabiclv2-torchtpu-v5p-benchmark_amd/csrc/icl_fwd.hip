@@ -1202,8 +1202,13 @@ int64_t workspace_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv) {
 // bf16 d = 64 with a large enough workspace: pipelined kernel, then icl_fwd_kernel on the work
 // items it flagged, then the split merge. Otherwise icl_fwd_kernel alone (splitting only if the
 // workspace holds the partials).
+// List modes of ragged calls: ICL_LIST_BUILD computes the live work-item list into the workspace and
+// runs the call; ICL_LIST_READY takes the list an earlier ICL_LIST_ONLY launch (same sizes, q_len
+// contents and workspace) left there; ICL_LIST_ONLY computes the list and launches nothing else.
+enum { ICL_LIST_BUILD = 0, ICL_LIST_READY = 1, ICL_LIST_ONLY = 2 };
+
 template <typename T, int NW, int QC, int D>
-void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
+void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream, int list_mode = ICL_LIST_BUILD) {
   IclParams p = p0;
   p.nqb = (p.Tq + 32 * QC * NW - 1) / (32 * QC * NW);
   const int64_t rows = (int64_t)p.N * p.H * p.Tq;
@@ -1240,9 +1245,11 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream)
   }
   if (fast && p.qlen && p.N < ICL_LIST_MAXN) {
     int32_t* list = (int32_t*)((char*)ws + flag_bytes(nblk) + pref_bytes(p.N));
-    hipLaunchKernelGGL(icl_live_list_kernel, dim3(1), dim3(1024), 0, stream, p, list);
+    if (list_mode != ICL_LIST_READY)
+      hipLaunchKernelGGL(icl_live_list_kernel, dim3(1), dim3(1024), 0, stream, p, list);
     p.live = list;
   }
+  if (list_mode == ICL_LIST_ONLY) return;
   if (fast)
     hipLaunchKernelGGL(icl_pipe_kernel, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
   if (p.bias)
@@ -1270,7 +1277,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream, const int32_t* qlen,
-                          int64_t qlen_n, const float* bias, int64_t bias_n, int64_t bias_sn) {
+                          int64_t qlen_n, const float* bias, int64_t bias_n, int64_t bias_sn, int list_mode) {
   IclParams p;
   p.q = q; p.k = k; p.v = v; p.o = out;
   p.valid = valid; p.valid_n = (int)valid_n;
@@ -1292,8 +1299,8 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
     else
       launch<float, 8, 1, 128>(p, ws, ws_bytes, stream);
   } else if (dtype == 0) {
-    launch<bf16, 4, 2, 64>(p, ws, ws_bytes, stream);
-  } else {
+    launch<bf16, 4, 2, 64>(p, ws, ws_bytes, stream, list_mode);
+  } else if (list_mode != ICL_LIST_ONLY) {
     launch<float, 4, 1, 64>(p, ws, ws_bytes, stream);
   }
   return (int)hipGetLastError();
@@ -1353,5 +1360,5 @@ int tabicl_launch_icl_fwd_noalloc(const void* q, const void* k, const void* v, c
   if (e != hipSuccess) return (int)e;
   return tabicl_launch_icl_fwd(q, k, v, valid, valid_n, out, N, H, Tq, Tkv, ICL_D, q_sn, q_sh, q_st, k_sn, k_sh, k_st,
                                v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype, ws, TABICL_ICL_SCRATCH_BYTES, stream,
-                               qlen, qlen_n, bias, bias_n, bias_sn);
+                               qlen, qlen_n, bias, bias_n, bias_sn, 0);
 }

@@ -23,7 +23,8 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream,
                           const int32_t* qlen = nullptr, int64_t qlen_n = 0,
-                          const float* bias = nullptr, int64_t bias_n = 0, int64_t bias_sn = 0);
+                          const float* bias = nullptr, int64_t bias_n = 0, int64_t bias_sn = 0,
+                          int list_mode = 0);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
 // The same launch (D = 64) with the library's per-GPU scratch array of TABICL_ICL_SCRATCH_BYTES in

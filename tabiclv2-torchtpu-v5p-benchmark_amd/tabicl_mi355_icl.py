@@ -52,7 +52,7 @@ def _workspace(N: int, H: int, Tq: int, Tkv: int, D: int, code: int, device) -> 
 
 
 def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float, out: Tensor,
-            q_len: Optional[Tensor] = None, key_bias: Optional[Tensor] = None) -> None:
+            q_len: Optional[Tensor] = None, key_bias: Optional[Tensor] = None, plan_ws: Optional[Tensor] = None) -> None:
     _nat.require_device(q, k, v, valid, out, q_len, key_bias)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("icl_cached_attn expects [N, H, T, D] tensors")
@@ -70,7 +70,13 @@ def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: flo
             raise ValueError("valid must be a contiguous int32 tensor")
         vptr, vn = valid.data_ptr(), valid.numel()
     code = _nat.dtype_code(q.dtype)
-    ws = _workspace(N, H, Tq, Tkv, D, code, q.device)
+    if plan_ws is not None:
+        if q_len is None or key_bias is not None:
+            raise ValueError("a ragged plan serves ragged calls without a key mask")
+        nbytes = _WS_BYTES.get((N, H, Tq, Tkv, D, code, q.device.index))
+        if nbytes is None or plan_ws.numel() != nbytes or plan_ws.device != q.device:
+            raise ValueError("the plan was made for other sizes, dtype or device")
+    ws = plan_ws if plan_ws is not None else _workspace(N, H, Tq, Tkv, D, code, q.device)
     tail = (*_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out), float(scale), code,
             None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _nat.stream_of(q))
     if q_len is not None and (q_len.dtype != torch.int32 or not q_len.is_contiguous() or q_len.numel() not in (1, N)):
@@ -88,8 +94,9 @@ def _launch(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: flo
         _nat.call("tabicl_icl_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
                   N, H, Tq, Tkv, D, *tail)
         return
-    _nat.call("tabicl_icl_fwd_ragged", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, q_len.data_ptr(),
-              q_len.numel(), out.data_ptr(), N, H, Tq, Tkv, D, *tail)
+    _nat.call("tabicl_icl_fwd_ragged_listed" if plan_ws is not None else "tabicl_icl_fwd_ragged", q.data_ptr(),
+              k.data_ptr(), v.data_ptr(), vptr, vn, q_len.data_ptr(), q_len.numel(), out.data_ptr(), N, H, Tq, Tkv, D,
+              *tail)
 
 
 @torch.library.custom_op("tabicl::icl_cached_attn", mutates_args=())
@@ -123,21 +130,45 @@ def _(q, k, v, valid, scale, out, key_bias=None):  # noqa: ANN001
 
 @torch.library.custom_op("tabicl::icl_cached_attn_ragged_out", mutates_args=("out",))
 def _icl_cached_attn_ragged_out(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], q_len: Tensor,
-                                scale: float, out: Tensor, key_bias: Optional[Tensor] = None) -> None:
+                                scale: float, out: Tensor, key_bias: Optional[Tensor] = None,
+                                plan_ws: Optional[Tensor] = None) -> None:
     """icl_cached_attn_out over a ragged batch: rows at or past q_len[n] (1 or N entries) are neither
     computed nor written (out keeps what it held). No counterpart in the reference, whose bucketed
-    runner attends with the padding rows of each table's test bucket too."""
-    _launch(q, k, v, valid, scale, out, q_len, key_bias)
+    runner attends with the padding rows of each table's test bucket too. plan_ws: the workspace of an
+    IclRaggedPlan for these sizes and q_len (IclRaggedPlan.workspace): the list of live work items is
+    taken from it instead of being computed by this call."""
+    _launch(q, k, v, valid, scale, out, q_len, key_bias, plan_ws)
 
 
 @_icl_cached_attn_ragged_out.register_fake
-def _(q, k, v, valid, q_len, scale, out, key_bias=None):  # noqa: ANN001
+def _(q, k, v, valid, q_len, scale, out, key_bias=None, plan_ws=None):  # noqa: ANN001
     return None
 
 
 ICL_FWD = torch.ops.tabicl.icl_cached_attn
 ICL_FWD_OUT = torch.ops.tabicl.icl_cached_attn_out
 ICL_FWD_RAGGED_OUT = torch.ops.tabicl.icl_cached_attn_ragged_out
+
+
+class IclRaggedPlan:
+    """The list of live work items of one ragged ICL call shape, computed once on the current stream
+    (tabicl_icl_ragged_plan) into a workspace that the calls then share: pass `plan.workspace` as
+    ICL_FWD_RAGGED_OUT's plan_ws for every call with the same N, H, Tq, Tkv, head dim, dtype and the
+    same q_len contents, e.g. the 12 ICL blocks of one bucket. The calls must follow each other on one
+    stream (they share the workspace); a q_len changed after the plan leaves rows unwritten. No
+    counterpart in the reference (its runner has no ragged calls)."""
+
+    def __init__(self, q_len: Tensor, N: int, H: int, Tq: int, Tkv: int, D: int = 64,
+                 dtype: torch.dtype = torch.bfloat16):
+        _nat.require_device(q_len)
+        if q_len.dtype != torch.int32 or not q_len.is_contiguous() or q_len.numel() not in (1, N):
+            raise ValueError(f"q_len must be a contiguous int32 tensor of 1 or {N} entries")
+        code = _nat.dtype_code(dtype)
+        ws = _workspace(N, H, Tq, Tkv, D, code, q_len.device)
+        self.workspace = ws if ws is not None else torch.empty(0, dtype=torch.uint8, device=q_len.device)
+        self.q_len = q_len
+        _nat.call("tabicl_icl_ragged_plan", q_len.data_ptr(), q_len.numel(), N, H, Tq, Tkv, D, code,
+                  None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _nat.stream_of(q_len))
 
 
 @torch.library.custom_op("tabicl::tpu_splash_sdpa_seg", mutates_args=())

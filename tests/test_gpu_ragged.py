@@ -79,6 +79,37 @@ def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
         check(out[0, 0, :n0], exp[0, 0, :n0], dtype, name)
 
 
+@pytest.mark.parametrize("name,N,H,Tq,Tkv,dtype", [
+    ("c5_bucket_shape_bf16", 80, 8, 1024, 2048, torch.bfloat16),  # 10 tables x 8 estimators, 1k test bucket
+    ("split_bf16", 3, 8, 520, 6000, torch.bfloat16),              # few work items: the keys split
+    ("fp32", 4, 2, 300, 900, torch.float32),                      # no list: the plan does nothing
+])
+def test_icl_ragged_plan_reused_across_blocks(dev, name, N, H, Tq, Tkv, dtype):
+    # one plan (the live work-item list, computed once) serves several calls with the same sizes and
+    # q_len, as the 12 ICL blocks of a bucket do; each equals the call that builds its own list, bit for bit
+    import tabicl_mi355_icl as icl
+    g = torch.Generator().manual_seed(13)
+    rng = np.random.default_rng(7)
+    q_len = torch.tensor([int(x) for x in rng.integers(0, Tq + 1, N)], dtype=torch.int32, device=dev)
+    valid = torch.tensor([int(x) for x in rng.integers(1, Tkv + 1, N)], dtype=torch.int32, device=dev)
+    plan = icl.IclRaggedPlan(q_len, N, H, Tq, Tkv, 64, dtype)
+    print(f"[ragged plan] {name}", flush=True)
+    for blk in range(3):
+        q = torch.randn(N, H, Tq, 64, generator=g).to(dtype).to(dev)
+        k = torch.randn(N, H, Tkv, 64, generator=g).to(dtype).to(dev)
+        v = torch.randn(N, H, Tkv, 64, generator=g).to(dtype).to(dev)
+        want = torch.full_like(q, float("nan"))
+        got = torch.full_like(q, float("nan"))
+        icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, q_len, 64 ** -0.5, want)
+        icl.ICL_FWD_RAGGED_OUT(q, k, v, valid, q_len, 64 ** -0.5, got, None, plan.workspace)
+        torch.cuda.synchronize()
+        assert torch.equal(torch.nan_to_num(got, nan=7.0), torch.nan_to_num(want, nan=7.0)), (name, blk)
+        n0 = int(q_len[0])
+        if n0 > 0 and blk == 0:
+            exp = O.splash_sdpa_ref(q[:1, :1].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu(), valid[:1].cpu().numpy())
+            check(got[0, 0, :n0], exp[0, 0, :n0], dtype, name)
+
+
 def _pk_cross_case(dev, B, Lq, Lk, dtype, seed):
     g = torch.Generator().manual_seed(seed)
     q = (torch.randn(B, Lq, 128, generator=g) * 0.5).to(dtype).to(dev)
