@@ -346,6 +346,19 @@ const char* tabicl_attn_last_error(void);
 /* Library version string. */
 const char* tabicl_attn_version(void);
 
+/*
+ * Row LayerNorm of the layers around the attention in the cached-KV query (the column, row and ICL
+ * blocks' pre-norms, the row stage's out-norm and the final norm): upstream's SafeLayerNorm
+ * (results/tpu_patch.diff:1385-1397, normalising in its fp32 weights' dtype). out = (s - mean)
+ * rsqrt(var + eps) weight + bias per row of `width` (128 or 512) values, rows contiguous, mean and biased
+ * variance in fp32; s = x, or with `residual` non-NULL s = x + residual rounded to the input dtype and
+ * also written to x_out (which may alias x). in_dtype / out_dtype: 0 bf16, 1 fp32; weight / bias fp32
+ * [width] or NULL (1 / 0). All pointers 16-byte aligned. Returns 0, >0 unsupported, <0 HIP error.
+ */
+int tabicl_layer_norm(const void* x, const void* residual, void* x_out, const float* weight, const float* bias,
+                      void* out, int64_t rows, int64_t width, float eps, int32_t in_dtype, int32_t out_dtype,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

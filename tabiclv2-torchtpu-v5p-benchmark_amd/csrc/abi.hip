@@ -537,3 +537,21 @@ int tabicl_icl_cache_append(void* k_cache, void* v_cache, int64_t dst_sn, int64_
 }
 
 }  // extern "C"
+
+int tabicl_layer_norm(const void* x, const void* residual, void* x_out, const float* weight, const float* bias,
+                      void* out, int64_t rows, int64_t width, float eps, int32_t in_dtype, int32_t out_dtype,
+                      void* stream) {
+  if (rows < 0) return fail(1, "layer_norm: negative row count");
+  if (width != 128 && width != 512) return fail(1, "layer_norm: width %lld not supported (128 or 512)", (long long)width);
+  if ((in_dtype != 0 && in_dtype != 1) || (out_dtype != 0 && out_dtype != 1))
+    return fail(1, "layer_norm: dtypes must be 0 (bf16) or 1 (fp32)");
+  if (!(eps > 0.f)) return fail(1, "layer_norm: eps must be positive");
+  if (rows == 0) return 0;
+  if (!x || !out || !aligned16(x) || !aligned16(out) || (weight && !aligned16(weight)) || (bias && !aligned16(bias)))
+    return fail(1, "layer_norm: x, out, weight and bias must be 16-byte aligned device pointers");
+  if (residual && (!x_out || !aligned16(residual) || !aligned16(x_out)))
+    return fail(1, "layer_norm: with a residual, x_out (16-byte aligned) receives x + residual");
+  return launch_status(tabicl_launch_layer_norm(x, residual, residual ? x_out : nullptr, weight, bias, out, rows, width,
+                                                eps, in_dtype, out_dtype, (hipStream_t)stream),
+                       "layer_norm");
+}

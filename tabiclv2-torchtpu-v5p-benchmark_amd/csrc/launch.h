@@ -75,3 +75,9 @@ int tabicl_launch_smallhead_bwd(const void* q, int64_t q_sb, int64_t q_sr, const
                                 int64_t B, int64_t Lq, int64_t Lk, int dtype, void* ws, int64_t ws_bytes,
                                 hipStream_t stream);
 int64_t tabicl_launch_smallhead_bwd_ws_bytes(int64_t B, int64_t Lq);
+
+// Row LayerNorm (layernorm.hip): rows x width (128 or 512) contiguous, fp32 / bf16 in (dtype codes 0 bf16,
+// 1 fp32) and out, fp32 weight / bias (null: 1 / 0); with r, xs = x + r (input dtype) is written and
+// normalised.
+int tabicl_launch_layer_norm(const void* x, const void* r, void* xs, const float* w, const float* b, void* y,
+                             int64_t rows, int64_t width, float eps, int in_dtype, int out_dtype, hipStream_t stream);

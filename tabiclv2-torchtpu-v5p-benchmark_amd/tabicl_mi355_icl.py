@@ -384,8 +384,8 @@ class IclKVCache:
             raise ValueError(f"{len(blocks)} blocks of weights for a cache of {self.keys.shape[1]} blocks")
         for b, w in enumerate(blocks):
             h = _safe_layer_norm(x, w.ln1_w, w.ln1_b, w.eps, w.in_w.dtype)
-            x = x + self.attention_layer(b, h, w.in_w, w.in_b, w.out_w, w.out_b, valid_kv_len, q_transform).to(x.dtype)
-            h = _safe_layer_norm(x, w.ln2_w, w.ln2_b, w.eps, w.ff1_w.dtype)
+            a = self.attention_layer(b, h, w.in_w, w.in_b, w.out_w, w.out_b, valid_kv_len, q_transform).to(x.dtype)
+            x, h = add_layer_norm(x, a, w.ln2_w, w.ln2_b, w.eps, w.ff1_w.dtype)  # x + attention, then norm2
             x = x + F.linear(activation(F.linear(h, w.ff1_w, w.ff1_b)), w.ff2_w, w.ff2_b).to(x.dtype)
         return x
 
@@ -462,10 +462,50 @@ class IclBlockWeights:
     eps: float = 1e-5
 
 
+_LN_WIDTHS = (128, 512)
+_LN_DTYPES = (torch.bfloat16, torch.float32)
+
+
+def _ln_native(x: Tensor, w: Tensor, b: Optional[Tensor], eps: float, out_dtype: torch.dtype,
+               r: Optional[Tensor] = None) -> bool:
+    """Whether the library's row LayerNorm (tabicl_layer_norm) takes this call: GPU tensors, rows of 128
+    or 512 contiguous values in bf16 / fp32, fp32 weights, an output dtype of bf16 / fp32."""
+    W = x.shape[-1]
+    return (x.device.type == "cuda" and W in _LN_WIDTHS and x.dtype in _LN_DTYPES and out_dtype in _LN_DTYPES
+            and w.dtype == torch.float32 and w.is_contiguous() and w.numel() == W
+            and (b is None or (b.dtype == torch.float32 and b.is_contiguous() and b.numel() == W))
+            and (r is None or (r.dtype == x.dtype and r.shape == x.shape)))
+
+
+def _ln_call(x: Tensor, r: Optional[Tensor], w: Tensor, b: Optional[Tensor], eps: float,
+             out_dtype: torch.dtype):
+    x = _nat.aligned16(x)
+    r = None if r is None else _nat.aligned16(r)
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    xs = torch.empty_like(x) if r is not None else None
+    _nat.call("tabicl_layer_norm", x.data_ptr(), None if r is None else r.data_ptr(),
+              None if xs is None else xs.data_ptr(), w.data_ptr(), None if b is None else b.data_ptr(),
+              out.data_ptr(), x.numel() // x.shape[-1], x.shape[-1], float(eps), _nat.dtype_code(x.dtype),
+              _nat.dtype_code(out_dtype), _nat.stream_of(x))
+    return xs, out
+
+
 def _safe_layer_norm(x: Tensor, w: Tensor, b: Optional[Tensor], eps: float, out_dtype: torch.dtype) -> Tensor:
     """LayerNorm over the last dim computed in the weights' dtype (results/tpu_patch.diff:1385-1397), the
-    result cast to the next GEMM's dtype."""
+    result cast to the next GEMM's dtype. On the GPU for rows of 128 / 512 values: the library's row
+    kernel (fp32 statistics, one pass over HBM); otherwise torch."""
+    if _ln_native(x, w, b, eps, out_dtype):
+        return _ln_call(x, None, w, b, eps, out_dtype)[1]
     return F.layer_norm(x.to(w.dtype), (x.shape[-1],), w, b, eps).to(out_dtype)
+
+
+def add_layer_norm(x: Tensor, r: Tensor, w: Tensor, b: Optional[Tensor], eps: float, out_dtype: torch.dtype):
+    """(s, LayerNorm(s)) with s = x + r in x's dtype: a residual add and the next pre-norm in one pass
+    over HBM on the GPU (tabicl_layer_norm with a residual); otherwise torch, the same two steps."""
+    if _ln_native(x, w, b, eps, out_dtype, r):
+        return _ln_call(x, r, w, b, eps, out_dtype)
+    s = x + r
+    return s, _safe_layer_norm(s, w, b, eps, out_dtype)
 
 
 def _valid_arg(valid_kv_len, Tkv: int, device) -> Optional[Tensor]:  # noqa: ANN001

@@ -53,6 +53,7 @@ SIGNATURES = {
     "tabicl_icl_fwd_ragged_listed": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64, _i64, _i64]
                                     + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_ragged_plan": [_c_p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _c_p, _i64, _c_p],
+    "tabicl_layer_norm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _f32, _i32, _i32, _c_p],
     "tabicl_icl_fwd_masked": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
                               _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_fwd_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,

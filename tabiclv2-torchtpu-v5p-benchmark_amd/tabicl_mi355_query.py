@@ -84,9 +84,13 @@ def _ln(x: Tensor, w: Tensor, b: Optional[Tensor], eps: float, out_dtype: torch.
     return _icl._safe_layer_norm(x, w, b, eps, out_dtype)
 
 
-def _ffn(x: Tensor, blk, activation) -> Tensor:  # noqa: ANN001
-    """x + W2 act(W1 LN2(x) + b1) + b2 (the feed-forward half of a pre-norm encoder layer)."""
-    h = _ln(x, blk.ln2_w, blk.ln2_b, blk.eps, blk.ff1_w.dtype)
+def _ffn(x: Tensor, blk, activation, delta: Optional[Tensor] = None) -> Tensor:  # noqa: ANN001
+    """x + W2 act(W1 LN2(x) + b1) + b2 (the feed-forward half of a pre-norm encoder layer); with delta
+    (the attention half's output) x + delta first, fused with LN2."""
+    if delta is None:
+        h = _ln(x, blk.ln2_w, blk.ln2_b, blk.eps, blk.ff1_w.dtype)
+    else:
+        x, h = _icl.add_layer_norm(x, delta.to(x.dtype), blk.ln2_w, blk.ln2_b, blk.eps, blk.ff1_w.dtype)
     return x + F.linear(activation(F.linear(h, blk.ff1_w, blk.ff1_b)), blk.ff2_w, blk.ff2_b).to(x.dtype)
 
 
@@ -163,8 +167,7 @@ def column_stage(X: Tensor, real_features: Optional[Tensor], cache: ColumnKVCach
         if kv.dtype != q.dtype:
             kv = kv.to(q.dtype)
         a = _pk.pk_cross_attention(q, kv, h, None, None, (E // h) ** -0.5)
-        out = src + F.linear(a, blk.out_w, blk.out_b).to(src.dtype)
-        src = torch.where(skip_mask, skip, _ffn(out, blk, activation))
+        src = torch.where(skip_mask, skip, _ffn(src, blk, activation, F.linear(a, blk.out_w, blk.out_b)))
     return src
 
 
@@ -196,13 +199,13 @@ def row_stage(src: Tensor, real_features: Optional[Tensor], w: RowWeights, rope,
     for blk in w.blocks[:-1]:
         qkv = F.linear(_ln(x, blk.ln1_w, blk.ln1_b, blk.eps, blk.in_w.dtype), blk.in_w, blk.in_b)
         a = _pk.pk_self_attention(qkv, h, kb, rope, scale)
-        x = _ffn(x + F.linear(a, blk.out_w, blk.out_b).to(x.dtype), blk, activation)
+        x = _ffn(x, blk, activation, F.linear(a, blk.out_w, blk.out_b))
     blk = w.blocks[-1]
     hk = _ln(x, blk.ln1_w, blk.ln1_b, blk.eps, blk.in_w.dtype)
     q = F.linear(hk[:, :, :C], blk.in_w[:E], None if blk.in_b is None else blk.in_b[:E])
     kv = F.linear(hk, blk.in_w[E:], None if blk.in_b is None else blk.in_b[E:])
     a = _pk.pk_cross_attention(q, kv, h, kb, rope, scale)
-    cls = _ffn(x[:, :, :C] + F.linear(a, blk.out_w, blk.out_b).to(x.dtype), blk, activation)
+    cls = _ffn(x[:, :, :C].contiguous(), blk, activation, F.linear(a, blk.out_w, blk.out_b))
     cls = _ln(cls, w.out_ln_w, w.out_ln_b, w.eps, cls.dtype)
     return cls.flatten(-2)
 
