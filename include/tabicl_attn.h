@@ -34,7 +34,7 @@ extern "C" {
 #define TABICL_ROPE_NONE 0
 #define TABICL_ROPE_PAIRS 1
 #define TABICL_ROPE_HALVES 2
-/* Flag ORed into TABICL_ROPE_PAIRS / _HALVES for the forward entry points only: cos/sin are [L, E/h]
+/* Flag ORed into TABICL_ROPE_PAIRS / _HALVES (forward and backward entry points): cos/sin are [L, E/h]
  * (one head's columns, used for every head) instead of [L, E]. rope_tables tiles the same columns over
  * the heads, so its [:, :E/h] slice is such a table; reading it instead of the tiled [L, E] one cuts
  * the table traffic by h. No counterpart in the reference (its Pallas kernel reads [L, E] tiles). */

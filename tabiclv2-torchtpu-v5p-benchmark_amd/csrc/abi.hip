@@ -49,10 +49,10 @@ int smallhead_shape(const char* op, int64_t B, int64_t Lq, int64_t Lk, int64_t E
 
 static_assert(TABICL_ROPE_SHARED_TABLES == TA_ROPE_SHARED, "shared-table RoPE flag");
 
-// shared: TABICL_ROPE_SHARED_TABLES is accepted (forward entry points)
-int rope_args(const char* op, int32_t rope, int32_t half, int32_t rot, bool shared) {
+// The rope code: none, or pairs / halves, optionally with TABICL_ROPE_SHARED_TABLES.
+int rope_args(const char* op, int32_t rope, int32_t half, int32_t rot) {
   if (rope == TABICL_ROPE_NONE) return 0;
-  if (shared && (rope & TABICL_ROPE_SHARED_TABLES)) rope &= ~TABICL_ROPE_SHARED_TABLES;
+  rope &= ~TABICL_ROPE_SHARED_TABLES;
   if (rope != TABICL_ROPE_PAIRS && rope != TABICL_ROPE_HALVES)
     return fail(1, "%s: rope code %d not supported", op, rope);
   if (rot < 2 || rot > 16 || (rot & 1) || half * 2 != rot)
@@ -226,7 +226,7 @@ int tabicl_pk_self_fwd(const void* qkv, const float* bias, int64_t bias_b, const
                        void* stream) {
   int st = smallhead_shape("pk_self_fwd", B, L, L, E, h, dtype);
   if (st) return st;
-  if ((st = rope_args("pk_self_fwd", rope, half, rot, true))) return st;
+  if ((st = rope_args("pk_self_fwd", rope, half, rot))) return st;
   if (rope && (!cos_t || !sin_t)) return fail(1, "pk_self_fwd: rope tables missing");
   if (bias && bias_b != 1 && bias_b != B)
     return fail(1, "pk_self_fwd: bias batch %lld must be 1 or B", (long long)bias_b);
@@ -260,7 +260,7 @@ int tabicl_pk_cross_fwd_ragged(const void* q, int64_t q_b, const void* kv, const
                                int32_t dtype, const int32_t* q_len, int64_t q_len_n, void* stream) {
   int st = smallhead_shape("pk_cross_fwd", B, Lq, Lk, E, h, dtype);
   if (st) return st;
-  if ((st = rope_args("pk_cross_fwd", rope, half, rot, true))) return st;
+  if ((st = rope_args("pk_cross_fwd", rope, half, rot))) return st;
   if (rope && (!cq || !sq || !ck || !sk)) return fail(1, "pk_cross_fwd: rope tables missing");
   if (q_b != 1 && q_b != B) return fail(1, "pk_cross_fwd: q batch must be 1 or B");
   if (q_len && q_len_n != 1 && q_len_n != B) return fail(1, "pk_cross_fwd: q_len must hold 1 or B entries");
@@ -308,7 +308,7 @@ int tabicl_pk_self_bwd(const void* qkv, const float* bias, int64_t bias_b, const
                        void* workspace, int64_t workspace_bytes, void* stream) {
   int st = bwd_common("pk_self_bwd", B, L, L, E, h, dtype, bias, bias_b, o, dout, workspace, workspace_bytes);
   if (st) return st;
-  if ((st = rope_args("pk_self_bwd", rope, half, rot, false))) return st;
+  if ((st = rope_args("pk_self_bwd", rope, half, rot))) return st;
   if (rope && (!cos_t || !sin_t)) return fail(1, "pk_self_bwd: rope tables missing");
   if (!aligned16(qkv) || !aligned16(dqkv) || (rope && (!aligned16(cos_t) || !aligned16(sin_t))))
     return fail(1, "pk_self_bwd: pointers must be 16-byte aligned");
@@ -332,7 +332,7 @@ int tabicl_pk_cross_bwd(const void* q, int64_t q_b, const void* kv, const float*
                         void* workspace, int64_t workspace_bytes, void* stream) {
   int st = bwd_common("pk_cross_bwd", B, Lq, Lk, E, h, dtype, bias, bias_b, o, dout, workspace, workspace_bytes);
   if (st) return st;
-  if ((st = rope_args("pk_cross_bwd", rope, half, rot, false))) return st;
+  if ((st = rope_args("pk_cross_bwd", rope, half, rot))) return st;
   if (rope && (!cq || !sq || !ck || !sk)) return fail(1, "pk_cross_bwd: rope tables missing");
   if (q_b != 1 && q_b != B) return fail(1, "pk_cross_bwd: q batch must be 1 or B");
   if (rope && (!aligned16(cq) || !aligned16(sq) || !aligned16(ck) || !aligned16(sk)))

@@ -58,6 +58,9 @@ struct SbParams {
   const float* ck;
   const float* sk;
   int rope, half, rot;
+  // RoPE tables: log2 of the row stride (elements) and the column mask; [L, E] tables: 7 (E = 128) and
+  // E - 1; one head's [L, 16] columns shared by every head (TABICL_ROPE_SHARED_TABLES): 4 and 15
+  int tab_ss, tab_cm;
   float scale;
   int B, Lq, Lk;
   int qbpw;  // query blocks per dq workgroup
@@ -83,14 +86,21 @@ __device__ __forceinline__ float sb_b2(const SbParams& p, int b, int key) {
   return p.bias ? fmaxf(p.bias[b * p.bias_sb + key] * TA_LOG2E, SB_BIAS_FLOOR) : 0.f;
 }
 
-// Dims d0..d0+3 of q' (rope, scale, cast) or of k' (rope, cast; scale = 1) of one row.
-template <typename T>
+// Head g's first column in row `row` of a RoPE table (either table form).
+__device__ __forceinline__ const float* sb_tab_row(const float* t, int64_t row, int g, const SbParams& p) {
+  return t + (row << p.tab_ss) + ((g * SB_D) & p.tab_cm);
+}
+
+// Dims d0..d0+3 of q' (rope, scale, cast) or of k' (rope, cast; scale = 1) of one row; cs / sn: the
+// row's table row at the first column of d0's head (sb_tab_row). RP: the call has a RoPE form
+// (p.rope != 0); the sb kernels are compiled with and without it.
+template <typename T, bool RP>
 __device__ __forceinline__ typename OpVec<T, 4>::type sb_prep4(const T* row, const float* cs, const float* sn,
                                                               int d0, const SbParams& p, float scale) {
   typedef typename OpVec<T, 4>::type Op4;
   Op4 r;
-  if (p.rope) {
-    const f32x4 y = rope4<T>(row, cs, sn, d0, p.rope, p.half, p.rot, d0);
+  if constexpr (RP) {
+    const f32x4 y = rope4<T>(row, cs, sn, d0, p.rope, p.half, p.rot, d0 & (SB_D - 1));
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = from_f32<T>(y[j] * scale);
   } else {
@@ -102,11 +112,12 @@ __device__ __forceinline__ typename OpVec<T, 4>::type sb_prep4(const T* row, con
 }
 
 // rope_bwd of one 16-dim head row held as 4 dims per lane (lane (l16, kap): dims 4 kap .. 4 kap + 3
-// of row l16), exchanged through this wave's LDS scratch [16][17]; cs / sn at the row's position
-// (dims of head g), or null rows for no RoPE.
+// of row l16), exchanged through this wave's LDS scratch [16][17]; cs / sn at the row's position,
+// head g's first column of the table row (sb_tab_row), or null rows for no RoPE.
+template <bool RP>
 __device__ __forceinline__ f32x4 sb_rope_bwd(f32x4 y, float* scr, int l16, int kap, const float* cs,
-                                            const float* sn, int g, const SbParams& p) {
-  if (!p.rope) return y;
+                                            const float* sn, const SbParams& p) {
+  if constexpr (!RP) return y;
 #pragma unroll
   for (int r = 0; r < 4; ++r) scr[l16 * 17 + 4 * kap + r] = y[r];
   __builtin_amdgcn_wave_barrier();
@@ -118,7 +129,7 @@ __device__ __forceinline__ f32x4 sb_rope_bwd(f32x4 y, float* scr, int l16, int k
     float sg;
     rope_partner(jd, p.rope, p.half, p.rot, &pt, &sg);
     const float yp = scr[l16 * 17 + pt];
-    out[r] = y[r] * cs[g * SB_D + jd] - sg * yp * sn[g * SB_D + pt];
+    out[r] = y[r] * cs[jd] - sg * yp * sn[pt];
   }
   __builtin_amdgcn_wave_barrier();
   return out;
@@ -144,7 +155,7 @@ __device__ __forceinline__ typename OpVec<T, 4>::type sb_opT(const T* rows, cons
 // ---------------------------------------------------------------------------------------------
 // dq (and the per-query softmax statistics and D)
 // ---------------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool RP>
 __device__ __forceinline__ void sb_fill_keys(const SbParams& p, T* lk, T* lkt, T* lv, float* lb2, int b, int g,
                                              int k0) {
   typedef SbTile<T> L;
@@ -159,7 +170,7 @@ __device__ __forceinline__ void sb_fill_keys(const SbParams& p, T* lk, T* lkt, T
 #pragma unroll
     for (int j = 0; j < 4; ++j) { kk[j] = from_f32<T>(0.f); vv[j] = from_f32<T>(0.f); }
     if (key < p.Lk) {
-      kk = sb_prep4<T>(kbase + (int64_t)key * p.k_sr, p.ck + (int64_t)key * SB_E, p.sk + (int64_t)key * SB_E,
+      kk = sb_prep4<T, RP>(kbase + (int64_t)key * p.k_sr, sb_tab_row(p.ck, key, g, p), sb_tab_row(p.sk, key, g, p),
                        g * SB_D + d4, p, 1.f);
       vv = *(const Op4*)(vbase + (int64_t)key * p.v_sr + g * SB_D + d4);
     }
@@ -214,7 +225,7 @@ __device__ __forceinline__ void sb_dq_tile(const T* lk, const T* lkt, const T* l
 }
 
 // ONE_TILE: all keys fit one tile (Lk <= SB_KT).
-template <typename T, bool ONE_TILE>
+template <typename T, bool ONE_TILE, bool RP>
 __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
   typedef SbTile<T> L;
   typedef typename OpVec<T, 4>::type Op4;
@@ -234,7 +245,7 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
   const int d0 = g * SB_D + 4 * kap;
   const int ntiles = (p.Lk + SB_KT - 1) / SB_KT;
   if (ONE_TILE) {  // fill once for every query block of the run
-    sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, 0);
+    sb_fill_keys<T, RP>(p, lk, lkt, lv, lb2, b, g, 0);
     __syncthreads();
   }
 
@@ -250,8 +261,8 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
     for (int j = 0; j < 4; ++j) { qop[j] = from_f32<T>(0.f); dop[j] = from_f32<T>(0.f); }
     float dsum = 0.f;
     if (qok) {
-      qop = sb_prep4<T>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SB_E,
-                        p.sq + (int64_t)qi * SB_E, d0, p, p.scale);
+      qop = sb_prep4<T, RP>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, sb_tab_row(p.cq, qi, g, p),
+                            sb_tab_row(p.sq, qi, g, p), d0, p, p.scale);
       const int64_t orow = ((int64_t)b * p.Lq + qi) * SB_E + d0;
       dop = *(const Op4*)((const T*)p.dout + orow);
       const Op4 ov = *(const Op4*)((const T*)p.o + orow);
@@ -285,7 +296,7 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
       float m = TA_NEG_INF, l = 0.f;
       for (int t = 0; t < ntiles; ++t) {
         __syncthreads();
-        sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
+        sb_fill_keys<T, RP>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
         __syncthreads();
         f32x4 x[NKT];
         sb_scores<T>(lk, lb2, qop, l16, kap, x);
@@ -310,7 +321,7 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
       // sweep 2: dq'
       for (int t = 0; t < ntiles; ++t) {
         __syncthreads();
-        sb_fill_keys<T>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
+        sb_fill_keys<T, RP>(p, lk, lkt, lv, lb2, b, g, t * SB_KT);
         __syncthreads();
         f32x4 x[NKT];
         sb_scores<T>(lk, lb2, qop, l16, kap, x);
@@ -329,7 +340,7 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
     const int qc = qok ? qi : 0;
-    y = sb_rope_bwd(y, scr[wave], l16, kap, p.cq + (int64_t)qc * SB_E, p.sq + (int64_t)qc * SB_E, g, p);
+    y = sb_rope_bwd<RP>(y, scr[wave], l16, kap, sb_tab_row(p.cq, qc, g, p), sb_tab_row(p.sq, qc, g, p), p);
     if (qok) {
       Op4 out;
 #pragma unroll
@@ -342,7 +353,7 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
 // ---------------------------------------------------------------------------------------------
 // dk, dv
 // ---------------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool RP>
 __device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt, T* ld, T* ldt, float* lmx,
                                                 float* lll, float* ldd, int b, int g, int q0) {
   typedef SbTile<T> L;
@@ -354,8 +365,8 @@ __device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt
 #pragma unroll
     for (int j = 0; j < 4; ++j) { qq[j] = from_f32<T>(0.f); dd[j] = from_f32<T>(0.f); }
     if (qi < p.Lq) {
-      qq = sb_prep4<T>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, p.cq + (int64_t)qi * SB_E,
-                       p.sq + (int64_t)qi * SB_E, g * SB_D + d4, p, p.scale);
+      qq = sb_prep4<T, RP>((const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_sr, sb_tab_row(p.cq, qi, g, p),
+                           sb_tab_row(p.sq, qi, g, p), g * SB_D + d4, p, p.scale);
       dd = *(const Op4*)((const T*)p.dout + ((int64_t)b * p.Lq + qi) * SB_E + g * SB_D + d4);
     }
     *(Op4*)(lq + row * L::RSTR + d4) = qq;
@@ -378,7 +389,7 @@ __device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt
   }
 }
 
-template <typename T>
+template <typename T, bool RP>
 __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
   typedef SbTile<T> L;
   typedef typename OpVec<T, 4>::type Op4;
@@ -405,8 +416,8 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) { kop[j] = from_f32<T>(0.f); vop[j] = from_f32<T>(0.f); }
   if (kok) {
-    kop = sb_prep4<T>((const T*)p.k + b * p.k_sb + (int64_t)kj * p.k_sr, p.ck + (int64_t)kj * SB_E,
-                      p.sk + (int64_t)kj * SB_E, d0, p, 1.f);
+    kop = sb_prep4<T, RP>((const T*)p.k + b * p.k_sb + (int64_t)kj * p.k_sr, sb_tab_row(p.ck, kj, g, p),
+                          sb_tab_row(p.sk, kj, g, p), d0, p, 1.f);
     vop = *(const Op4*)((const T*)p.v + b * p.v_sb + (int64_t)kj * p.v_sr + d0);
   }
   const float b2 = sb_b2(p, b, kj);
@@ -415,7 +426,7 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
   const int ntiles = (p.Lq + SB_QT - 1) / SB_QT;
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
-    sb_fill_queries<T>(p, lq, lqt, ld, ldt, lmx, lll, ldd, b, g, t * SB_QT);
+    sb_fill_queries<T, RP>(p, lq, lqt, ld, ldt, lmx, lll, ldd, b, g, t * SB_QT);
     __syncthreads();
 #pragma unroll 2
     for (int qs = 0; qs < SB_QT / 16; ++qs) {
@@ -440,7 +451,7 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
   }
 
   const int kc = kok ? kj : 0;
-  const f32x4 y = sb_rope_bwd(dk, scr[wave], l16, kap, p.ck + (int64_t)kc * SB_E, p.sk + (int64_t)kc * SB_E, g, p);
+  const f32x4 y = sb_rope_bwd<RP>(dk, scr[wave], l16, kap, sb_tab_row(p.ck, kc, g, p), sb_tab_row(p.sk, kc, g, p), p);
   if (kok) {
     Op4 ok, ov;
 #pragma unroll
@@ -475,9 +486,19 @@ struct SsLds {
   bf16 d[SS_ROWS * SS_STR];  // dO
   float mx[SS_HG][SS_ROWS];  // per head and query: row maximum (log2 units), +inf past Lq
   float lg[SS_HG][SS_ROWS];  // log2 of the row sum (with a key bias; else mx holds -(m + lg), -inf past Lq)
-  float dd[SS_HG][SS_ROWS];  // D
+  float nd[SS_HG][SS_ROWS];  // -D: the accumulator input of the dP products, which then give dP - D
   float b2[SS_ROWS];         // per key: additive term, log2 units, -inf past Lk
 };
+
+// 16x16 tile with a 32-deep contraction over two 16-deep halves: A = [a0 | a1], B = [b0 | b1], i.e. the
+// sum of the two 16x16x16 products a0 b0 + a1 b1 in one v_mfma_f32_16x16x32_bf16 (k-slot 8 kap + j of
+// lane (l16, kap) holds slot 4 kap + j of the first half for j < 4 and of the second half for j >= 4,
+// in A and B alike). On gfx950 it issues in the cycles of one 16x16x16 product.
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x4 a0, bf16x4 a1, bf16x4 b0, bf16x4 b1, f32x4 c) {
+  const bf16x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  const bf16x8 b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
 // RoPE of a 4-dim chunk (chunk index c4 = (dim within the head) / 4) in the fill: pairs in-lane,
 // halves from the partner chunk c4 ^ 2, held by lane ^ 2.
@@ -586,10 +607,11 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
         kx[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(krs, (rk * (int)p.k_sr + dg) * 2, 0, 0));
         vx[u] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(vrs, (rk * (int)p.v_sr + dg) * 2, 0, 0));
         if constexpr (RM != 0) {
-          qc[u] = *(const float4*)(p.cq + rq * SB_E + dg);
-          qs[u] = *(const float4*)(p.sq + rq * SB_E + dg);
-          kc[u] = *(const float4*)(p.ck + rk * SB_E + dg);
-          ks[u] = *(const float4*)(p.sk + rk * SB_E + dg);
+          const int tc = dg & p.tab_cm;
+          qc[u] = *(const float4*)(p.cq + (rq << p.tab_ss) + tc);
+          qs[u] = *(const float4*)(p.sq + (rq << p.tab_ss) + tc);
+          kc[u] = *(const float4*)(p.ck + (rk << p.tab_ss) + tc);
+          ks[u] = *(const float4*)(p.sk + (rk << p.tab_ss) + tc);
         }
       }
 #pragma unroll
@@ -603,7 +625,7 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
         part += __shfl_xor(part, 2, 64);
         *(bf16x4*)(sh.q + row * SS_STR + dl) = cvt_bf16x4(yq * p.scale);
         *(bf16x4*)(sh.d + row * SS_STR + dl) = dx[u];
-        if ((c & 3) == 0) sh.dd[c >> 2][row] = part;
+        if ((c & 3) == 0) sh.nd[c >> 2][row] = -part;
         if constexpr (RM != 0)
           *(bf16x4*)(sh.k + row * SS_STR + dl) = cvt_bf16x4(ss_rope_fwd<RM>(kx[u], kc[u], ks[u], c & 3));
         else
@@ -622,11 +644,13 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
 
   // ---- phase 1: per query block, statistics, dq. Without a key bias the scores are reduced raw
   // (b2 only masks the padded keys of the last block) and the log2e factor goes into the exponent's fma.
+  // dq' = (1 / l) sum_k e_k (dP_k - D) k' with e = exp2(x - m): the products take e (dP - D), rounded
+  // to bf16 as dS is, and 1 / l scales their sum (one multiply per query instead of one per score).
   for (int qb = par; qb < nqb; qb += 2) {
     const int qr = 16 * qb + l16;
     const bf16x4 qop = ss_row4(sh.q, qr, hd + 4 * kap);
     const bf16x4 dop = ss_row4(sh.d, qr, hd + 4 * kap);
-    const float dsum = sh.dd[gl][qr];
+    const float nds = sh.nd[gl][qr];
     f32x4 x[8];
     float tm = TA_NEG_INF;
 #pragma unroll
@@ -657,16 +681,26 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
     }
     l = quad_sum(l);  // >= 1
     const float inv = __builtin_amdgcn_rcpf(l);
-    const float dinv = dsum * inv;
+    const f32x4 cnd = {nds, nds, nds, nds};
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // key tiles in pairs: one 32-deep product per pair (a lone last tile: a 16-deep one)
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
+    for (int kt = 0; kt < 8; kt += 2) {
       if (kt < nkb) {
-        const f32x4 dp = mfma16x16x16(ss_row4(sh.v, 16 * kt + l16, hd + 4 * kap), dop, f32x4{0.f, 0.f, 0.f, 0.f});
-        f32x4 dsf;
+        const f32x4 dp0 = mfma16x16x16(ss_row4(sh.v, 16 * kt + l16, hd + 4 * kap), dop, cnd);  // dP - D
+        f32x4 e0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dsf[r] = x[kt][r] * fmaf(dp[r], inv, -dinv);  // P (dP - D)
-        acc = mfma16x16x16(ss_opT(sh.k, 16 * kt, hd, l16, kap), cvt_bf16x4(dsf), acc);
+        for (int r = 0; r < 4; ++r) e0[r] = x[kt][r] * dp0[r];
+        if (kt + 1 < nkb) {
+          const f32x4 dp1 = mfma16x16x16(ss_row4(sh.v, 16 * kt + 16 + l16, hd + 4 * kap), dop, cnd);
+          f32x4 e1;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) e1[r] = x[kt + 1][r] * dp1[r];
+          acc = mfma16x16x32(ss_opT(sh.k, 16 * kt, hd, l16, kap), ss_opT(sh.k, 16 * kt + 16, hd, l16, kap),
+                             cvt_bf16x4(e0), cvt_bf16x4(e1), acc);
+        } else {
+          acc = mfma16x16x16(ss_opT(sh.k, 16 * kt, hd, l16, kap), cvt_bf16x4(e0), acc);
+        }
       }
     }
     const float lg = __builtin_amdgcn_logf(l);
@@ -679,10 +713,12 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
       }
     }
     f32x4 y;
+    const float ysc = p.scale * inv;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
+    for (int r = 0; r < 4; ++r) y[r] = acc[r] * ysc;
     const int qc = qr < p.Lq ? qr : 0;
-    y = ss_rope_bwd<RM>(y, p.cq + (int64_t)qc * SB_E + hg * SS_W + hd, p.sq + (int64_t)qc * SB_E + hg * SS_W + hd,
+    y = ss_rope_bwd<RM>(y, p.cq + ((int64_t)qc << p.tab_ss) + ((hg * SS_W + hd) & p.tab_cm),
+                        p.sq + ((int64_t)qc << p.tab_ss) + ((hg * SS_W + hd) & p.tab_cm),
                         kap);
     if (qr < p.Lq) *(bf16x4*)((bf16*)p.dq + b * p.dq_sb + (int64_t)qr * p.dq_sr + dglob) = cvt_bf16x4(y);
   }
@@ -690,18 +726,20 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
 
   // ---- phase 2: per key block, dk and dv over every query block. P = exp2(s log2e + b2 - m - lg);
   // without a key bias one fma against -(m + lg) (padded keys: not stored, their P is not used).
+  // The query blocks go in pairs, each pair's dv and dk in one 32-deep product (a lone last block: a
+  // 16-deep one); the loop is unrolled over the at most 8 blocks, so the LDS offsets are constants.
   for (int kb = par; kb < nkb; kb += 2) {
     const int kr = 16 * kb + l16;
     const bf16x4 kop = ss_row4(sh.k, kr, hd + 4 * kap);
     const bf16x4 vop = ss_row4(sh.v, kr, hd + 4 * kap);
     const float b2 = HB ? sh.b2[kr] : 0.f;
-    f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
-    for (int qs = 0; qs < nqb; ++qs) {
-      // S[query 16 qs + 4 kap + r][key kr], dP likewise
+    // bf16 P and dS of query block qs against this key block: S[query 16 qs + 4 kap + r][key kr],
+    // dP - D likewise (the accumulator input is -D of those queries)
+    auto pds = [&](int qs, bf16x4& pb, bf16x4& db) {
       const f32x4 s = mfma16x16x16(ss_row4(sh.q, 16 * qs + l16, hd + 4 * kap), kop, f32x4{0.f, 0.f, 0.f, 0.f});
-      const f32x4 dp = mfma16x16x16(ss_row4(sh.d, 16 * qs + l16, hd + 4 * kap), vop, f32x4{0.f, 0.f, 0.f, 0.f});
+      const f32x4 dp = mfma16x16x16(ss_row4(sh.d, 16 * qs + l16, hd + 4 * kap), vop,
+                                    *(const f32x4*)(&sh.nd[gl][16 * qs + 4 * kap]));
       const f32x4 ms = *(const f32x4*)(&sh.mx[gl][16 * qs + 4 * kap]);
-      const f32x4 dq = *(const f32x4*)(&sh.dd[gl][16 * qs + 4 * kap]);
       f32x4 pr, dsf;
       if constexpr (HB) {
         const f32x4 ls = *(const f32x4*)(&sh.lg[gl][16 * qs + 4 * kap]);
@@ -712,13 +750,30 @@ __global__ __launch_bounds__(SS_NT, 4) void ss_bwd_kernel(SbParams p) {
         for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(fmaf(s[r], TA_LOG2E, ms[r]));
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dsf[r] = pr[r] * (dp[r] - dq[r]);
-      dv = mfma16x16x16(ss_opT(sh.d, 16 * qs, hd, l16, kap), cvt_bf16x4(pr), dv);
-      dk = mfma16x16x16(ss_opT(sh.q, 16 * qs, hd, l16, kap), cvt_bf16x4(dsf), dk);
+      for (int r = 0; r < 4; ++r) dsf[r] = pr[r] * dp[r];
+      pb = cvt_bf16x4(pr);
+      db = cvt_bf16x4(dsf);
+    };
+    f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int qs = 0; qs < 8; qs += 2) {
+      if (qs < nqb) {
+        bf16x4 pa, da;
+        pds(qs, pa, da);
+        if (qs + 1 < nqb) {
+          bf16x4 pb, db;
+          pds(qs + 1, pb, db);
+          dv = mfma16x16x32(ss_opT(sh.d, 16 * qs, hd, l16, kap), ss_opT(sh.d, 16 * qs + 16, hd, l16, kap), pa, pb, dv);
+          dk = mfma16x16x32(ss_opT(sh.q, 16 * qs, hd, l16, kap), ss_opT(sh.q, 16 * qs + 16, hd, l16, kap), da, db, dk);
+        } else {
+          dv = mfma16x16x16(ss_opT(sh.d, 16 * qs, hd, l16, kap), pa, dv);
+          dk = mfma16x16x16(ss_opT(sh.q, 16 * qs, hd, l16, kap), da, dk);
+        }
+      }
     }
     const int kc = kr < p.Lk ? kr : 0;
-    const f32x4 y = ss_rope_bwd<RM>(dk, p.ck + (int64_t)kc * SB_E + hg * SS_W + hd,
-                                    p.sk + (int64_t)kc * SB_E + hg * SS_W + hd, kap);
+    const f32x4 y = ss_rope_bwd<RM>(dk, p.ck + ((int64_t)kc << p.tab_ss) + ((hg * SS_W + hd) & p.tab_cm),
+                                    p.sk + ((int64_t)kc << p.tab_ss) + ((hg * SS_W + hd) & p.tab_cm), kap);
     if (kr < p.Lk) {
       *(bf16x4*)((bf16*)p.dk + b * p.dk_sb + (int64_t)kr * p.dk_sr + dglob) = cvt_bf16x4(y);
       *(bf16x4*)((bf16*)p.dv + b * p.dv_sb + (int64_t)kr * p.dv_sr + dglob) = cvt_bf16x4(dv);
@@ -732,6 +787,16 @@ int ss_mode(const SbParams& p) {
   if (p.rope == 1 && p.rot == 16) return 1;
   if (p.rope == 2 && p.half == 8 && p.rot == 16) return 2;
   return -1;
+}
+
+template <typename T, bool RP>
+void launch_sb(const SbParams& p, int64_t nwg_q, int64_t nkb, hipStream_t stream) {
+  const dim3 block(SB_NW * 64);
+  if (nwg_q > 0 && p.Lk <= SB_KT)
+    hipLaunchKernelGGL((sb_dq_kernel<T, true, RP>), dim3((unsigned)(p.B * nwg_q * SB_H)), block, 0, stream, p);
+  else if (nwg_q > 0)
+    hipLaunchKernelGGL((sb_dq_kernel<T, false, RP>), dim3((unsigned)(p.B * nwg_q * SB_H)), block, 0, stream, p);
+  hipLaunchKernelGGL((sb_dkdv_kernel<T, RP>), dim3((unsigned)(p.B * nkb * SB_H)), block, 0, stream, p);
 }
 
 template <typename T>
@@ -770,11 +835,10 @@ void launch_bwd(SbParams p, hipStream_t stream) {
   p.qbpw = (int)qbpw;
   const int64_t nwg_q = nqb > 0 ? (nqb + qbpw - 1) / qbpw : 0;
   // no query (Lq = 0): only the dk/dv kernel runs, and writes zeros
-  if (nwg_q > 0 && p.Lk <= SB_KT)
-    hipLaunchKernelGGL((sb_dq_kernel<T, true>), dim3((unsigned)(p.B * nwg_q * SB_H)), dim3(SB_NW * 64), 0, stream, p);
-  else if (nwg_q > 0)
-    hipLaunchKernelGGL((sb_dq_kernel<T, false>), dim3((unsigned)(p.B * nwg_q * SB_H)), dim3(SB_NW * 64), 0, stream, p);
-  hipLaunchKernelGGL((sb_dkdv_kernel<T>), dim3((unsigned)(p.B * nkb * SB_H)), dim3(SB_NW * 64), 0, stream, p);
+  if (p.rope)
+    launch_sb<T, true>(p, nwg_q, nkb, stream);
+  else
+    launch_sb<T, false>(p, nwg_q, nkb, stream);
 }
 
 }  // namespace
@@ -803,7 +867,11 @@ int tabicl_launch_smallhead_bwd(const void* q, int64_t q_sb, int64_t q_sr, const
   p.dv = dv; p.dv_sb = dv_sb; p.dv_sr = dv_sr;
   p.bias = bias; p.bias_sb = bias_sb;
   p.cq = cq; p.sq = sq; p.ck = ck; p.sk = sk;
-  p.rope = rope; p.half = half; p.rot = rot;
+  const bool shared = (rope & TA_ROPE_SHARED) != 0;
+  p.rope = rope & ~TA_ROPE_SHARED; p.half = half; p.rot = rot;
+  p.tab_ss = shared ? 4 : 7;
+  static_assert(SB_D == 16 && SB_E == 128, "table row strides as shifts");
+  p.tab_cm = shared ? SB_D - 1 : SB_E - 1;
   p.scale = scale;
   p.B = (int)B; p.Lq = (int)Lq; p.Lk = (int)Lk;
   const int64_t part = tabicl_launch_smallhead_bwd_ws_bytes(B, Lq) / 3;

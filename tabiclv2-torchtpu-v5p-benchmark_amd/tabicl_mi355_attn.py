@@ -547,7 +547,7 @@ def pk_self_attention(qkv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,
     L, E3 = qkv.shape[-2], qkv.shape[-1]
     E = E3 // 3
     lkp = -(-L // 128) * 128
-    cos, sin, rc, half, rot = _tables(rope_mod, L, E, h, qkv.device, not _needs_grad(qkv, key_bias))
+    cos, sin, rc, half, rot = _tables(rope_mod, L, E, h, qkv.device)
     prec = _fp32_prec_code() if qkv.dtype == torch.float32 else 0
     out = PK_SELF(_flat(qkv, L, E3).contiguous(), _bias_arg(key_bias, lead, L, qkv.device), cos, sin, h, lkp, rc,
                   half, rot, prec, float(scale))
@@ -557,14 +557,10 @@ def pk_self_attention(qkv: Tensor, h: int, key_bias: Optional[Tensor], rope_mod,
 ROPE_SHARED_TABLES = 0x10  # TABICL_ROPE_SHARED_TABLES of include/tabicl_attn.h
 
 
-def _needs_grad(*ts) -> bool:
-    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
-
-
 def _shared_tables(cos: Tensor, sin: Tensor, rc: int, d: int):
-    """Forward-only form of rope_tables' output: its columns repeat every head (d columns), so one
-    head's [L, d] slice serves all heads and the kernels read h times fewer table bytes. The backward
-    kernels take the [L, E] tables, so this is used only when no gradient is needed."""
+    """Shared-head form of rope_tables' output: its columns repeat every head (d columns), so one
+    head's [L, d] slice serves all heads and the kernels read h times fewer table bytes (forward and
+    backward kernels alike)."""
     return cos[:, :d].contiguous(), sin[:, :d].contiguous(), rc | ROPE_SHARED_TABLES
 
 
@@ -582,8 +578,8 @@ def _freqs_stamp(rope_mod) -> tuple:  # noqa: ANN001
     return (f.data_ptr(), f._version, tuple(f.shape), f.dtype, getattr(rope_mod, "interpolate_factor", None))
 
 
-def _tables(rope_mod, L: int, E: int, h: int, device, shared: bool):  # noqa: ANN001
-    """rope_tables(...) (shared=False) or its shared-head form (shared=True), cached per rope module."""
+def _tables(rope_mod, L: int, E: int, h: int, device):  # noqa: ANN001
+    """The shared-head form of rope_tables(...), cached per rope module."""
     if rope_mod is None:
         # rope code 0: the kernels never read the tables, so one cached row stands in for [L, E]
         key = (E, str(device))
@@ -595,12 +591,12 @@ def _tables(rope_mod, L: int, E: int, h: int, device, shared: bool):  # noqa: AN
         per_mod = _TABLES.setdefault(rope_mod, {})
     except TypeError:  # not weak-referenceable: no cache
         per_mod = None
-    key = (L, E, h, str(device), bool(shared), bool(rope_mod.interleaved), _freqs_stamp(rope_mod))
+    key = (L, E, h, str(device), bool(rope_mod.interleaved), _freqs_stamp(rope_mod))
     hit = None if per_mod is None else per_mod.get(key)
     if hit is not None:
         return hit
     cos, sin, rc, half, rot = rope_tables(rope_mod, L, E, h, device)
-    if rc and shared:
+    if rc:
         cos, sin, rc = _shared_tables(cos, sin, rc, E // h)
     out = (cos, sin, rc, half, rot)
     if per_mod is not None and not cos.requires_grad:  # learned frequencies under autograd: not cached
@@ -623,9 +619,8 @@ def pk_cross_attention(q: Tensor, kv: Tensor, h: int, key_bias: Optional[Tensor]
     Lk = kv.shape[-2]
     lkp = -(-Lk // 128) * 128
     bq = _pick_bq(Lq, lkp)
-    shared = q_len is not None or not _needs_grad(q, kv, key_bias)
-    cq, sq, rc, half, rot = _tables(rope_mod, Lq, E, h, q.device, shared)
-    ck, sk, _, _, _ = _tables(rope_mod, Lk, E, h, q.device, shared)
+    cq, sq, rc, half, rot = _tables(rope_mod, Lq, E, h, q.device)
+    ck, sk, _, _, _ = _tables(rope_mod, Lk, E, h, q.device)
     prec = _fp32_prec_code() if q.dtype == torch.float32 else 0
     q3 = _flat(q, Lq, E)
     kv3 = _flat(kv, Lk, 2 * E)

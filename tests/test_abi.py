@@ -56,10 +56,12 @@ def test_bad_arguments_rejected_before_launch():
     assert st == 1 and "rope" in nat.last_error()
     st = lib.tabicl_icl_cache_append(None, None, 64, 64, 10, 12, None, None, 64, 64, 64, 1, 1, 5, 64, 0, None)
     assert st == 1 and "capacity" in nat.last_error()
-    # shared-table RoPE flag: forward entry points only
+    # rope codes other than none / pairs / halves (with or without the shared-table flag) are refused by
+    # the backward entry points too
     a = 0x1000  # 16-byte aligned placeholder address: the rope code is refused before any use
-    st = lib.tabicl_pk_self_bwd(a, None, 1, a, a, a, a, a, 1, 8, 128, 8, 2 | 0x10, 8, 16, 0.25, 0, a, 1 << 20, None)
-    assert st == 1 and "rope code" in nat.last_error()
+    for code in (3, 3 | 0x10, 0x20 | 2):
+        st = lib.tabicl_pk_self_bwd(a, None, 1, a, a, a, a, a, 1, 8, 128, 8, code, 8, 16, 0.25, 0, a, 1 << 20, None)
+        assert st == 1 and "rope code" in nat.last_error()
     # ragged entry points: a q_len array of neither 1 nor N (B) entries is refused before any launch
     qlen = ctypes.c_int32(3)
     st = lib.tabicl_icl_fwd_ragged(None, None, None, None, 0, ctypes.byref(qlen), 2, None, 3, 1, 1, 1, 64,
@@ -130,17 +132,19 @@ def test_rope_tables_cached_per_module():
     rope.freqs = torch.nn.Parameter(torch.tensor(O.textbook_freqs(16, 10000.0), dtype=torch.float32),
                                     requires_grad=False)
     rope.get_seq_pos = lambda L, device=None, dtype=torch.float32: torch.arange(L, device=device, dtype=dtype)
-    a = pk._tables(rope, 104, 128, 8, "cpu", True)
-    b = pk._tables(rope, 104, 128, 8, "cpu", True)
+    a = pk._tables(rope, 104, 128, 8, "cpu")
+    b = pk._tables(rope, 104, 128, 8, "cpu")
     assert a[0] is b[0] and a[2] == 2 | pk.ROPE_SHARED_TABLES and tuple(a[0].shape) == (104, 16)
-    full = pk._tables(rope, 104, 128, 8, "cpu", False)
+    full = pk.rope_tables(rope, 104, 128, 8, "cpu")
     assert tuple(full[0].shape) == (104, 128) and full[2] == 2
-    np.testing.assert_allclose(a[0].numpy(), full[0][:, :16].numpy())
+    for hd in range(8):  # the shared table is every head's columns of the full one
+        np.testing.assert_array_equal(a[0].numpy(), full[0][:, 16 * hd:16 * hd + 16].numpy())
+        np.testing.assert_array_equal(a[1].numpy(), full[1][:, 16 * hd:16 * hd + 16].numpy())
     with torch.no_grad():
         rope.freqs.mul_(2.0)  # in-place change of the frequencies: the cached tables are not reused
-    c = pk._tables(rope, 104, 128, 8, "cpu", True)
+    c = pk._tables(rope, 104, 128, 8, "cpu")
     assert c[0] is not a[0] and not torch.allclose(c[1], a[1])
-    n1, n2 = pk._tables(None, 50, 128, 8, "cpu", True), pk._tables(None, 70, 128, 8, "cpu", False)
+    n1, n2 = pk._tables(None, 50, 128, 8, "cpu"), pk._tables(None, 70, 128, 8, "cpu")
     assert n1[2] == 0 and n1[0] is n2[0]  # no RoPE: one stand-in row, never read by the kernels
 
 

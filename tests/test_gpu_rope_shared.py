@@ -2,8 +2,10 @@
 head's [L, 16] columns of rope_tables' output must return exactly (bit for bit) what they return for
 the tiled [L, 128] tables, for every forward kernel that reads tables: the resident bf16 kernel (row
 stage, 104 tokens; CLS cross attention), the general bf16 kernel (keys past the resident limit, and a
-partial-rotary form) and the fp32 kernel. The tiled-table results are checked against the oracle by
-test_gpu_smallhead.py; the wrappers use the shared form whenever no gradient is needed.
+partial-rotary form) and the fp32 kernel; and the backward kernels likewise (the fused short kernel,
+the tiled dq / dk-dv pair, partial rotary, fp32). The tiled-table results are checked against the
+oracle by test_gpu_smallhead.py and test_gpu_smallhead_bwd.py; the wrappers always pass the shared
+form (the gradient tests run through it).
 """
 import pytest
 import torch
@@ -121,3 +123,51 @@ def test_pk_cross_ragged_with_rope(dev, name, B, Lq, Lk, dtype, q_len):
     exp = O.pk_cross_ref(q[:1].cpu(), kv[:1].cpu(), 8, None, rq, rk, 0.25)
     err = float(np.abs(ref[:1].double().cpu().numpy() - exp).max())
     assert err <= (2e-2 if dtype == torch.bfloat16 else 1e-4), (name, err)
+
+
+@pytest.mark.parametrize("name,B,L,dtype,interleaved,rot", [
+    ("fused_short_halves", 16, 104, torch.bfloat16, False, 16),
+    ("fused_short_pairs", 8, 104, torch.bfloat16, True, 16),
+    ("tiled_long_bf16", 2, 300, torch.bfloat16, False, 16),
+    ("partial_rotary_bf16", 4, 104, torch.bfloat16, False, 8),
+    ("fp32", 4, 104, torch.float32, False, 16),
+])
+def test_pk_self_bwd_shared_tables(dev, name, B, L, dtype, interleaved, rot):
+    import tabicl_mi355_attn as pk
+    g = torch.Generator().manual_seed(25)
+    qkv = torch.randn(B, L, 384, generator=g).to(dtype).to(dev)
+    do = torch.randn(B, L, 128, generator=g).to(dtype).to(dev)
+    bias = torch.zeros(B, 1, L, device=dev)
+    bias[:, :, L - 3:] = -1e30
+    rope = _Rope(interleaved, rot)
+    cos, sin, rc, half, r = pk.rope_tables(rope, L, 128, 8, dev)
+    lkp = -(-L // 128) * 128
+    o = pk.PK_SELF(qkv, bias, cos, sin, 8, lkp, rc, half, r, 0, 0.25)
+    full = pk.PK_SELF_BWD(qkv, bias, cos, sin, o, do, 8, lkp, rc, half, r, 0, 0.25)
+    cs, sn, rcs = pk._shared_tables(cos, sin, rc, 16)
+    shared = pk.PK_SELF_BWD(qkv, bias, cs, sn, o, do, 8, lkp, rcs, half, r, 0, 0.25)
+    torch.cuda.synchronize()
+    assert torch.isfinite(full.float()).all() and torch.equal(full, shared), name
+
+
+@pytest.mark.parametrize("name,B,Lq,Lk", [("cls_fused_short", 64, 4, 104), ("tiled", 4, 200, 300)])
+def test_pk_cross_bwd_shared_tables(dev, name, B, Lq, Lk):
+    import tabicl_mi355_attn as pk
+    g = torch.Generator().manual_seed(26)
+    q = (torch.randn(B, Lq, 128, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    kv = torch.randn(B, Lk, 256, generator=g).to(torch.bfloat16).to(dev)
+    do = torch.randn(B, Lq, 128, generator=g).to(torch.bfloat16).to(dev)
+    rope = _Rope(False)
+    cq, sq, rc, half, r = pk.rope_tables(rope, Lq, 128, 8, dev)
+    ck, sk, _, _, _ = pk.rope_tables(rope, Lk, 128, 8, dev)
+    none = torch.empty(0, device=dev)
+    lkp = -(-Lk // 128) * 128
+    bq = pk._pick_bq(Lq, lkp)
+    o = pk.PK_CROSS(q, kv, none, cq, sq, ck, sk, 8, lkp, bq, rc, half, r, 0, 0.25)
+    full = pk.PK_CROSS_BWD(q, kv, none, cq, sq, ck, sk, o, do, 8, lkp, bq, rc, half, r, 0, 0.25)
+    cqs, sqs, _ = pk._shared_tables(cq, sq, rc, 16)
+    cks, sks, rcs = pk._shared_tables(ck, sk, rc, 16)
+    shared = pk.PK_CROSS_BWD(q, kv, none, cqs, sqs, cks, sks, o, do, 8, lkp, bq, rcs, half, r, 0, 0.25)
+    torch.cuda.synchronize()
+    for a, b in zip(full, shared):
+        assert torch.isfinite(a.float()).all() and torch.equal(a, b), name
