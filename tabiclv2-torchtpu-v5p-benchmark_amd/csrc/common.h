@@ -12,6 +12,7 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define TA_LOG2E 1.4426950408889634f
+#define TA_LN2 0.6931471805599453f
 #define TA_NEG_INF (-__builtin_inff())
 // word 3 of a raw (stride 0) buffer resource on gfx9-family parts: 32-bit data format, no swizzle;
 // accesses at byte offsets >= num_records are dropped (stores) or return 0 (loads)

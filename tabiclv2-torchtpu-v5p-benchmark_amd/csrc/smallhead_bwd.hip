@@ -72,6 +72,16 @@ struct SbParams {
   float* dd;
 };
 
+// 16x16 tile with a 32-deep contraction over two 16-deep halves: A = [a0 | a1], B = [b0 | b1], i.e. the
+// sum of the two 16x16x16 products a0 b0 + a1 b1 in one v_mfma_f32_16x16x32_bf16 (k-slot 8 kap + j of
+// lane (l16, kap) holds slot 4 kap + j of the first half for j < 4 and of the second half for j >= 4,
+// in A and B alike). On gfx950 it issues in the cycles of one 16x16x16 product.
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x4 a0, bf16x4 a1, bf16x4 b0, bf16x4 b1, f32x4 c) {
+  const bf16x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  const bf16x8 b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 template <typename T> struct SbTile {
   static constexpr int PAD = 16 / sizeof(T);
   static constexpr int RSTR = SB_D + PAD;   // row-major tile: 16 dims per row
@@ -201,26 +211,41 @@ __device__ __forceinline__ void sb_scores(const T* lk, const float* lb2, typenam
   }
 }
 
-// dq' += dS k' over the key tile, P = exp2((x - m) - log2 l).
+// dq' l += e (dP - D) k' over the key tile, from e = exp2(x - m) = P l (the caller scales the sum by
+// 1 / l): dP - D straight from the product with -D (nds) as its accumulator input, and e (dP - D)
+// rounded to the input dtype as dS is. bf16: two key blocks per 32-deep product.
 template <typename T>
-__device__ __forceinline__ void sb_dq_tile(const T* lk, const T* lkt, const T* lv, const f32x4 (&x)[SB_KT / 16],
-                                           typename OpVec<T, 4>::type dop, float mq, float lgl, float dsum, int l16,
-                                           int kap, f32x4& acc) {
+__device__ __forceinline__ void sb_dq_tile(const T* lk, const T* lkt, const T* lv, const f32x4 (&e)[SB_KT / 16],
+                                           typename OpVec<T, 4>::type dop, float nds, int l16, int kap, f32x4& acc) {
   typedef SbTile<T> L;
   typedef typename OpVec<T, 4>::type Op4;
+  const f32x4 cnd = {nds, nds, nds, nds};
+  if constexpr (sizeof(T) == 2) {
 #pragma unroll
-  for (int kt = 0; kt < SB_KT / 16; ++kt) {
-    const Op4 av = *(const Op4*)(lv + (16 * kt + l16) * L::RSTR + 4 * kap);
-    const f32x4 dp = mfma16x16x16(av, dop, f32x4{0.f, 0.f, 0.f, 0.f});
-    Op4 ds;
+    for (int kt = 0; kt < SB_KT / 16; kt += 2) {
+      const f32x4 dp0 = mfma16x16x16(*(const Op4*)(lv + (16 * kt + l16) * L::RSTR + 4 * kap), dop, cnd);
+      const f32x4 dp1 = mfma16x16x16(*(const Op4*)(lv + (16 * kt + 16 + l16) * L::RSTR + 4 * kap), dop, cnd);
+      f32x4 d0, d1;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float pr = __builtin_amdgcn_exp2f((x[kt][r] - mq) - lgl);
-      ds[r] = from_f32<T>(pr * (dp[r] - dsum));
+      for (int r = 0; r < 4; ++r) {
+        d0[r] = e[kt][r] * dp0[r];
+        d1[r] = e[kt + 1][r] * dp1[r];
+      }
+      acc = mfma16x16x32(sb_opT<T>(lk, lkt, 16 * kt, l16, kap), sb_opT<T>(lk, lkt, 16 * kt + 16, l16, kap),
+                         cvt_bf16x4(d0), cvt_bf16x4(d1), acc);
+      // two key blocks at a time: hoisting every block's dP first costs registers
+      __builtin_amdgcn_sched_barrier(0);
     }
-    acc = mfma16x16x16(sb_opT<T>(lk, lkt, 16 * kt, l16, kap), ds, acc);
-    // one key block at a time: hoisting every block's dP first costs registers
-    __builtin_amdgcn_sched_barrier(0);
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < SB_KT / 16; ++kt) {
+      const f32x4 dp = mfma16x16x16(*(const Op4*)(lv + (16 * kt + l16) * L::RSTR + 4 * kap), dop, cnd);
+      Op4 ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ds[r] = e[kt][r] * dp[r];
+      acc = mfma16x16x16(sb_opT<T>(lk, lkt, 16 * kt, l16, kap), ds, acc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -273,7 +298,7 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
     dsum = xor_sum(dsum, 32);
 
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float mq, lgl;
+    float mq, lgl, inv;
     if (ONE_TILE) {
       // one pass: the scores stay in registers between the statistics and dq'
       f32x4 x[NKT];
@@ -288,9 +313,14 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) l += __builtin_amdgcn_exp2f(x[kt][r] - mq);
-      lgl = __builtin_amdgcn_logf(quad_sum(l));  // log2; >= 0
-      sb_dq_tile<T>(lk, lkt, lv, x, dop, mq, lgl, dsum, l16, kap, acc);
+        for (int r = 0; r < 4; ++r) {
+          x[kt][r] = __builtin_amdgcn_exp2f(x[kt][r] - mq);  // e, kept for dq'
+          l += x[kt][r];
+        }
+      l = quad_sum(l);  // >= 1
+      lgl = __builtin_amdgcn_logf(l);
+      inv = __builtin_amdgcn_rcpf(l);
+      sb_dq_tile<T>(lk, lkt, lv, x, dop, -dsum, l16, kap, acc);
     } else {
       // sweep 1: statistics over this lane's keys (4 per 16-key block), merged over the lane quad
       float m = TA_NEG_INF, l = 0.f;
@@ -317,7 +347,9 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
         }
       }
       mq = quad_max(m);
-      lgl = __builtin_amdgcn_logf(quad_sum(m > TA_NEG_INF ? l * __builtin_amdgcn_exp2f(m - mq) : 0.f));
+      const float lt = quad_sum(m > TA_NEG_INF ? l * __builtin_amdgcn_exp2f(m - mq) : 0.f);  // >= 1
+      lgl = __builtin_amdgcn_logf(lt);
+      inv = __builtin_amdgcn_rcpf(lt);
       // sweep 2: dq'
       for (int t = 0; t < ntiles; ++t) {
         __syncthreads();
@@ -325,7 +357,11 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
         __syncthreads();
         f32x4 x[NKT];
         sb_scores<T>(lk, lb2, qop, l16, kap, x);
-        sb_dq_tile<T>(lk, lkt, lv, x, dop, mq, lgl, dsum, l16, kap, acc);
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x[kt][r] = __builtin_amdgcn_exp2f(x[kt][r] - mq);
+        sb_dq_tile<T>(lk, lkt, lv, x, dop, -dsum, l16, kap, acc);
       }
     }
     if (qok && kap == 0) {
@@ -335,10 +371,11 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
       p.dd[s] = dsum;
     }
 
-    // dq = rope_bwd(dq' scale), lane: dims 4 kap .. 4 kap + 3 of head g, query qi
+    // dq = rope_bwd(dq' scale), lane: dims 4 kap .. 4 kap + 3 of head g, query qi (acc holds dq' l)
     f32x4 y;
+    const float ysc = p.scale * inv;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = acc[r] * p.scale;
+    for (int r = 0; r < 4; ++r) y[r] = acc[r] * ysc;
     const int qc = qok ? qi : 0;
     y = sb_rope_bwd<RP>(y, scr[wave], l16, kap, sb_tab_row(p.cq, qc, g, p), sb_tab_row(p.sq, qc, g, p), p);
     if (qok) {
@@ -353,7 +390,12 @@ __global__ __launch_bounds__(SB_NW * 64, 4) void sb_dq_kernel(SbParams p) {
 // ---------------------------------------------------------------------------------------------
 // dk, dv
 // ---------------------------------------------------------------------------------------------
-template <typename T, bool RP>
+// The query tile of the dk / dv kernel: q' and dO rows (and their transposed copies for fp32), and per
+// query the statistics in the form the kernel's P takes (HB: m and log2 l apart, a key bias may sit at
+// the floor; else c = -(m + log2 l) ln 2, the accumulator input of the score product, so that
+// P = exp2((s + c) log2 e)) and -D (the accumulator input of the dP product). Queries past Lq: m = +inf
+// or c = -inf, so P = 0.
+template <typename T, bool RP, bool HB>
 __device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt, T* ld, T* ldt, float* lmx,
                                                 float* lll, float* ldd, int b, int g, int q0) {
   typedef SbTile<T> L;
@@ -382,14 +424,19 @@ __device__ __forceinline__ void sb_fill_queries(const SbParams& p, T* lq, T* lqt
   for (int j = tid; j < SB_QT; j += SB_NW * 64) {
     const int qi = q0 + j;
     const int64_t s = ((int64_t)b * SB_H + g) * p.Lq + qi;
-    // queries past Lq: m = +inf gives P = 0
-    lmx[j] = qi < p.Lq ? p.mx[s] : __builtin_inff();
-    lll[j] = qi < p.Lq ? p.ll[s] : 0.f;
-    ldd[j] = qi < p.Lq ? p.dd[s] : 0.f;
+    if (HB) {
+      lmx[j] = qi < p.Lq ? p.mx[s] : __builtin_inff();
+      lll[j] = qi < p.Lq ? p.ll[s] : 0.f;
+    } else {
+      lmx[j] = qi < p.Lq ? -(p.mx[s] + p.ll[s]) * TA_LN2 : TA_NEG_INF;
+    }
+    ldd[j] = qi < p.Lq ? -p.dd[s] : 0.f;
   }
 }
 
-template <typename T, bool RP>
+// HB: the call has a key bias (else b2 only marks keys past Lk, whose dk / dv are not stored, so the
+// kernel ignores it and takes P from the score product with c as its accumulator input).
+template <typename T, bool RP, bool HB>
 __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
   typedef SbTile<T> L;
   typedef typename OpVec<T, 4>::type Op4;
@@ -420,33 +467,57 @@ __global__ __launch_bounds__(SB_NW * 64) void sb_dkdv_kernel(SbParams p) {
                           sb_tab_row(p.sk, kj, g, p), d0, p, 1.f);
     vop = *(const Op4*)((const T*)p.v + b * p.v_sb + (int64_t)kj * p.v_sr + d0);
   }
-  const float b2 = sb_b2(p, b, kj);
+  const float b2 = HB ? sb_b2(p, b, kj) : 0.f;
 
   f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dv = {0.f, 0.f, 0.f, 0.f};
   const int ntiles = (p.Lq + SB_QT - 1) / SB_QT;
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
-    sb_fill_queries<T, RP>(p, lq, lqt, ld, ldt, lmx, lll, ldd, b, g, t * SB_QT);
+    sb_fill_queries<T, RP, HB>(p, lq, lqt, ld, ldt, lmx, lll, ldd, b, g, t * SB_QT);
     __syncthreads();
-#pragma unroll 2
-    for (int qs = 0; qs < SB_QT / 16; ++qs) {
-      // S[query 16 qs + 4 kap + r][key kj], dP likewise
+    // P and dS of query block qs against this wave's keys: S[query 16 qs + 4 kap + r][key kj], dP - D
+    // likewise
+    auto pds = [&](int qs, Op4& pt, Op4& ds) {
       const Op4 aq = *(const Op4*)(lq + (16 * qs + l16) * L::RSTR + 4 * kap);
-      const f32x4 s = mfma16x16x16(aq, kop, f32x4{0.f, 0.f, 0.f, 0.f});
       const Op4 ad = *(const Op4*)(ld + (16 * qs + l16) * L::RSTR + 4 * kap);
-      const f32x4 dp = mfma16x16x16(ad, vop, f32x4{0.f, 0.f, 0.f, 0.f});
       const f32x4 ms = *(const f32x4*)(lmx + 16 * qs + 4 * kap);
-      const f32x4 ls = *(const f32x4*)(lll + 16 * qs + 4 * kap);
-      const f32x4 dq = *(const f32x4*)(ldd + 16 * qs + 4 * kap);
-      Op4 pt, ds;
+      const f32x4 dp = mfma16x16x16(ad, vop, *(const f32x4*)(ldd + 16 * qs + 4 * kap));
+      f32x4 pr;
+      if constexpr (HB) {
+        const f32x4 s = mfma16x16x16(aq, kop, f32x4{0.f, 0.f, 0.f, 0.f});
+        const f32x4 ls = *(const f32x4*)(lll + 16 * qs + 4 * kap);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2) - ms[r]) - ls[r]);
+      } else {
+        const f32x4 s = mfma16x16x16(aq, kop, ms);  // s - (m + log2 l) ln 2
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(s[r] * TA_LOG2E);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], TA_LOG2E, b2) - ms[r]) - ls[r]);
-        pt[r] = from_f32<T>(pr);
-        ds[r] = from_f32<T>(pr * (dp[r] - dq[r]));
+        pt[r] = from_f32<T>(pr[r]);
+        ds[r] = from_f32<T>(pr[r] * dp[r]);
       }
-      dv = mfma16x16x16(sb_opT<T>(ld, ldt, 16 * qs, l16, kap), pt, dv);
-      dk = mfma16x16x16(sb_opT<T>(lq, lqt, 16 * qs, l16, kap), ds, dk);
+    };
+    if constexpr (sizeof(T) == 2) {
+      // query blocks in pairs: one 32-deep product each for dv and dk
+#pragma unroll
+      for (int qs = 0; qs < SB_QT / 16; qs += 2) {
+        Op4 pa, da, pb, db;
+        pds(qs, pa, da);
+        pds(qs + 1, pb, db);
+        dv = mfma16x16x32(sb_opT<T>(ld, ldt, 16 * qs, l16, kap), sb_opT<T>(ld, ldt, 16 * qs + 16, l16, kap), pa, pb, dv);
+        dk = mfma16x16x32(sb_opT<T>(lq, lqt, 16 * qs, l16, kap), sb_opT<T>(lq, lqt, 16 * qs + 16, l16, kap), da, db, dk);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll 2
+      for (int qs = 0; qs < SB_QT / 16; ++qs) {
+        Op4 pt, ds;
+        pds(qs, pt, ds);
+        dv = mfma16x16x16(sb_opT<T>(ld, ldt, 16 * qs, l16, kap), pt, dv);
+        dk = mfma16x16x16(sb_opT<T>(lq, lqt, 16 * qs, l16, kap), ds, dk);
+      }
     }
   }
 
@@ -490,15 +561,6 @@ struct SsLds {
   float b2[SS_ROWS];         // per key: additive term, log2 units, -inf past Lk
 };
 
-// 16x16 tile with a 32-deep contraction over two 16-deep halves: A = [a0 | a1], B = [b0 | b1], i.e. the
-// sum of the two 16x16x16 products a0 b0 + a1 b1 in one v_mfma_f32_16x16x32_bf16 (k-slot 8 kap + j of
-// lane (l16, kap) holds slot 4 kap + j of the first half for j < 4 and of the second half for j >= 4,
-// in A and B alike). On gfx950 it issues in the cycles of one 16x16x16 product.
-__device__ __forceinline__ f32x4 mfma16x16x32(bf16x4 a0, bf16x4 a1, bf16x4 b0, bf16x4 b1, f32x4 c) {
-  const bf16x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-  const bf16x8 b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 
 // RoPE of a 4-dim chunk (chunk index c4 = (dim within the head) / 4) in the fill: pairs in-lane,
 // halves from the partner chunk c4 ^ 2, held by lane ^ 2.
@@ -796,7 +858,10 @@ void launch_sb(const SbParams& p, int64_t nwg_q, int64_t nkb, hipStream_t stream
     hipLaunchKernelGGL((sb_dq_kernel<T, true, RP>), dim3((unsigned)(p.B * nwg_q * SB_H)), block, 0, stream, p);
   else if (nwg_q > 0)
     hipLaunchKernelGGL((sb_dq_kernel<T, false, RP>), dim3((unsigned)(p.B * nwg_q * SB_H)), block, 0, stream, p);
-  hipLaunchKernelGGL((sb_dkdv_kernel<T, RP>), dim3((unsigned)(p.B * nkb * SB_H)), block, 0, stream, p);
+  if (p.bias)
+    hipLaunchKernelGGL((sb_dkdv_kernel<T, RP, true>), dim3((unsigned)(p.B * nkb * SB_H)), block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((sb_dkdv_kernel<T, RP, false>), dim3((unsigned)(p.B * nkb * SB_H)), block, 0, stream, p);
 }
 
 template <typename T>
