@@ -1297,13 +1297,14 @@ __device__ __forceinline__ void sf_tile(const float* lkt, const float* lvt, cons
 // O finite) decides whether the exact pass must redo the block. Even and odd 16-key groups
 // accumulate O into separate registers (summed at the end): the PV products of consecutive groups
 // do not wait on each other.
-template <bool FIRST>
+// NG: 16-key groups of the tile (8: a 128-key tile; 4: one half of it, the streaming sweep's tiles).
+template <bool FIRST, int NG = SF_KT / 16>
 __device__ __forceinline__ void sf_tile_fix(const float* lkt, const float* lvt, const float* lb2, int nkb,
                                             f32x4 qop, int hd, int l16, int kap, bool addb, f32x4& o, float& m,
                                             float& l) {
   f32x4 o1 = {0.f, 0.f, 0.f, 0.f};  // odd groups: two independent PV accumulation chains
 #pragma unroll
-  for (int kt = 0; kt < SF_KT / 16; ++kt) {
+  for (int kt = 0; kt < NG; ++kt) {
     if (kt < nkb) {
       const bool first = FIRST && kt == 0;
       const f32x4 a = *(const f32x4*)(lkt + (16 * kt + l16) * SF_KSTR + hd + 4 * kap);
@@ -1462,22 +1463,90 @@ __global__ __launch_bounds__(512, 4) void sf_kernel(ShParams p) {
       l[j] = 0.f;
     }
     if (threadIdx.x == 0) sf_bad = 0;
-    for (int t = 0; t < ntiles; ++t) {
-      __syncthreads();
-      sf_fill(p, lkt, lvt, lb2, b, hg, t, lk);
-      __syncthreads();
-      const int rem = lk - t * SF_KT;
-      const int nkb = rem >= SF_KT ? SF_KT / 16 : (rem + 15) >> 4;
-      const bool addb = p.bias != nullptr || (rem < SF_KT && (rem & 15) != 0);
+    if (!p.rope) {
+      // 64-key tiles in the two halves of the LDS tile: the next tile's K / V rows and b2 are loaded
+      // into registers before the current one is computed and stored to the other half after it,
+      // so the loads are in flight during the products (one barrier per tile). With RoPE the fill
+      // rotates K at the store: the unpipelined 128-key sweep below.
+      constexpr int HK = SF_KT / 2;
+      constexpr int HU = HK * (SF_W / 4) / 512;  // 16-byte K / V chunks per thread and tile
+      const int nt = (lk + HK - 1) / HK;
+      const int tid = threadIdx.x;
+      const float* kbase = (const float*)p.k + b * p.k_sb;
+      const float* vbase = (const float*)p.v + b * p.v_sb;
+      f32x4 rk[HU], rv[HU];
+      float rb = TA_NEG_INF;
+      auto fetch = [&](int t) {
 #pragma unroll
-      for (int j = 0; j < SF_SB; ++j) {
-        if (par + 2 * j < nb) {
-          if (t == 0)
-            sf_tile_fix<true>(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, addb, o[j], m[j], l[j]);
-          else
-            sf_tile_fix<false>(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, addb, o[j], m[j], l[j]);
+        for (int i = 0; i < HU; ++i) {
+          const int u = tid + 512 * i, key = u >> 4, c = u & 15;
+          const int gk = t * HK + key, gc = gk < lk ? gk : lk - 1;
+          rk[i] = *(const f32x4*)(kbase + (int64_t)gc * p.k_sr + hg * SF_W + 4 * c);
+          rv[i] = *(const f32x4*)(vbase + (int64_t)gc * p.v_sr + hg * SF_W + 4 * c);
+          if (gk >= lk) rk[i] = rv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        __builtin_amdgcn_sched_barrier(0);  // one block at a time: interleaving them costs registers
+        if (tid < HK) {
+          const int gk = t * HK + tid;
+          rb = TA_NEG_INF;
+          if (gk < lk) rb = p.bias ? fmaxf(p.bias[b * p.bias_sb + gk] * TA_LOG2E, SH_BIAS_FLOOR) : 0.f;
+        }
+      };
+      auto put = [&](int h) {
+#pragma unroll
+        for (int i = 0; i < HU; ++i) {
+          const int u = tid + 512 * i, key = HK * h + (u >> 4), c = u & 15;
+          *(f32x4*)(lkt + key * SF_KSTR + 4 * c) = rk[i];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lvt[(4 * c + j) * SF_VSTR + key] = rv[i][j];
+        }
+        if (tid < HK) lb2[HK * h + tid] = rb;
+      };
+      if (nt > 0) {  // lk >= 1: the clamped row lk - 1 exists
+        fetch(0);
+        put(0);
+      }
+      __syncthreads();
+      for (int t = 0; t < nt; ++t) {
+        const int h = t & 1;
+        if (t + 1 < nt) fetch(t + 1);
+        const int rem = lk - t * HK;
+        const int nkb = rem >= HK ? HK / 16 : (rem + 15) >> 4;
+        const bool addb = p.bias != nullptr || (rem < HK && (rem & 15) != 0);
+#pragma unroll
+        for (int j = 0; j < SF_SB; ++j) {
+          if (par + 2 * j < nb) {
+            if (t == 0)
+              sf_tile_fix<true, HK / 16>(lkt + HK * h * SF_KSTR, lvt + HK * h, lb2 + HK * h, nkb, qop[j], hd, l16,
+                                         kap, addb, o[j], m[j], l[j]);
+            else
+              sf_tile_fix<false, HK / 16>(lkt + HK * h * SF_KSTR, lvt + HK * h, lb2 + HK * h, nkb, qop[j], hd,
+                                          l16, kap, addb, o[j], m[j], l[j]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // half h ^ 1 was last read by tile t - 1's products, which every wave finished before the
+        // previous barrier
+        if (t + 1 < nt) put(h ^ 1);
+        __syncthreads();
+      }
+    } else {
+      for (int t = 0; t < ntiles; ++t) {
+        __syncthreads();
+        sf_fill(p, lkt, lvt, lb2, b, hg, t, lk);
+        __syncthreads();
+        const int rem = lk - t * SF_KT;
+        const int nkb = rem >= SF_KT ? SF_KT / 16 : (rem + 15) >> 4;
+        const bool addb = p.bias != nullptr || (rem < SF_KT && (rem & 15) != 0);
+#pragma unroll
+        for (int j = 0; j < SF_SB; ++j) {
+          if (par + 2 * j < nb) {
+            if (t == 0)
+              sf_tile_fix<true>(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, addb, o[j], m[j], l[j]);
+            else
+              sf_tile_fix<false>(lkt, lvt, lb2, nkb, qop[j], hd, l16, kap, addb, o[j], m[j], l[j]);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // one block at a time: interleaving them costs registers
+        }
       }
     }
     bool bad = false;

@@ -1,5 +1,4 @@
 """pytest setup: the `gpu` marker, import paths for the package and the oracle, shared helpers."""
-import os
 import sys
 from pathlib import Path
 

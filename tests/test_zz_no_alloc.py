@@ -2,7 +2,6 @@
 its output must match tabicl_icl_fwd's (with a workspace from torch) on two calls in a row, the second
 with a smaller input, to the kernel's bar (bit-identical when both split the keys the same way; within
 2e-2 bf16 / 1e-4 fp32 otherwise), plus a key-masked call and the refusal of an oversized call."""
-import ctypes
 
 import pytest
 import torch
