@@ -101,6 +101,9 @@ def test_hx_bwd(dev, name, B, Lq, Lk, dtype, bias):
     ("self_bf16_norope_long", 2, 700, torch.bfloat16, None, False),
     ("self_bf16_rope_pairs", 8, 104, torch.bfloat16, True, False),
     ("self_bf16_rope_halves_bias_128", 4, 128, torch.bfloat16, False, True),
+    # past 128 tokens with RoPE: the tiled dq / dk-dv kernels' RoPE instances (two key sweeps)
+    ("self_bf16_rope_halves_long", 2, 300, torch.bfloat16, False, False),
+    ("self_fp32_rope_pairs_long_bias", 2, 260, torch.float32, True, True),
 ])
 def test_pk_self_bwd(dev, name, B, L, dtype, interleaved, bias):
     pk = _attn()
@@ -170,11 +173,12 @@ def test_pk_cross_bwd(dev, name, B, Lq, Lk, dtype, interleaved, shared_q):
     _check("dkv", yr.grad, dkv, dtype)
 
 
-def test_bwd_all_keys_masked_is_uniform(dev):
+@pytest.mark.parametrize("Lq,Lk", [(24, 20), (40, 200)], ids=["fused_short", "tiled"])
+def test_bwd_all_keys_masked_is_uniform(dev, Lq, Lk):
     # every key at -1e30: P is uniform (the reference's finite sentinel); gradients stay finite
     pk = _attn()
     g = _gen(33)
-    B, Lq, Lk = 2, 24, 20
+    B = 2
     q = (torch.randn(B, Lq, E, generator=g) * 0.25).to(torch.bfloat16)
     k = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
     v = torch.randn(B, Lk, E, generator=g).to(torch.bfloat16)
