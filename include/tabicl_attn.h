@@ -290,6 +290,24 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
                           float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Gradients of the ICL attention O = softmax(scale q k^T + mask) v (keys at or past valid[n] masked,
+ * key_bias as in tabicl_icl_fwd_masked or NULL): dq, dk, dv [N, H, T, 64] from q, k, v, the forward
+ * output o and its gradient dout, all contiguous [N, H, T, 64] (T = Tq for q, o, dout, dq; Tkv for k, v,
+ * dk, dv) in one dtype. P is recomputed in fp32; dS = P (dP - D) with D = sum over the head's dims of
+ * dout * o, rounded to the input dtype; dq = scale dS k, dk = scale dS^T q, dv = P^T dout (fp32
+ * accumulation); keys at or past valid get zero gradients. Replaces the gradient of the reference's
+ * autograd fallback for masked / grad-enabled long-key ICL attention, _tiled_online_sdpa
+ * (results/tpu_patch.diff:158-193, routed at :263-270). workspace: at least
+ * tabicl_icl_bwd_workspace_bytes(N, H, Tq) bytes of device memory (16-byte aligned); calls that overlap
+ * on the GPU must not share it.
+ */
+int64_t tabicl_icl_bwd_workspace_bytes(int64_t N, int64_t H, int64_t Tq);
+int tabicl_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                   const float* key_bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout, void* dq,
+                   void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, float scale,
+                   int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * tabicl_icl_fwd_masked without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
  * in the reference. The key-split partials, work-item flags and the prefix view of a key mask live in

@@ -357,6 +357,41 @@ def splash_sdpa_ref(q, k, v, valid=None, bias=None):
     return out
 
 
+def splash_sdpa_bwd_ref(q, k, v, do, valid=None, bias=None, o=None):
+    """Gradients (dq, dk, dv) of splash_sdpa_ref's attention, float64 (the quantities the reference's
+    autograd fallback _tiled_online_sdpa, results/tpu_patch.diff:158-193, differentiates): with
+    S = D^-0.5 q k^T + bias over the visible keys, P = softmax(S), dP = dO V^T, D_row = sum over the
+    head dims of dO * O (O = `o` when given, else the exact output), dS = P (dP - D_row),
+    dq = D^-0.5 dS k, dk = D^-0.5 dS^T q, dv = P^T dO; keys at or past valid get zero gradients."""
+    q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
+    N, H, Tq, D = q.shape
+    Tkv = k.shape[2]
+    sc = D ** -0.5
+    if o is None:
+        o = splash_sdpa_ref(q, k, v, valid, bias)
+    o = _f64(o)
+    vl = None if valid is None else np.asarray(_f64(valid)).reshape(-1).astype(np.int64)
+    bb = None if bias is None else np.asarray(_f64(bias), np.float32).reshape(-1, Tkv)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    for n in range(N):
+        nv = Tkv if vl is None else int(min(max(vl[0 if vl.size == 1 else n], 0), Tkv))
+        if nv == 0:
+            continue
+        s = np.einsum("htd,hsd->hts", q[n] * sc, k[n, :, :nv])
+        if bb is not None:
+            s = (s.astype(np.float32) + bb[0 if bb.shape[0] == 1 else n, :nv]).astype(np.float64)
+        s -= s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        dp = np.einsum("htd,hsd->hts", do[n], v[n, :, :nv])
+        drow = (do[n] * o[n]).sum(axis=-1, keepdims=True)
+        ds = p * (dp - drow)
+        dq[n] = sc * np.einsum("hts,hsd->htd", ds, k[n, :, :nv])
+        dk[n, :, :nv] = sc * np.einsum("hts,htd->hsd", ds, q[n])
+        dv[n, :, :nv] = np.einsum("hts,htd->hsd", p, do[n])
+    return dq, dk, dv
+
+
 def splash_sdpa_torch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, valid: Optional[int] = None):
     """The same ICL attention as splash_sdpa_ref in CPU torch float32 (head split, matmul, fp32
     softmax, matmul) -- the CPU baseline the bench times."""

@@ -23,7 +23,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form", "-Wall", "-Wno-unused-function",
          "-Wno-unused-command-line-argument"]
-SOURCES = ["abi.hip", "icl_fwd.hip", "smallhead_fwd.hip", "smallhead_stream.hip", "smallhead_bwd.hip", "keymask.hip",
+SOURCES = ["abi.hip", "icl_fwd.hip", "icl_bwd.hip", "smallhead_fwd.hip", "smallhead_stream.hip", "smallhead_bwd.hip", "keymask.hip",
            "layernorm.hip"]
 
 

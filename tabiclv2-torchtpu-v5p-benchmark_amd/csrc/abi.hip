@@ -430,6 +430,35 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
       "icl_fwd");
 }
 
+int64_t tabicl_icl_bwd_workspace_bytes(int64_t N, int64_t H, int64_t Tq) {
+  if (N < 0 || H < 0 || Tq < 0) return fail(-1, "icl_bwd_workspace_bytes: bad sizes");
+  return tabicl_launch_icl_bwd_ws_bytes(N, H, Tq);
+}
+
+int tabicl_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                   const float* key_bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout, void* dq,
+                   void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, float scale,
+                   int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  // contiguous [N, H, T, 64] tensors: the strides the shared checks take
+  const int64_t sq[3] = {H * Tq * D, Tq * D, D}, sk[3] = {H * Tkv * D, Tkv * D, D};
+  const int64_t strides[12] = {sq[0], sq[1], sq[2], sk[0], sk[1], sk[2], sk[0], sk[1], sk[2], sq[0], sq[1], sq[2]};
+  int st = icl_args("icl_bwd", q, k, v, valid, valid_n, key_bias, bias_n, bias_sn, nullptr, 0, o, N, H, Tq, Tkv, D,
+                    strides, scale, dtype);
+  if (st) return st;
+  if (!(scale > 0.f) || !(scale < 1e30f)) return fail(1, "icl_bwd: scale must be positive and finite");
+  if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return fail(1, "icl_bwd: pointers must be 16-byte aligned");
+  if (N * H * ((Tkv + 63) / 64) > (1LL << 31) - 1) return fail(1, "icl_bwd: grid too large");
+  if (N == 0 || H == 0) return 0;
+  if (!workspace || !aligned16(workspace) || workspace_bytes < tabicl_launch_icl_bwd_ws_bytes(N, H, Tq))
+    return fail(1, "icl_bwd: workspace of %lld bytes (16-byte aligned) required",
+                (long long)tabicl_launch_icl_bwd_ws_bytes(N, H, Tq));
+  return launch_status(tabicl_launch_icl_bwd(q, k, v, valid, valid ? valid_n : 0, key_bias, key_bias ? bias_n : 0,
+                                             key_bias ? bias_sn : 0, o, dout, dq, dk, dv, N, H, Tq, Tkv, scale, dtype,
+                                             workspace, workspace_bytes, (hipStream_t)stream),
+                       "icl_bwd");
+}
+
 int tabicl_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
                            const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,
                            int64_t q_len_n, void* out, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,

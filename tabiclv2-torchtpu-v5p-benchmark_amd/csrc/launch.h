@@ -27,6 +27,15 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int list_mode = 0);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
+// Backward of the D = 64 ICL attention (icl_bwd.hip) over contiguous [N, H, T, 64] tensors: dq, dk, dv
+// from q, k, v, the forward output o and its gradient dout; valid / bias as in the forward. ws: at least
+// tabicl_launch_icl_bwd_ws_bytes(N, H, Tq) bytes (per-query statistics passed between the two kernels).
+int64_t tabicl_launch_icl_bwd_ws_bytes(int64_t N, int64_t H, int64_t Tq);
+int tabicl_launch_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                          const float* bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout,
+                          void* dq, void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, float scale,
+                          int dtype, void* ws, int64_t ws_bytes, hipStream_t stream);
+
 // The same launch (D = 64) with the library's per-GPU scratch array of TABICL_ICL_SCRATCH_BYTES in
 // place of a workspace: no allocation. Key splits whose partials do not fit run unsplit; a call whose
 // unsplit need (tabicl_launch_icl_noalloc_min_bytes) exceeds the array must be refused by the caller.

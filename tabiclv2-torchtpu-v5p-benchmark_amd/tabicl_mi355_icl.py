@@ -115,6 +115,66 @@ def _(q, k, v, valid, scale, key_bias=None):  # noqa: ANN001
     return torch.empty_like(q)
 
 
+@torch.library.custom_op("tabicl::icl_cached_attn_bwd", mutates_args=())
+def _icl_cached_attn_bwd(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], key_bias: Optional[Tensor],
+                         out: Tensor, dout: Tensor, scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    """Gradients (dq, dk, dv) of icl_cached_attn for the upstream gradient dout, given the forward's
+    inputs and its output `out` (tabicl_icl_bwd). The reference's calls with a gradient take autograd
+    through its tiled online-softmax attention (results/tpu_patch.diff:158-193, chosen at :263-270);
+    here both products and the softmax recompute run in the library's two backward kernels. Keys past
+    the valid length get zero gradients; key_bias gets none (a mask, not a parameter)."""
+    _nat.require_device(q, k, v, valid, key_bias, out, dout)
+    q, k, v, out, dout = (_nat.aligned16(t) for t in (q, k, v, out, dout))
+    N, H, Tq, D = q.shape
+    Tkv = k.shape[2]
+    if k.shape != v.shape or k.shape[:2] != q.shape[:2] or k.shape[3] != D or out.shape != q.shape \
+            or dout.shape != q.shape:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)} "
+                         f"out {tuple(out.shape)} dout {tuple(dout.shape)}")
+    if not (q.dtype == k.dtype == v.dtype == out.dtype == dout.dtype):
+        raise ValueError("q, k, v, out and dout must share a dtype")
+    vptr, vn = None, 0
+    if valid is not None:
+        if valid.dtype != torch.int32 or not valid.is_contiguous():
+            raise ValueError("valid must be a contiguous int32 tensor")
+        vptr, vn = valid.data_ptr(), valid.numel()
+    bptr, bn, bsn = None, 0, 0
+    if key_bias is not None:
+        if key_bias.dtype != torch.float32 or key_bias.dim() != 2 or key_bias.shape[1] != Tkv \
+                or key_bias.shape[0] not in (1, N) or key_bias.stride(1) != 1:
+            raise ValueError(f"key_bias must be a float32 [1 or {N}, {Tkv}] tensor with contiguous rows")
+        bptr, bn, bsn = key_bias.data_ptr(), key_bias.shape[0], key_bias.stride(0)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    nbytes = int(_nat.load().tabicl_icl_bwd_workspace_bytes(N, H, Tq))
+    if nbytes < 0:
+        raise RuntimeError(f"tabicl_icl_bwd_workspace_bytes: {_nat.last_error()}")
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    _nat.call("tabicl_icl_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, bptr, bn, bsn, out.data_ptr(),
+              dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), N, H, Tq, Tkv, D, float(scale),
+              _nat.dtype_code(q.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(q))
+    return dq, dk, dv
+
+
+@_icl_cached_attn_bwd.register_fake
+def _(q, k, v, valid, key_bias, out, dout, scale):  # noqa: ANN001
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _icl_setup_context(ctx, inputs, output):  # noqa: ANN001
+    q, k, v, valid, scale, key_bias = inputs
+    ctx.save_for_backward(q, k, v, valid, key_bias, output)
+    ctx.scale = scale
+
+
+def _icl_backward(ctx, grad):  # noqa: ANN001
+    q, k, v, valid, key_bias, out = ctx.saved_tensors
+    dq, dk, dv = torch.ops.tabicl.icl_cached_attn_bwd(q, k, v, valid, key_bias, out, grad, ctx.scale)
+    return dq, dk, dv, None, None, None
+
+
+_icl_cached_attn.register_autograd(_icl_backward, setup_context=_icl_setup_context)
+
+
 @torch.library.custom_op("tabicl::icl_cached_attn_out", mutates_args=("out",))
 def _icl_cached_attn_out(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], scale: float,
                          out: Tensor, key_bias: Optional[Tensor] = None) -> None:

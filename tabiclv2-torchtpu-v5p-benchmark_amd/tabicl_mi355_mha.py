@@ -566,9 +566,11 @@ def _hook_bias(attn_mask: Optional[Tensor], q: Tensor, Tkv: int):
 def icl_hook(upstream_sdpa):  # noqa: ANN001
     """sdpa_with_flattened_batch with its attention on the HIP ICL kernel (the reference's Splash
     branch, results/tpu_patch.diff:261-281, on this GPU): q, k, v [..., H, T, D] on the GPU, same
-    dtype (bf16 or fp32), D the kernel's head dim, no dropout, no gradient, and either no mask or one
-    that varies over keys only. SSMax is applied to q with n = src_len_override or the key count first
-    (diff:251-254); valid_kv_len masks the key tail. Anything else goes to upstream."""
+    dtype (bf16 or fp32), D the kernel's head dim, no dropout, and either no mask or one that varies
+    over keys only (and needs no gradient itself). SSMax is applied to q with n = src_len_override or the
+    key count first (diff:251-254); valid_kv_len masks the key tail. Calls with a gradient take the
+    library's backward kernels through the op's autograd formula, where the reference's take autograd
+    through its tiled online softmax (diff:158-193, 263-270). Anything else goes to upstream."""
 
     global _ICL
     if _ICL is None:
@@ -580,7 +582,8 @@ def icl_hook(upstream_sdpa):  # noqa: ANN001
                                   src_len_override=None, valid_kv_len=None):
         Tkv = k.shape[-2]
         kb = _hook_bias(attn_mask, q, Tkv)
-        if (kb is not False and q.device.type == _DEVICE and dropout_p == 0.0 and not torch.is_grad_enabled()
+        if (kb is not False and q.device.type == _DEVICE and dropout_p == 0.0
+                and not (torch.is_grad_enabled() and attn_mask is not None and attn_mask.requires_grad)
                 and q.dtype in (torch.bfloat16, torch.float32) and q.dtype == k.dtype == v.dtype
                 and _ICL.icl_supported(q.shape[-2], Tkv, q.shape[-1], q.dtype)):
             lead = q.shape[:-3]

@@ -56,6 +56,9 @@ SIGNATURES = {
     "tabicl_layer_norm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _f32, _i32, _i32, _c_p],
     "tabicl_icl_fwd_masked": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
                               _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_bwd_workspace_bytes": [_i64, _i64, _i64],
+    "tabicl_icl_bwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64,
+                       _i64, _i64, _i64, _f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_fwd_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
                                _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p],
     "tabicl_icl_noalloc_scratch_bytes": [],
@@ -69,7 +72,7 @@ SIGNATURES = {
 _RESTYPES = {"tabicl_attn_last_error": ctypes.c_char_p, "tabicl_attn_version": ctypes.c_char_p,
              "tabicl_icl_workspace_bytes": ctypes.c_int64, "tabicl_hxq_workspace_bytes": ctypes.c_int64,
              "tabicl_smallhead_bwd_workspace_bytes": ctypes.c_int64, "tabicl_hxf_workspace_bytes": ctypes.c_int64,
-             "tabicl_icl_noalloc_scratch_bytes": ctypes.c_int64}
+             "tabicl_icl_noalloc_scratch_bytes": ctypes.c_int64, "tabicl_icl_bwd_workspace_bytes": ctypes.c_int64}
 
 
 class NativeLibraryError(RuntimeError):

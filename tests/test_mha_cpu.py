@@ -406,6 +406,24 @@ def test_cached_icl_with_tensor_train_size_reaches_the_icl_kernel(routed, T, tra
     torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
 
 
+def test_icl_hook_keeps_gradient_calls(routed):
+    # the ICL op has a backward: calls under autograd reach the kernel; a key mask that itself needs a
+    # gradient (the op gives a mask none) goes to upstream
+    mod, ref_mod, seen = routed
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(2, 4, 6, 64, generator=g, requires_grad=True)
+    k, v = torch.randn(2, 4, 50, 64, generator=g), torch.randn(2, 4, 50, 64, generator=g)
+    kb = torch.zeros(2, 1, 1, 50)
+    kb[1, ..., 40:] = torch.finfo(torch.float32).min
+    with torch.enable_grad():
+        mod.sdpa_with_flattened_batch(q, k, v, kb, valid_kv_len=torch.tensor(45))
+        assert seen == ["icl_sdpa"]
+        got = mod.sdpa_with_flattened_batch(q, k, v, kb.clone().requires_grad_())
+        want = ref_mod.sdpa_with_flattened_batch(q, k, v, kb)
+    assert seen == ["icl_sdpa"]
+    torch.testing.assert_close(got, want)
+
+
 @pytest.mark.parametrize("with_mask", [False, True])
 def test_cached_column_attention_takes_pk_cross(routed, with_mask):
     # the column blocks' second attention at query time: test rows over the cached head-split K/V of

@@ -385,3 +385,52 @@ def test_splash_ref_key_bias():
     w1 = 1.0 / (1.0 + np.exp(-(np.float64(np.float32(s[1]) + np.float32(1.5)) - np.float32(s[0]))))
     want = (1 - w1) * v2[0, 0, 0].double().numpy() + w1 * v2[0, 0, 1].double().numpy()
     np.testing.assert_allclose(O.splash_sdpa_ref(q2, k2, v2, bias=np.array([[0.0, 1.5]]))[0, 0, 0], want, atol=1e-6)
+
+
+@pytest.mark.parametrize("case", ["plain", "valid", "bias"])
+def test_splash_bwd_matches_autograd(case):
+    # the ICL attention's gradients against torch autograd in float64 through an independent forward
+    # (scaled scores, masked keys as -inf, softmax, product)
+    rng = np.random.default_rng(40)
+    N, Hh, Tq, Tkv, D = 2, 3, 5, 11, 64
+    q, k, v, do = _rand(rng, N, Hh, Tq, D), _rand(rng, N, Hh, Tkv, D), _rand(rng, N, Hh, Tkv, D), _rand(rng, N, Hh, Tq, D)
+    valid = np.array([7, 11]) if case == "valid" else None
+    bias = None
+    if case == "bias":
+        bias = _rand(rng, N, Tkv).astype(np.float32)
+        bias[:, -3:] = -1e30  # masked by the mask: zero gradients there
+    dq, dk, dv = O.splash_sdpa_bwd_ref(q, k, v, do, valid, bias)
+    qt, kt, vt = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    s = (qt * D ** -0.5) @ kt.transpose(-1, -2)
+    if valid is not None:
+        keep = torch.arange(Tkv)[None, :] < torch.tensor(valid)[:, None]
+        s = s.masked_fill(~keep[:, None, None, :], float("-inf"))
+    if bias is not None:
+        # the kernel adds the bias to float32 scores; the rounded value enters with an identity gradient
+        b32 = torch.tensor(bias)[:, None, None, :]
+        s = s + ((s.detach().float() + b32).double() - s.detach())
+    out = torch.softmax(s, dim=-1) @ vt
+    out.backward(torch.tensor(do))
+    for got, t in ((dq, qt), (dk, kt), (dv, vt)):
+        np.testing.assert_allclose(got, t.grad.numpy(), rtol=0, atol=1e-10)
+    if valid is not None:
+        assert np.abs(dk[0, :, 7:]).max() == 0 and np.abs(dv[0, :, 7:]).max() == 0
+    if bias is not None:
+        assert np.abs(dk[:, :, -3:]).max() < 1e-300 and np.abs(dv[:, :, -3:]).max() < 1e-300
+
+
+def test_splash_bwd_finite_differences():
+    # central differences of <dO, O> through splash_sdpa_ref on a tiny case
+    rng = np.random.default_rng(41)
+    q, k, v, do = _rand(rng, 1, 1, 2, 64), _rand(rng, 1, 1, 3, 64), _rand(rng, 1, 1, 3, 64), _rand(rng, 1, 1, 2, 64)
+    dq, dk, dv = O.splash_sdpa_bwd_ref(q, k, v, do)
+    f = lambda q_, k_, v_: float((O.splash_sdpa_ref(q_, k_, v_) * do).sum())  # noqa: E731
+    eps = 1e-6
+    for grad, which in ((dq, 0), (dk, 1), (dv, 2)):
+        for idx in [(0, 0, 0, 0), (0, 0, 1, 33), (0, 0, 0, 63)]:
+            args = [q.copy(), k.copy(), v.copy()]
+            args[which][idx] += eps
+            up = f(*args)
+            args[which][idx] -= 2 * eps
+            dn = f(*args)
+            assert abs((up - dn) / (2 * eps) - grad[idx]) < 1e-6
