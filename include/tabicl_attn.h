@@ -290,6 +290,20 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
                           float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * tabicl_icl_fwd that also writes each query row's softmax statistics for tabicl_icl_bwd: stat
+ * [N, H, Tq, 2] fp32 (contiguous, 16-byte aligned) receives (m, l), m in log2 units and l the sum over
+ * the visible keys of exp2(scale log2(e) q.k - m) (l = 0: no visible key). The forward half of the
+ * reference's gradient path (autograd through _tiled_online_sdpa, results/tpu_patch.diff:158-193,
+ * routed at :263-270), whose saved tensors the backward uses; no key mask (masked calls with a gradient
+ * use tabicl_icl_fwd_masked and take their statistics in the backward).
+ */
+int tabicl_icl_fwd_stats(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                         void* out, float* stat, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                         int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                         int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                         float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Gradients of the ICL attention O = softmax(scale q k^T + mask) v (keys at or past valid[n] masked,
  * key_bias as in tabicl_icl_fwd_masked or NULL): dq, dk, dv [N, H, T, 64] from q, k, v, the forward
  * output o and its gradient dout, all contiguous [N, H, T, 64] (T = Tq for q, o, dout, dq; Tkv for k, v,
@@ -297,15 +311,16 @@ int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int
  * dout * o, rounded to the input dtype; dq = scale dS k, dk = scale dS^T q, dv = P^T dout (fp32
  * accumulation); keys at or past valid get zero gradients. Replaces the gradient of the reference's
  * autograd fallback for masked / grad-enabled long-key ICL attention, _tiled_online_sdpa
- * (results/tpu_patch.diff:158-193, routed at :263-270). workspace: at least
- * tabicl_icl_bwd_workspace_bytes(N, H, Tq) bytes of device memory (16-byte aligned); calls that overlap
- * on the GPU must not share it.
+ * (results/tpu_patch.diff:158-193, routed at :263-270). stat: NULL, or (calls without key_bias) the
+ * statistics tabicl_icl_fwd_stats wrote for this o; the bf16 path then skips its own statistics sweep
+ * over the keys. workspace: at least tabicl_icl_bwd_workspace_bytes(N, H, Tq) bytes of device memory
+ * (16-byte aligned); calls that overlap on the GPU must not share it.
  */
 int64_t tabicl_icl_bwd_workspace_bytes(int64_t N, int64_t H, int64_t Tq);
 int tabicl_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
-                   const float* key_bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout, void* dq,
-                   void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, float scale,
-                   int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
+                   const float* key_bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout,
+                   const float* stat, void* dq, void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                   int64_t D, float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * tabicl_icl_fwd_masked without a workspace argument, for callers that cannot allocate device memory

@@ -436,9 +436,9 @@ int64_t tabicl_icl_bwd_workspace_bytes(int64_t N, int64_t H, int64_t Tq) {
 }
 
 int tabicl_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
-                   const float* key_bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout, void* dq,
-                   void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, float scale,
-                   int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+                   const float* key_bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout,
+                   const float* stat, void* dq, void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv,
+                   int64_t D, float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   // contiguous [N, H, T, 64] tensors: the strides the shared checks take
   const int64_t sq[3] = {H * Tq * D, Tq * D, D}, sk[3] = {H * Tkv * D, Tkv * D, D};
   const int64_t strides[12] = {sq[0], sq[1], sq[2], sk[0], sk[1], sk[2], sk[0], sk[1], sk[2], sq[0], sq[1], sq[2]};
@@ -446,17 +446,36 @@ int tabicl_icl_bwd(const void* q, const void* k, const void* v, const int32_t* v
                     strides, scale, dtype);
   if (st) return st;
   if (!(scale > 0.f) || !(scale < 1e30f)) return fail(1, "icl_bwd: scale must be positive and finite");
-  if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+  if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(stat))
     return fail(1, "icl_bwd: pointers must be 16-byte aligned");
+  if (stat && key_bias) return fail(1, "icl_bwd: forward statistics are taken for calls without a key mask only");
   if (N * H * ((Tkv + 63) / 64) > (1LL << 31) - 1) return fail(1, "icl_bwd: grid too large");
   if (N == 0 || H == 0) return 0;
   if (!workspace || !aligned16(workspace) || workspace_bytes < tabicl_launch_icl_bwd_ws_bytes(N, H, Tq))
     return fail(1, "icl_bwd: workspace of %lld bytes (16-byte aligned) required",
                 (long long)tabicl_launch_icl_bwd_ws_bytes(N, H, Tq));
   return launch_status(tabicl_launch_icl_bwd(q, k, v, valid, valid ? valid_n : 0, key_bias, key_bias ? bias_n : 0,
-                                             key_bias ? bias_sn : 0, o, dout, dq, dk, dv, N, H, Tq, Tkv, scale, dtype,
-                                             workspace, workspace_bytes, (hipStream_t)stream),
+                                             key_bias ? bias_sn : 0, o, dout, stat, dq, dk, dv, N, H, Tq, Tkv, scale,
+                                             dtype, workspace, workspace_bytes, (hipStream_t)stream),
                        "icl_bwd");
+}
+
+int tabicl_icl_fwd_stats(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
+                         void* out, float* stat, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D,
+                         int64_t q_sn, int64_t q_sh, int64_t q_st, int64_t k_sn, int64_t k_sh, int64_t k_st,
+                         int64_t v_sn, int64_t v_sh, int64_t v_st, int64_t o_sn, int64_t o_sh, int64_t o_st,
+                         float scale, int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int64_t strides[12] = {q_sn, q_sh, q_st, k_sn, k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st};
+  int st = icl_args("icl_fwd_stats", q, k, v, valid, valid_n, nullptr, 0, 0, nullptr, 0, out, N, H, Tq, Tkv, D,
+                    strides, scale, dtype);
+  if (st || N == 0 || H == 0 || Tq == 0) return st;
+  if (!stat || !aligned16(stat)) return fail(1, "icl_fwd_stats: stat ([N, H, Tq, 2] fp32, 16-byte aligned) is required");
+  return launch_status(
+      tabicl_launch_icl_fwd(q, k, v, valid, valid ? valid_n : 0, out, N, H, Tq, Tkv, 64, q_sn, q_sh, q_st, k_sn,
+                            k_sh, k_st, v_sn, v_sh, v_st, o_sn, o_sh, o_st, scale, dtype,
+                            workspace && aligned16(workspace) ? workspace : nullptr, workspace_bytes,
+                            (hipStream_t)stream, nullptr, 0, nullptr, 0, 0, 0, stat),
+      "icl_fwd_stats");
 }
 
 int tabicl_icl_fwd_noalloc(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,

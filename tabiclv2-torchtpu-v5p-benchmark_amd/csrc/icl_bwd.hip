@@ -49,6 +49,9 @@ struct IbParams {
   float* mx;
   float* lg;
   float* dd;
+  // optional (bf16, no key mask): the forward's per-query (m, l) [N * H][Tq][2], m in log2 units, l
+  // the sum of exp2(x - m); with it the dq kernel skips its statistics sweep
+  const float* stat;
 };
 
 template <typename T> struct IbTile {
@@ -410,6 +413,9 @@ __device__ __forceinline__ void ic_store(const IcStage& s, bf16* tile) {
 // statistics over 64-key tiles (S^T = K Q^T, K rows from LDS, q in registers); sweep 2 forms
 // dS^T = e (dP^T - D) per key block and dq^T += K^T dS^T over key-block pairs. Stores dq and, per
 // query, m (+inf for a row with no visible key), log2 l and -D for the dk / dv kernel.
+// FS: the statistics come from the forward (p.stat; no key mask), there is no sweep 1, and the score
+// product starts from -(m + log2 l) / c, so that exp2(S^T c) is P itself (one fma fewer per score).
+template <bool FS>
 __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lk[2][IB_T * IC_RS];
   __shared__ __attribute__((aligned(16))) bf16 lv[2][IB_T * IC_RS];
@@ -452,10 +458,22 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
 
   const int ntiles = (valid + IB_T - 1) / IB_T;
   const int tid = threadIdx.x;
-  // sweep 1: per lane and query block, the running max and sum over the lane's keys (4 per key block)
-  float m[2] = {TA_NEG_INF, TA_NEG_INF}, l[2] = {0.f, 0.f};
   IcStage sk, sv;
   float b2r = 0.f;
+  float mq[2], inv[2], lgv[2];
+  if constexpr (FS) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int qi = q0 + 16 * b + l16;
+      const float2 ml = qi < p.Tq ? *(const float2*)(p.stat + (rbase + qi) * 2) : make_float2(0.f, 1.f);
+      const bool any = ml.y > 0.f;
+      mq[b] = any ? ml.x : __builtin_inff();  // no visible key: P = 0 in the dk / dv kernel
+      lgv[b] = any ? __builtin_amdgcn_logf(ml.y) : 0.f;
+      inv[b] = 1.f;
+    }
+  } else {
+  // sweep 1: per lane and query block, the running max and sum over the lane's keys (4 per key block)
+  float m[2] = {TA_NEG_INF, TA_NEG_INF}, l[2] = {0.f, 0.f};
   if (ntiles > 0) {
     ic_load(sk, kbase, 0, valid);
     if (tid < IB_T) b2r = ib_b2(p, n, tid, valid);
@@ -500,7 +518,6 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
       }
     }
   }
-  float mq[2], inv[2], lgv[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     mq[b] = quad_max(m[b]);
@@ -510,6 +527,11 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
     if (!(lt > 0.f)) mq[b] = __builtin_inff();  // no visible key: P = 0 in the dk / dv kernel
   }
   __syncthreads();  // sweep 2 refills both buffers
+  }
+  // FS: the score product's start value -(m + log2 l) / c (rows past Tq hold m = 0, l = 1)
+  float s0[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) s0[b] = FS ? -(mq[b] + lgv[b]) / c : 0.f;
 
   // sweep 2: dq^T l = sum over keys of K^T e (dP^T - D), e = exp2(x - m)
   f32x4 acc[2][4];
@@ -544,11 +566,16 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
         const f32x4 b2 = *(const f32x4*)(lb2[buf] + 16 * kb + 4 * kap);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-          const f32x4 s = ic_mfma(a1, qop[b][1], ic_mfma(a0, qop[b][0], f32x4{0.f, 0.f, 0.f, 0.f}));
+          const f32x4 s = ic_mfma(a1, qop[b][1], ic_mfma(a0, qop[b][0], f32x4{s0[b], s0[b], s0[b], s0[b]}));
           const f32x4 dp = ic_mfma(v1, dop[b][1], ic_mfma(v0, dop[b][0], f32x4{nd[b], nd[b], nd[b], nd[b]}));
           f32x4 e;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) e[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, b2[r]) - mq[b]) * dp[r];
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (FS)
+              e[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, b2[r])) * dp[r];
+            else
+              e[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, b2[r]) - mq[b]) * dp[r];
+          }
           ds[h][b] = cvt_bf16x4(e);
         }
       }
@@ -628,15 +655,15 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dkdv_kernel(IbParams p) {
     const bf16* qbase = (const bf16*)p.q + rbase * IB_D;
     const bf16* dbase = (const bf16*)p.dout + rbase * IB_D;
     const int ntiles = (p.Tq + IB_T - 1) / IB_T;
-    // per-query values: threads 0-63 -(m + log2 l) (m with HB; past Tq -inf, +inf with HB: P = 0),
-    // threads 64-127 -D, threads 128-191 log2 l (HB)
+    // per-query values: threads 0-63 -(m + log2 l) / c, the score product's start value (m with HB;
+    // past Tq -inf, +inf with HB: P = 0), threads 64-127 -D, threads 128-191 log2 l (HB)
     constexpr int NST = HB ? 3 * IB_T : 2 * IB_T;
     auto stat = [&](int q0) -> float {
       const int qi = q0 + (tid & 63);
       const bool in = qi < p.Tq;
       if (tid < IB_T) {
         if (HB) return in ? p.mx[rbase + qi] : __builtin_inff();
-        return in ? -(p.mx[rbase + qi] + p.lg[rbase + qi]) : TA_NEG_INF;
+        return in ? -(p.mx[rbase + qi] + p.lg[rbase + qi]) / c : TA_NEG_INF;
       }
       if (tid < 2 * IB_T) return in ? p.dd[rbase + qi] : 0.f;
       return in ? p.lg[rbase + qi] : 0.f;
@@ -675,7 +702,7 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dkdv_kernel(IbParams p) {
           if constexpr (HB) lgq = *(const f32x4*)(llg[buf] + 16 * qb + 4 * kap);
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const f32x4 s = ic_mfma(aq1, kop[h][1], ic_mfma(aq0, kop[h][0], f32x4{0.f, 0.f, 0.f, 0.f}));
+            const f32x4 s = ic_mfma(aq1, kop[h][1], ic_mfma(aq0, kop[h][0], HB ? f32x4{0.f, 0.f, 0.f, 0.f} : ms));
             const f32x4 dp = ic_mfma(ad1, vop[h][1], ic_mfma(ad0, vop[h][0], ndv));
             f32x4 pr, dsv;
 #pragma unroll
@@ -683,7 +710,7 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dkdv_kernel(IbParams p) {
               if constexpr (HB)
                 pr[r] = __builtin_amdgcn_exp2f((fmaf(s[r], c, b2[h]) - ms[r]) - lgq[r]);
               else
-                pr[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, b2[h]) + ms[r]);
+                pr[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, b2[h]));
               dsv[r] = pr[r] * dp[r];
             }
             pt[g][h] = cvt_bf16x4(pr);
@@ -725,6 +752,7 @@ int64_t tabicl_launch_icl_bwd_ws_bytes(int64_t N, int64_t H, int64_t Tq) { retur
 
 int tabicl_launch_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
                           const float* bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout,
+                          const float* stat,
                           void* dq, void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, float scale,
                           int dtype, void* ws, int64_t ws_bytes, hipStream_t stream) {
   if (ws_bytes < tabicl_launch_icl_bwd_ws_bytes(N, H, Tq)) return (int)hipErrorInvalidValue;
@@ -735,6 +763,7 @@ int tabicl_launch_icl_bwd(const void* q, const void* k, const void* v, const int
   p.bias = bias; p.bias_sn = bias_sn; p.bias_n = (int)bias_n;
   p.N = (int)N; p.H = (int)H; p.Tq = (int)Tq; p.Tkv = (int)Tkv;
   p.scale = scale;
+  p.stat = stat;
   const int64_t part = ib_part_bytes(N, H, Tq);
   p.mx = (float*)ws;
   p.lg = (float*)((char*)ws + part);
@@ -742,7 +771,12 @@ int tabicl_launch_icl_bwd(const void* q, const void* k, const void* v, const int
   const dim3 block(IB_NW * 64);
   if (dtype == 0) {
     const int64_t nqb = (Tq + IC_ROWS - 1) / IC_ROWS, nkb = (Tkv + IC_ROWS - 1) / IC_ROWS;
-    if (nqb > 0) hipLaunchKernelGGL(ic_dq_kernel, dim3((unsigned)(N * H * nqb)), block, 0, stream, p);
+    if (nqb > 0) {
+      if (p.stat && !bias)
+        hipLaunchKernelGGL(ic_dq_kernel<true>, dim3((unsigned)(N * H * nqb)), block, 0, stream, p);
+      else
+        hipLaunchKernelGGL(ic_dq_kernel<false>, dim3((unsigned)(N * H * nqb)), block, 0, stream, p);
+    }
     if (nkb > 0) {
       if (bias)
         hipLaunchKernelGGL(ic_dkdv_kernel<true>, dim3((unsigned)(N * H * nkb)), block, 0, stream, p);

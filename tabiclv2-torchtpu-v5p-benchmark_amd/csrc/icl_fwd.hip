@@ -67,6 +67,10 @@ struct IclParams {
   // ragged calls of the pipelined kernel: [count, work items...] of the work items that hold a live
   // query row, in work-item order (written by icl_live_list_kernel; null: every work item is run)
   const int32_t* live;
+  // optional, calls without a key mask: per query row [N * H][Tq][2] the softmax statistics (m, l) of
+  // the final result, m in log2 units and l the sum of exp2(x - m) (the backward's normalisation),
+  // written by whichever kernel writes the row's output
+  float* stat;
 };
 
 __device__ __forceinline__ int icl_live_rows(const IclParams& p, int n) {
@@ -508,6 +512,7 @@ __global__ __launch_bounds__(NW * 64) void icl_fwd_kernel(IclParams p) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const int qi = qw0 + qc * 32 + lr;
     if (qi < live) {
+      if (p.stat && hh == 0) *(float2*)(p.stat + ((int64_t)nh * p.Tq + qi) * 2) = make_float2(st.m_run[qc] * sc, lt);
       T* orow = (T*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st;
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
@@ -551,6 +556,7 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclParams p) {
     l += w * ml.y;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (p.stat && c4 == 0) *(float2*)(p.stat + row * 2) = make_float2(mstar, l);
   T* dst = (T*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st + c4;
   typename OpVec<T, 4>::type ov;
   ov[0] = from_f32<T>(acc.x * inv); ov[1] = from_f32<T>(acc.y * inv);
@@ -1042,6 +1048,7 @@ swept:
     const float inv = lt[qc] > 0.f ? 1.f / lt[qc] : 0.f;
     const int qi = qw0 + qc * 32 + lr;
     if (qi < live) {
+      if (p.stat && hh == 0) *(float2*)(p.stat + ((int64_t)nh * p.Tq + qi) * 2) = make_float2(-st.nm[qc], lt[qc]);
       bf16* orow = (bf16*)p.o + n * p.o_sn + h * p.o_sh + (int64_t)qi * p.o_st;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
@@ -1277,7 +1284,8 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           int64_t k_sh, int64_t k_st, int64_t v_sn, int64_t v_sh, int64_t v_st,
                           int64_t o_sn, int64_t o_sh, int64_t o_st, float scale, int dtype,
                           void* ws, int64_t ws_bytes, hipStream_t stream, const int32_t* qlen,
-                          int64_t qlen_n, const float* bias, int64_t bias_n, int64_t bias_sn, int list_mode) {
+                          int64_t qlen_n, const float* bias, int64_t bias_n, int64_t bias_sn, int list_mode,
+                          float* stat) {
   IclParams p;
   p.q = q; p.k = k; p.v = v; p.o = out;
   p.valid = valid; p.valid_n = (int)valid_n;
@@ -1293,6 +1301,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.bias = bias; p.bias_n = (int)bias_n; p.bias_sn = bias_sn;
   p.bias_inv_scale = 1.0f / scale;
   p.pvalid = nullptr; p.pok = nullptr; p.pn = 0; p.live = nullptr;
+  p.stat = stat;
   if (D == 128) {
     if (dtype == 0)
       launch<bf16, 4, 1, 128>(p, ws, ws_bytes, stream);

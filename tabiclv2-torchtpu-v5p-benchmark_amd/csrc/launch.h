@@ -24,15 +24,17 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
                           void* ws, int64_t ws_bytes, hipStream_t stream,
                           const int32_t* qlen = nullptr, int64_t qlen_n = 0,
                           const float* bias = nullptr, int64_t bias_n = 0, int64_t bias_sn = 0,
-                          int list_mode = 0);
+                          int list_mode = 0, float* stat = nullptr);
 int64_t tabicl_launch_icl_ws_bytes(int64_t N, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int dtype);
 
 // Backward of the D = 64 ICL attention (icl_bwd.hip) over contiguous [N, H, T, 64] tensors: dq, dk, dv
-// from q, k, v, the forward output o and its gradient dout; valid / bias as in the forward. ws: at least
+// from q, k, v, the forward output o and its gradient dout; valid / bias as in the forward; stat (optional,
+// no bias): the forward's per-query (m, l) from tabicl_launch_icl_fwd(..., stat). ws: at least
 // tabicl_launch_icl_bwd_ws_bytes(N, H, Tq) bytes (per-query statistics passed between the two kernels).
 int64_t tabicl_launch_icl_bwd_ws_bytes(int64_t N, int64_t H, int64_t Tq);
 int tabicl_launch_icl_bwd(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
                           const float* bias, int64_t bias_n, int64_t bias_sn, const void* o, const void* dout,
+                          const float* stat,
                           void* dq, void* dk, void* dv, int64_t N, int64_t H, int64_t Tq, int64_t Tkv, float scale,
                           int dtype, void* ws, int64_t ws_bytes, hipStream_t stream);
 

@@ -117,13 +117,16 @@ def _(q, k, v, valid, scale, key_bias=None):  # noqa: ANN001
 
 @torch.library.custom_op("tabicl::icl_cached_attn_bwd", mutates_args=())
 def _icl_cached_attn_bwd(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], key_bias: Optional[Tensor],
-                         out: Tensor, dout: Tensor, scale: float) -> tuple[Tensor, Tensor, Tensor]:
+                         out: Tensor, dout: Tensor, scale: float,
+                         stat: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
     """Gradients (dq, dk, dv) of icl_cached_attn for the upstream gradient dout, given the forward's
     inputs and its output `out` (tabicl_icl_bwd). The reference's calls with a gradient take autograd
     through its tiled online-softmax attention (results/tpu_patch.diff:158-193, chosen at :263-270);
     here both products and the softmax recompute run in the library's two backward kernels. Keys past
-    the valid length get zero gradients; key_bias gets none (a mask, not a parameter)."""
-    _nat.require_device(q, k, v, valid, key_bias, out, dout)
+    the valid length get zero gradients; key_bias gets none (a mask, not a parameter). stat: the
+    forward's softmax statistics [N, H, Tq, 2] (icl_cached_attn_train; calls without key_bias), which
+    spare the backward its own sweep over the keys."""
+    _nat.require_device(q, k, v, valid, key_bias, out, dout, stat)
     q, k, v, out, dout = (_nat.aligned16(t) for t in (q, k, v, out, dout))
     N, H, Tq, D = q.shape
     Tkv = k.shape[2]
@@ -144,20 +147,80 @@ def _icl_cached_attn_bwd(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor
                 or key_bias.shape[0] not in (1, N) or key_bias.stride(1) != 1:
             raise ValueError(f"key_bias must be a float32 [1 or {N}, {Tkv}] tensor with contiguous rows")
         bptr, bn, bsn = key_bias.data_ptr(), key_bias.shape[0], key_bias.stride(0)
+    sptr = None
+    if stat is not None:
+        if stat.dtype != torch.float32 or stat.shape != (N, H, Tq, 2) or key_bias is not None:
+            raise ValueError(f"stat must be the float32 [{N}, {H}, {Tq}, 2] statistics of a call without key_bias")
+        stat = _nat.aligned16(stat)
+        sptr = stat.data_ptr()
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     nbytes = int(_nat.load().tabicl_icl_bwd_workspace_bytes(N, H, Tq))
     if nbytes < 0:
         raise RuntimeError(f"tabicl_icl_bwd_workspace_bytes: {_nat.last_error()}")
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     _nat.call("tabicl_icl_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, bptr, bn, bsn, out.data_ptr(),
-              dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), N, H, Tq, Tkv, D, float(scale),
+              dout.data_ptr(), sptr, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), N, H, Tq, Tkv, D, float(scale),
               _nat.dtype_code(q.dtype), ws.data_ptr(), ws.numel(), _nat.stream_of(q))
     return dq, dk, dv
 
 
 @_icl_cached_attn_bwd.register_fake
-def _(q, k, v, valid, key_bias, out, dout, scale):  # noqa: ANN001
+def _(q, k, v, valid, key_bias, out, dout, scale, stat=None):  # noqa: ANN001
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+@torch.library.custom_op("tabicl::icl_cached_attn_train", mutates_args=())
+def _icl_cached_attn_train(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor],
+                           scale: float) -> tuple[Tensor, Tensor]:
+    """icl_cached_attn without a key mask for calls with a gradient: returns (out, stat), stat the
+    softmax statistics [N, H, Tq, 2] (m, l) of each query row (tabicl_icl_fwd_stats), which its
+    backward hands to icl_cached_attn_bwd. The forward of the reference's gradient path (autograd
+    through _tiled_online_sdpa, results/tpu_patch.diff:158-193), whose saved tensors play this part."""
+    _nat.require_device(q, k, v, valid)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("icl_cached_attn_train expects [N, H, T, D] tensors")
+    N, H, Tq, D = q.shape
+    Tkv = k.shape[2]
+    if k.shape != v.shape or k.shape[0] != N or k.shape[1] != H or k.shape[3] != D:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if q.dtype != k.dtype or k.dtype != v.dtype:
+        raise ValueError("q, k and v must share a dtype")
+    vptr, vn = None, 0
+    if valid is not None:
+        if valid.dtype != torch.int32 or not valid.is_contiguous():
+            raise ValueError("valid must be a contiguous int32 tensor")
+        vptr, vn = valid.data_ptr(), valid.numel()
+    out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    stat = torch.empty((N, H, Tq, 2), device=q.device, dtype=torch.float32)
+    code = _nat.dtype_code(q.dtype)
+    ws = _workspace(N, H, Tq, Tkv, D, code, q.device)
+    _nat.call("tabicl_icl_fwd_stats", q.data_ptr(), k.data_ptr(), v.data_ptr(), vptr, vn, out.data_ptr(),
+              stat.data_ptr(), N, H, Tq, Tkv, D, *_strides3(q), *_strides3(k), *_strides3(v), *_strides3(out),
+              float(scale), code, None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+              _nat.stream_of(q))
+    return out, stat
+
+
+@_icl_cached_attn_train.register_fake
+def _(q, k, v, valid, scale):  # noqa: ANN001
+    return torch.empty_like(q), q.new_empty((*q.shape[:3], 2), dtype=torch.float32)
+
+
+def _icl_train_setup_context(ctx, inputs, output):  # noqa: ANN001
+    q, k, v, valid, scale = inputs
+    out, stat = output
+    ctx.save_for_backward(q, k, v, valid, out, stat)
+    ctx.scale = scale
+    ctx.mark_non_differentiable(stat)
+
+
+def _icl_train_backward(ctx, grad, grad_stat):  # noqa: ANN001
+    q, k, v, valid, out, stat = ctx.saved_tensors
+    dq, dk, dv = torch.ops.tabicl.icl_cached_attn_bwd(q, k, v, valid, None, out, grad, ctx.scale, stat)
+    return dq, dk, dv, None, None
+
+
+_icl_cached_attn_train.register_autograd(_icl_train_backward, setup_context=_icl_train_setup_context)
 
 
 def _icl_setup_context(ctx, inputs, output):  # noqa: ANN001
@@ -206,6 +269,7 @@ def _(q, k, v, valid, q_len, scale, out, key_bias=None, plan_ws=None):  # noqa: 
 
 
 ICL_FWD = torch.ops.tabicl.icl_cached_attn
+ICL_FWD_TRAIN = torch.ops.tabicl.icl_cached_attn_train
 ICL_FWD_OUT = torch.ops.tabicl.icl_cached_attn_out
 ICL_FWD_RAGGED_OUT = torch.ops.tabicl.icl_cached_attn_ragged_out
 
@@ -295,7 +359,10 @@ def icl_sdpa(q: Tensor, k: Tensor, v: Tensor, valid_kv_len: Optional[Union[int, 
         if kb.shape[0] not in (1, q4.shape[0]):
             raise ValueError(f"key_bias rows {kb.shape[0]} must be 1 or the flattened batch {q4.shape[0]}")
         kb = _nat.aligned16(kb)
-    out = ICL_FWD(q4, k4, v4, valid, float(D) ** -0.5, kb)
+    if kb is None and torch.is_grad_enabled() and (q4.requires_grad or k4.requires_grad or v4.requires_grad):
+        out = ICL_FWD_TRAIN(q4, k4, v4, valid, float(D) ** -0.5)[0]  # keeps the statistics for the backward
+    else:
+        out = ICL_FWD(q4, k4, v4, valid, float(D) ** -0.5, kb)
     return out.reshape(*lead, H, Tq, D)
 
 

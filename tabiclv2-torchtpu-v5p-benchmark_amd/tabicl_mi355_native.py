@@ -57,8 +57,10 @@ SIGNATURES = {
     "tabicl_icl_fwd_masked": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
                               _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_bwd_workspace_bytes": [_i64, _i64, _i64],
-    "tabicl_icl_bwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64,
-                       _i64, _i64, _i64, _f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_bwd": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64,
+                       _i64, _i64, _i64, _i64, _f32, _i32, _c_p, _i64, _c_p],
+    "tabicl_icl_fwd_stats": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _c_p, _i64, _c_p],
     "tabicl_icl_fwd_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _i64, _c_p, _i64, _i64, _i64,
                                _i64, _i64] + [_i64] * 12 + [_f32, _i32, _c_p],
     "tabicl_icl_noalloc_scratch_bytes": [],

@@ -194,3 +194,61 @@ def test_icl_hook_gradients(dev, dtype, monkeypatch):
         b = b.detach().double().cpu().numpy()
         _check(name, a, b, dtype)
     assert float(grads[0][2][:, :, train:].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_icl_train_forward_statistics(dev, dtype):
+    # tabicl::icl_cached_attn_train: the output equals the inference op's, and each row's statistics
+    # (m, l) give its log2-sum-exp: m + log2 l = log2 sum over visible keys of exp2(scale log2(e) q.k)
+    # (float64 from the same rounded inputs); rows with no visible key hold l = 0. Bar: bf16 sums the
+    # bf16-rounded probabilities (the ones its O is made of), each within half a bf16 ulp (2^-8
+    # relative), so log2 l is within 2^-8 / ln 2 < 6e-3: <= 8e-3 in log2 units; fp32 1e-4 x max(1, |lse|)
+    import tabicl_mi355_icl as icl
+    print(f"[icl_bwd] train forward statistics {dtype}", flush=True)
+    N, H, Tq, Tkv = 3, 4, 150, 700
+    q, k, v, _ = _inputs(12, N, H, Tq, Tkv, dtype, qscale=3.0)
+    valid = torch.tensor([700, 333, 0], dtype=torch.int32)
+    qd, kd, vd, vt = q.to(dev), k.to(dev), v.to(dev), valid.to(dev)
+    out, stat = icl.ICL_FWD_TRAIN(qd, kd, vd, vt, 0.125)
+    ref_out = icl.ICL_FWD(qd, kd, vd, vt, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out) or float((out.float() - ref_out.float()).abs().max()) <= ABS[dtype]
+    s = torch.einsum("nhqd,nhkd->nhqk", q.double(), k.double()) * 0.125 * np.log2(np.e)
+    keep = torch.arange(Tkv)[None, :] < valid[:, None].long()
+    s = s.masked_fill(~keep[:, None, None, :], float("-inf"))
+    lse = torch.logsumexp(s * np.log(2.0), dim=-1) / np.log(2.0)
+    st = stat.double().cpu()
+    for n in range(2):
+        got = st[n, ..., 0] + torch.log2(st[n, ..., 1])
+        err = float((got - lse[n]).abs().max())
+        print(f"  n={n}: max |lse err| {err:.3e} (log2 units)", flush=True)
+        assert err <= (8e-3 if dtype == torch.bfloat16 else 1e-4 * max(1.0, float(lse[n].abs().max()))), err
+    assert float(st[2, ..., 1].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_icl_bwd_without_forward_statistics(dev, dtype):
+    # the inference op under autograd (no statistics from the forward: the backward takes its own)
+    # against the oracle, and against the statistics path on the same inputs
+    import tabicl_mi355_icl as icl
+    print(f"[icl_bwd] own statistics {dtype}", flush=True)
+    N, H, Tq, Tkv = 2, 8, 200, 900
+    q, k, v, do = _inputs(13, N, H, Tq, Tkv, dtype)
+    valid = torch.tensor([900, 450], dtype=torch.int32)
+    grads = []
+    for train in (False, True):
+        qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+        if train:
+            out = icl.ICL_FWD_TRAIN(qd, kd, vd, valid.to(dev), 0.125)[0]
+        else:
+            out = icl.ICL_FWD(qd, kd, vd, valid.to(dev), 0.125, None)
+        out.backward(do.to(dev))
+        torch.cuda.synchronize()
+        grads.append((out.detach(), qd.grad, kd.grad, vd.grad))
+    rdq, rdk, rdv = O.splash_sdpa_bwd_ref(q, k, v, do, valid, None, grads[0][0].cpu())
+    for name, g, r in (("dq", grads[0][1], rdq), ("dk", grads[0][2], rdk), ("dv", grads[0][3], rdv)):
+        _check(name, g, r, dtype)
+    for name, a, b in zip(("dq", "dk", "dv"), grads[0][1:], grads[1][1:]):
+        d = float((a.float() - b.float()).abs().max())
+        print(f"  {name}: own vs forward statistics max diff {d:.3e}", flush=True)
+        assert d <= ABS[dtype] * max(1.0, float(b.float().abs().max()))
