@@ -360,7 +360,69 @@ def bench_train(steps: int, warmup: int) -> list:
                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
                                   "over": "kernels_ms"}})
+    recs.append(bench_icl_train(steps, warmup))
     return recs
+
+
+def bench_icl_train(steps: int, warmup: int) -> dict:
+    """fwd+bwd step of the d=64 ICL attention with a gradient (the reference takes autograd through
+    _tiled_online_sdpa for it, results/tpu_patch.diff:158-193, 263-270) at the reference's Splash
+    threshold: 8 tables x 8 heads, 1024 test rows over 16384 train rows, bf16, loss =
+    out.float().square().mean(). Algorithmic FLOPs = the forward's 4 Tq Tkv d per (table, head) x 3.5
+    (backward = 2.5 forwards); MFMA roofline over the attention kernels alone (forward with statistics,
+    dq, dk/dv, from a given upstream gradient). torch's own flash attention (SDPA, same GPU, same
+    inputs) is timed beside it when this build of torch has it."""
+    import torch
+
+    import tabicl_mi355_icl as icl
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(20)
+    N, H, Tq, Tkv = 8, 8, 1024, 16384
+    q = torch.randn(N, H, Tq, 64, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+    k = torch.randn(N, H, Tkv, 64, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+    v = torch.randn(N, H, Tkv, 64, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+    g_out = torch.randn(N, H, Tq, 64, generator=g, device=dev).to(torch.bfloat16)
+
+    def clear():
+        q.grad = k.grad = v.grad = None
+
+    def step():
+        clear()
+        icl.icl_sdpa(q, k, v).float().square().mean().backward()
+
+    def step_kernels():
+        clear()
+        icl.icl_sdpa(q, k, v).backward(g_out)
+
+    ms = _time(step, steps, warmup)
+    ms_k = _time(step_kernels, steps, warmup)
+    flops = 3.5 * 4.0 * N * H * Tq * Tkv * 64
+    tf = flops / (ms_k * 1e-3) / 1e12
+    torch_ms = None
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        from torch.nn import functional as F
+
+        def step_torch():
+            clear()
+            F.scaled_dot_product_attention(q, k, v).backward(g_out)
+
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            torch_ms = round(_time(step_torch, steps, warmup), 4)
+    except (RuntimeError, ImportError):  # no flash kernel in this torch build
+        torch_ms = None
+    clear()
+    return {"metric": "ms per fwd+bwd ICL attention step (d=64, 1024 q over 16384 keys)", "value": round(ms, 4),
+            "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1)",
+            "config": {"workload": f"{N} tables x {H} heads, {Tq} q over {Tkv} keys, d=64, "
+                                   "loss = out.float().square().mean()"},
+            "attn_tflops": round(tf, 2), "kernels_ms": round(ms_k, 4),
+            "kernels_note": "forward (with statistics) + dq + dk/dv kernels from a given bf16 upstream gradient",
+            "torch_flash_sdpa_kernels_ms": torch_ms,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4), "over": "kernels_ms"}}
 
 
 def bench_hxf(steps: int, warmup: int) -> list:
