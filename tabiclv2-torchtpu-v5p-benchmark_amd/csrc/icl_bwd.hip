@@ -6,18 +6,15 @@
 // a gradient, diff:263-270). With P recomputed in fp32:
 //   dP = dO V^T,  D = sum over the 64 dims of dO * O,  dS = P (dP - D) (cast to the input dtype),
 //   dq = scale dS k,  dk = scale dS^T q,  dv = cast(P)^T dO   (fp32 accumulation).
-// Two kernels, no atomics, every gradient element written once:
-//   ib_dq_kernel   workgroup = ((n, h), 64 queries), wave = 16 queries. Keys stream through LDS in
-//                  64-key tiles: a first sweep takes each query's softmax statistics (row maximum m and
-//                  log2 of the sum, log2 units) and D, written to the workspace; a second sweep forms
-//                  e = exp2(x - m), dP - D (the dP product's accumulator input is -D) and dq' += e (dP - D) k,
-//                  scaled by 1 / l at the end.
-//   ib_dkdv_kernel workgroup = ((n, h), 64 keys), wave = 16 keys. Queries stream through LDS in 64-row
-//                  tiles with their statistics and -D: P, dP - D, dS, dk' and dv.
-// MFMA 16x16x16 (bf16) or 4 x 16x16x4 (fp32) in the lane layout of mfma16x16x16 (common.h); the head's
-// 64 dims are four 16-dim chunks of every contraction over dims. Transposed operands come from
-// ds_read_b64_tr_b16 on the row-major tiles (bf16) or from transposed copies (fp32). All tensors are
-// contiguous [N, H, T, 64].
+// Two kernels per call, no atomics, every gradient element written once: a dq kernel (one workgroup per
+// (n, h) and query block, keys streamed through LDS) that also leaves each query's softmax statistics
+// and D in the workspace, then a dk / dv kernel (one workgroup per (n, h) and key block, queries and
+// their statistics streamed through LDS).
+//   bf16: ic_dq_kernel / ic_dkdv_kernel, 16x16x32 products with two 16-row blocks per wave; the
+//         statistics come from the forward (tabicl_icl_fwd_stats) when the call has no key mask.
+//   fp32: ib_dq_kernel / ib_dkdv_kernel, 4 x 16x16x4 products in the lane layout of mfma16x16x16
+//         (common.h), one 16-row block per wave, transposed operands from transposed LDS copies.
+// All tensors are contiguous [N, H, T, 64].
 #include "common.h"
 #include "launch.h"
 
@@ -54,12 +51,10 @@ struct IbParams {
   const float* stat;
 };
 
-template <typename T> struct IbTile {
-  static constexpr int PAD = 16 / sizeof(T);
-  static constexpr int RSTR = IB_D + PAD;  // row-major tile: 64 dims per row
-  static constexpr int TSTR = IB_T + PAD;  // transposed copy (fp32 only): 64 rows of IB_T
-  static constexpr int T_ELEMS = sizeof(T) == 2 ? 4 : IB_D * TSTR;
-};
+// fp32 tiles: row-major [64 rows][64 dims] and the transposed copy [64 dims][64 rows], each row padded
+// by 16 bytes
+constexpr int IB_RSTR = IB_D + 4;
+constexpr int IB_TSTR = IB_T + 4;
 
 __device__ __forceinline__ int ib_valid(const IbParams& p, int n) {
   if (!p.valid) return p.Tkv;
@@ -75,56 +70,39 @@ __device__ __forceinline__ float ib_b2(const IbParams& p, int n, int key, int va
   return fmaxf(p.bias[(int64_t)(p.bias_n == 1 ? 0 : n) * p.bias_sn + key] * TA_LOG2E, IB_BIAS_FLOOR);
 }
 
-// Rows r0 .. r0 + 63 of a [rows, 64] slab into a row-major tile (and, for fp32 with a non-null tcopy,
-// its transposed copy); rows at or past lim are zero.
-template <typename T>
-__device__ __forceinline__ void ib_fill(const T* base, int r0, int lim, T* tile, T* tcopy) {
-  typedef IbTile<T> L;
-  typedef typename OpVec<T, 4>::type Op4;
+// Rows r0 .. r0 + 63 of a [rows, 64] fp32 slab into a row-major tile (and, with a non-null tcopy, its
+// transposed copy); rows at or past lim are zero.
+__device__ __forceinline__ void ib_fill(const float* base, int r0, int lim, float* tile, float* tcopy) {
   for (int u = threadIdx.x; u < IB_T * (IB_D / 4); u += IB_NW * 64) {
     const int row = u >> 4, c = (u & 15) * 4;
-    Op4 x;
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    if (r0 + row < lim) x = *(const f32x4*)(base + (int64_t)(r0 + row) * IB_D + c);
+    *(f32x4*)(tile + row * IB_RSTR + c) = x;
+    if (tcopy != nullptr) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x[j] = from_f32<T>(0.f);
-    if (r0 + row < lim) x = *(const Op4*)(base + (int64_t)(r0 + row) * IB_D + c);
-    *(Op4*)(tile + row * L::RSTR + c) = x;
-    if constexpr (sizeof(T) == 4) {
-      if (tcopy != nullptr) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) tcopy[(c + j) * L::TSTR + row] = x[j];
-      }
+      for (int j = 0; j < 4; ++j) tcopy[(c + j) * IB_TSTR + row] = x[j];
     }
   }
 }
 
 // Row operand: dims 16 jd + 4 kap .. + 3 of tile row `row`.
-template <typename T>
-__device__ __forceinline__ typename OpVec<T, 4>::type ib_row(const T* tile, int row, int jd, int kap) {
-  return *(const typename OpVec<T, 4>::type*)(tile + row * IbTile<T>::RSTR + 16 * jd + 4 * kap);
+__device__ __forceinline__ f32x4 ib_row(const float* tile, int row, int jd, int kap) {
+  return *(const f32x4*)(tile + row * IB_RSTR + 16 * jd + 4 * kap);
 }
 
-// Transposed operand A[i][4 kap + j] = tile[row0 + 4 kap + j][16 jd + i] for lane (i = l16, kap).
-template <typename T>
-__device__ __forceinline__ typename OpVec<T, 4>::type ib_rowT(const T* tile, const T* tcopy, int row0, int jd,
-                                                             int l16, int kap) {
-  typedef IbTile<T> L;
-  if constexpr (sizeof(T) == 2) {
-    const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4*)(tile + (row0 + 4 * kap + (l16 >> 2)) * L::RSTR + 16 * jd + 4 * (l16 & 3)));
-    return __builtin_bit_cast(bf16x4, t);
-  } else {
-    return *(const f32x4*)(tcopy + (16 * jd + l16) * L::TSTR + row0 + 4 * kap);
-  }
+// Transposed operand A[i][4 kap + j] = tile[row0 + 4 kap + j][16 jd + i] for lane (i = l16, kap), from
+// the transposed copy.
+__device__ __forceinline__ f32x4 ib_rowT(const float* tcopy, int row0, int jd, int l16, int kap) {
+  return *(const f32x4*)(tcopy + (16 * jd + l16) * IB_TSTR + row0 + 4 * kap);
 }
 
 // x = S^T log2e + b2 of keys 16 kt + 4 kap + r (tile rows) against this lane's query: the score
 // product over the four dim chunks.
-template <typename T>
-__device__ __forceinline__ f32x4 ib_scores_t(const T* lk, const float* lb2, const typename OpVec<T, 4>::type (&qop)[4],
-                                             int kt, int l16, int kap, float c) {
+__device__ __forceinline__ f32x4 ib_scores_t(const float* lk, const float* lb2, const f32x4 (&qop)[4], int kt,
+                                             int l16, int kap, float c) {
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int jd = 0; jd < 4; ++jd) s = mfma16x16x16(ib_row<T>(lk, 16 * kt + l16, jd, kap), qop[jd], s);
+  for (int jd = 0; jd < 4; ++jd) s = mfma16x16x16(ib_row(lk, 16 * kt + l16, jd, kap), qop[jd], s);
   const f32x4 b2 = *(const f32x4*)(lb2 + 16 * kt + 4 * kap);
   f32x4 x;
 #pragma unroll
@@ -132,13 +110,15 @@ __device__ __forceinline__ f32x4 ib_scores_t(const T* lk, const float* lb2, cons
   return x;
 }
 
-template <typename T>
+// fp32 dq: workgroup = ((n, h), 64 queries), wave = 16 queries. Keys stream through LDS in 64-key tiles:
+// a first sweep takes each query's softmax statistics (row maximum m and log2 of the sum, log2 units)
+// and D, written to the workspace; a second sweep forms e = exp2(x - m), dP - D (the dP product's
+// accumulator input is -D) and dq' += e (dP - D) k, scaled by 1 / l at the end.
 __global__ __launch_bounds__(IB_NW * 64) void ib_dq_kernel(IbParams p) {
-  typedef IbTile<T> L;
-  typedef typename OpVec<T, 4>::type Op4;
-  __shared__ __attribute__((aligned(16))) T lk[IB_T * L::RSTR];
-  __shared__ __attribute__((aligned(16))) T lkt[L::T_ELEMS];
-  __shared__ __attribute__((aligned(16))) T lv[IB_T * L::RSTR];
+  typedef f32x4 Op4;
+  __shared__ __attribute__((aligned(16))) float lk[IB_T * IB_RSTR];
+  __shared__ __attribute__((aligned(16))) float lkt[IB_D * IB_TSTR];
+  __shared__ __attribute__((aligned(16))) float lv[IB_T * IB_RSTR];
   __shared__ __attribute__((aligned(16))) float lb2[IB_T];
 
   const int nqb = (p.Tq + IB_T - 1) / IB_T;
@@ -148,27 +128,25 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dq_kernel(IbParams p) {
   const int valid = ib_valid(p, n);
   const int qi = qb * IB_T + wave * 16 + l16;
   const bool qok = qi < p.Tq;
-  const T* qrow = (const T*)p.q + ((int64_t)nh * p.Tq + qi) * IB_D;
-  const T* kbase = (const T*)p.k + (int64_t)nh * p.Tkv * IB_D;
-  const T* vbase = (const T*)p.v + (int64_t)nh * p.Tkv * IB_D;
+  const float* qrow = (const float*)p.q + ((int64_t)nh * p.Tq + qi) * IB_D;
+  const float* kbase = (const float*)p.k + (int64_t)nh * p.Tkv * IB_D;
+  const float* vbase = (const float*)p.v + (int64_t)nh * p.Tkv * IB_D;
   const float c = p.scale * TA_LOG2E;
 
   // q and dO operands of query qi (B operands of S^T = K Q^T and dP^T = V dO^T), D
   Op4 qop[4], dop[4];
   float dsum = 0.f;
 #pragma unroll
-  for (int jd = 0; jd < 4; ++jd)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { qop[jd][j] = from_f32<T>(0.f); dop[jd][j] = from_f32<T>(0.f); }
+  for (int jd = 0; jd < 4; ++jd) qop[jd] = dop[jd] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (qok) {
     const int64_t orow = ((int64_t)nh * p.Tq + qi) * IB_D;
 #pragma unroll
     for (int jd = 0; jd < 4; ++jd) {
       qop[jd] = *(const Op4*)(qrow + 16 * jd + 4 * kap);
-      dop[jd] = *(const Op4*)((const T*)p.dout + orow + 16 * jd + 4 * kap);
-      const Op4 ov = *(const Op4*)((const T*)p.o + orow + 16 * jd + 4 * kap);
+      dop[jd] = *(const Op4*)((const float*)p.dout + orow + 16 * jd + 4 * kap);
+      const Op4 ov = *(const Op4*)((const float*)p.o + orow + 16 * jd + 4 * kap);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dsum += to_f32<T>(dop[jd][j]) * to_f32<T>(ov[j]);
+      for (int j = 0; j < 4; ++j) dsum += dop[jd][j] * ov[j];
     }
   }
   dsum = xor_sum(dsum, 16);
@@ -179,14 +157,14 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dq_kernel(IbParams p) {
   float m = TA_NEG_INF, l = 0.f;
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
-    ib_fill<T>(kbase, t * IB_T, valid, lk, (T*)nullptr);
+    ib_fill(kbase, t * IB_T, valid, lk, nullptr);
     for (int j = threadIdx.x; j < IB_T; j += IB_NW * 64) lb2[j] = ib_b2(p, n, t * IB_T + j, valid);
     __syncthreads();
     f32x4 x[4];
     float tm = TA_NEG_INF;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      x[kt] = ib_scores_t<T>(lk, lb2, qop, kt, l16, kap, c);
+      x[kt] = ib_scores_t(lk, lb2, qop, kt, l16, kap, c);
 #pragma unroll
       for (int r = 0; r < 4; ++r) tm = fmaxf(tm, x[kt][r]);
     }
@@ -213,32 +191,32 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dq_kernel(IbParams p) {
   const f32x4 cnd = {-dsum, -dsum, -dsum, -dsum};
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
-    ib_fill<T>(kbase, t * IB_T, valid, lk, lkt);
-    ib_fill<T>(vbase, t * IB_T, valid, lv, (T*)nullptr);
+    ib_fill(kbase, t * IB_T, valid, lk, lkt);
+    ib_fill(vbase, t * IB_T, valid, lv, nullptr);
     for (int j = threadIdx.x; j < IB_T; j += IB_NW * 64) lb2[j] = ib_b2(p, n, t * IB_T + j, valid);
     __syncthreads();
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      const f32x4 x = ib_scores_t<T>(lk, lb2, qop, kt, l16, kap, c);
+      const f32x4 x = ib_scores_t(lk, lb2, qop, kt, l16, kap, c);
       f32x4 dp = cnd;
 #pragma unroll
-      for (int jd = 0; jd < 4; ++jd) dp = mfma16x16x16(ib_row<T>(lv, 16 * kt + l16, jd, kap), dop[jd], dp);
+      for (int jd = 0; jd < 4; ++jd) dp = mfma16x16x16(ib_row(lv, 16 * kt + l16, jd, kap), dop[jd], dp);
       Op4 ds;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ds[r] = from_f32<T>(__builtin_amdgcn_exp2f(x[r] - mq) * dp[r]);
+      for (int r = 0; r < 4; ++r) ds[r] = __builtin_amdgcn_exp2f(x[r] - mq) * dp[r];
 #pragma unroll
-      for (int jd = 0; jd < 4; ++jd) acc[jd] = mfma16x16x16(ib_rowT<T>(lk, lkt, 16 * kt, jd, l16, kap), ds, acc[jd]);
+      for (int jd = 0; jd < 4; ++jd) acc[jd] = mfma16x16x16(ib_rowT(lkt, 16 * kt, jd, l16, kap), ds, acc[jd]);
       __builtin_amdgcn_sched_barrier(0);  // one key block at a time: hoisting them costs registers
     }
   }
   if (qok) {
     const float ysc = p.scale * inv;
-    T* dqrow = (T*)p.dq + ((int64_t)nh * p.Tq + qi) * IB_D;
+    float* dqrow = (float*)p.dq + ((int64_t)nh * p.Tq + qi) * IB_D;
 #pragma unroll
     for (int jd = 0; jd < 4; ++jd) {
       Op4 out;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) out[r] = from_f32<T>(acc[jd][r] * ysc);
+      for (int r = 0; r < 4; ++r) out[r] = acc[jd][r] * ysc;
       *(Op4*)(dqrow + 16 * jd + 4 * kap) = out;
     }
     if (kap == 0) {
@@ -250,14 +228,14 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dq_kernel(IbParams p) {
   }
 }
 
-template <typename T>
+// fp32 dk / dv: workgroup = ((n, h), 64 keys), wave = 16 keys. Queries stream through LDS in 64-row tiles
+// with their statistics and -D: P, dP - D, dS, dk' and dv.
 __global__ __launch_bounds__(IB_NW * 64) void ib_dkdv_kernel(IbParams p) {
-  typedef IbTile<T> L;
-  typedef typename OpVec<T, 4>::type Op4;
-  __shared__ __attribute__((aligned(16))) T lq[IB_T * L::RSTR];
-  __shared__ __attribute__((aligned(16))) T lqt[L::T_ELEMS];
-  __shared__ __attribute__((aligned(16))) T ld[IB_T * L::RSTR];
-  __shared__ __attribute__((aligned(16))) T ldt[L::T_ELEMS];
+  typedef f32x4 Op4;
+  __shared__ __attribute__((aligned(16))) float lq[IB_T * IB_RSTR];
+  __shared__ __attribute__((aligned(16))) float lqt[IB_D * IB_TSTR];
+  __shared__ __attribute__((aligned(16))) float ld[IB_T * IB_RSTR];
+  __shared__ __attribute__((aligned(16))) float ldt[IB_D * IB_TSTR];
   __shared__ __attribute__((aligned(16))) float lmx[IB_T];
   __shared__ __attribute__((aligned(16))) float llg[IB_T];
   __shared__ __attribute__((aligned(16))) float lnd[IB_T];
@@ -277,25 +255,23 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dkdv_kernel(IbParams p) {
     // k and V operands of key kj (B operands of S = Q K^T and dP = dO V^T) and its b2
     Op4 kop[4], vop[4];
 #pragma unroll
-    for (int jd = 0; jd < 4; ++jd)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { kop[jd][j] = from_f32<T>(0.f); vop[jd][j] = from_f32<T>(0.f); }
+    for (int jd = 0; jd < 4; ++jd) kop[jd] = vop[jd] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (kj < valid) {
       const int64_t row = ((int64_t)nh * p.Tkv + kj) * IB_D;
 #pragma unroll
       for (int jd = 0; jd < 4; ++jd) {
-        kop[jd] = *(const Op4*)((const T*)p.k + row + 16 * jd + 4 * kap);
-        vop[jd] = *(const Op4*)((const T*)p.v + row + 16 * jd + 4 * kap);
+        kop[jd] = *(const Op4*)((const float*)p.k + row + 16 * jd + 4 * kap);
+        vop[jd] = *(const Op4*)((const float*)p.v + row + 16 * jd + 4 * kap);
       }
     }
     const float b2 = ib_b2(p, n, kj, valid);
-    const T* qbase = (const T*)p.q + (int64_t)nh * p.Tq * IB_D;
-    const T* dbase = (const T*)p.dout + (int64_t)nh * p.Tq * IB_D;
+    const float* qbase = (const float*)p.q + (int64_t)nh * p.Tq * IB_D;
+    const float* dbase = (const float*)p.dout + (int64_t)nh * p.Tq * IB_D;
     const int ntiles = (p.Tq + IB_T - 1) / IB_T;
     for (int t = 0; t < ntiles; ++t) {
       __syncthreads();
-      ib_fill<T>(qbase, t * IB_T, p.Tq, lq, lqt);
-      ib_fill<T>(dbase, t * IB_T, p.Tq, ld, ldt);
+      ib_fill(qbase, t * IB_T, p.Tq, lq, lqt);
+      ib_fill(dbase, t * IB_T, p.Tq, ld, ldt);
       for (int j = threadIdx.x; j < IB_T; j += IB_NW * 64) {
         const int qi = t * IB_T + j;
         const int64_t s = (int64_t)nh * p.Tq + qi;
@@ -312,8 +288,8 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dkdv_kernel(IbParams p) {
         f32x4 dp = *(const f32x4*)(lnd + 16 * qs + 4 * kap);
 #pragma unroll
         for (int jd = 0; jd < 4; ++jd) {
-          s = mfma16x16x16(ib_row<T>(lq, 16 * qs + l16, jd, kap), kop[jd], s);
-          dp = mfma16x16x16(ib_row<T>(ld, 16 * qs + l16, jd, kap), vop[jd], dp);
+          s = mfma16x16x16(ib_row(lq, 16 * qs + l16, jd, kap), kop[jd], s);
+          dp = mfma16x16x16(ib_row(ld, 16 * qs + l16, jd, kap), vop[jd], dp);
         }
         const f32x4 ms = *(const f32x4*)(lmx + 16 * qs + 4 * kap);
         const f32x4 ls = *(const f32x4*)(llg + 16 * qs + 4 * kap);
@@ -321,13 +297,13 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dkdv_kernel(IbParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float pr = __builtin_amdgcn_exp2f((fmaf(s[r], c, b2) - ms[r]) - ls[r]);
-          pt[r] = from_f32<T>(pr);
-          ds[r] = from_f32<T>(pr * dp[r]);
+          pt[r] = pr;
+          ds[r] = pr * dp[r];
         }
 #pragma unroll
         for (int jd = 0; jd < 4; ++jd) {
-          dv[jd] = mfma16x16x16(ib_rowT<T>(ld, ldt, 16 * qs, jd, l16, kap), pt, dv[jd]);
-          dk[jd] = mfma16x16x16(ib_rowT<T>(lq, lqt, 16 * qs, jd, l16, kap), ds, dk[jd]);
+          dv[jd] = mfma16x16x16(ib_rowT(ldt, 16 * qs, jd, l16, kap), pt, dv[jd]);
+          dk[jd] = mfma16x16x16(ib_rowT(lqt, 16 * qs, jd, l16, kap), ds, dk[jd]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -340,11 +316,11 @@ __global__ __launch_bounds__(IB_NW * 64) void ib_dkdv_kernel(IbParams p) {
       Op4 ok, ov;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        ok[r] = from_f32<T>(dk[jd][r] * p.scale);
-        ov[r] = from_f32<T>(dv[jd][r]);
+        ok[r] = dk[jd][r] * p.scale;
+        ov[r] = dv[jd][r];
       }
-      *(Op4*)((T*)p.dk + row + 16 * jd + 4 * kap) = ok;
-      *(Op4*)((T*)p.dv + row + 16 * jd + 4 * kap) = ov;
+      *(Op4*)((float*)p.dk + row + 16 * jd + 4 * kap) = ok;
+      *(Op4*)((float*)p.dv + row + 16 * jd + 4 * kap) = ov;
     }
   }
 }
@@ -785,8 +761,8 @@ int tabicl_launch_icl_bwd(const void* q, const void* k, const void* v, const int
     }
   } else {
     const int64_t nqb = (Tq + IB_T - 1) / IB_T, nkb = (Tkv + IB_T - 1) / IB_T;
-    if (nqb > 0) hipLaunchKernelGGL(ib_dq_kernel<float>, dim3((unsigned)(N * H * nqb)), block, 0, stream, p);
-    if (nkb > 0) hipLaunchKernelGGL(ib_dkdv_kernel<float>, dim3((unsigned)(N * H * nkb)), block, 0, stream, p);
+    if (nqb > 0) hipLaunchKernelGGL(ib_dq_kernel, dim3((unsigned)(N * H * nqb)), block, 0, stream, p);
+    if (nkb > 0) hipLaunchKernelGGL(ib_dkdv_kernel, dim3((unsigned)(N * H * nkb)), block, 0, stream, p);
   }
   return (int)hipGetLastError();
 }
