@@ -252,3 +252,42 @@ def test_icl_bwd_without_forward_statistics(dev, dtype):
         d = float((a.float() - b.float()).abs().max())
         print(f"  {name}: own vs forward statistics max diff {d:.3e}", flush=True)
         assert d <= ABS[dtype] * max(1.0, float(b.float().abs().max()))
+
+
+def test_icl_bwd_bench_shape_sampled(dev):
+    # the bench's training shape (8 tables x 8 heads, 1024 q over 16384 keys, bf16, q x 2): three (n, h)
+    # slices against the float64 oracle, and over every slice two identities of the exact gradients:
+    # sum over keys of dv = sum over queries of dO (each P row sums to 1) and sum over keys of dk = 0
+    # (each dS row sums to 0: the -D term), both within 2e-3 of the sums' magnitudes (measured ~1.5e-4;
+    # a dropped -D term leaves sum dk = scale sum_i q_i D_i, ~3% of them here)
+    print("[icl_bwd] bench shape, sampled slices and identities", flush=True)
+    icl = _icl()
+    dtype = torch.bfloat16
+    N, H, Tq, Tkv = 8, 8, 1024, 16384
+    g = torch.Generator(device=dev).manual_seed(21)
+    q = (torch.randn(N, H, Tq, 64, generator=g, device=dev) * 2).to(dtype).requires_grad_()
+    k = torch.randn(N, H, Tkv, 64, generator=g, device=dev).to(dtype).requires_grad_()
+    v = torch.randn(N, H, Tkv, 64, generator=g, device=dev).to(dtype).requires_grad_()
+    do = torch.randn(N, H, Tq, 64, generator=g, device=dev).to(dtype)
+    out = icl.icl_sdpa(q, k, v)
+    out.backward(do)
+    torch.cuda.synchronize()
+    for t in (q.grad, k.grad, v.grad):
+        assert bool(torch.isfinite(t.float()).all())
+    sdv = v.grad.double().sum(dim=2)
+    sdo = do.double().sum(dim=2)
+    err_v = float((sdv - sdo).abs().max())
+    sdk = k.grad.double().sum(dim=2)
+    err_k = float(sdk.abs().max())
+    mag_k = float(k.grad.double().abs().sum(dim=2).max())
+    print(f"  sum dv - sum dO: {err_v:.3e} (max |sum dO| {float(sdo.abs().max()):.3e}); "
+          f"max |sum dk| {err_k:.3e} (sum |dk| up to {mag_k:.3e})", flush=True)
+    assert err_v <= 2e-3 * max(1.0, float(sdo.abs().max()))
+    assert err_k <= 2e-3 * mag_k
+    for n, h in ((0, 0), (3, 5), (7, 7)):
+        sl = (slice(n, n + 1), slice(h, h + 1))
+        args = [t[sl].detach().cpu() for t in (q, k, v, do)]
+        rdq, rdk, rdv = O.splash_sdpa_bwd_ref(*args, None, None, out[sl].detach().cpu())
+        _check(f"dq[{n},{h}]", q.grad[sl], rdq, dtype)
+        _check(f"dk[{n},{h}]", k.grad[sl], rdk, dtype)
+        _check(f"dv[{n},{h}]", v.grad[sl], rdv, dtype)
