@@ -8,7 +8,8 @@ equal (bit for bit) an eager call of the same op on the same inputs, with a sync
 between. Cases: the cached ICL attention with a valid length (pipelined kernel, trust-flag gate, key
 split merge), the same with a prefix key mask (device-side prefix reduction), the ragged ICL entry
 point (device-built list of live work items, row counts rewritten between replays), the persistent
-row-stage kernel (pk_self, RoPE) and the few-query streaming hxq with a key mask.
+row-stage kernel (pk_self, RoPE), the few-query streaming hxq with a key mask, and a training step of
+the ICL attention (forward with statistics, autograd backward through the dq and dk/dv kernels).
 """
 import pytest
 import torch
@@ -140,3 +141,29 @@ def test_graph_hxq_key_mask(dev):
     refresh(0)
     print("[graph] hxq key mask", flush=True)
     _replays(dev, lambda: pk.hxq_attention(q, kv, None, H, bias), (q, kv, bias), refresh)
+
+
+def test_graph_icl_forward_backward(dev):
+    # forward + backward captured together (gradients allocated from the graph's pool inside the
+    # capture); q and the valid length rewritten between replays
+    import tabicl_mi355_icl as icl
+    g = torch.Generator(device=dev).manual_seed(75)
+    q = torch.randn(4, 8, 700, 64, generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    k = torch.randn(4, 8, 5000, 64, generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    v = torch.randn(4, 8, 5000, 64, generator=g, device=dev).to(torch.bfloat16).requires_grad_()
+    go = torch.randn(4, 8, 700, 64, generator=g, device=dev).to(torch.bfloat16)
+    valid = torch.tensor([4500, 5000, 3000, 1], dtype=torch.int32, device=dev)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = icl.icl_sdpa(q, k, v, valid)
+        out.backward(go)
+        return torch.cat([out.detach().flatten(), q.grad.flatten(), k.grad.flatten(), v.grad.flatten()])
+
+    def refresh(i):
+        with torch.no_grad():
+            q.copy_(torch.randn(q.shape, generator=g, device=dev).to(torch.bfloat16))
+            valid[0] = 4000 + 300 * i
+
+    print("[graph] icl forward + backward", flush=True)
+    _replays(dev, step, (q, k, v, go, valid), refresh)
