@@ -87,6 +87,22 @@ def test_bad_arguments_rejected_before_launch():
     assert st == 1 and "key_bias" in nat.last_error()
     st = lib.tabicl_hxf_fwd_masked(None, 0, a, 3, a, 1, a, a, 2, 64, 300, 128, 0, None, 0, None)
     assert st == 1 and "key_bias" in nat.last_error()
+    # ICL gradient path: the statistics forward needs its stat array; the backward takes forward
+    # statistics only without a key mask, needs a positive scale and a workspace of the size it names
+    st = lib.tabicl_icl_fwd_stats(a, a, a, None, 0, a, None, 2, 1, 3, 64, 64, *([64] * 12), 0.125, 0, None, 0, None)
+    assert st == 1 and "stat" in nat.last_error()
+    bwd = lambda bias, stat, scale, ws, wsb: lib.tabicl_icl_bwd(  # noqa: E731
+        a, a, a, None, 0, bias, 1, 64, a, a, stat, a, a, a, 2, 1, 3, 64, 64, scale, 0, ws, wsb, None)
+    st = bwd(a, a, 0.125, a, 1 << 20)
+    assert st == 1 and "key mask" in nat.last_error()
+    st = bwd(None, None, -0.125, a, 1 << 20)
+    assert st == 1 and "scale" in nat.last_error()
+    need = lib.tabicl_icl_bwd_workspace_bytes(2, 1, 3)
+    assert need > 0 and lib.tabicl_icl_bwd_workspace_bytes(-1, 1, 3) < 0
+    st = bwd(None, a, 0.125, a, need - 1)
+    assert st == 1 and "workspace" in nat.last_error()
+    st = bwd(None, a, 0.125, None, need)
+    assert st == 1 and "workspace" in nat.last_error()
     with pytest.raises(nat.UnsupportedShapeError):
         nat.check(1, "x")
 
