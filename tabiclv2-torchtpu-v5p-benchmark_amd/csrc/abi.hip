@@ -449,7 +449,8 @@ int tabicl_icl_bwd(const void* q, const void* k, const void* v, const int32_t* v
   if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(stat))
     return fail(1, "icl_bwd: pointers must be 16-byte aligned");
   if (stat && key_bias) return fail(1, "icl_bwd: forward statistics are taken for calls without a key mask only");
-  if (N * H * ((Tkv + 63) / 64) > (1LL << 31) - 1) return fail(1, "icl_bwd: grid too large");
+  if (N * H * ((Tkv + 63) / 64) > (1LL << 31) - 1 || N * H * ((Tq + 63) / 64) > (1LL << 31) - 1)
+    return fail(1, "icl_bwd: grid too large");
   if (N == 0 || H == 0) return 0;
   if (!workspace || !aligned16(workspace) || workspace_bytes < tabicl_launch_icl_bwd_ws_bytes(N, H, Tq))
     return fail(1, "icl_bwd: workspace of %lld bytes (16-byte aligned) required",
