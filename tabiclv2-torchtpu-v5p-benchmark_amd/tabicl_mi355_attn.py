@@ -579,7 +579,16 @@ def _freqs_stamp(rope_mod) -> tuple:  # noqa: ANN001
 
 
 def _tables(rope_mod, L: int, E: int, h: int, device):  # noqa: ANN001
-    """The shared-head form of rope_tables(...), cached per rope module."""
+    """The shared-head form of rope_tables(...), cached per rope module. Under torch.compile the tables
+    are computed in the traced graph instead (the cache key holds the frequencies' storage address,
+    which a trace cannot guard on), as the reference computes them at trace time."""
+    if torch.compiler.is_compiling():
+        if rope_mod is None:
+            return torch.ones(1, E, device=device), torch.zeros(1, E, device=device), 0, 0, 0
+        cos, sin, rc, half, rot = rope_tables(rope_mod, L, E, h, device)
+        if rc:
+            cos, sin, rc = _shared_tables(cos, sin, rc, E // h)
+        return cos, sin, rc, half, rot
     if rope_mod is None:
         # rope code 0: the kernels never read the tables, so one cached row stands in for [L, E]
         key = (E, str(device))

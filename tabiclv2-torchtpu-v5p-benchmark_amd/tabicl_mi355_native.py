@@ -144,8 +144,9 @@ def ptr(t: torch.Tensor | None) -> int | None:
 def aligned16(t: torch.Tensor) -> torch.Tensor:
     """t when it is contiguous and starts on a 16-byte boundary (what the entry points require of a
     key bias), else a contiguous copy in a fresh allocation (the caching allocator aligns those).
-    `.contiguous()` alone returns a contiguous view that starts off the boundary unchanged."""
-    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+    `.contiguous()` alone returns a contiguous view that starts off the boundary unchanged. Under
+    torch.compile (no storage address to test) always the copy."""
+    if not torch.compiler.is_compiling() and t.is_contiguous() and t.data_ptr() % 16 == 0:
         return t
     return t.clone(memory_format=torch.contiguous_format)
 
@@ -164,8 +165,11 @@ def call(name: str, *args) -> None:
     check(getattr(lib, name)(*args), name)
 
 
+@torch.compiler.assume_constant_result
 def supported(op: int, Lq: int, Lk: int, E: int, h: int, dt: torch.dtype) -> bool:
-    """Shape predicate of the library (pure host logic; needs the library loaded, no GPU)."""
+    """Shape predicate of the library (pure host logic; needs the library loaded, no GPU). A trace
+    (torch.compile) takes its value for the traced shapes as a constant, as the reference's pure-Python
+    predicates are."""
     try:
         code = dtype_code(dt)
     except UnsupportedShapeError:
