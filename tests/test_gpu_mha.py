@@ -6,7 +6,9 @@ the HIP op of the route ran, and the output is compared with the same upstream s
 running torch math on the same GPU from the same inputs (the projections are the same GEMMs on both
 sides, so the difference is the kernel's).
 
-Bar (written here): max abs error <= 2e-2 with bf16 activations, <= 1e-4 with fp32. The long-key routes
+Bar (written here): max abs error <= 2e-2 with bf16 activations, <= 1e-4 with fp32; training
+gradients through the dispatch (mean-square loss: small gradients) to the same factors times the
+reference gradient's largest entry. The long-key routes
 (cached ICL over 45,000 / 5,000 keys, ISAB-1 over 50,000 rows) also take the scale-aware bar of
 tests/parity.py on the attention's part of the block output (output minus the out-projection bias):
 max abs error <= 2e-2 (bf16) / 1e-3 (fp32) times its max. The SSMax stand-in scales q by s_h log n
@@ -204,3 +206,60 @@ def test_small_head_attention_pk_branch(dev, mha, monkeypatch, dtype):
         ref2[:, i:i + 1] = O.attention_f64(q[:, i:i + 1].double().numpy(), k.double().numpy(), v.double().numpy(), H,
                                            qmask[:, 0, i].double().numpy())
     assert float(np.abs(out2.double().cpu().numpy() - ref2).max()) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("case,dtype", [("row_rope", torch.bfloat16), ("row_rope", torch.float32),
+                                        ("isab2_cross", torch.bfloat16), ("icl_train_size", torch.bfloat16),
+                                        ("icl_train_size", torch.float32)])
+def test_block_training_gradients(dev, mha, monkeypatch, case, dtype):
+    # training through the installed dispatch, as the reference's CPU equivalence test does per mode
+    # (scripts/tests/test_mha_cpu.py:78-104): the loss out.float().square().mean(), then the gradients of
+    # the block input and of every weight, against the same stand-in without the dispatch (torch math on
+    # the same GPU). Routes: the row stage's self attention with RoPE and a key-padding mask (pk_self),
+    # ISAB-2 cross attention (pk_cross), the ICL stage's self attention with a tensor train size (the
+    # additive train mask through the ICL hook to the masked ICL kernel and its backward)
+    seen = _spy(monkeypatch)
+    g = torch.Generator().manual_seed(60)
+    icl_case = case == "icl_train_size"
+    Ew, nh = (512, 8) if icl_case else (E, H)
+    params = list(_weights(Ew, 61, dev, dtype))
+    mod, ref_mod = U.make_module(), U.make_module()
+    assert mha.install(mod, None, mode="col1=pk,col2=pk,row=pk,cls=pk")
+    if case == "row_rope":
+        x = torch.randn(8, 104, Ew, generator=g).to(dev, dtype)
+        kpm = torch.zeros(8, 104)
+        kpm[:, 90:] = torch.finfo(torch.float32).min
+        kw = dict(rope=U.RopeStub(), key_padding_mask=kpm.to(dev, dtype))
+        route = "pk_self_attention"
+    elif case == "isab2_cross":
+        x = torch.randn(4, 300, Ew, generator=g).to(dev, dtype)
+        hidden = torch.randn(4, 128, Ew, generator=g).to(dev, dtype)
+        kw = dict(k=hidden, v=hidden)
+        route = "pk_cross_attention"
+    else:
+        x = torch.randn(2, 700, Ew, generator=g).to(dev, dtype)
+        ts = torch.tensor(600, device=dev)
+        kw = dict(train_size=ts, ssmax_layer=U.SSMaxStub(nh))
+        route = "icl_sdpa"
+    print(f"[mha] training gradients {case} {dtype}", flush=True)
+
+    def run(m):
+        leaves = [t.detach().clone().requires_grad_() for t in [x] + params]
+        out = U.block_attention(m, leaves[0], nh, *leaves[1:], **kw)
+        loss = out.float().square().mean()
+        return loss, torch.autograd.grad(loss, leaves)
+
+    loss, grads = run(mod)
+    assert route in seen, seen
+    ref_loss, ref_grads = run(ref_mod)
+    torch.cuda.synchronize()
+    # relative bars (the mean-square loss makes every gradient small): 2e-2 (bf16) / 1e-4 (fp32) of the
+    # reference gradient's largest entry; the loss to the same relative bar
+    tol = TOL[dtype]
+    assert abs(float(loss) - float(ref_loss)) <= tol * abs(float(ref_loss))
+    for name, a, b in zip(("x", "in_proj_w", "in_proj_b", "out_proj_w", "out_proj_b"), grads, ref_grads):
+        scale = float(b.float().abs().max())
+        err = _err(a, b)
+        print(f"  d{name}: max abs err {err:.3e} (ref max {scale:.3e}, {err / scale:.2e} of it)", flush=True)
+        assert torch.isfinite(a.float()).all() and scale > 0
+        assert err <= tol * scale, (name, err, scale)
