@@ -247,7 +247,7 @@ def test_block_training_gradients(dev, mha, monkeypatch, case, dtype):
         leaves = [t.detach().clone().requires_grad_() for t in [x] + params]
         out = U.block_attention(m, leaves[0], nh, *leaves[1:], **kw)
         loss = out.float().square().mean()
-        return loss, torch.autograd.grad(loss, leaves)
+        return loss.detach(), torch.autograd.grad(loss, leaves)
 
     loss, grads = run(mod)
     assert route in seen, seen
