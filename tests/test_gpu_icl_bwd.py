@@ -5,7 +5,8 @@ attention takes for calls with a gradient (diff:263-270).
 
 Cases: key counts and query counts off the 64-row tiles, a valid length (one for the batch, one per
 entry, including 0), an additive key mask (per entry, with a row masked everywhere: uniform attention),
-mask and valid length together, a cache view that is not contiguous, and the ICL hook on an upstream
+mask and valid length together, NaN in the keys past the valid length (never read: gradients there are exact
+zeros), a cache view that is not contiguous, and the ICL hook on an upstream
 stand-in under autograd with SSMax (gradients to q, k and v through the whole call, against the
 stand-in's torch float32 math on the same GPU). The upstream gradient is N(0, 1) in the output dtype;
 the oracle gets the same rounded inputs. Bars (written here): max abs error <= 2e-2 * max(1, max |grad|)
@@ -73,6 +74,11 @@ def _run(dev, q, k, v, do, valid=None, bias=None):
 def test_icl_bwd_parity(dev, name, N, H, Tq, Tkv, valid, dtype):
     print(f"[icl_bwd] {name}", flush=True)
     q, k, v, do = _inputs(7, N, H, Tq, Tkv, dtype)
+    if valid is not None:  # keys past the valid length are never read: NaN there must not reach anything
+        vl = np.broadcast_to(np.asarray(valid), (N,))
+        for n in range(N):
+            k[n, :, vl[n]:] = float("nan")
+            v[n, :, vl[n]:] = float("nan")
     out, dq, dk, dv = _run(dev, q, k, v, do, valid)
     rdq, rdk, rdv = O.splash_sdpa_bwd_ref(q, k, v, do, valid, None, out.detach().cpu())
     _check("dq", dq, rdq, dtype)
