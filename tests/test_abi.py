@@ -275,3 +275,24 @@ def test_rope_tables_match_oracle(interleaved):
     np.testing.assert_allclose(sin.numpy(), s2, atol=1e-5)
     c0, s0, code0, _, _ = pk.rope_tables(None, 4, 128, 8, "cpu")
     assert code0 == 0 and torch.all(c0 == 1) and torch.all(s0 == 0)
+
+
+def test_error_message_is_per_thread():
+    # the library's last-error message is thread-local: a refusal in another host thread leaves this
+    # thread's message as it was
+    import threading
+    import tabicl_mi355_native as nat
+    lib = nat.load()
+    st = lib.tabicl_icl_fwd(None, None, None, None, 0, None, 1, 1, 1, 1, 32, *([64] * 12), 1.0, 0, None, 0, None)
+    assert st == 1 and "head dim" in nat.last_error()
+    other = {}
+
+    def refuse():
+        other["st"] = lib.tabicl_hx_fwd(None, None, None, None, 1, None, 2, 3, 4, 64, 8, 0, None)
+        other["msg"] = nat.last_error()
+
+    t = threading.Thread(target=refuse)
+    t.start()
+    t.join()
+    assert other["st"] == 1 and "E == 128" in other["msg"]
+    assert "head dim" in nat.last_error()
