@@ -8,7 +8,8 @@ ragged rows are pinned to the oracle through it. The ICL kernels never write the
 q_len (checked with a NaN sentinel); for pk_cross their contents are unspecified (the resident
 kernel skips them, the others compute them). Cases: whole work items past q_len, a work item cut
 inside, q_len = 0, q_len >= Lq, one q_len for the whole batch, key splits, the fp32 kernel, many
-work items (the pipelined kernel's list of live work items), and for
+work items (the pipelined kernel's list of live work items), q_len with an additive key mask (prefix
+and scattered), and for
 pk_cross the resident kernel (short runs, long runs, the exact-scale long runs of the column ISAB-2)
 plus the streaming and fp32 kernels.
 """
@@ -77,6 +78,42 @@ def test_icl_ragged(dev, name, N, H, Tq, Tkv, valid, q_len, dtype):
         vl = Tkv if valid is None else valid[0]
         exp = O.splash_sdpa_ref(q[:1, :1], k[:1, :1], v[:1, :1], [vl])
         check(out[0, 0, :n0], exp[0, 0, :n0], dtype, name)
+
+
+@pytest.mark.parametrize("name,mask,dtype", [
+    ("prefix_bf16", "prefix", torch.bfloat16),      # prefix masks: the pipelined kernel at their lengths
+    ("scattered_bf16", "scattered", torch.bfloat16),  # any other mask: the exact kernel adds it
+    ("scattered_fp32", "scattered", torch.float32),
+])
+def test_icl_ragged_key_mask(dev, name, mask, dtype):
+    # q_len together with an additive key mask (tabicl_icl_fwd_masked with q_len): the live rows equal
+    # the plain masked call's bit for bit, the rows past q_len are left as they were, and the masked
+    # call is checked against the oracle on batch 0
+    import tabicl_mi355_icl as icl
+    print(f"[ragged] key mask {name}", flush=True)
+    N, H, Tq, Tkv = 3, 8, 600, 2000
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(N, H, Tq, 64, generator=g).to(dtype)
+    k = torch.randn(N, H, Tkv, 64, generator=g).to(dtype)
+    v = torch.randn(N, H, Tkv, 64, generator=g).to(dtype)
+    bias = torch.zeros(N, Tkv)
+    if mask == "prefix":
+        for n, L in enumerate((2000, 1300, 41)):
+            bias[n, L:] = torch.finfo(torch.float32).min
+    else:
+        bias = -3 * torch.rand(N, Tkv, generator=g)
+        bias[:, ::5] = -1e30
+    q_len = [37, 600, 0]
+    qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), bias.to(dev)
+    ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+    ref = torch.empty_like(qd)
+    icl.ICL_FWD_OUT(qd, kd, vd, None, 64 ** -0.5, ref, bd)
+    out = torch.full_like(qd, float("nan"))
+    icl.ICL_FWD_RAGGED_OUT(qd, kd, vd, None, ql, 64 ** -0.5, out, bd)
+    torch.cuda.synchronize()
+    _check_rows(out, ref, q_len, 2, untouched=True)
+    exp = O.splash_sdpa_ref(q[:1], k[:1], v[:1], None, bias[:1].numpy())
+    check(ref[0], exp[0], dtype, name)
 
 
 @pytest.mark.parametrize("name,N,H,Tq,Tkv,dtype", [
