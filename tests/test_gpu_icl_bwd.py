@@ -297,3 +297,28 @@ def test_icl_bwd_bench_shape_sampled(dev):
         _check(f"dq[{n},{h}]", q.grad[sl], rdq, dtype)
         _check(f"dk[{n},{h}]", k.grad[sl], rdk, dtype)
         _check(f"dv[{n},{h}]", v.grad[sl], rdv, dtype)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_icl_bwd_random_shapes(dev, seed):
+    # seeded shapes: batch 1-4, heads 1-8, 1-700 queries over 1-1500 keys, a valid length per entry or
+    # none, a scattered key mask or none, bf16 or fp32, q scaled 0.5-3
+    rng = np.random.default_rng(1000 + seed)
+    N, H = int(rng.integers(1, 5)), int(rng.integers(1, 9))
+    Tq, Tkv = int(rng.integers(1, 701)), int(rng.integers(1, 1501))
+    dtype = torch.bfloat16 if rng.random() < 0.6 else torch.float32
+    valid = [int(x) for x in rng.integers(0, Tkv + 1, N)] if rng.random() < 0.5 else None
+    bias = None
+    if rng.random() < 0.4:
+        bias = torch.tensor(-2 * rng.random((N, Tkv)), dtype=torch.float32)
+        bias[torch.tensor(rng.random((N, Tkv)) < 0.2)] = -1e30
+    qscale = float(rng.uniform(0.5, 3.0))
+    print(f"[icl_bwd] random seed={seed}: N={N} H={H} Tq={Tq} Tkv={Tkv} {dtype} valid={valid} "
+          f"bias={bias is not None} qscale={qscale:.2f}", flush=True)
+    q, k, v, do = _inputs(2000 + seed, N, H, Tq, Tkv, dtype, qscale)
+    out, dq, dk, dv = _run(dev, q, k, v, do, valid, bias)
+    rdq, rdk, rdv = O.splash_sdpa_bwd_ref(q, k, v, do, valid, None if bias is None else bias.numpy(),
+                                          out.detach().cpu())
+    _check("dq", dq, rdq, dtype)
+    _check("dk", dk, rdk, dtype)
+    _check("dv", dv, rdv, dtype)
