@@ -757,8 +757,8 @@ def bench_icl_masked(steps: int, warmup: int) -> list:
     icl_sdpa with an additive fp32 key mask, one row per estimator: a prefix mask (0 on the first 44000
     keys, finfo.min after: the train mask upstream builds from a tensor train size) runs on the
     pipelined kernel as a valid length; a scattered mask (finfo.min on a random 10% of the keys, 0
-    elsewhere) runs on the exact kernel, which adds it term by term. TFLOP/s over the keys each kernel
-    sweeps (44000 and 45000)."""
+    elsewhere) runs on the pipelined kernel's masked instance, which starts each score product from the
+    keys' mask terms. TFLOP/s over the keys each kernel sweeps (44000 and 45000)."""
     import torch
 
     import tabicl_mi355_icl as icl
@@ -774,7 +774,7 @@ def bench_icl_masked(steps: int, warmup: int) -> list:
     scattered = torch.where(torch.rand(EST, TRAIN, generator=g, device=dev) < 0.1, fmin, 0.0)
     recs = []
     for name, mask, keys in (("prefix mask (pipelined kernel)", prefix, TRAIN - 1000),
-                             ("scattered mask (exact kernel)", scattered, TRAIN)):
+                             ("scattered mask (pipelined kernel, mask as accumulator input)", scattered, TRAIN)):
         with torch.no_grad():
             ms = _time(lambda: icl.icl_sdpa(q, k, v, None, mask), steps, warmup)
         tf = 4.0 * TEST * keys * D * HEADS * EST / (ms * 1e-3) / 1e12

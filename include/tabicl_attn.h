@@ -278,9 +278,11 @@ int tabicl_icl_fwd_ragged_listed(const void* q, const void* k, const void* v, co
  * 158-193, which sends every masked call to a torch fallback). Rows of N whose mask is a prefix mask
  * (0 on the first v >= 1 keys, <= -1e30 after: what upstream builds from a tensor train size,
  * diff:1526-1542) run on the pipelined kernel as the valid length min(v, valid[n]), decided on the
- * device; other rows are computed by the exact kernel with the mask added term by term (every key
- * carrying <= -1e30 gives equal weights, like the reference's softmax over finfo.min terms). scale
- * must be positive with a mask. q_len may be NULL (all rows).
+ * device; other rows run on the pipelined kernel's masked instance, which adds each key's mask term
+ * to its scores (bf16 with a power-of-two scale and a workspace), or on the exact kernel, which also
+ * takes the rows the masked instance cannot keep (every key carrying <= -1e30 gives equal weights,
+ * like the reference's softmax over finfo.min terms). scale must be positive with a mask. q_len may
+ * be NULL (all rows).
  */
 int tabicl_icl_fwd_masked(const void* q, const void* k, const void* v, const int32_t* valid, int64_t valid_n,
                           const float* key_bias, int64_t bias_n, int64_t bias_sn, const int32_t* q_len,

@@ -210,6 +210,17 @@ __device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, ui
                : "v"(voff), "s"((const void*)(uintptr_t)bu), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }
+// The 4-byte form (global_load_lds_dword): LDS[lds_addr + 4 * lane] = *(sbase + voff).
+__device__ __forceinline__ void lds_dma4_s(uint32_t voff, const void* sbase, uint32_t lds_addr) {
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | lo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(voff), "s"((const void*)(uintptr_t)bu), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Byte address of a __shared__ object in the LDS aperture.

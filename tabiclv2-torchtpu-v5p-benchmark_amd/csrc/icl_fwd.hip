@@ -22,6 +22,7 @@
 //    with the running max updated lazily (accumulators rescaled only when the tile max exceeds the
 //    running max by more than 2^8; exact because O and l always share the same reference max).
 #include <atomic>
+#include <cmath>
 #include <mutex>
 
 #include "common.h"
@@ -59,8 +60,10 @@ struct IclParams {
   int64_t bias_sn;
   int bias_n;
   float bias_inv_scale;
+  float scale;  // the score scale itself
   // prefix view of that mask for the pipelined kernel (pvalid / pok [pn], pn in {1, N}): rows whose
-  // mask is a prefix mask run with valid length pvalid; the others are flagged for icl_fwd_kernel
+  // mask is a prefix mask run with valid length pvalid; the others run on icl_pipe_kernel<true> (a
+  // power-of-two scale) or are flagged for icl_fwd_kernel
   const int32_t* pvalid;
   const int32_t* pok;
   int pn;
@@ -586,6 +589,7 @@ constexpr int IP_QW = 64;
 constexpr int IP_NBUF = 4;
 constexpr int IP_TILE = 2 * ICL_KT * ICL_D;  // bf16 elements per buffer: K tile then V tile (16 KB)
 constexpr float IP_L_HI = 0x1p96f;
+constexpr float IP_L_LO = 0x1p-64f;  // with a key mask: below it the fixed reference lost the row
 
 // 16-byte chunk swizzle of a 128-byte tile row: a bijection on key % 8 that keeps (a) any 8
 // consecutive rows at one chunk and (b) the chunk pairs {c, c^1} of 4 consecutive rows on distinct
@@ -645,12 +649,35 @@ __device__ __forceinline__ bf16x8 ip_vop(const bf16* lv, int kr, int m, int db, 
   return __builtin_bit_cast(bf16x8, w);
 }
 
-// S^T of keys kr..kr+31 of the K tile for both column blocks.
-__device__ __forceinline__ void ip_s(f32x16 (&s)[2], const IpState& st, const bf16* lk, int kr, int lr, int hh) {
+// Key mask of keys kr..kr+31 of a tile in the S^T accumulator's order (reg r = key kr + 8 (r / 4) +
+// 4 hh + r % 4), from this wave's copy of the tile's mask row.
+__device__ __forceinline__ f32x16 ip_bias(const float* lb, int kr, int hh) {
+  f32x16 b;
 #pragma unroll
-  for (int qc = 0; qc < 2; ++qc)
+  for (int g = 0; g < 4; ++g) {
+    const float4 v = *(const float4*)(lb + kr + 8 * g + 4 * hh);
+    b[4 * g] = v.x;
+    b[4 * g + 1] = v.y;
+    b[4 * g + 2] = v.z;
+    b[4 * g + 3] = v.w;
+  }
+  return b;
+}
+
+// S^T of keys kr..kr+31 of the K tile for both column blocks (KB: started from the keys' mask, lb).
+template <bool KB = false>
+__device__ __forceinline__ void ip_s(f32x16 (&s)[2], const IpState& st, const bf16* lk, const float* lb, int kr, int lr,
+                                     int hh) {
+  if constexpr (KB) {
+    const f32x16 b = ip_bias(lb, kr, hh);
+    s[0] = b;
+    s[1] = b;
+  } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[qc][r] = 0.f;
+    for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[qc][r] = 0.f;
+  }
 #pragma unroll
   for (int sl = 0; sl < 4; ++sl) {
     const bf16x8 a = ip_kop(lk, kr, sl, lr, hh);
@@ -698,11 +725,12 @@ __device__ __forceinline__ void ip_exp2(const f32x16 (&s)[2], const IpState& st,
 // One half-tile phase: probabilities of `cur` (keys k0..k0+31) into `pcur`; if DO_S, S^T of the
 // next half tile (rows kr_next.. of lk_next) into `nxt`; if DO_PV, the PV product of the previous
 // half tile's probabilities `pprev` (rows kr_prev.. of lv_prev). Eight steps of up to two MFMAs,
-// each MFMA followed by two probabilities; operands are read from LDS two steps ahead.
-template <bool MASK, bool DO_S, bool DO_PV>
+// each MFMA followed by two probabilities; operands are read from LDS two steps ahead. KB: the next
+// half tile's scores start from its key mask (lb_next), the first score product's accumulator input.
+template <bool MASK, bool DO_S, bool DO_PV, bool KB = false>
 __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pcur)[2][2],
-                                         const bf16x8 (&pprev)[2][2], const bf16* lk_next, int kr_next,
-                                         const bf16* lv_prev, int kr_prev, int k0, int valid, float sc,
+                                         const bf16x8 (&pprev)[2][2], const bf16* lk_next, const float* lb_next,
+                                         int kr_next, const bf16* lv_prev, int kr_prev, int k0, int valid, float sc,
                                          int lane) {
   const int lr = lane & 31, hh = lane >> 5;
   if (MASK) ip_mask(cur, k0, valid, hh);
@@ -712,7 +740,10 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
     const int j = i - 4;  // (db, m) = (j >> 1, j & 1)
     return ip_vop(lv_prev, kr_prev, j & 1, j >> 1, lane);
   };
-  if (DO_S) {
+  f32x16 bnext;
+  if constexpr (DO_S && KB) {
+    bnext = ip_bias(lb_next, kr_next, hh);
+  } else if (DO_S) {
 #pragma unroll
     for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
@@ -733,7 +764,7 @@ __device__ __forceinline__ void ip_phase(IpState& st, f32x16 (&cur)[2], f32x16 (
 #pragma unroll
     for (int qc = 0; qc < 2; ++qc) {
       if (i < 4) {
-        nxt[qc] = mfma32x32x16(op[i], st.qop[qc][i], nxt[qc]);
+        nxt[qc] = mfma32x32x16(op[i], st.qop[qc][i], KB && i == 0 ? bnext : nxt[qc]);
       } else {
         const int j = i - 4;
         st.o[qc][j >> 1] = mfma32x32x16(op[i], pprev[qc][j & 1], st.o[qc][j >> 1]);
@@ -756,14 +787,21 @@ struct IpCtx {
   uint32_t lds0;
   int t0, nt, valid, wave, lane;
   float sc;
+  // KB: the row's key mask (global) and this wave's copy of tile buffer 0's mask row (LDS; buffer b's
+  // at + b IP_NW ICL_KT floats)
+  const float* brow;
+  const float* lb;
 };
 
 // Queue the copy of the tile at key k0 into the buffer at LDS byte address buf: wave w copies K
 // rows 16w..16w+15 and V rows 16w..16w+15, 8 rows (1 KB) per instruction, from the tile's
 // (wave-uniform) base plus each lane's 32-bit offset. Rows 16w+8.. share the swizzle of rows 16w..
 // (it depends on row & 7). Rows past `valid` are read from row valid-1 (in bounds, and finite
-// whenever the visible rows are); k0 < valid always.
-__device__ __forceinline__ void ip_issue(const IpCtx& c, uint32_t buf, int k0) {
+// whenever the visible rows are); k0 < valid always. KB: and each wave copies the tile's 64 mask
+// entries into its own slot of the buffer's mask rows (entries past `valid` from entry valid-1).
+template <bool KB = false>
+__device__ __forceinline__ void ip_issue(const IpCtx& c, int bi, int k0) {
+  const uint32_t buf = c.lds0 + bi * IP_TILE * 2;
   const bf16* kt = c.kbase + (int64_t)k0 * c.k_st;
   const bf16* vt = c.vbase + (int64_t)k0 * c.v_st;
   const int lim = c.valid - k0;  // rows below lim are visible
@@ -778,6 +816,15 @@ __device__ __forceinline__ void ip_issue(const IpCtx& c, uint32_t buf, int k0) {
                                : (in ? c.voff + (uint32_t)(j * 16 * c.v_st) : vcl);
     lds_dma16_s(off, i < 2 ? kt : vt, buf + (i < 2 ? 0 : ICL_KT * ICL_D * 2) + (16 * c.wave + 8 * j) * ICL_D * 2);
   }
+  if constexpr (KB)
+    lds_dma4_s((uint32_t)min(k0 + c.lane, c.valid - 1) * 4u, c.brow, lds_addr(c.lb + bi * (IP_NW * ICL_KT)));
+}
+
+// Tile copies per wave and tile (the constant vmcnt of the joins counts them).
+template <bool KB> constexpr int ip_copies() { return KB ? 5 : 4; }
+template <bool KB> __device__ __forceinline__ void ip_join_tile() {
+  if constexpr (KB) TA_WAIT_JOIN(5);
+  else TA_WAIT_JOIN(4);
 }
 
 // Sweep iteration t (tile t0 + t, buffer t % IP_NBUF, no key past `valid`): phase A = softmax of
@@ -786,7 +833,7 @@ __device__ __forceinline__ void ip_issue(const IpCtx& c, uint32_t buf, int k0) {
 // softmax of the second half, S of the next tile's first half (unless LAST), PV of this tile's first
 // half. B = t % IP_NBUF when the caller knows it (unrolled sweep: buffer addresses become
 // immediate offsets), else -1.
-template <bool FIRST, bool LAST, int B = -1>
+template <bool FIRST, bool LAST, int B = -1, bool KB = false>
 __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&sB)[2], bf16x8 (&pA)[2][2],
                                         bf16x8 (&pB)[2][2], bf16 (*lds)[IP_TILE], const IpCtx& c, int t) {
   const int b = B >= 0 ? B : t % IP_NBUF;
@@ -794,33 +841,35 @@ __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&s
   const bf16* lv = lk + ICL_KT * ICL_D;
   const bf16* lvp = lds[(b + IP_NBUF - 1) % IP_NBUF] + ICL_KT * ICL_D;
   const bf16* lkn = lds[(b + 1) % IP_NBUF];
+  const float* lb = c.lb + b * (IP_NW * ICL_KT);
+  const float* lbn = c.lb + ((b + 1) % IP_NBUF) * (IP_NW * ICL_KT);
   const int k0 = (c.t0 + t) * ICL_KT;
-  ip_phase<false, true, !FIRST>(st, sA, sB, pA, pB, lk, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
-  static_assert(IP_NBUF == 4, "one tile (4 copies per wave) may stay in flight below");
-  TA_WAIT_JOIN(4);
-  ip_issue(c, c.lds0 + ((b + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
-           min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
-  ip_phase<false, !LAST, true>(st, sB, sA, pB, pA, lkn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
+  ip_phase<false, true, !FIRST, KB>(st, sA, sB, pA, pB, lk, lb, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
+  static_assert(IP_NBUF == 4, "one tile's copies may stay in flight below");
+  ip_join_tile<KB>();
+  ip_issue<KB>(c, (b + IP_NBUF - 1) % IP_NBUF, min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
+  ip_phase<false, !LAST, true, KB>(st, sB, sA, pB, pA, lkn, lbn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
 }
 
 // Sweep iteration t of a wave whose query rows are all past the live count (ragged calls): the same
 // join and tile copy as ip_iter, in the same order, without the products and the softmax.
+template <bool KB = false>
 __device__ __forceinline__ void ip_iter_idle(const IpCtx& c, int t) {
-  TA_WAIT_JOIN(4);
-  ip_issue(c, c.lds0 + ((t + IP_NBUF - 1) % IP_NBUF) * IP_TILE * 2,
-           min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
+  ip_join_tile<KB>();
+  ip_issue<KB>(c, (t + IP_NBUF - 1) % IP_NBUF, min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
 }
 
 // The tile that crosses `valid` (buffer b, keys k0..): S, mask, probabilities and PV per half,
 // without the MFMA/VALU interleave (once per work item at most).
-__device__ __forceinline__ void ip_tail(IpState& st, const bf16* lk, const bf16* lv, int k0, int valid, float sc,
-                                        int lane) {
+template <bool KB = false>
+__device__ __forceinline__ void ip_tail(IpState& st, const bf16* lk, const bf16* lv, const float* lb, int k0, int valid,
+                                        float sc, int lane) {
   const int lr = lane & 31, hh = lane >> 5;
 #pragma unroll 1
   for (int half = 0; half < 2; ++half) {
     f32x16 sT[2];
     bf16x8 pT[2][2];
-    ip_s(sT, st, lk, 32 * half, lr, hh);
+    ip_s<KB>(sT, st, lk, lb, 32 * half, lr, hh);
     ip_mask(sT, k0 + 32 * half, valid, hh);
 #pragma unroll
     for (int j = 0; j < 16; ++j) ip_exp2(sT, st, sc, pT, j >> 3, j & 7);
@@ -828,8 +877,15 @@ __device__ __forceinline__ void ip_tail(IpState& st, const bf16* lk, const bf16*
   }
 }
 
+// KB (a call with a key mask and a power-of-two scale, launched after the KB = false instance, which
+// took the rows whose mask is a prefix mask and flagged the others): the rows whose mask is not a prefix
+// mask, adding it in raw score units as the score product's accumulator input (q is taken times the
+// scale, exactly, and the exponent's factor is log2 e alone); rows whose sum then leaves [2^-64, 2^96]
+// (every key masked, say) stay flagged for icl_fwd_kernel.
+template <bool KB>
 __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
   __shared__ __attribute__((aligned(1024))) bf16 lds[IP_NBUF][IP_TILE];
+  __shared__ __attribute__((aligned(16))) float lbias[KB ? IP_NBUF * IP_NW * ICL_KT : 4];
   __shared__ int wg_bad;
 
   int work;
@@ -870,14 +926,14 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     return;
   }
   if (p.pok) {
-    // key mask: a prefix mask is the valid length pvalid; any other mask is left to icl_fwd_kernel,
-    // which adds it term by term
+    // key mask: a prefix mask is the valid length pvalid; any other mask is flagged here for the KB
+    // instance or for icl_fwd_kernel (which adds it term by term), and added by the KB instance
     const int pr = p.pn == 1 ? 0 : n;
-    if (!p.pok[pr]) {
-      if (threadIdx.x == 0) p.flags[work] = 1;
+    if (KB == (p.pok[pr] != 0)) {
+      if (!KB && threadIdx.x == 0) p.flags[work] = 1;
       return;
     }
-    valid = p.pvalid[pr];
+    valid = p.pvalid[pr];  // the plain valid length for a row whose mask is not a prefix mask
   }
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -894,6 +950,10 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     for (int s = 0; s < 4; ++s) {
       bf16x8 z = {};
       st.qop[qc][s] = qi < p.Tq ? *(const bf16x8*)(qbase + (int64_t)qi * p.q_st + 16 * s + 8 * hh) : z;
+      if (KB) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.qop[qc][s][j] = (bf16)((float)st.qop[qc][s][j] * p.scale);
+      }
     }
     st.nm[qc] = 0.f;
     st.lacc[qc] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -928,7 +988,9 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     c.valid = valid;
     c.wave = wave;
     c.lane = lane;
-    c.sc = p.sc;
+    c.sc = KB ? TA_LOG2E : p.sc;
+    c.brow = KB ? p.bias + (p.bias_n == 1 ? 0 : (int64_t)n * p.bias_sn) : nullptr;
+    c.lb = &lbias[KB ? wave * ICL_KT : 0];
     {
       const int row = 16 * wave + (lane >> 3);
       const int ch = (lane & 7) ^ ip_swz(row);
@@ -938,13 +1000,16 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
       c.voff = (uint32_t)((row * c.v_st + ch * 8) * 2);
     }
 #pragma unroll
-    for (int i = 0; i < IP_NBUF - 1; ++i) ip_issue(c, c.lds0 + i * IP_TILE * 2, min(t0 + i, t1 - 1) * ICL_KT);
-    TA_WAIT_JOIN(8);  // tile t0 landed, two more tiles (8 copies) in flight
+    for (int i = 0; i < IP_NBUF - 1; ++i) ip_issue<KB>(c, i, min(t0 + i, t1 - 1) * ICL_KT);
+    // tile t0 landed, two more tiles' copies in flight
+    if constexpr (KB) TA_WAIT_JOIN(10);
+    else TA_WAIT_JOIN(8);
+    static_assert(ip_copies<true>() == 5 && ip_copies<false>() == 4, "the joins' vmcnt counts");
     // tiles entirely below `valid` through the pipelined sweep, the crossing one (if any) after it
     const int nfull = (t1 == ntiles && valid % ICL_KT != 0) ? nt - 1 : nt;
     if (qw0 >= live) {
       // a ragged call's wave with no live row: only its share of the tile copies and the joins
-      for (int t = 0; t < nfull; ++t) ip_iter_idle(c, t);
+      for (int t = 0; t < nfull; ++t) ip_iter_idle<KB>(c, t);
       TA_WAIT_JOIN(0);
       goto swept;
     }
@@ -952,7 +1017,7 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     // reference m: ceiled maximum over the first 32 keys of the range
     f32x16 sA[2], sB[2];
     bf16x8 pA[2][2], pB[2][2];
-    ip_s(sA, st, lds[0], 0, lr, hh);
+    ip_s<KB>(sA, st, lds[0], c.lb, 0, lr, hh);
     if (t0 == ntiles - 1) ip_mask(sA, t0 * ICL_KT, valid, hh);
 #pragma unroll
     for (int qc = 0; qc < 2; ++qc) {
@@ -964,29 +1029,30 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     }
 
     if (nfull > 1) {
-      ip_iter<true, false>(st, sA, sB, pA, pB, lds, c, 0);
+      ip_iter<true, false, -1, KB>(st, sA, sB, pA, pB, lds, c, 0);
       int t = 1;
       for (; t + IP_NBUF < nfull; t += IP_NBUF) {  // t % IP_NBUF == 1 at the top
-        ip_iter<false, false, 1>(st, sA, sB, pA, pB, lds, c, t);
-        ip_iter<false, false, 2>(st, sA, sB, pA, pB, lds, c, t + 1);
-        ip_iter<false, false, 3>(st, sA, sB, pA, pB, lds, c, t + 2);
-        ip_iter<false, false, 0>(st, sA, sB, pA, pB, lds, c, t + 3);
+        ip_iter<false, false, 1, KB>(st, sA, sB, pA, pB, lds, c, t);
+        ip_iter<false, false, 2, KB>(st, sA, sB, pA, pB, lds, c, t + 1);
+        ip_iter<false, false, 3, KB>(st, sA, sB, pA, pB, lds, c, t + 2);
+        ip_iter<false, false, 0, KB>(st, sA, sB, pA, pB, lds, c, t + 3);
       }
-      for (; t + 1 < nfull; ++t) ip_iter<false, false>(st, sA, sB, pA, pB, lds, c, t);
-      ip_iter<false, true>(st, sA, sB, pA, pB, lds, c, nfull - 1);
+      for (; t + 1 < nfull; ++t) ip_iter<false, false, -1, KB>(st, sA, sB, pA, pB, lds, c, t);
+      ip_iter<false, true, -1, KB>(st, sA, sB, pA, pB, lds, c, nfull - 1);
       ip_pv(st, pB, lds[(nfull - 1) % IP_NBUF] + ICL_KT * ICL_D, 32, lane);
     } else if (nfull == 1) {
       // one full tile: the unpipelined form (the same probabilities, products and order), then the
       // join that the pipelined iteration would make (tile 1 landed; the idle waves make it too).
       // A pipelined instance for this case kept the first tile's probabilities live across the
       // sweep and made the compiler spill 25 VGPRs around it.
-      ip_tail(st, lds[0], lds[0] + ICL_KT * ICL_D, t0 * ICL_KT, valid, c.sc, lane);
-      TA_WAIT_JOIN(4);
+      ip_tail<KB>(st, lds[0], lds[0] + ICL_KT * ICL_D, c.lb, t0 * ICL_KT, valid, c.sc, lane);
+      ip_join_tile<KB>();
     }
     if (nfull < nt) {
       // the crossing tile landed at the last join (or before the sweep when it is the only tile)
       const bf16* lk = lds[nfull % IP_NBUF];
-      ip_tail(st, lk, lk + ICL_KT * ICL_D, (t0 + nfull) * ICL_KT, valid, c.sc, lane);
+      ip_tail<KB>(st, lk, lk + ICL_KT * ICL_D, c.lb + (nfull % IP_NBUF) * (IP_NW * ICL_KT), (t0 + nfull) * ICL_KT,
+                  valid, c.sc, lane);
     }
     TA_WAIT_JOIN(0);  // no copy into this workgroup's LDS may outlive it
   }
@@ -1014,6 +1080,7 @@ swept:
   for (int qc = 0; qc < 2; ++qc) {
     lt[qc] = lane_pair_sum(st.lacc[qc][0]);
     bad |= !(lt[qc] <= IP_L_HI);
+    if (KB) bad |= qw0 + qc * 32 + lr < live && !(lt[qc] >= IP_L_LO);
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -1083,7 +1150,7 @@ Residency residency() {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return {0, 0};
   const hipError_t e =
       sizeof(T) == 2 && D == ICL_D
-          ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel, IP_NW * 64, 0)
+          ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_pipe_kernel<false>, IP_NW * 64, 0)
           : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, icl_fwd_kernel<T, NW, QC, D>, NW * 64, 0);
   const int64_t per_cu = e == hipSuccess && n > 0 ? (n < 255 ? n : 255) : 1;
   if (dev >= 0 && dev < ICL_DEV_CACHE) cache[dev].store((int64_t)cus * 256 + per_cu, std::memory_order_relaxed);
@@ -1257,8 +1324,14 @@ void launch(const IclParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream,
     p.live = list;
   }
   if (list_mode == ICL_LIST_ONLY) return;
-  if (fast)
-    hipLaunchKernelGGL(icl_pipe_kernel, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
+  if (fast) {
+    hipLaunchKernelGGL(icl_pipe_kernel<false>, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
+    // rows whose key mask is not a prefix mask: the pipelined kernel adds it when the scale is a
+    // power of two (q times the scale is then exact in bf16)
+    int e = 0;
+    if (p.bias && std::frexp(p.scale, &e) == 0.5f)
+      hipLaunchKernelGGL(icl_pipe_kernel<true>, dim3((unsigned)nblk), dim3(IP_NW * 64), 0, stream, p);
+  }
   if (p.bias)
     hipLaunchKernelGGL((icl_fwd_kernel<T, NW, QC, D, true>), dim3((unsigned)nblk), dim3(NW * 64), 0, stream, p);
   else
@@ -1300,6 +1373,7 @@ int tabicl_launch_icl_fwd(const void* q, const void* k, const void* v, const int
   p.nsplit = 1; p.ws_o = nullptr; p.ws_ml = nullptr; p.flags = nullptr;
   p.bias = bias; p.bias_n = (int)bias_n; p.bias_sn = bias_sn;
   p.bias_inv_scale = 1.0f / scale;
+  p.scale = scale;
   p.pvalid = nullptr; p.pok = nullptr; p.pn = 0; p.live = nullptr;
   p.stat = stat;
   if (D == 128) {

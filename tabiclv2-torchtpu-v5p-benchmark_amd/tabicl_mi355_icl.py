@@ -104,7 +104,8 @@ def _icl_cached_attn(q: Tensor, k: Tensor, v: Tensor, valid: Optional[Tensor], s
                      key_bias: Optional[Tensor] = None) -> Tensor:
     """key_bias: optional additive fp32 key mask [1 or N, Tkv] (the reference's masked path,
     results/tpu_patch.diff:263-270); a prefix mask (0 then <= -1e30) runs as a valid length on the
-    pipelined kernel, any other mask on the exact kernel, which adds it term by term."""
+    pipelined kernel, any other mask on its masked instance (the mask terms start each score product;
+    power-of-two scale) or on the exact kernel, which adds it tile by tile."""
     out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
     _launch(q, k, v, valid, scale, out, None, key_bias)
     return out

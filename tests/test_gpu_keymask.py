@@ -65,6 +65,58 @@ def test_icl_key_mask(dev, name, N, Hh, Tq, Tkv, kind, rows, dtype):
     check(out, O.splash_sdpa_ref(q, k, v, None, b), dtype, "icl_key_mask")
 
 
+def _scattered(case, N, Tkv, g):
+    b = torch.zeros(N, Tkv)
+    if case in ("scattered", "sharp", "key_split"):
+        b[torch.rand(N, Tkv, generator=g) < 0.1] = FMIN
+    elif case == "finite_terms":  # finite terms only, no key masked
+        b = -4.0 * torch.rand(N, Tkv, generator=g)
+    elif case == "head_masked":  # the first 40 keys masked (no reference from the first 32), then scattered
+        b[:, :40] = FMIN
+        b[torch.rand(N, Tkv, generator=g) < 0.05] = FMIN
+    elif case == "inf_scattered":
+        b[torch.rand(N, Tkv, generator=g) < 0.3] = float("-inf")
+    elif case == "row_masked":  # row 0 masked everywhere (equal weights), row 1 scattered
+        b[0] = FMIN
+        b[1, torch.rand(Tkv, generator=g) < 0.5] = FMIN
+    elif case == "nonpow2_scale":
+        b[torch.rand(N, Tkv, generator=g) < 0.2] = -3.0
+    return b
+
+
+@pytest.mark.parametrize("case,N,Hh,Tq,Tkv,qscale", [
+    ("scattered", 2, 8, 300, 3000, 1.0),
+    ("sharp", 2, 8, 300, 3000, 6.0),
+    ("finite_terms", 2, 8, 200, 2500, 3.0),
+    ("head_masked", 2, 8, 256, 3000, 1.0),
+    ("head_masked_sharp", 2, 8, 256, 3000, 8.0),
+    ("inf_scattered", 3, 4, 130, 1000, 2.0),
+    ("row_masked", 2, 8, 100, 1500, 2.0),
+    ("key_split", 1, 2, 64, 20000, 4.0),
+    ("nonpow2_scale", 2, 8, 200, 2000, 2.0),
+])
+def test_icl_scattered_mask_pipelined(dev, case, N, Hh, Tq, Tkv, qscale):
+    # masks that are not prefix masks, bf16: with a power-of-two scale the pipelined kernel adds them as
+    # the score product's accumulator input (rows that leave its trust range recomputed exactly); a
+    # scale of 0.1 runs on the exact kernel. Sharp queries (x qscale) make the outputs O(0.3-1).
+    import tabicl_mi355_icl as icl
+    g = torch.Generator().manual_seed(64)
+    q = (torch.randn(N, Hh, Tq, 64, generator=g) * qscale).to(torch.bfloat16)
+    k = torch.randn(N, Hh, Tkv, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(N, Hh, Tkv, 64, generator=g).to(torch.bfloat16)
+    b = _scattered(case.replace("_sharp", ""), N, Tkv, g)
+    print(f"[keymask] icl pipelined mask {case}: N={N} H={Hh} Tq={Tq} Tkv={Tkv}", flush=True)
+    if case == "nonpow2_scale":
+        out = icl.ICL_FWD(q.to(dev), k.to(dev), v.to(dev), None, 0.1, b.to(dev))
+        ref = O.splash_sdpa_ref(q.double() * (0.1 / 0.125), k, v, None, b)
+    else:
+        out = icl.icl_sdpa(q.to(dev), k.to(dev), v.to(dev), None, b.to(dev))
+        ref = O.splash_sdpa_ref(q, k, v, None, b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    check(out, ref, torch.bfloat16, f"icl_pipelined_mask_{case}")
+
+
 def test_icl_prefix_mask_is_the_valid_length(dev):
     # a prefix mask runs as the valid length on the pipelined kernel: identical bits to the length call,
     # and the NaN rows past the prefix are never read
