@@ -388,11 +388,13 @@ __device__ __forceinline__ void ic_store(const IcStage& s, bf16* tile) {
 // dq: workgroup = ((n, h), 128 queries), wave = 32 queries (blocks b = 0, 1). Sweep 1 takes the
 // statistics over 64-key tiles (S^T = K Q^T, K rows from LDS, q in registers); sweep 2 forms
 // dS^T = e (dP^T - D) per key block and dq^T += K^T dS^T over key-block pairs. Stores dq and, per
-// query, m (+inf for a row with no visible key), log2 l and -D for the dk / dv kernel.
+// query, m (+inf for a row with no visible key), log2 l and -D for the dk / dv kernel (before sweep 2,
+// so that they are not held across it: the launch bound of three workgroups per CU, i.e. three waves
+// per SIMD, leaves 168 VGPRs).
 // FS: the statistics come from the forward (p.stat; no key mask), there is no sweep 1, and the score
 // product starts from -(m + log2 l) / c, so that exp2(S^T c) is P itself (one fma fewer per score).
 template <bool FS>
-__global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
+__global__ __launch_bounds__(IB_NW * 64, 3) void ic_dq_kernel(IbParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lk[2][IB_T * IC_RS];
   __shared__ __attribute__((aligned(16))) bf16 lv[2][IB_T * IC_RS];
   __shared__ __attribute__((aligned(16))) float lb2[2][IB_T];
@@ -508,6 +510,16 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
   float s0[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b) s0[b] = FS ? -(mq[b] + lgv[b]) / c : 0.f;
+  // the statistics for the dk / dv kernel, stored before the sweep (not kept live across it)
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int qi = q0 + 16 * b + l16;
+    if (qi < p.Tq && kap == 0) {
+      p.mx[rbase + qi] = mq[b];
+      p.lg[rbase + qi] = lgv[b];
+      p.dd[rbase + qi] = nd[b];
+    }
+  }
 
   // sweep 2: dq^T l = sum over keys of K^T e (dP^T - D), e = exp2(x - m)
   f32x4 acc[2][4];
@@ -571,11 +583,6 @@ __global__ __launch_bounds__(IB_NW * 64) void ic_dq_kernel(IbParams p) {
       bf16* dqrow = (bf16*)p.dq + (rbase + qi) * IB_D;
 #pragma unroll
       for (int jd = 0; jd < 4; ++jd) *(bf16x4*)(dqrow + 16 * jd + 4 * kap) = cvt_bf16x4(acc[b][jd] * ysc);
-      if (kap == 0) {
-        p.mx[rbase + qi] = mq[b];
-        p.lg[rbase + qi] = lgv[b];
-        p.dd[rbase + qi] = nd[b];
-      }
     }
   }
 }
