@@ -117,6 +117,32 @@ def test_icl_scattered_mask_pipelined(dev, case, N, Hh, Tq, Tkv, qscale):
     check(out, ref, torch.bfloat16, f"icl_pipelined_mask_{case}")
 
 
+def test_icl_scattered_mask_with_valid_lengths(dev):
+    # a scattered mask together with per-entry valid lengths (one of them 0): the masked instance runs to
+    # the valid length, NaN keys past it are never read, the empty entry gives zeros
+    import tabicl_mi355_icl as icl
+    g = torch.Generator().manual_seed(65)
+    N, Hh, Tq, Tkv = 4, 4, 150, 2600
+    q = (torch.randn(N, Hh, Tq, 64, generator=g) * 3.0).to(torch.bfloat16)
+    k = torch.randn(N, Hh, Tkv, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(N, Hh, Tkv, 64, generator=g).to(torch.bfloat16)
+    lens = [2600, 1777, 0, 65]
+    kn, vn = k.clone(), v.clone()
+    for n, L in enumerate(lens):
+        kn[n, :, L:] = float("nan")
+        vn[n, :, L:] = float("nan")
+    b = torch.zeros(N, Tkv)
+    b[torch.rand(N, Tkv, generator=g) < 0.15] = FMIN
+    b[:, 1] = -2.5  # a finite term: no row is a prefix mask
+    vt = torch.tensor(lens, dtype=torch.int32)
+    print("[keymask] icl pipelined mask with valid lengths", flush=True)
+    out = icl.icl_sdpa(q.to(dev), kn.to(dev), vn.to(dev), vt.to(dev), b.to(dev))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert float(out[2].abs().max()) == 0.0
+    check(out, O.splash_sdpa_ref(q, k, v, vt, b), torch.bfloat16, "icl_pipelined_mask_valid_lengths")
+
+
 def test_icl_prefix_mask_is_the_valid_length(dev):
     # a prefix mask runs as the valid length on the pipelined kernel: identical bits to the length call,
     # and the NaN rows past the prefix are never read
