@@ -187,8 +187,18 @@ def hxq_ref(q, kv, valid, h):
     return attention_f64(q, kv[..., :E], kv[..., E:], h, valid=_f64(valid).astype(np.int64))
 
 
-def pk_self_ref(qkv, h, bias, rope, scale):
-    """pk_self_attention - reference :722-732; rope = None or (cos, sin, code, half, rot)."""
+def _cast(x: np.ndarray, dtype) -> np.ndarray:
+    """x rounded as the reference's packed kernels round their operands: to fp32, then to `dtype`
+    (`(rope(q) * scale).astype(dt)`, `rope(k).astype(dt)`, scripts/tabicl_tpu_pallas_attn.py:500-501);
+    dtype None: unrounded."""
+    if dtype is None:
+        return x
+    return torch.from_numpy(np.ascontiguousarray(x)).to(torch.float32).to(dtype).double().numpy()
+
+
+def pk_self_ref(qkv, h, bias, rope, scale, cast=None):
+    """pk_self_attention - reference :722-732; rope = None or (cos, sin, code, half, rot). cast (a torch
+    dtype): q' = rope(q) scale and k' = rope(k) rounded to it, the reference kernel's rounding points."""
     x = _f64(qkv)
     E = x.shape[-1] // 3
     q, k, v = x[..., :E], x[..., E:2 * E], x[..., 2 * E:]
@@ -196,11 +206,12 @@ def pk_self_ref(qkv, h, bias, rope, scale):
         cos, sin, code, half, rot = rope
         q = rope_merged_ref(q, _f64(cos), _f64(sin), h, code, half, rot)
         k = rope_merged_ref(k, _f64(cos), _f64(sin), h, code, half, rot)
-    return attention_f64(q * scale, k, v, h, None if bias is None else _f64(bias))
+    return attention_f64(_cast(q * scale, cast), _cast(k, cast), v, h, None if bias is None else _f64(bias))
 
 
-def pk_cross_ref(q, kv, h, bias, rope_q, rope_k, scale):
-    """pk_cross_attention - reference :735-752 (RoPE positions 0..L-1 on q and on k)."""
+def pk_cross_ref(q, kv, h, bias, rope_q, rope_k, scale, cast=None):
+    """pk_cross_attention - reference :735-752 (RoPE positions 0..L-1 on q and on k); cast as in
+    pk_self_ref."""
     q = _f64(q)
     kv = _f64(kv)
     E = q.shape[-1]
@@ -210,7 +221,7 @@ def pk_cross_ref(q, kv, h, bias, rope_q, rope_k, scale):
         k = rope_merged_ref(k, _f64(rope_k[0]), _f64(rope_k[1]), h, *rope_k[2:])
     if q.shape[0] != k.shape[0]:
         q = np.broadcast_to(q, (k.shape[0],) + q.shape[1:])
-    return attention_f64(q * scale, k, v, h, None if bias is None else _f64(bias))
+    return attention_f64(_cast(q * scale, cast), _cast(k, cast), v, h, None if bias is None else _f64(bias))
 
 
 # -------------------------------------------------------------------------------------------

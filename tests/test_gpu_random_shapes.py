@@ -7,7 +7,8 @@ terms), a RoPE form (none, pairs, halves), bf16 or fp32 and the query sharpness.
 before each launch. Bars: tests/parity.py's for the forwards (2e-2 / 1e-4 times max |ref| for bf16 /
 fp32), with the absolute bar (2e-2 / 1e-4) taken times max(1, max |ref|): inputs drawn up to 2x N(0, 1)
 give outputs up to ~5, where half an ulp of the bf16 output alone is 1.6e-2; for the gradients 2e-2 /
-1e-4 times max(1, max |grad|), as in test_gpu_smallhead_bwd.py.
+1e-4 times max(1, max |grad|), as in test_gpu_smallhead_bwd.py. The packed ops' oracle rounds q' and k'
+to the input dtype where the reference's kernel does (`cast=`).
 """
 import numpy as np
 import pytest
@@ -139,7 +140,7 @@ def test_pk_self_random(dev, seed):
     x = (torch.randn(B, L, 3 * E, generator=g) * xs).to(dtype)
     out = pk.pk_self_attention(x.to(dev), H, None if kb is None else kb.to(dev), rope, 16 ** -0.5)
     torch.cuda.synchronize()
-    _check(out, O.pk_self_ref(x, H, kb, _rope_np(rope, L), 16 ** -0.5), dtype, f"pk_self_random_{seed}")
+    _check(out, O.pk_self_ref(x, H, kb, _rope_np(rope, L), 16 ** -0.5, cast=dtype), dtype, f"pk_self_random_{seed}")
 
 
 @pytest.mark.parametrize("seed", SEEDS)
@@ -160,7 +161,7 @@ def test_pk_cross_random(dev, seed):
     out = pk.pk_cross_attention(xd.expand(B, Lq, E) if shared else xd, y.to(dev), H,
                                 None if kb is None else kb.to(dev), rope, 16 ** -0.5)
     torch.cuda.synchronize()
-    ref = O.pk_cross_ref(x, y, H, kb, _rope_np(rope, Lq), _rope_np(rope, Lk), 16 ** -0.5)
+    ref = O.pk_cross_ref(x, y, H, kb, _rope_np(rope, Lq), _rope_np(rope, Lk), 16 ** -0.5, cast=dtype)
     _check(out, ref, dtype, f"pk_cross_random_{seed}")
 
 

@@ -434,3 +434,29 @@ def test_splash_bwd_finite_differences():
             args[which][idx] -= 2 * eps
             dn = f(*args)
             assert abs((up - dn) / (2 * eps) - grad[idx]) < 1e-6
+
+
+def test_operand_rounding_points():
+    # the packed ops' oracle option that rounds q' = rope(q) scale and k' = rope(k) to the input dtype
+    # where the reference's kernel casts them (scripts/tabicl_tpu_pallas_attn.py:500-501)
+    g = torch.Generator().manual_seed(91)
+    x = torch.randn(3, 40, 384, generator=g).double().numpy() * 3.0
+    r = O._cast(x, torch.bfloat16)
+    assert np.array_equal(O._cast(r, torch.bfloat16), r)  # representable: rounding again changes nothing
+    assert np.all(np.abs(r - x) <= 2.0 ** -8 * np.abs(x))  # within half a bf16 ulp: 8 significant bits
+    assert np.array_equal(O._cast(x, None), x)
+    # without RoPE and with a power-of-two scale the operands are exact in bf16: rounding changes nothing
+    qkv = torch.randn(2, 30, 384, generator=g).to(torch.bfloat16)
+    a = O.pk_self_ref(qkv, 8, None, None, 0.25)
+    b = O.pk_self_ref(qkv, 8, None, None, 0.25, cast=torch.bfloat16)
+    assert np.array_equal(a, b)
+    # with RoPE the rotated operands are not bf16 values: rounding moves the result, by ~2^-9 relative
+    rope = O.rope_tables_ref(O.textbook_freqs(16, 100000.0), 30, 128, 8, False)
+    a = O.pk_self_ref(qkv, 8, None, rope, 0.25)
+    b = O.pk_self_ref(qkv, 8, None, rope, 0.25, cast=torch.bfloat16)
+    d = float(np.abs(a - b).max()) / float(np.abs(a).max())
+    assert 1e-5 < d < 2e-2, d
+    y = torch.randn(2, 30, 256, generator=g).to(torch.bfloat16)
+    qc = torch.randn(1, 7, 128, generator=g).to(torch.bfloat16)
+    assert np.array_equal(O.pk_cross_ref(qc, y, 8, None, None, None, 0.25),
+                          O.pk_cross_ref(qc, y, 8, None, None, None, 0.25, cast=torch.bfloat16))
