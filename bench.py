@@ -161,6 +161,21 @@ def bench_smallhead(configs: set, steps: int, warmup: int) -> list:
         by = 4.0 * B * (128 * E + 2 * 1024 * E + 128 * E)  # Q + K + V + O; the same for both passes
         line("C1 column ISAB-1 fp32 (hx)", ms1, fl, by, "f32", "mfma", "400 x 128 q over 1024 keys, 8x16, fp32")
         line("C1 column ISAB-2 fp32 (hx)", ms2, fl, by, "f32", "mfma", "400 x 1024 q over 128 keys, 8x16, fp32")
+    if "c1_batch" in configs:
+        # C1's two passes at other sequence counts: the cost per sequence shows what C1's 400 sequences
+        # pay for their grid's partial last round (not a BASELINE configuration)
+        for Lq, Lk, leg in ((128, 1024, "ISAB-1"), (1024, 128, "ISAB-2")):
+            for B in (256, 384, 400, 448, 512, 640, 768, 800, 1024):
+                g.manual_seed(0)
+                q = torch.randn(B, Lq, E, generator=g, device=dev) * 0.25
+                k = torch.randn(B, Lk, E, generator=g, device=dev)
+                v = torch.randn(B, Lk, E, generator=g, device=dev)
+                ms = _time(lambda: pk.hx_attention(q, k, v, H), steps, warmup)
+                fl = 4.0 * Lq * Lk * 16 * H * B
+                by = 4.0 * B * (2 * Lq * E + 2 * Lk * E)
+                line(f"C1 column {leg} fp32 (hx) at {B} sequences", ms, fl, by, "f32", "mfma",
+                     f"{B} x {Lq} q over {Lk} keys, 8x16, fp32; {1e3 * ms / B:.3f} us per sequence")
+                del q, k, v
     if configs & {"c2", "all"}:
         g.manual_seed(1)
         B, L = 16384, 104
@@ -899,8 +914,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-c3", action="store_true", help="default run: skip the C3 line printed before the headline")
     ap.add_argument("--config", default="c4",
-                    help="c4 (default) is the headline line; c1, c2, c3, c5, train, hxf, icl_layer, icl_stage, "
-                         "icl_masked, query "
+                    help="c4 (default) is the headline line; c1, c1_batch, c2, c3, c5, train, hxf, icl_layer, "
+                         "icl_stage, icl_masked, query "
                          "(comma-separated) or all print the other BASELINE configs' lines, the fwd+bwd training "
                          "lines, the folded first-ISAB lines, the ICL cache build / attention sub-layer lines, the "
                          "cached ICL query stage (12 blocks with norms and feed-forward), key-masked ICL launches "
@@ -914,8 +929,8 @@ def main() -> int:
     import torch
 
     configs = set(args.config.split(","))
-    if not configs <= {"c1", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "icl_masked", "query",
-                       "all"}:
+    if not configs <= {"c1", "c1_batch", "c2", "c3", "c4", "c5", "train", "hxf", "icl_layer", "icl_stage", "icl_masked",
+                       "query", "all"}:
         ap.error(f"unknown --config {args.config}")
     if configs != {"c4"}:
         torch.cuda.set_device(0)
