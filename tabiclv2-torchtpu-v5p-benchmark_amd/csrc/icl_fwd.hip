@@ -793,7 +793,7 @@ struct IpCtx {
   const float* lb;
 };
 
-// Queue the copy of the tile at key k0 into the buffer at LDS byte address buf: wave w copies K
+// Queue the copy of the tile at key k0 into tile buffer bi (LDS byte address lds0 + bi 16 KB): wave w copies K
 // rows 16w..16w+15 and V rows 16w..16w+15, 8 rows (1 KB) per instruction, from the tile's
 // (wave-uniform) base plus each lane's 32-bit offset. Rows 16w+8.. share the swizzle of rows 16w..
 // (it depends on row & 7). Rows past `valid` are read from row valid-1 (in bounds, and finite
