@@ -6,7 +6,8 @@ Each case captures one call on static input tensors, then replays the graph thre
 each replay the inputs are rewritten in place by eager work, and after it the graph's output must
 equal (bit for bit) an eager call of the same op on the same inputs, with a synchronisation in
 between. Cases: the cached ICL attention with a valid length (pipelined kernel, trust-flag gate, key
-split merge), the same with a prefix key mask (device-side prefix reduction), the ragged ICL entry
+split merge), the same with a prefix key mask (device-side prefix reduction) and with masks that are
+not prefix masks (the pipelined kernel's masked instance, the gate's exact recompute), the ragged ICL entry
 point (device-built list of live work items, row counts rewritten between replays), the persistent
 row-stage kernel (pk_self, RoPE), the few-query streaming hxq with a key mask, and a training step of
 the ICL attention (forward with statistics, autograd backward through the dq and dk/dv kernels).
@@ -74,6 +75,32 @@ def test_graph_icl_prefix_key_mask(dev):
 
     refresh(0)
     print("[graph] icl key mask", flush=True)
+    _replays(dev, lambda: icl.icl_sdpa(q, k, v, None, bias), (q, k, v, bias), refresh)
+
+
+def test_graph_icl_scattered_key_mask(dev):
+    # masks that are not prefix masks (the pipelined kernel's masked instance), rewritten between
+    # replays: every row scattered, then rows 0-1 prefix masks and rows 2-3 scattered, then row 3
+    # masked everywhere (its work items recomputed by the gated exact kernel inside the graph)
+    import tabicl_mi355_icl as icl
+    g = torch.Generator(device=dev).manual_seed(74)
+    q = torch.randn(4, 8, 600, 64, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(4, 8, 9000, 64, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(4, 8, 9000, 64, generator=g, device=dev).to(torch.bfloat16)
+    bias = torch.zeros(4, 9000, device=dev)
+    fmin = torch.finfo(torch.float32).min
+
+    def refresh(step):
+        bias.copy_(torch.where(torch.rand(4, 9000, generator=g, device=dev) < 0.1, fmin, 0.0))
+        if step >= 1:
+            bias[:2] = 0.0
+            bias[0, 7000:] = fmin
+            bias[1, 4000:] = fmin
+        if step == 2:
+            bias[3] = fmin
+
+    refresh(0)
+    print("[graph] icl scattered key mask", flush=True)
     _replays(dev, lambda: icl.icl_sdpa(q, k, v, None, bias), (q, k, v, bias), refresh)
 
 
