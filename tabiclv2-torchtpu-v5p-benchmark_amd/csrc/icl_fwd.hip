@@ -799,7 +799,8 @@ struct IpCtx {
 // (it depends on row & 7). Rows past `valid` are read from row valid-1 (in bounds, and finite
 // whenever the visible rows are); k0 < valid always. KB: and each wave copies the tile's 64 mask
 // entries into its own slot of the buffer's mask rows (entries past `valid` from entry valid-1).
-template <bool KB = false>
+// FULL: the caller knows that k0 + 64 <= valid (no row to clamp: no per-lane compare or select).
+template <bool KB = false, bool FULL = false>
 __device__ __forceinline__ void ip_issue(const IpCtx& c, int bi, int k0) {
   const uint32_t buf = c.lds0 + bi * IP_TILE * 2;
   const bf16* kt = c.kbase + (int64_t)k0 * c.k_st;
@@ -811,7 +812,7 @@ __device__ __forceinline__ void ip_issue(const IpCtx& c, int bi, int k0) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int j = i & 1;
-    const bool in = c.lrow + 8 * j < lim;
+    const bool in = FULL || c.lrow + 8 * j < lim;
     const uint32_t off = i < 2 ? (in ? c.koff + (uint32_t)(j * 16 * c.k_st) : kcl)
                                : (in ? c.voff + (uint32_t)(j * 16 * c.v_st) : vcl);
     lds_dma16_s(off, i < 2 ? kt : vt, buf + (i < 2 ? 0 : ICL_KT * ICL_D * 2) + (16 * c.wave + 8 * j) * ICL_D * 2);
@@ -833,7 +834,8 @@ template <bool KB> __device__ __forceinline__ void ip_join_tile() {
 // softmax of the second half, S of the next tile's first half (unless LAST), PV of this tile's first
 // half. B = t % IP_NBUF when the caller knows it (unrolled sweep: buffer addresses become
 // immediate offsets), else -1.
-template <bool FIRST, bool LAST, int B = -1, bool KB = false>
+// FULL: tile t + IP_NBUF - 1, the one this iteration queues, lies below `valid` (the steady state).
+template <bool FIRST, bool LAST, int B = -1, bool KB = false, bool FULL = false>
 __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&sB)[2], bf16x8 (&pA)[2][2],
                                         bf16x8 (&pB)[2][2], bf16 (*lds)[IP_TILE], const IpCtx& c, int t) {
   const int b = B >= 0 ? B : t % IP_NBUF;
@@ -847,7 +849,8 @@ __device__ __forceinline__ void ip_iter(IpState& st, f32x16 (&sA)[2], f32x16 (&s
   ip_phase<false, true, !FIRST, KB>(st, sA, sB, pA, pB, lk, lb, 32, lvp, 32, k0, c.valid, c.sc, c.lane);
   static_assert(IP_NBUF == 4, "one tile's copies may stay in flight below");
   ip_join_tile<KB>();
-  ip_issue<KB>(c, (b + IP_NBUF - 1) % IP_NBUF, min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1) * ICL_KT);
+  ip_issue<KB, FULL>(c, (b + IP_NBUF - 1) % IP_NBUF,
+                     (FULL ? c.t0 + t + IP_NBUF - 1 : min(c.t0 + t + IP_NBUF - 1, c.t0 + c.nt - 1)) * ICL_KT);
   ip_phase<false, !LAST, true, KB>(st, sB, sA, pB, pA, lkn, lbn, 0, lv, 0, k0 + 32, c.valid, c.sc, c.lane);
 }
 
@@ -1031,11 +1034,12 @@ __global__ __launch_bounds__(IP_NW * 64, 2) void icl_pipe_kernel(IclParams p) {
     if (nfull > 1) {
       ip_iter<true, false, -1, KB>(st, sA, sB, pA, pB, lds, c, 0);
       int t = 1;
-      for (; t + IP_NBUF < nfull; t += IP_NBUF) {  // t % IP_NBUF == 1 at the top
-        ip_iter<false, false, 1, KB>(st, sA, sB, pA, pB, lds, c, t);
-        ip_iter<false, false, 2, KB>(st, sA, sB, pA, pB, lds, c, t + 1);
-        ip_iter<false, false, 3, KB>(st, sA, sB, pA, pB, lds, c, t + 2);
-        ip_iter<false, false, 0, KB>(st, sA, sB, pA, pB, lds, c, t + 3);
+      // t % IP_NBUF == 1 at the top; the four iterations queue tiles t + 3 .. t + 6, all below nfull
+      for (; t + IP_NBUF + 2 < nfull; t += IP_NBUF) {
+        ip_iter<false, false, 1, KB, true>(st, sA, sB, pA, pB, lds, c, t);
+        ip_iter<false, false, 2, KB, true>(st, sA, sB, pA, pB, lds, c, t + 1);
+        ip_iter<false, false, 3, KB, true>(st, sA, sB, pA, pB, lds, c, t + 2);
+        ip_iter<false, false, 0, KB, true>(st, sA, sB, pA, pB, lds, c, t + 3);
       }
       for (; t + 1 < nfull; ++t) ip_iter<false, false, -1, KB>(st, sA, sB, pA, pB, lds, c, t);
       ip_iter<false, true, -1, KB>(st, sA, sB, pA, pB, lds, c, nfull - 1);
